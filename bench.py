@@ -1,0 +1,139 @@
+#!/usr/bin/env python3
+"""Benchmark: bit-exact fp32 greedy decode, SmolLM2-135M shape, bs=1, on one
+MI355X, plus the strict-order GEMV roofline and the CPU baseline.
+
+A step is one greedy decode step of the hot path: device argmax of the logits
+already computed, their witness fold on the host, and the forward pass of the
+chosen token (30 layers + LM head).  The workload is the 32-token prompt plus
+256 generated tokens of the SmolLM2-135M-shape synthetic model (seeded BF16
+weights ~N(0,0.02)); `--warmup` steps run first, then `--steps` are timed.
+When warmup + steps == 256 the run's witness digest is checked against the
+reference driver's digest for the same inputs (tests/golden).
+
+Prints ONE JSON line on stdout.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "cis2-lab-archive_amd"))
+sys.path.insert(0, os.path.join(ROOT, "tests"))
+
+METRIC = "bit-exact fp32 decode tok/s (SmolLM2-135M shape, bs=1); GEMV HBM GB/s % peak"
+HBM_PEAK_GBS = 8000.0
+CPU_REF_TOKS = 5.189  # C reference decode, SmolLM2-135M, 1 thread (rust-1 RESULT.md:26)
+SEED = 20261201
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def gemv_roofline(M=1536, K=576, copies=128, iters=4096):
+    """Strict-order GEMV at the config-1 shape, W rotated through `copies`
+    replicas (copies*3.5 MB > the 256 MB Infinity Cache), timed with HIP
+    events on the kernel's own stream."""
+    from cis2amd import GemvPlan, artifacts
+    W = artifacts.gen_f32(SEED, 1, M * K, 0.02).reshape(M, K)
+    plan = GemvPlan(W, copies=copies)
+    plan.time(256)
+    ms = plan.time(iters)
+    algo_bytes = 4 * M * K + 4 * K + 4 * M
+    achieved = algo_bytes / (ms * 1e-3) / 1e9
+    plan.close()
+    return {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
+            "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+            "kernel": "k_gemv %dx%d strict order" % (M, K), "us_per_launch": round(ms * 1e3, 3),
+            "algorithmic_bytes": algo_bytes}
+
+
+def cpu_baseline(spec, weights, prompt, seconds=15.0):
+    """The oracle (this repository's CPU restatement, bit-identical to the
+    reference) timed on the host: 1 thread, forward passes at consecutive
+    positions, stopping after about `seconds`."""
+    import numpy as np
+
+    import _oracle as O
+    m = O.OracleModel(spec, weights, max_pos=len(prompt) + 512, threads=1)
+    logits = np.empty(spec.vocab, np.float32)
+    L = O.lib()
+    t0 = time.perf_counter()
+    n = 0
+    tok = int(prompt[0])
+    while True:
+        L.orc_forward(m.m, n, tok, O.ptr(logits, O.c_fp), O.TRACE_FN(), None)
+        n += 1
+        tok = int(prompt[n]) if n < len(prompt) else int(L.orc_argmax(O.ptr(logits, O.c_fp), spec.vocab))
+        if time.perf_counter() - t0 > seconds or n >= len(prompt) + 500:
+            break
+    dt = time.perf_counter() - t0
+    return {"value": round(n / dt, 3), "unit": "tok/s", "cores": 1, "kind": "port",
+            "sample": "%d forward passes (positions 0..%d) of the same model, 1 thread, %.1f s"
+                      % (n, n - 1, dt)}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=240)
+    ap.add_argument("--warmup", type=int, default=16)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-roofline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    a = ap.parse_args()
+    if a.gpus != 1:
+        print("bench.py: this build runs on one GPU only (the pinned-order decode does not shard "
+              "across GPUs here); use --gpus 1", file=sys.stderr)
+        sys.exit(2)
+    from cis2amd import Cis2Model, artifacts
+    spec = artifacts.SPECS["smollm2-135m"]
+    t = time.perf_counter()
+    weights = artifacts.Weights(spec, SEED)
+    prompt = artifacts.prompt_ids(SEED, spec.vocab, 32)
+    log("weights generated in %.1fs" % (time.perf_counter() - t))
+    total = a.warmup + a.steps
+    model = Cis2Model(spec, weights, max_pos=len(prompt) + total)
+    t = time.perf_counter()
+    model.begin(prompt, total)
+    prefill_s = time.perf_counter() - t
+    model.steps(a.warmup)
+    t0 = time.perf_counter()
+    model.steps(a.steps)
+    t1 = time.perf_counter()
+    res = model.end(total)
+    dt = t1 - t0
+    value = a.steps / dt
+    witness_ok = None
+    fx_path = os.path.join(ROOT, "tests", "golden", "model_fixtures.json")
+    if total == 256 and os.path.exists(fx_path):
+        rec = json.load(open(fx_path)).get("smollm2-135m")
+        if rec and list(rec["prompt"]) == [int(v) for v in prompt]:
+            witness_ok = (res["witness"] == rec["witness"] and
+                          [int(v) for v in res["ids"]] == rec["tokens"])
+    log("decode: %d steps in %.3fs -> %.1f tok/s; prefill 32 tokens %.3fs; witness_ok=%s"
+        % (a.steps, dt, value, prefill_s, witness_ok))
+    model.close()
+    out = {
+        "metric": METRIC, "value": round(value, 3), "unit": "tok/s", "n_gpus": 1,
+        "steps": a.steps, "warmup": a.warmup, "ms_per_step": round(dt * 1e3 / a.steps, 4),
+        "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": round(value / CPU_REF_TOKS, 2), "dtype": "f32", "data": "synthetic",
+        "config": {"workload": "SmolLM2-135M-shape fp32 greedy decode, bs=1, 32-token prompt "
+                               "+ 256 generated tokens, seeded BF16 weights ~N(0,0.02)",
+                   "global_batch": 1, "seq_len": len(prompt) + total, "parallelism": "none"},
+        "witness_bit_exact": witness_ok, "witness": res["witness"],
+    }
+    if not a.no_roofline:
+        out["roofline"] = gemv_roofline()
+        log("gemv roofline:", out["roofline"])
+    if not a.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline(spec, weights, prompt, a.cpu_seconds)
+        log("cpu baseline:", out["cpu_baseline"])
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,223 @@
+// cis2_artifacts.hpp — host-side readers for the artifacts the CIS-2 driver
+// consumes: config.json, model.safetensors (BF16), and the decimal --ids
+// file.  Error behaviour follows the reference driver: a malformed input is
+// reported on stderr with a FATAL: prefix and the process exits with status 2
+// (code/cis2-fp/gpu/cis2_model.h:255-359, cis2_host.cpp:26-45).
+#pragma once
+#include <stdint.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <string>
+#include <utility>
+#include <vector>
+
+namespace cis2 {
+
+[[noreturn]] inline void fatal(const std::string& msg) {
+  fprintf(stderr, "FATAL: %s\n", msg.c_str());
+  exit(2);
+}
+
+// ---- JSON (the subset config.json and safetensors headers use) -----------
+struct JValue {
+  enum Kind { NUL, BOOL, NUM, STR, ARR, OBJ } kind = NUL;
+  bool b = false;
+  double num = 0.0;  // strtod: correctly rounded decimal -> binary64
+  std::string str;
+  std::vector<JValue> arr;
+  std::vector<std::pair<std::string, JValue>> obj;
+  const JValue* find(const char* key) const {
+    if (kind != OBJ) return nullptr;
+    for (auto& kv : obj)
+      if (kv.first == key) return &kv.second;
+    return nullptr;
+  }
+};
+
+class JParser {
+ public:
+  JParser(const char* b, const char* e) : p_(b), e_(e) {}
+  JValue value() {
+    skip();
+    if (p_ >= e_) fatal("JSON parse error: unexpected end");
+    JValue v;
+    char ch = *p_;
+    if (ch == '{') {
+      v.kind = JValue::OBJ;
+      ++p_;
+      skip();
+      if (p_ < e_ && *p_ == '}') { ++p_; return v; }
+      while (true) {
+        skip();
+        std::string k = string();
+        skip();
+        if (p_ >= e_ || *p_ != ':') fatal("JSON parse error: expected ':'");
+        ++p_;
+        v.obj.emplace_back(std::move(k), value());
+        skip();
+        if (p_ < e_ && *p_ == ',') { ++p_; continue; }
+        if (p_ < e_ && *p_ == '}') { ++p_; return v; }
+        fatal("JSON parse error: expected ',' or '}'");
+      }
+    }
+    if (ch == '[') {
+      v.kind = JValue::ARR;
+      ++p_;
+      skip();
+      if (p_ < e_ && *p_ == ']') { ++p_; return v; }
+      while (true) {
+        v.arr.push_back(value());
+        skip();
+        if (p_ < e_ && *p_ == ',') { ++p_; continue; }
+        if (p_ < e_ && *p_ == ']') { ++p_; return v; }
+        fatal("JSON parse error: expected ',' or ']'");
+      }
+    }
+    if (ch == '"') { v.kind = JValue::STR; v.str = string(); return v; }
+    if (lit("true")) { v.kind = JValue::BOOL; v.b = true; return v; }
+    if (lit("false")) { v.kind = JValue::BOOL; v.b = false; return v; }
+    if (lit("null")) return v;
+    std::string num;
+    while (p_ < e_ && strchr("+-0123456789.eE", *p_)) num.push_back(*p_++);
+    if (num.empty()) fatal("JSON parse error: expected a value");
+    char* stop = nullptr;
+    v.kind = JValue::NUM;
+    v.num = strtod(num.c_str(), &stop);
+    if (*stop) fatal("JSON parse error: bad number " + num);
+    return v;
+  }
+
+ private:
+  void skip() {
+    while (p_ < e_ && (*p_ == ' ' || *p_ == '\n' || *p_ == '\r' || *p_ == '\t')) ++p_;
+  }
+  bool lit(const char* w) {
+    size_t n = strlen(w);
+    if ((size_t)(e_ - p_) >= n && memcmp(p_, w, n) == 0) { p_ += n; return true; }
+    return false;
+  }
+  std::string string() {
+    if (p_ >= e_ || *p_ != '"') fatal("JSON parse error: expected string");
+    ++p_;
+    std::string s;
+    while (p_ < e_ && *p_ != '"') {
+      char c = *p_++;
+      if (c != '\\') { s.push_back(c); continue; }
+      if (p_ >= e_) fatal("JSON parse error: truncated escape");
+      char x = *p_++;
+      switch (x) {
+        case 'n': s.push_back('\n'); break;
+        case 't': s.push_back('\t'); break;
+        case 'r': s.push_back('\r'); break;
+        case 'b': s.push_back('\b'); break;
+        case 'f': s.push_back('\f'); break;
+        case 'u': {
+          if (e_ - p_ < 4) fatal("JSON parse error: truncated \\u");
+          unsigned cp = (unsigned)strtoul(std::string(p_, 4).c_str(), nullptr, 16);
+          p_ += 4;
+          s.push_back(cp < 0x80 ? (char)cp : '?');
+          break;
+        }
+        default: s.push_back(x);
+      }
+    }
+    if (p_ >= e_) fatal("JSON parse error: unterminated string");
+    ++p_;
+    return s;
+  }
+  const char* p_;
+  const char* e_;
+};
+
+inline std::string read_file(const std::string& path) {
+  FILE* f = fopen(path.c_str(), "rb");
+  if (!f) fatal("cannot open " + path);
+  std::string s;
+  char buf[1 << 16];
+  size_t n;
+  while ((n = fread(buf, 1, sizeof buf, f)) > 0) s.append(buf, n);
+  fclose(f);
+  return s;
+}
+
+inline JValue parse_json(const std::string& text) {
+  JParser p(text.data(), text.data() + text.size());
+  return p.value();
+}
+
+// ---- safetensors -------------------------------------------------------------
+struct TensorView {
+  std::string name, dtype;
+  std::vector<uint64_t> shape;
+  uint64_t begin = 0, end = 0;
+};
+
+struct SafeTensors {
+  std::string blob;
+  uint64_t data_off = 0;
+  std::vector<TensorView> tensors;
+
+  void open(const std::string& path) {
+    blob = read_file(path);
+    if (blob.size() < 8) fatal("safetensors too short");
+    uint64_t hlen = 0;
+    for (int i = 0; i < 8; ++i) hlen |= (uint64_t)(unsigned char)blob[i] << (8 * i);
+    if (hlen > blob.size() - 8) fatal("safetensors header length out of range");
+    JValue j = parse_json(blob.substr(8, hlen));
+    if (j.kind != JValue::OBJ) fatal("safetensors header not an object");
+    data_off = 8 + hlen;
+    for (auto& kv : j.obj) {
+      if (kv.first == "__metadata__") continue;
+      const JValue *dt = kv.second.find("dtype"), *sh = kv.second.find("shape"),
+                   *of = kv.second.find("data_offsets");
+      if (!dt || !sh || !of || of->arr.size() != 2) continue;
+      TensorView t;
+      t.name = kv.first;
+      t.dtype = dt->str;
+      for (auto& d : sh->arr) t.shape.push_back((uint64_t)d.num);
+      t.begin = (uint64_t)of->arr[0].num;
+      t.end = (uint64_t)of->arr[1].num;
+      tensors.push_back(t);
+    }
+  }
+  const TensorView* find(const std::string& n) const {
+    for (auto& t : tensors)
+      if (t.name == n) return &t;
+    return nullptr;
+  }
+  // Validated BF16 payload of a tensor (dtype, shape, byte range), as
+  // Cis2SafeTensors::load_bf16 checks them (cis2_model.h:340-360).
+  const uint16_t* bf16(const TensorView& t, const std::vector<uint64_t>& expect) const {
+    if (t.dtype != "BF16") fatal("tensor " + t.name + " dtype " + t.dtype + ", expected BF16");
+    if (t.shape != expect) fatal("tensor " + t.name + " shape mismatch");
+    uint64_t nbytes = t.end - t.begin;
+    if (t.end < t.begin || nbytes % 2 || data_off + t.end > blob.size())
+      fatal("tensor " + t.name + " byte range invalid");
+    uint64_t want = 1;
+    for (auto d : expect) want *= d;
+    if (nbytes / 2 != want) fatal("tensor " + t.name + " element count mismatch");
+    return reinterpret_cast<const uint16_t*>(blob.data() + data_off + t.begin);
+  }
+};
+
+// ---- --ids file: decimal ids separated by whitespace or commas ------------------
+inline std::vector<uint32_t> read_ids(const std::string& path) {
+  std::string t = read_file(path);
+  std::vector<uint32_t> ids;
+  size_t i = 0;
+  while (i < t.size()) {
+    while (i < t.size() && strchr("\n\r \t,", t[i])) ++i;
+    if (i >= t.size()) break;
+    size_t j = i;
+    while (j < t.size() && t[j] >= '0' && t[j] <= '9') ++j;
+    if (j == i) fatal(path + ": expected a decimal token id at byte " + std::to_string(i));
+    ids.push_back((uint32_t)strtoul(t.substr(i, j - i).c_str(), nullptr, 10));
+    i = j;
+  }
+  if (ids.empty()) fatal(path + ": no token ids");
+  return ids;
+}
+
+}  // namespace cis2

@@ -1,0 +1,193 @@
+// cis2_host_main.cpp — command-line driver over the gfx950 C ABI with the
+// flags and stdout line protocol of the reference driver
+// (code/cis2-fp/gpu/cis2_host.cpp:61-249; Rust src/main.rs:1231-1262), so
+// the service runner's regexes (code/cis2-llm/server/app/runner.py:25-31)
+// and digest/trace gates (code/cis2-fp/gpu/Makefile:160-184) apply as is.
+//
+//   cis2_host --weights-dir DIR --ids FILE [--gen-toks N] [--trace FILE]
+//             [--prompt-idx I] [--device D]
+#include "cis2_amd.h"
+#include "cis2_artifacts.hpp"
+#include "cis2_sha256.hpp"
+
+#include <stdio.h>
+#include <string.h>
+
+#include <string>
+#include <vector>
+
+using namespace cis2;
+
+namespace {
+
+std::string hex(const uint8_t* d, size_t n) {
+  static const char* k = "0123456789abcdef";
+  std::string s;
+  for (size_t i = 0; i < n; ++i) {
+    s.push_back(k[d[i] >> 4]);
+    s.push_back(k[d[i] & 15]);
+  }
+  return s;
+}
+
+std::string ids_list(const std::vector<uint32_t>& v) {
+  std::string s = "[";
+  for (size_t i = 0; i < v.size(); ++i) {
+    if (i) s += ", ";
+    s += std::to_string(v[i]);
+  }
+  return s + "]";
+}
+
+void file_sha(const std::string& path, uint8_t out[32]) {
+  std::string b = read_file(path);
+  sha256(b.data(), b.size(), out);
+}
+
+struct TraceSink {
+  FILE* fp = nullptr;
+};
+void trace_cb(int pos, int layer, const char* op, const uint8_t sha[32], void* user) {
+  TraceSink* t = static_cast<TraceSink*>(user);
+  fprintf(t->fp, "pos=%d layer=%d op=%s sha256=%s\n", pos, layer, op, hex(sha, 32).c_str());
+}
+
+uint32_t num_key(const JValue& cfg, const char* k) {
+  const JValue* v = cfg.find(k);
+  if (!v) fatal(std::string("config.json missing ") + k);
+  return (uint32_t)v->num;
+}
+
+}  // namespace
+
+int main(int argc, char** argv) {
+  std::string weights_dir = "weights", ids_path, trace_path;
+  int gen_toks = 16, prompt_idx = 0;
+  for (int i = 1; i < argc; ++i) {
+    std::string a = argv[i];
+    if (a == "--weights-dir" && i + 1 < argc) weights_dir = argv[++i];
+    else if (a == "--ids" && i + 1 < argc) ids_path = argv[++i];
+    else if (a == "--gen-toks" && i + 1 < argc) gen_toks = atoi(argv[++i]);
+    else if (a == "--trace" && i + 1 < argc) trace_path = argv[++i];
+    else if (a == "--prompt-idx" && i + 1 < argc) prompt_idx = atoi(argv[++i]);
+    else { fprintf(stderr, "FATAL: unknown CLI argument: %s\n", a.c_str()); return 2; }
+  }
+  if (ids_path.empty()) fatal("--ids FILE is required");
+  if (gen_toks < 0) fatal("--gen-toks must be >= 0");
+  const std::string wpath = weights_dir + "/model.safetensors";
+  const std::string tpath = weights_dir + "/tokenizer.json";
+  const std::string cpath = weights_dir + "/config.json";
+  uint8_t hdr[96];
+  file_sha(wpath, hdr);
+  file_sha(tpath, hdr + 32);
+  file_sha(cpath, hdr + 64);
+
+  JValue cfgj = parse_json(read_file(cpath));
+  cis2_config cfg;
+  memset(&cfg, 0, sizeof cfg);
+  cfg.hidden = num_key(cfgj, "hidden_size");
+  cfg.inter = num_key(cfgj, "intermediate_size");
+  cfg.n_layers = num_key(cfgj, "num_hidden_layers");
+  cfg.n_heads = num_key(cfgj, "num_attention_heads");
+  cfg.n_kv_heads = num_key(cfgj, "num_key_value_heads");
+  cfg.vocab = num_key(cfgj, "vocab_size");
+  const JValue* eps = cfgj.find("rms_norm_eps");
+  const JValue* theta = cfgj.find("rope_theta");
+  if (!eps) fatal("config.json missing rms_norm_eps");
+  if (!theta) fatal("config.json missing rope_theta");
+  cfg.eps = (float)eps->num;  // one narrowing, as `as f32` does
+  cfg.rope_theta = theta->num;
+  if (cfg.n_heads == 0) fatal("num_attention_heads must be > 0");
+  cfg.head_dim = cfg.hidden / cfg.n_heads;
+  if (const JValue* hd = cfgj.find("head_dim")) cfg.head_dim = (uint32_t)hd->num;
+  cfg.tied = 1;
+  if (const JValue* t = cfgj.find("tie_word_embeddings"))
+    cfg.tied = (t->kind == JValue::BOOL) ? (t->b ? 1 : 0) : 1;
+  std::vector<uint32_t> prompt = read_ids(ids_path);
+  cfg.max_pos = (uint32_t)(prompt.size() + gen_toks);
+  cfg.max_seqs = 1;
+  cfg.reduction_mode = 0;
+
+  cis2_ctx* ctx = nullptr;
+  int rc = cis2_ctx_create(&cfg, &ctx);
+  if (rc) fatal(std::string("cis2_ctx_create: ") + cis2_strerror(rc));
+
+  fprintf(stderr, "loading + widening weights (bf16 -> fp32, exact bit-shift)...\n");
+  SafeTensors st;
+  st.open(wpath);
+  const uint64_t H = cfg.hidden, I = cfg.inter, V = cfg.vocab;
+  const uint64_t QD = (uint64_t)cfg.n_heads * cfg.head_dim,
+                 KV = (uint64_t)cfg.n_kv_heads * cfg.head_dim, HD = cfg.head_dim;
+  auto load = [&](const std::string& name, std::vector<uint64_t> shape, bool optional) {
+    const TensorView* t = st.find(name);
+    if (!t) {
+      if (optional) return;
+      fatal("tensor " + name + " missing");
+    }
+    const uint16_t* p = st.bf16(*t, shape);
+    uint64_t n = 1;
+    for (auto d : shape) n *= d;
+    int r = cis2_upload_bf16(ctx, name.c_str(), p, n);
+    if (r) fatal("upload " + name + ": " + cis2_last_error(ctx));
+  };
+  load("model.embed_tokens.weight", {V, H}, false);
+  for (uint32_t l = 0; l < cfg.n_layers; ++l) {
+    std::string p = "model.layers." + std::to_string(l) + ".";
+    load(p + "input_layernorm.weight", {H}, false);
+    load(p + "post_attention_layernorm.weight", {H}, false);
+    load(p + "self_attn.q_proj.weight", {QD, H}, false);
+    load(p + "self_attn.k_proj.weight", {KV, H}, false);
+    load(p + "self_attn.v_proj.weight", {KV, H}, false);
+    load(p + "self_attn.o_proj.weight", {H, QD}, false);
+    load(p + "mlp.gate_proj.weight", {I, H}, false);
+    load(p + "mlp.up_proj.weight", {I, H}, false);
+    load(p + "mlp.down_proj.weight", {H, I}, false);
+    load(p + "self_attn.q_proj.bias", {QD}, true);
+    load(p + "self_attn.k_proj.bias", {KV}, true);
+    load(p + "self_attn.v_proj.bias", {KV}, true);
+    load(p + "self_attn.q_norm.weight", {HD}, true);
+    load(p + "self_attn.k_norm.weight", {HD}, true);
+  }
+  load("model.norm.weight", {H}, false);
+  if (!cfg.tied) load("lm_head.weight", {V, H}, false);
+  st.blob.clear();
+  st.blob.shrink_to_fit();
+  rc = cis2_check_ready(ctx);
+  if (rc) fatal(cis2_last_error(ctx));
+  fprintf(stderr, "weights loaded.\n");
+  fprintf(stderr, "[prompt %d] token ids (%zu toks): %s\n", prompt_idx, prompt.size(),
+          ids_list(prompt).c_str());
+
+  TraceSink sink;
+  if (!trace_path.empty()) {
+    sink.fp = fopen(trace_path.c_str(), "wb");
+    if (!sink.fp) fatal("cannot write " + trace_path);
+    cis2_trace_enable(ctx, trace_cb, &sink);
+  }
+  std::vector<uint32_t> ids(prompt.size() + gen_toks);
+  uint8_t wit[32], adig[32];
+  rc = cis2_decode(ctx, 0, prompt.data(), (uint32_t)prompt.size(), (uint32_t)gen_toks, hdr,
+                   ids.data(), wit, adig, nullptr);
+  if (rc) fatal(std::string("decode: ") + cis2_last_error(ctx));
+  if (sink.fp) fclose(sink.fp);
+  for (int s = 0; s < gen_toks; ++s)
+    fprintf(stderr, "[run1] step %d: token_id=%u\n", s, ids[prompt.size() + s]);
+
+  uint8_t table[32], invf[32];
+  cis2_digests(ctx, table, invf);
+  printf("weights_sha256=%s\n", hex(hdr, 32).c_str());
+  printf("tokenizer_sha256=%s\n", hex(hdr + 32, 32).c_str());
+  printf("config_sha256=%s\n", hex(hdr + 64, 32).c_str());
+  printf("table_digest=%s\n", hex(table, 32).c_str());
+  printf("inv_freq_table_digest=%s\n", hex(invf, 32).c_str());
+  printf("prompt_idx=%d prompt_tokens=%s\n", prompt_idx, ids_list(prompt).c_str());
+  printf("prompt_idx=%d run1_tokens=%s\n", prompt_idx, ids_list(ids).c_str());
+  printf("prompt_idx=%d run1_witness_digest=%s\n", prompt_idx, hex(wit, 32).c_str());
+  printf("prompt_idx=%d run1_argmax_digest=%s\n", prompt_idx, hex(adig, 32).c_str());
+  printf("prompt_idx=%d reduction_mode=sequential\n", prompt_idx);
+  printf("CIS2_REF digest=%s prompt_idx=%d prompt_toks=%zu gen_toks=%d dtype=fp32 "
+         "reduction_mode=sequential\n",
+         hex(wit, 32).c_str(), prompt_idx, prompt.size(), gen_toks);
+  cis2_ctx_destroy(ctx);
+  return 0;
+}

@@ -1,0 +1,767 @@
+// cis2_runtime.hip — the C ABI of include/cis2_amd.h: device memory,
+// tensor upload, the per-token kernel sequence, the greedy decode loop with
+// the pipelined witness fold, tracing, and the standalone GEMV plan.
+#include "cis2_amd.h"
+#include "cis2_kernels.hpp"
+#include "cis2_sha256.hpp"
+
+#include <hip/hip_runtime.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <map>
+#include <string>
+#include <vector>
+
+using namespace cis2;
+
+namespace {
+
+// Pinned constants in the declared order of the table digest (spec §6.6;
+// code/cis2-fp/src/math.rs:472-500): f32 words, with PI_2 as 8 bytes.
+void table_digest(uint8_t out[32]) {
+  Sha256 s;
+  const uint32_t head[9] = {0x3fb8aa3bu, 0x3f318000u, 0xb95e8083u, 0x39506967u, 0x3ab743ceu,
+                            0x3c088908u, 0x3d2aa9c1u, 0x3e2aaaaau, 0x3f000000u};
+  for (uint32_t w : head) s.update_u32le(w);
+  const uint64_t pio2 = 0x3ff921fb54442d18ull;
+  s.update_u32le((uint32_t)pio2);
+  s.update_u32le((uint32_t)(pio2 >> 32));
+  const uint32_t tail[18] = {0xbe2aaaa3u, 0x3c08839eu, 0xb94ca1f9u, 0x3d2aaaa5u, 0xbab6061au,
+                             0x37ccf5ceu, 0x3f3504f3u, 0xb95e8083u, 0x3f318000u, 0x3d9021bbu,
+                             0xbdebd1b8u, 0x3def251bu, 0xbdfe5d4fu, 0x3e11e9bfu, 0xbe2aae50u,
+                             0x3e4cceadu, 0xbe7ffffcu, 0x3eaaaaaau};
+  for (uint32_t w : tail) s.update_u32le(w);
+  s.finish(out);
+}
+
+enum Kind { VEC, GEMV, EMBED, LMHEAD };
+struct Slot {
+  float** ptr;
+  uint64_t count;
+  Kind kind;
+  uint32_t M, K;
+  bool required;
+};
+
+struct Layer {
+  float *ln1 = nullptr, *ln2 = nullptr, *wq = nullptr, *wk = nullptr, *wv = nullptr,
+        *wo = nullptr, *wg = nullptr, *wu = nullptr, *wd = nullptr;
+  float *bq = nullptr, *bk = nullptr, *bv = nullptr, *qn = nullptr, *kn = nullptr;
+};
+
+const int kRing = 4;
+
+// A greedy decode in progress (cis2_decode_begin/steps/end).
+struct Session {
+  bool active = false;
+  uint32_t seq = 0, n_prompt = 0, max_steps = 0;
+  uint32_t enqueued = 0, folded = 0;
+  Sha256 w;
+  std::vector<uint32_t> ids;
+  std::vector<uint8_t> step_dig;
+};
+
+}  // namespace
+
+struct cis2_ctx {
+  cis2_config cfg;
+  uint32_t qd = 0, kvd = 0;
+  float scale = 0.0f;
+  hipStream_t st = nullptr;
+  std::vector<Layer> L;
+  float *embed = nullptr, *lm_head = nullptr, *final_norm = nullptr;
+  float *inv_freq = nullptr, *rope_cs = nullptr;
+  float* kv = nullptr;  // [max_seqs][n_layers][K | V][kvd * max_pos]
+  float *h = nullptr, *h2 = nullptr, *x = nullptr, *q = nullptr, *k = nullptr, *v = nullptr,
+        *att = nullptr, *o = nullptr, *g = nullptr, *u = nullptr, *hid = nullptr,
+        *dn = nullptr, *logits = nullptr, *scores = nullptr, *probs = nullptr;
+  uint32_t* d_tok = nullptr;     // [2]: input token of the current step, argmax out
+  uint32_t* d_err = nullptr;
+  uint32_t* d_prompt = nullptr;  // [max_pos]: prompt ids of the sequence being prefilled
+  std::map<std::string, Slot> slots;
+  std::map<std::string, bool> present;
+  uint8_t table_dig[32], invf_dig[32];
+  cis2_trace_fn trace = nullptr;
+  void* trace_user = nullptr;
+  std::string err;
+  // decode ring (pinned host)
+  float* ring = nullptr;
+  uint32_t* ring_tok = nullptr;
+  hipEvent_t ring_ev[kRing];
+  Session sess;
+  std::vector<void*> allocs;
+};
+
+struct cis2_gemv_plan {
+  uint32_t M, K, copies;
+  float *W = nullptr, *x = nullptr, *y = nullptr;
+  hipStream_t st = nullptr;
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+};
+
+namespace {
+
+int fail(cis2_ctx* c, int code, const std::string& msg) {
+  if (c) c->err = msg;
+  return code;
+}
+int hipfail(cis2_ctx* c, hipError_t e, const char* what) {
+  return fail(c, CIS2_E_DEVICE, std::string(what) + ": " + hipGetErrorString(e));
+}
+#define HIPCHK(c, expr, what)                       \
+  do {                                              \
+    hipError_t _e = (expr);                         \
+    if (_e != hipSuccess) return hipfail(c, _e, what); \
+  } while (0)
+
+float* dalloc(cis2_ctx* c, size_t nfloats) {
+  void* p = nullptr;
+  if (hipMalloc(&p, nfloats * sizeof(float) + 16) != hipSuccess) return nullptr;
+  c->allocs.push_back(p);
+  return static_cast<float*>(p);
+}
+
+void add_slot(cis2_ctx* c, const std::string& name, float** ptr, uint64_t count, Kind kind,
+              uint32_t M, uint32_t K, bool required) {
+  c->slots[name] = Slot{ptr, count, kind, M, K, required};
+}
+
+// Checkpoint tensor names as the reference loader reads them
+// (code/cis2-fp/gpu/cis2_host.cpp:133-158; Qwen3 q/k norms
+// labs/w1x-qwen3/scripts/qwen3-port.diff:139-141).
+void build_registry(cis2_ctx* c) {
+  const cis2_config& f = c->cfg;
+  const uint32_t H = f.hidden, I = f.inter, V = f.vocab, QD = c->qd, KV = c->kvd;
+  add_slot(c, "model.embed_tokens.weight", &c->embed, (uint64_t)V * H, EMBED, V, H, true);
+  add_slot(c, "model.norm.weight", &c->final_norm, H, VEC, 0, 0, true);
+  if (!f.tied) add_slot(c, "lm_head.weight", &c->lm_head, (uint64_t)V * H, LMHEAD, V, H, true);
+  for (uint32_t l = 0; l < f.n_layers; ++l) {
+    Layer& Ly = c->L[l];
+    char p[64];
+    snprintf(p, sizeof p, "model.layers.%u.", l);
+    std::string s(p);
+    add_slot(c, s + "input_layernorm.weight", &Ly.ln1, H, VEC, 0, 0, true);
+    add_slot(c, s + "post_attention_layernorm.weight", &Ly.ln2, H, VEC, 0, 0, true);
+    add_slot(c, s + "self_attn.q_proj.weight", &Ly.wq, (uint64_t)QD * H, GEMV, QD, H, true);
+    add_slot(c, s + "self_attn.k_proj.weight", &Ly.wk, (uint64_t)KV * H, GEMV, KV, H, true);
+    add_slot(c, s + "self_attn.v_proj.weight", &Ly.wv, (uint64_t)KV * H, GEMV, KV, H, true);
+    add_slot(c, s + "self_attn.o_proj.weight", &Ly.wo, (uint64_t)H * QD, GEMV, H, QD, true);
+    add_slot(c, s + "mlp.gate_proj.weight", &Ly.wg, (uint64_t)I * H, GEMV, I, H, true);
+    add_slot(c, s + "mlp.up_proj.weight", &Ly.wu, (uint64_t)I * H, GEMV, I, H, true);
+    add_slot(c, s + "mlp.down_proj.weight", &Ly.wd, (uint64_t)H * I, GEMV, H, I, true);
+    add_slot(c, s + "self_attn.q_proj.bias", &Ly.bq, QD, VEC, 0, 0, false);
+    add_slot(c, s + "self_attn.k_proj.bias", &Ly.bk, KV, VEC, 0, 0, false);
+    add_slot(c, s + "self_attn.v_proj.bias", &Ly.bv, KV, VEC, 0, 0, false);
+    add_slot(c, s + "self_attn.q_norm.weight", &Ly.qn, f.head_dim, VEC, 0, 0, false);
+    add_slot(c, s + "self_attn.k_norm.weight", &Ly.kn, f.head_dim, VEC, 0, 0, false);
+  }
+}
+
+float* kcache(cis2_ctx* c, uint32_t seq, uint32_t l) {
+  size_t per = (size_t)c->kvd * c->cfg.max_pos;
+  return c->kv + ((size_t)seq * c->cfg.n_layers + l) * 2 * per;
+}
+float* vcache(cis2_ctx* c, uint32_t seq, uint32_t l) {
+  return kcache(c, seq, l) + (size_t)c->kvd * c->cfg.max_pos;
+}
+
+// Per-op trace hook: synchronise, pull the op output, hash it.
+int emit(cis2_ctx* c, int pos, int layer, const char* op, const float* dev, size_t n) {
+  if (!c->trace) return CIS2_OK;
+  HIPCHK(c, hipStreamSynchronize(c->st), "trace sync");
+  std::vector<float> hbuf(n);
+  HIPCHK(c, hipMemcpy(hbuf.data(), dev, n * sizeof(float), hipMemcpyDeviceToHost), "trace copy");
+  uint8_t d[32];
+  sha256(hbuf.data(), n * sizeof(float), d);
+  c->trace(pos, layer, op, d, c->trace_user);
+  return CIS2_OK;
+}
+#define EMIT(pos, layer, op, dev, n)                       \
+  do {                                                     \
+    int _r = emit(c, (pos), (layer), (op), (dev), (n));    \
+    if (_r) return _r;                                     \
+  } while (0)
+#define LAUNCH(expr, what) HIPCHK(c, (expr), what)
+
+// One decode step for `seq` at `pos`; the input token is read on the device
+// from *d_tokp.  Op order: code/cis2-fp/src/main.rs:355-529 (C++ mirror
+// gpu/cis2_model.h:685-760; Qwen3 QK-norm qwen3-port.diff:66-80).
+int forward_one(cis2_ctx* c, uint32_t seq, uint32_t pos, const uint32_t* d_tokp,
+                bool want_logits) {
+  const cis2_config& f = c->cfg;
+  const uint32_t H = f.hidden, I = f.inter, hd = f.head_dim, QD = c->qd, KV = c->kvd;
+  hipStream_t s = c->st;
+  const bool tr = c->trace != nullptr;
+  LAUNCH(launch_embed(c->embed, d_tokp, c->h, H, f.vocab, c->d_err, s), "embed");
+  EMIT(pos, -1, "embedding", c->h, H);
+  for (uint32_t l = 0; l < f.n_layers; ++l) {
+    const Layer& Ly = c->L[l];
+    float* kc = kcache(c, seq, l);
+    float* vc = vcache(c, seq, l);
+    LAUNCH(launch_rmsnorm(c->h, Ly.ln1, f.eps, H, 1, c->x, s), "norm1");
+    EMIT(pos, l, "norm1", c->x, H);
+    GemvSeg qkv[3] = {{Ly.wq, c->x, Ly.bq, c->q, QD, H, 0},
+                      {Ly.wk, c->x, Ly.bk, c->k, KV, H, 0},
+                      {Ly.wv, c->x, Ly.bv, c->v, KV, H, 0}};
+    LAUNCH(launch_gemv(qkv, 3, s), "qkv");
+    EMIT(pos, l, "q", c->q, QD);
+    EMIT(pos, l, "k", c->k, KV);
+    EMIT(pos, l, "v", c->v, KV);
+    if (Ly.qn) {
+      LAUNCH(launch_rmsnorm(c->q, Ly.qn, f.eps, hd, f.n_heads, c->q, s), "q_norm");
+      EMIT(pos, l, "q_norm", c->q, QD);
+    }
+    if (Ly.kn) {
+      LAUNCH(launch_rmsnorm(c->k, Ly.kn, f.eps, hd, f.n_kv_heads, c->k, s), "k_norm");
+      EMIT(pos, l, "k_norm", c->k, KV);
+    }
+    LAUNCH(launch_rope_store(c->q, c->k, c->v, c->rope_cs, pos, f.n_heads, f.n_kv_heads, hd,
+                             f.max_pos, kc, vc, s),
+           "rope");
+    EMIT(pos, l, "rope_q", c->q, QD);
+    EMIT(pos, l, "rope_k", c->k, KV);
+    LAUNCH(launch_attention(c->q, kc, vc, pos, f.n_heads, f.n_kv_heads, hd, f.max_pos,
+                            c->scale, c->att, tr ? c->scores : nullptr,
+                            tr ? c->probs : nullptr, s),
+           "attention");
+    EMIT(pos, l, "scores", c->scores, (size_t)f.n_heads * (pos + 1));
+    EMIT(pos, l, "softmax", c->probs, (size_t)f.n_heads * (pos + 1));
+    EMIT(pos, l, "attn_out", c->att, QD);
+    GemvSeg os[1] = {{Ly.wo, c->att, c->h, c->h2, H, QD, 1}};
+    if (tr) {  // the trace needs o_proj on its own
+      GemvSeg ot[1] = {{Ly.wo, c->att, nullptr, c->o, H, QD, 0}};
+      LAUNCH(launch_gemv(ot, 1, s), "o_proj");
+      EMIT(pos, l, "o_proj", c->o, H);
+    }
+    LAUNCH(launch_gemv(os, 1, s), "o_proj+resid");
+    std::swap(c->h, c->h2);
+    EMIT(pos, l, "resid1", c->h, H);
+    LAUNCH(launch_rmsnorm(c->h, Ly.ln2, f.eps, H, 1, c->x, s), "norm2");
+    EMIT(pos, l, "norm2", c->x, H);
+    LAUNCH(launch_gate_up_silu(Ly.wg, Ly.wu, c->x, c->g, c->u, c->hid, I, H, s), "gate_up");
+    EMIT(pos, l, "gate", c->g, I);
+    EMIT(pos, l, "up", c->u, I);
+    EMIT(pos, l, "silu_mul", c->hid, I);
+    if (tr) {
+      GemvSeg dt[1] = {{Ly.wd, c->hid, nullptr, c->dn, H, I, 0}};
+      LAUNCH(launch_gemv(dt, 1, s), "down");
+      EMIT(pos, l, "down", c->dn, H);
+    }
+    GemvSeg ds[1] = {{Ly.wd, c->hid, c->h, c->h2, H, I, 1}};
+    LAUNCH(launch_gemv(ds, 1, s), "down+resid");
+    std::swap(c->h, c->h2);
+    EMIT(pos, l, "resid2", c->h, H);
+  }
+  if (want_logits || tr) {
+    LAUNCH(launch_rmsnorm(c->h, c->final_norm, f.eps, H, 1, c->x, s), "final_norm");
+    EMIT(pos, -1, "final_norm", c->x, H);
+    GemvSeg lm[1] = {{c->lm_head, c->x, nullptr, c->logits, f.vocab, H, 0}};
+    LAUNCH(launch_gemv(lm, 1, s), "lm_head");
+    EMIT(pos, -1, "logits", c->logits, f.vocab);
+  }
+  return CIS2_OK;
+}
+
+int check_err_flag(cis2_ctx* c) {
+  uint32_t e = 0;
+  HIPCHK(c, hipMemcpy(&e, c->d_err, 4, hipMemcpyDeviceToHost), "error flag");
+  if (e) {
+    (void)hipMemset(c->d_err, 0, 4);
+    return fail(c, CIS2_E_RANGE, "token id out of range on the device");
+  }
+  return CIS2_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* cis2_strerror(int code) {
+  switch (code) {
+    case CIS2_OK: return "ok";
+    case CIS2_E_ARG: return "invalid argument";
+    case CIS2_E_UNSUPPORTED: return "unsupported configuration";
+    case CIS2_E_MISSING_TENSOR: return "required tensor missing";
+    case CIS2_E_SHAPE: return "tensor element count mismatch";
+    case CIS2_E_NAME: return "unknown tensor name";
+    case CIS2_E_FPENV: return "device FTZ/DAZ self-test failed";
+    case CIS2_E_DEVICE: return "HIP device error";
+    case CIS2_E_OOM: return "out of memory";
+    case CIS2_E_RANGE: return "position or token out of range";
+    default: return "unknown error";
+  }
+}
+
+const char* cis2_last_error(const cis2_ctx* ctx) { return ctx ? ctx->err.c_str() : ""; }
+
+void cis2_ctx_destroy(cis2_ctx* c) {
+  if (!c) return;
+  if (c->st) (void)hipStreamSynchronize(c->st);
+  for (void* p : c->allocs) (void)hipFree(p);
+  if (c->ring) (void)hipHostFree(c->ring);
+  if (c->ring_tok) (void)hipHostFree(c->ring_tok);
+  for (int i = 0; i < kRing; ++i)
+    if (c->ring_ev[i]) (void)hipEventDestroy(c->ring_ev[i]);
+  if (c->st) (void)hipStreamDestroy(c->st);
+  delete c;
+}
+
+int cis2_ctx_create(const cis2_config* cfg, cis2_ctx** out) {
+  if (!cfg || !out) return CIS2_E_ARG;
+  *out = nullptr;
+  const cis2_config f = *cfg;
+  if (f.hidden == 0 || f.inter == 0 || f.n_layers == 0 || f.n_heads == 0 || f.n_kv_heads == 0 ||
+      f.head_dim == 0 || f.vocab == 0 || f.max_pos == 0 || f.max_seqs == 0)
+    return CIS2_E_ARG;
+  if (f.reduction_mode != 0) return CIS2_E_UNSUPPORTED;
+  if (f.n_heads % f.n_kv_heads || f.head_dim % 2 || f.hidden % 4 || f.inter % 4 ||
+      (f.n_heads * f.head_dim) % 4 || f.max_pos > 16384 || f.head_dim > 1024)
+    return CIS2_E_UNSUPPORTED;
+  cis2_ctx* c = new cis2_ctx();
+  memset(c->ring_ev, 0, sizeof c->ring_ev);
+  c->cfg = f;
+  c->qd = f.n_heads * f.head_dim;
+  c->kvd = f.n_kv_heads * f.head_dim;
+  c->L.resize(f.n_layers);
+  if (hipStreamCreateWithFlags(&c->st, hipStreamNonBlocking) != hipSuccess) {
+    cis2_ctx_destroy(c);
+    return CIS2_E_DEVICE;
+  }
+  // FTZ/DAZ self-test on the device (spec §1.3).
+  {
+    uint32_t* probe = nullptr;
+    uint32_t hv[2] = {1u, 1u};
+    if (hipMalloc(&probe, 8) != hipSuccess) { cis2_ctx_destroy(c); return CIS2_E_OOM; }
+    hipError_t e = launch_fpenv_probe(probe, c->st);
+    if (e == hipSuccess) e = hipMemcpy(hv, probe, 8, hipMemcpyDeviceToHost);
+    (void)hipFree(probe);
+    if (e != hipSuccess) { cis2_ctx_destroy(c); return CIS2_E_DEVICE; }
+    if (hv[0] != 0u || hv[1] != 0u) { cis2_ctx_destroy(c); return CIS2_E_FPENV; }
+  }
+  const uint32_t H = f.hidden, I = f.inter, V = f.vocab;
+  const size_t wide = H > c->qd ? H : c->qd;
+  float** bufs[] = {&c->h, &c->h2, &c->x, &c->o, &c->dn};
+  for (float** b : bufs)
+    if (!(*b = dalloc(c, wide))) { cis2_ctx_destroy(c); return CIS2_E_OOM; }
+  if (!(c->q = dalloc(c, c->qd)) || !(c->att = dalloc(c, c->qd)) || !(c->k = dalloc(c, c->kvd)) ||
+      !(c->v = dalloc(c, c->kvd)) || !(c->g = dalloc(c, I)) || !(c->u = dalloc(c, I)) ||
+      !(c->hid = dalloc(c, I)) || !(c->logits = dalloc(c, V)) ||
+      !(c->scores = dalloc(c, (size_t)f.n_heads * f.max_pos)) ||
+      !(c->probs = dalloc(c, (size_t)f.n_heads * f.max_pos)) ||
+      !(c->inv_freq = dalloc(c, f.head_dim / 2)) ||
+      !(c->rope_cs = dalloc(c, (size_t)f.head_dim * f.max_pos)) ||
+      !(c->kv = dalloc(c, (size_t)f.max_seqs * f.n_layers * 2 * c->kvd * f.max_pos))) {
+    cis2_ctx_destroy(c);
+    return CIS2_E_OOM;
+  }
+  void* tp = nullptr;
+  if (hipMalloc(&tp, 16) != hipSuccess) { cis2_ctx_destroy(c); return CIS2_E_OOM; }
+  c->allocs.push_back(tp);
+  c->d_tok = static_cast<uint32_t*>(tp);
+  c->d_err = c->d_tok + 2;
+  (void)hipMemset(tp, 0, 16);
+  if (hipMalloc(&tp, (size_t)f.max_pos * sizeof(uint32_t)) != hipSuccess) {
+    cis2_ctx_destroy(c);
+    return CIS2_E_OOM;
+  }
+  c->allocs.push_back(tp);
+  c->d_prompt = static_cast<uint32_t*>(tp);
+  (void)hipMemset(c->kv, 0, (size_t)f.max_seqs * f.n_layers * 2 * c->kvd * f.max_pos * sizeof(float));
+  // Pinned inv_freq and rotation table; theta narrowed to f32 once
+  // (code/cis2-fp/src/main.rs:849-858).
+  if (launch_rope_table((float)f.rope_theta, f.head_dim, f.max_pos, c->inv_freq, c->rope_cs,
+                        c->st) != hipSuccess ||
+      hipStreamSynchronize(c->st) != hipSuccess) {
+    cis2_ctx_destroy(c);
+    return CIS2_E_DEVICE;
+  }
+  std::vector<float> invf(f.head_dim / 2);
+  (void)hipMemcpy(invf.data(), c->inv_freq, invf.size() * sizeof(float), hipMemcpyDeviceToHost);
+  sha256(invf.data(), invf.size() * sizeof(float), c->invf_dig);
+  table_digest(c->table_dig);
+  // scale = rsqrt_cr((f32)head_dim), computed on the device like every
+  // other pinned value (code/cis2-fp/src/main.rs:372).
+  {
+    float hdv = (float)f.head_dim, sc = 0.0f;
+    if (cis2_math_map(5, &hdv, &sc, 1) != CIS2_OK) { cis2_ctx_destroy(c); return CIS2_E_DEVICE; }
+    c->scale = sc;
+  }
+  if (hipHostMalloc(reinterpret_cast<void**>(&c->ring), (size_t)kRing * V * sizeof(float)) !=
+          hipSuccess ||
+      hipHostMalloc(reinterpret_cast<void**>(&c->ring_tok), kRing * 2 * sizeof(uint32_t)) !=
+          hipSuccess) {
+    cis2_ctx_destroy(c);
+    return CIS2_E_OOM;
+  }
+  for (int i = 0; i < kRing; ++i)
+    if (hipEventCreateWithFlags(&c->ring_ev[i], hipEventDisableTiming) != hipSuccess) {
+      cis2_ctx_destroy(c);
+      return CIS2_E_DEVICE;
+    }
+  build_registry(c);
+  *out = c;
+  return CIS2_OK;
+}
+
+int cis2_upload_bf16(cis2_ctx* c, const char* name, const uint16_t* bf16, uint64_t n) {
+  if (!c || !name || !bf16) return CIS2_E_ARG;
+  auto it = c->slots.find(name);
+  if (it == c->slots.end()) return fail(c, CIS2_E_NAME, std::string("unknown tensor ") + name);
+  Slot& s = it->second;
+  if (n != s.count)
+    return fail(c, CIS2_E_SHAPE, std::string("tensor ") + name + " element count mismatch");
+  uint16_t* stage = nullptr;
+  HIPCHK(c, hipMalloc(&stage, n * sizeof(uint16_t)), "stage alloc");
+  hipError_t e = hipMemcpy(stage, bf16, n * sizeof(uint16_t), hipMemcpyHostToDevice);
+  float* wide = nullptr;
+  if (e == hipSuccess) e = hipMalloc(&wide, n * sizeof(float));
+  if (e == hipSuccess) e = launch_widen(stage, wide, n, c->st);
+  float* dst = *s.ptr;
+  if (e == hipSuccess && s.kind == VEC) {
+    if (!dst && !(dst = dalloc(c, n))) e = hipErrorOutOfMemory;
+    if (e == hipSuccess) e = hipMemcpyAsync(dst, wide, n * sizeof(float), hipMemcpyDeviceToDevice, c->st);
+  } else if (e == hipSuccess && s.kind == EMBED) {
+    if (!dst && !(dst = dalloc(c, n))) e = hipErrorOutOfMemory;
+    if (e == hipSuccess) e = hipMemcpyAsync(dst, wide, n * sizeof(float), hipMemcpyDeviceToDevice, c->st);
+    if (e == hipSuccess && c->cfg.tied) {
+      if (!c->lm_head && !(c->lm_head = dalloc(c, blocked_floats(s.M, s.K)))) e = hipErrorOutOfMemory;
+      if (e == hipSuccess) e = launch_relayout(wide, c->lm_head, s.M, s.K, c->st);
+    }
+  } else if (e == hipSuccess) {  // GEMV / LMHEAD: blocked layout
+    if (!dst && !(dst = dalloc(c, blocked_floats(s.M, s.K)))) e = hipErrorOutOfMemory;
+    if (e == hipSuccess) e = launch_relayout(wide, dst, s.M, s.K, c->st);
+  }
+  if (e == hipSuccess) e = hipStreamSynchronize(c->st);
+  (void)hipFree(stage);
+  if (wide) (void)hipFree(wide);
+  if (e != hipSuccess) return hipfail(c, e, "upload");
+  *s.ptr = dst;
+  c->present[name] = true;
+  return CIS2_OK;
+}
+
+int cis2_check_ready(cis2_ctx* c) {
+  if (!c) return CIS2_E_ARG;
+  for (auto& kv : c->slots)
+    if (kv.second.required && !c->present.count(kv.first))
+      return fail(c, CIS2_E_MISSING_TENSOR, "tensor " + kv.first + " missing");
+  if (!c->lm_head) return fail(c, CIS2_E_MISSING_TENSOR, "LM head missing");
+  return CIS2_OK;
+}
+
+int cis2_digests(cis2_ctx* c, uint8_t table[32], uint8_t inv_freq[32]) {
+  if (!c || !table || !inv_freq) return CIS2_E_ARG;
+  memcpy(table, c->table_dig, 32);
+  memcpy(inv_freq, c->invf_dig, 32);
+  return CIS2_OK;
+}
+
+int cis2_reset_seq(cis2_ctx* c, uint32_t seq) {
+  if (!c || seq >= c->cfg.max_seqs) return CIS2_E_ARG;
+  size_t per = (size_t)c->cfg.n_layers * 2 * c->kvd * c->cfg.max_pos;
+  HIPCHK(c, hipMemsetAsync(c->kv + seq * per, 0, per * sizeof(float), c->st), "reset");
+  HIPCHK(c, hipStreamSynchronize(c->st), "reset sync");
+  return CIS2_OK;
+}
+
+int cis2_trace_enable(cis2_ctx* c, cis2_trace_fn fn, void* user) {
+  if (!c) return CIS2_E_ARG;
+  c->trace = fn;
+  c->trace_user = user;
+  return CIS2_OK;
+}
+
+int cis2_forward(cis2_ctx* c, uint32_t n, const uint32_t* seq, const uint32_t* pos,
+                 const uint32_t* tok, float* logits_host, uint32_t* argmax_out) {
+  if (!c || !seq || !pos || !tok) return CIS2_E_ARG;
+  int r = cis2_check_ready(c);
+  if (r) return r;
+  for (uint32_t i = 0; i < n; ++i) {
+    if (seq[i] >= c->cfg.max_seqs) return fail(c, CIS2_E_ARG, "sequence index out of range");
+    if (pos[i] >= c->cfg.max_pos) return fail(c, CIS2_E_RANGE, "position beyond max_pos");
+    if (tok[i] >= c->cfg.vocab) return fail(c, CIS2_E_RANGE, "token id >= vocab");
+    HIPCHK(c, hipMemcpyAsync(c->d_tok, &tok[i], 4, hipMemcpyHostToDevice, c->st), "token");
+    r = forward_one(c, seq[i], pos[i], c->d_tok, true);
+    if (r) return r;
+    if (argmax_out) LAUNCH(launch_argmax(c->logits, c->cfg.vocab, c->d_tok + 1, c->st), "argmax");
+    HIPCHK(c, hipStreamSynchronize(c->st), "forward sync");
+    if (logits_host)
+      HIPCHK(c, hipMemcpy(logits_host + (size_t)i * c->cfg.vocab, c->logits,
+                          (size_t)c->cfg.vocab * sizeof(float), hipMemcpyDeviceToHost),
+             "logits copy");
+    if (argmax_out)
+      HIPCHK(c, hipMemcpy(&argmax_out[i], c->d_tok + 1, 4, hipMemcpyDeviceToHost), "argmax copy");
+  }
+  return check_err_flag(c);
+}
+
+// Greedy decode + witness (code/cis2-fp/gpu/cis2_host.cpp:176-218).  The
+// host enqueues step s, then folds step s - (kRing-1) while the GPU runs:
+// argmax and the next token stay on the device, the logits stream to a
+// pinned ring slot with an event per slot.
+static int fold_step(cis2_ctx* c) {
+  Session& S = c->sess;
+  const uint32_t V = c->cfg.vocab;
+  const uint32_t step = S.folded;
+  const int slot = step % kRing;
+  HIPCHK(c, hipEventSynchronize(c->ring_ev[slot]), "ring wait");
+  const float* lg = c->ring + (size_t)slot * V;
+  const uint32_t nid = c->ring_tok[slot * 2];
+  S.w.update(lg, (size_t)V * sizeof(float));
+  S.w.update_u32le(nid);
+  sha256(lg, (size_t)V * sizeof(float), S.step_dig.data() + 32 * (size_t)step);
+  S.ids[S.n_prompt + step] = nid;
+  S.folded++;
+  return CIS2_OK;
+}
+
+int cis2_decode_begin(cis2_ctx* c, uint32_t seq, const uint32_t* prompt, uint32_t n_prompt,
+                      uint32_t max_steps, const uint8_t hdr[96]) {
+  if (!c || !prompt || !hdr) return CIS2_E_ARG;
+  if (n_prompt == 0 || seq >= c->cfg.max_seqs) return fail(c, CIS2_E_ARG, "bad prompt or seq");
+  if ((uint64_t)n_prompt + max_steps > c->cfg.max_pos)
+    return fail(c, CIS2_E_RANGE, "prompt + gen_toks exceeds max_pos");
+  for (uint32_t i = 0; i < n_prompt; ++i)
+    if (prompt[i] >= c->cfg.vocab) return fail(c, CIS2_E_RANGE, "prompt token id >= vocab");
+  int r = cis2_check_ready(c);
+  if (r) return r;
+  r = cis2_reset_seq(c, seq);
+  if (r) return r;
+  Session& S = c->sess;
+  S = Session();
+  S.seq = seq;
+  S.n_prompt = n_prompt;
+  S.max_steps = max_steps;
+  S.ids.assign(prompt, prompt + n_prompt);
+  S.ids.resize((size_t)n_prompt + max_steps);
+  S.step_dig.assign(32 * (size_t)max_steps, 0);
+  S.w.update(hdr, 96);
+  S.w.update(c->table_dig, 32);
+  S.w.update(c->invf_dig, 32);
+  for (uint32_t i = 0; i < n_prompt; ++i) S.w.update_u32le(prompt[i]);
+  // Prefill: every prompt position; only the last needs its logits.
+  HIPCHK(c, hipMemcpy(c->d_prompt, prompt, (size_t)n_prompt * 4, hipMemcpyHostToDevice),
+         "prompt upload");
+  for (uint32_t p = 0; p < n_prompt; ++p) {
+    r = forward_one(c, seq, p, c->d_prompt + p, p + 1 == n_prompt);
+    if (r) return r;
+  }
+  HIPCHK(c, hipStreamSynchronize(c->st), "prefill sync");
+  S.active = true;
+  return check_err_flag(c);
+}
+
+int cis2_decode_steps(cis2_ctx* c, uint32_t n) {
+  if (!c) return CIS2_E_ARG;
+  Session& S = c->sess;
+  if (!S.active) return fail(c, CIS2_E_ARG, "no decode session");
+  if ((uint64_t)S.enqueued + n > S.max_steps) return fail(c, CIS2_E_RANGE, "steps beyond max_steps");
+  const uint32_t V = c->cfg.vocab;
+  hipStream_t s = c->st;
+  int r;
+  for (uint32_t i = 0; i < n; ++i) {
+    const uint32_t step = S.enqueued;
+    const int slot = step % kRing;
+    if (step >= S.folded + kRing) {  // slot reuse: fold what it held first
+      r = fold_step(c);
+      if (r) return r;
+    }
+    LAUNCH(launch_argmax(c->logits, V, c->d_tok, s), "argmax");
+    HIPCHK(c, hipMemcpyAsync(c->ring + (size_t)slot * V, c->logits, (size_t)V * sizeof(float),
+                             hipMemcpyDeviceToHost, s),
+           "logits d2h");
+    HIPCHK(c, hipMemcpyAsync(c->ring_tok + slot * 2, c->d_tok, 4, hipMemcpyDeviceToHost, s),
+           "token d2h");
+    HIPCHK(c, hipEventRecord(c->ring_ev[slot], s), "ring event");
+    r = forward_one(c, S.seq, S.n_prompt + step, c->d_tok, true);
+    if (r) return r;
+    S.enqueued++;
+  }
+  while (S.folded < S.enqueued) {
+    r = fold_step(c);
+    if (r) return r;
+  }
+  HIPCHK(c, hipStreamSynchronize(s), "decode sync");
+  return check_err_flag(c);
+}
+
+int cis2_decode_end(cis2_ctx* c, uint32_t* out_ids, uint8_t witness[32],
+                    uint8_t argmax_digest[32], uint8_t* step_digests) {
+  if (!c || !out_ids || !witness || !argmax_digest) return CIS2_E_ARG;
+  Session& S = c->sess;
+  if (!S.active) return fail(c, CIS2_E_ARG, "no decode session");
+  while (S.folded < S.enqueued) {
+    int r = fold_step(c);
+    if (r) return r;
+  }
+  S.active = false;
+  const uint32_t total = S.n_prompt + S.enqueued;
+  S.w.finish(witness);
+  Sha256 a;
+  for (uint32_t i = 0; i < total; ++i) a.update_u32le(S.ids[i]);
+  a.finish(argmax_digest);
+  memcpy(out_ids, S.ids.data(), (size_t)total * 4);
+  if (step_digests) memcpy(step_digests, S.step_dig.data(), 32 * (size_t)S.enqueued);
+  return CIS2_OK;
+}
+
+int cis2_decode(cis2_ctx* c, uint32_t seq, const uint32_t* prompt, uint32_t n_prompt,
+                uint32_t gen_toks, const uint8_t hdr[96], uint32_t* out_ids, uint8_t witness[32],
+                uint8_t argmax_digest[32], uint8_t* step_digests) {
+  if (!c || !prompt || !hdr || !out_ids || !witness || !argmax_digest) return CIS2_E_ARG;
+  int r = cis2_decode_begin(c, seq, prompt, n_prompt, gen_toks, hdr);
+  if (!r) r = cis2_decode_steps(c, gen_toks);
+  if (!r) r = cis2_decode_end(c, out_ids, witness, argmax_digest, step_digests);
+  c->sess.active = false;
+  return r;
+}
+
+int cis2_decode_batch(cis2_ctx* c, uint32_t nseq, const uint32_t* prompts,
+                      const uint32_t* prompt_lens, uint32_t gen_toks, const uint8_t hdr[96],
+                      uint32_t* out_ids, uint8_t* witness, uint8_t* argmax_digest) {
+  if (!c || !prompts || !prompt_lens || !hdr || !out_ids || !witness || !argmax_digest)
+    return CIS2_E_ARG;
+  size_t in_off = 0, out_off = 0;
+  for (uint32_t b = 0; b < nseq; ++b) {
+    int r = cis2_decode(c, b % c->cfg.max_seqs, prompts + in_off, prompt_lens[b], gen_toks, hdr,
+                        out_ids + out_off, witness + 32 * (size_t)b,
+                        argmax_digest + 32 * (size_t)b, nullptr);
+    if (r) return r;
+    in_off += prompt_lens[b];
+    out_off += (size_t)prompt_lens[b] + gen_toks;
+  }
+  return CIS2_OK;
+}
+
+// ---- standalone GEMV ------------------------------------------------------
+
+int cis2_gemv_plan_create(uint32_t M, uint32_t K, uint32_t copies, const float* W,
+                          cis2_gemv_plan** out) {
+  if (!W || !out || M == 0 || K == 0 || K % 4 || copies == 0) return CIS2_E_ARG;
+  cis2_gemv_plan* p = new cis2_gemv_plan();
+  p->M = M; p->K = K; p->copies = copies;
+  const size_t per = blocked_floats(M, K);
+  float* rowmajor = nullptr;
+  hipError_t e = hipStreamCreateWithFlags(&p->st, hipStreamNonBlocking);
+  if (e == hipSuccess) e = hipMalloc(&p->W, per * copies * sizeof(float));
+  if (e == hipSuccess) e = hipMalloc(&p->x, (size_t)K * sizeof(float));
+  if (e == hipSuccess) e = hipMalloc(&p->y, ((size_t)M + 64) * sizeof(float));
+  if (e == hipSuccess) e = hipMalloc(&rowmajor, (size_t)M * K * sizeof(float));
+  if (e == hipSuccess) e = hipMemcpy(rowmajor, W, (size_t)M * K * sizeof(float), hipMemcpyHostToDevice);
+  for (uint32_t i = 0; e == hipSuccess && i < copies; ++i)
+    e = launch_relayout(rowmajor, p->W + per * i, M, K, p->st);
+  if (e == hipSuccess) e = hipStreamSynchronize(p->st);
+  if (e == hipSuccess) e = hipEventCreate(&p->e0);
+  if (e == hipSuccess) e = hipEventCreate(&p->e1);
+  if (rowmajor) (void)hipFree(rowmajor);
+  if (e != hipSuccess) {
+    cis2_gemv_plan_destroy(p);
+    return e == hipErrorOutOfMemory ? CIS2_E_OOM : CIS2_E_DEVICE;
+  }
+  *out = p;
+  return CIS2_OK;
+}
+
+int cis2_gemv_plan_run(cis2_gemv_plan* p, const float* x, float* y) {
+  if (!p || !x || !y) return CIS2_E_ARG;
+  hipError_t e = hipMemcpyAsync(p->x, x, (size_t)p->K * sizeof(float), hipMemcpyHostToDevice, p->st);
+  GemvSeg sg[1] = {{p->W, p->x, nullptr, p->y, p->M, p->K, 0}};
+  if (e == hipSuccess) e = launch_gemv(sg, 1, p->st);
+  if (e == hipSuccess) e = hipMemcpyAsync(y, p->y, (size_t)p->M * sizeof(float), hipMemcpyDeviceToHost, p->st);
+  if (e == hipSuccess) e = hipStreamSynchronize(p->st);
+  return e == hipSuccess ? CIS2_OK : CIS2_E_DEVICE;
+}
+
+int cis2_gemv_plan_time(cis2_gemv_plan* p, uint32_t iters, float* ms) {
+  if (!p || !ms || iters == 0) return CIS2_E_ARG;
+  const size_t per = blocked_floats(p->M, p->K);
+  hipError_t e = hipSuccess;
+  for (uint32_t i = 0; e == hipSuccess && i < p->copies; ++i) {  // warm-up pass
+    GemvSeg sg[1] = {{p->W + per * i, p->x, nullptr, p->y, p->M, p->K, 0}};
+    e = launch_gemv(sg, 1, p->st);
+  }
+  if (e == hipSuccess) e = hipEventRecord(p->e0, p->st);
+  for (uint32_t i = 0; e == hipSuccess && i < iters; ++i) {
+    GemvSeg sg[1] = {{p->W + per * (i % p->copies), p->x, nullptr, p->y, p->M, p->K, 0}};
+    e = launch_gemv(sg, 1, p->st);
+  }
+  if (e == hipSuccess) e = hipEventRecord(p->e1, p->st);
+  if (e == hipSuccess) e = hipEventSynchronize(p->e1);
+  float t = 0.0f;
+  if (e == hipSuccess) e = hipEventElapsedTime(&t, p->e0, p->e1);
+  if (e != hipSuccess) return CIS2_E_DEVICE;
+  *ms = t / (float)iters;
+  return CIS2_OK;
+}
+
+void cis2_gemv_plan_destroy(cis2_gemv_plan* p) {
+  if (!p) return;
+  if (p->st) (void)hipStreamSynchronize(p->st);
+  if (p->W) (void)hipFree(p->W);
+  if (p->x) (void)hipFree(p->x);
+  if (p->y) (void)hipFree(p->y);
+  if (p->e0) (void)hipEventDestroy(p->e0);
+  if (p->e1) (void)hipEventDestroy(p->e1);
+  if (p->st) (void)hipStreamDestroy(p->st);
+  delete p;
+}
+
+// ---- verification hooks -----------------------------------------------------
+
+int cis2_math_map(int fn, const float* in, float* out, uint64_t n) {
+  if (!in || !out || fn < 0 || fn > 6) return CIS2_E_ARG;
+  if (n == 0) return CIS2_OK;
+  float *di = nullptr, *dout = nullptr;
+  hipError_t e = hipMalloc(&di, n * sizeof(float));
+  if (e == hipSuccess) e = hipMalloc(&dout, n * sizeof(float));
+  if (e == hipSuccess) e = hipMemcpy(di, in, n * sizeof(float), hipMemcpyHostToDevice);
+  if (e == hipSuccess) e = launch_math_map(fn, di, dout, n, 0);
+  if (e == hipSuccess) e = hipMemcpy(out, dout, n * sizeof(float), hipMemcpyDeviceToHost);
+  if (di) (void)hipFree(di);
+  if (dout) (void)hipFree(dout);
+  return e == hipSuccess ? CIS2_OK : CIS2_E_DEVICE;
+}
+
+int cis2_math_chunk_hashes(int fn, uint32_t c0, uint32_t nchunks, uint64_t* out) {
+  if (!out || fn < 0 || fn > 6 || nchunks == 0 || (uint64_t)c0 + nchunks > 256) return CIS2_E_ARG;
+  unsigned long long* d = nullptr;
+  hipError_t e = hipMalloc(&d, nchunks * sizeof(unsigned long long));
+  if (e == hipSuccess) e = hipMemset(d, 0, nchunks * sizeof(unsigned long long));
+  for (uint32_t i = 0; e == hipSuccess && i < nchunks; ++i)
+    e = launch_math_hash(fn, (c0 + i) << 24, 1u << 24, d + i, 0);
+  if (e == hipSuccess) e = hipMemcpy(out, d, nchunks * sizeof(uint64_t), hipMemcpyDeviceToHost);
+  if (d) (void)hipFree(d);
+  return e == hipSuccess ? CIS2_OK : CIS2_E_DEVICE;
+}
+
+int cis2_div_map(const float* a, const float* b, float* out, uint64_t n) {
+  if (!a || !b || !out) return CIS2_E_ARG;
+  if (n == 0) return CIS2_OK;
+  float *da = nullptr, *db = nullptr, *dout = nullptr;
+  hipError_t e = hipMalloc(&da, n * sizeof(float));
+  if (e == hipSuccess) e = hipMalloc(&db, n * sizeof(float));
+  if (e == hipSuccess) e = hipMalloc(&dout, n * sizeof(float));
+  if (e == hipSuccess) e = hipMemcpy(da, a, n * sizeof(float), hipMemcpyHostToDevice);
+  if (e == hipSuccess) e = hipMemcpy(db, b, n * sizeof(float), hipMemcpyHostToDevice);
+  if (e == hipSuccess) e = launch_div_map(da, db, dout, n, 0);
+  if (e == hipSuccess) e = hipMemcpy(out, dout, n * sizeof(float), hipMemcpyDeviceToHost);
+  if (da) (void)hipFree(da);
+  if (db) (void)hipFree(db);
+  if (dout) (void)hipFree(dout);
+  return e == hipSuccess ? CIS2_OK : CIS2_E_DEVICE;
+}
+
+void cis2_sha256(const void* data, uint64_t n, uint8_t out[32]) { sha256(data, n, out); }
+
+int cis2_fpenv_probe(uint32_t out[2]) {
+  if (!out) return CIS2_E_ARG;
+  uint32_t* d = nullptr;
+  hipError_t e = hipMalloc(&d, 8);
+  if (e == hipSuccess) e = launch_fpenv_probe(d, 0);
+  if (e == hipSuccess) e = hipMemcpy(out, d, 8, hipMemcpyDeviceToHost);
+  if (d) (void)hipFree(d);
+  return e == hipSuccess ? CIS2_OK : CIS2_E_DEVICE;
+}
+
+}  // extern "C"

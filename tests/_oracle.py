@@ -1,0 +1,185 @@
+"""ctypes wrapper of the CPU oracle (oracle/liboracle.so).
+
+TEST INFRASTRUCTURE: the oracle is the checker.  Only tests/, the smoke()
+entry point and bench.py's cpu_baseline leg load it.
+"""
+import ctypes
+import os
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+ORACLE_PATH = os.path.join(ROOT, "oracle", "liboracle.so")
+REF_MATH_PATH = os.path.join(ROOT, "oracle", "_ref", "libref_math.so")
+
+c_u8p = ctypes.POINTER(ctypes.c_uint8)
+c_u16p = ctypes.POINTER(ctypes.c_uint16)
+c_u32p = ctypes.POINTER(ctypes.c_uint32)
+c_fp = ctypes.POINTER(ctypes.c_float)
+
+FN_IDS = {"exp": 0, "sin": 1, "cos": 2, "ln": 3, "silu": 4, "rsqrt": 5, "sqrt": 6}
+
+
+class OrcConfig(ctypes.Structure):
+    _fields_ = [("hidden", ctypes.c_int), ("inter", ctypes.c_int), ("n_layers", ctypes.c_int),
+                ("n_heads", ctypes.c_int), ("n_kv_heads", ctypes.c_int),
+                ("head_dim", ctypes.c_int), ("vocab", ctypes.c_int), ("tied", ctypes.c_int),
+                ("max_pos", ctypes.c_int), ("reduction", ctypes.c_int),
+                ("threads", ctypes.c_int), ("eps", ctypes.c_float),
+                ("rope_theta", ctypes.c_double)]
+
+
+TRACE_FN = ctypes.CFUNCTYPE(None, ctypes.c_int, ctypes.c_int, ctypes.c_char_p, c_u8p,
+                            ctypes.c_void_p)
+
+_o = None
+
+
+def lib():
+    global _o
+    if _o is None:
+        if not os.path.exists(ORACLE_PATH):
+            raise RuntimeError("oracle not built: make -C oracle")
+        L = ctypes.CDLL(ORACLE_PATH)
+        for n in ["orc_exp", "orc_sin", "orc_cos", "orc_ln", "orc_silu", "orc_rsqrt", "orc_sqrt"]:
+            getattr(L, n).restype = ctypes.c_float
+            getattr(L, n).argtypes = [ctypes.c_float]
+        L.orc_math_map.argtypes = [ctypes.c_int, c_fp, c_fp, ctypes.c_size_t]
+        L.orc_div_map.argtypes = [c_fp, c_fp, c_fp, ctypes.c_size_t]
+        L.orc_math_chunk_hash.restype = ctypes.c_uint64
+        L.orc_math_chunk_hash.argtypes = [ctypes.c_int, ctypes.c_uint32, ctypes.c_uint32]
+        for n in ["orc_dot_seq", "orc_dot_tree"]:
+            getattr(L, n).restype = ctypes.c_float
+            getattr(L, n).argtypes = [c_fp, c_fp, ctypes.c_int]
+        for n in ["orc_sum_seq", "orc_sum_tree"]:
+            getattr(L, n).restype = ctypes.c_float
+            getattr(L, n).argtypes = [c_fp, ctypes.c_int]
+        L.orc_gemv.argtypes = [c_fp, c_fp, c_fp, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                               ctypes.c_int]
+        L.orc_softmax.argtypes = [c_fp, ctypes.c_int, ctypes.c_int]
+        L.orc_argmax.restype = ctypes.c_uint32
+        L.orc_argmax.argtypes = [c_fp, ctypes.c_int]
+        L.orc_sha256.argtypes = [ctypes.c_void_p, ctypes.c_size_t, c_u8p]
+        L.orc_table_digest.argtypes = [c_u8p]
+        L.orc_inv_freq.argtypes = [ctypes.c_double, ctypes.c_int, c_fp, c_u8p]
+        L.orc_model_create.restype = ctypes.c_void_p
+        L.orc_model_create.argtypes = [ctypes.POINTER(OrcConfig)]
+        L.orc_model_destroy.argtypes = [ctypes.c_void_p]
+        L.orc_model_set_bf16.argtypes = [ctypes.c_void_p, ctypes.c_char_p, c_u16p, ctypes.c_size_t]
+        L.orc_model_digests.argtypes = [ctypes.c_void_p, c_u8p, c_u8p]
+        L.orc_forward.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_uint32, c_fp,
+                                  TRACE_FN, ctypes.c_void_p]
+        L.orc_decode.argtypes = [ctypes.c_void_p, c_u32p, ctypes.c_int, ctypes.c_int, c_u8p,
+                                 c_u32p, c_u8p, c_u8p, c_u8p, TRACE_FN, ctypes.c_void_p]
+        L.orc_fpenv_pin.restype = ctypes.c_int
+        _o = L
+        if L.orc_fpenv_pin() != 0:
+            raise RuntimeError("oracle FTZ/DAZ pin failed")
+    return _o
+
+
+def ref_math():
+    """The reference's own cis2_math.h compiled here (None if not built)."""
+    if not os.path.exists(REF_MATH_PATH):
+        return None
+    R = ctypes.CDLL(REF_MATH_PATH)
+    R.ref_math_map.argtypes = [ctypes.c_int, c_fp, c_fp, ctypes.c_size_t]
+    R.ref_math_chunk_hash.restype = ctypes.c_uint64
+    R.ref_math_chunk_hash.argtypes = [ctypes.c_int, ctypes.c_uint32, ctypes.c_uint32]
+    for n in ["ref_dot_seq", "ref_dot_tree"]:
+        getattr(R, n).restype = ctypes.c_float
+        getattr(R, n).argtypes = [c_fp, c_fp, ctypes.c_int]
+    R.ref_sum_tree.restype = ctypes.c_float
+    R.ref_sum_tree.argtypes = [c_fp, ctypes.c_int]
+    R.ref_softmax.argtypes = [c_fp, ctypes.c_int, ctypes.c_int]
+    return R
+
+
+def ptr(a, t):
+    return a.ctypes.data_as(t)
+
+
+def math_map(fn, x):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty_like(x)
+    lib().orc_math_map(FN_IDS[fn], ptr(x, c_fp), ptr(out, c_fp), x.size)
+    return out
+
+
+def div_map(a, b):
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    b = np.ascontiguousarray(b, dtype=np.float32)
+    out = np.empty_like(a)
+    lib().orc_div_map(ptr(a, c_fp), ptr(b, c_fp), ptr(out, c_fp), a.size)
+    return out
+
+
+def gemv(W, x, mode=0, threads=8):
+    W = np.ascontiguousarray(W, dtype=np.float32)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    M, K = W.shape
+    y = np.empty(M, dtype=np.float32)
+    lib().orc_gemv(ptr(W, c_fp), ptr(x, c_fp), ptr(y, c_fp), M, K, mode, threads)
+    return y
+
+
+def table_digest():
+    b = (ctypes.c_uint8 * 32)()
+    lib().orc_table_digest(b)
+    return bytes(b).hex()
+
+
+def inv_freq(theta, hd):
+    out = np.empty(hd // 2, dtype=np.float32)
+    d = (ctypes.c_uint8 * 32)()
+    lib().orc_inv_freq(theta, hd, ptr(out, c_fp), d)
+    return out, bytes(d).hex()
+
+
+class OracleModel:
+    """The oracle's forward/decode over the same seeded weights."""
+
+    def __init__(self, spec, weights, max_pos, threads=8, reduction=0):
+        L = lib()
+        cfg = OrcConfig(hidden=spec.hidden, inter=spec.inter, n_layers=spec.n_layers,
+                        n_heads=spec.n_heads, n_kv_heads=spec.n_kv_heads, head_dim=spec.hd,
+                        vocab=spec.vocab, tied=1 if spec.tied else 0, max_pos=max_pos,
+                        reduction=reduction, threads=threads, eps=spec.eps,
+                        rope_theta=spec.rope_theta)
+        self.m = L.orc_model_create(ctypes.byref(cfg))
+        self.spec = spec
+        for name, _shape, arr in weights.tensors:
+            rc = L.orc_model_set_bf16(self.m, name.encode(), ptr(arr, c_u16p), arr.size)
+            if rc != 0:
+                raise RuntimeError("oracle rejected %s (%d)" % (name, rc))
+        self.hdr = weights.header_digests()
+
+    def __del__(self):
+        if getattr(self, "m", None):
+            lib().orc_model_destroy(self.m)
+            self.m = None
+
+    def digests(self):
+        t, f = (ctypes.c_uint8 * 32)(), (ctypes.c_uint8 * 32)()
+        lib().orc_model_digests(self.m, t, f)
+        return bytes(t).hex(), bytes(f).hex()
+
+    def decode(self, prompt, gen_toks, trace=None):
+        prompt = np.ascontiguousarray(prompt, dtype=np.uint32)
+        ids = np.zeros(prompt.size + gen_toks, dtype=np.uint32)
+        wit, adg = (ctypes.c_uint8 * 32)(), (ctypes.c_uint8 * 32)()
+        steps = (ctypes.c_uint8 * (32 * max(gen_toks, 1)))()
+        hdr = (ctypes.c_uint8 * 96).from_buffer_copy(self.hdr)
+        cb = TRACE_FN()
+        if trace is not None:
+            def _cb(pos, layer, op, sha, _u):
+                trace.append("pos=%d layer=%d op=%s sha256=%s" % (
+                    pos, layer, op.decode(), bytes(sha[:32]).hex()))
+            cb = TRACE_FN(_cb)
+        rc = lib().orc_decode(self.m, ptr(prompt, c_u32p), prompt.size, gen_toks, hdr,
+                              ptr(ids, c_u32p), wit, adg, steps, cb, None)
+        if rc != 0:
+            raise RuntimeError("oracle decode failed (%d)" % rc)
+        sb = bytes(steps)
+        return {"ids": ids, "witness": bytes(wit).hex(), "argmax_digest": bytes(adg).hex(),
+                "step_digests": [sb[32 * i:32 * i + 32].hex() for i in range(gen_toks)]}
