@@ -1,0 +1,56 @@
+// cis2_decode.hpp — the persistent per-token decode kernel (one launch per
+// position: all layers, the LM head and the greedy argmax).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace cis2 {
+
+// Device-side weight pointers of one layer (blocked GEMV layout, see
+// cis2_kernels.hpp; biases / QK-norm weights may be null).
+struct LayerW {
+  const float *ln1, *ln2, *wq, *wk, *wv, *wo, *wg, *wu, *wd;
+  const float *bq, *bk, *bv, *qn, *kn;
+};
+
+// Rows per GEMV row block for a reduction length K: the block (R x K
+// floats) of one task fits the 144 KiB LDS weight budget.
+inline uint32_t rows_per_block(uint32_t K) {
+  uint32_t r = 36864u / K;
+  return r > 64 ? 64 : (r < 1 ? 1 : r);
+}
+
+struct DecodeArgs {
+  const LayerW* layers;  // device array [L]
+  const float* embed;    // row-major [V][H]
+  const float* lm;       // blocked [V][H], Rl rows per block
+  const float* fnorm;    // [H]
+  const float* rope_cs;  // [max_pos][hd/2][2]
+  float* kc0;            // this sequence's caches: layer l at kc0 + l*cache_stride
+  float* vc0;
+  float* act;            // per-layer activations
+  uint32_t* cnt;         // per-layer phase counters
+  float* logits;         // [V]
+  uint32_t* cand;        // [nl][2] (value bits, index) per LM block
+  uint32_t* tok_in;      // token of this position
+  uint32_t* tok_out;     // argmax written here (may alias tok_in)
+  uint32_t* err;
+  uint64_t cache_stride;
+  uint32_t H, I, V, L, nh, nkv, hd, qd, kvd, max_pos;
+  uint32_t Rq, Ro, Rg, Rd, Rl;
+  uint32_t nq_q, nq_k, nq;  // QKV tasks: q blocks, k blocks, total (q + k + v)
+  uint32_t no, ng, nd, nl;  // O, gate/up, down, LM-head task counts
+  uint32_t base_q, base_a, base_o, base_g, base_d;  // first workgroup of each phase
+  uint32_t nwg;
+  float eps, scale;
+  uint32_t pos, epoch, lm_epoch, want_logits;
+};
+
+// Floats of per-layer activation storage, and counters per layer.
+size_t decode_act_floats(uint32_t H, uint32_t I, uint32_t qd, uint32_t kvd);
+constexpr uint32_t kCountersPerLayer = 8;
+// Dynamic LDS bytes the kernel needs for this configuration.
+size_t decode_lds_bytes(const DecodeArgs& a);
+hipError_t launch_decode(const DecodeArgs& a, hipStream_t s);
+
+}  // namespace cis2

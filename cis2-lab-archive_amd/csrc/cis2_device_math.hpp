@@ -84,22 +84,31 @@ __device__ __forceinline__ double round_away(double x) {
   return __longlong_as_double((long long)(mag | sgn));
 }
 
+// The value-level compiler treats NaN bits as unspecified and may fold an
+// explicit NaN return into the sqrt of a negative input; selecting on the
+// integer bits after an opaque copy keeps the x86 pattern.
+__device__ __forceinline__ uint32_t opaque_u32(uint32_t v) {
+  __asm__ volatile("" : "+v"(v));
+  return v;
+}
+__device__ __forceinline__ float nan_fixup(float r, uint32_t in_bits) {
+  uint32_t rb = opaque_u32(bf(r));
+  if (is_nan_bits(in_bits)) rb = in_bits | 0x00400000u;  // quiet the input NaN
+  else if ((in_bits >> 31) && (in_bits & 0x7FFFFFFFu)) rb = kIndefinite;  // sqrt(x<0)
+  return fb(rb);
+}
 // Correctly rounded sqrt (IEEE), code/cis2-fp/src/math.rs:133-135.
 __device__ __forceinline__ float sqrt_cr(float x) {
   x = daz(x);
   uint32_t b = bf(x);
-  if (is_nan_bits(b)) return fb(b | 0x00400000u);
-  if (x < 0.0f) return fb(kIndefinite);
-  return __builtin_sqrtf(x);
+  return nan_fixup(__builtin_sqrtf(x), b);
 }
 // rsqrt_cr(x) = 1 / sqrt(x), two correctly rounded operations.
 __device__ __forceinline__ float rsqrt_cr(float x) {
   x = daz(x);
   uint32_t b = bf(x);
-  if (is_nan_bits(b)) return fb(b | 0x00400000u);
-  if (x < 0.0f) return fb(kIndefinite);
   float s = __builtin_sqrtf(x);
-  return 1.0f / s;
+  return nan_fixup(1.0f / s, b);
 }
 
 // Exponent-field scaling (code/cis2-fp/src/math.rs:206-225): underflow is

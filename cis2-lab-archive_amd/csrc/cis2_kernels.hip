@@ -11,9 +11,9 @@
 
 namespace cis2 {
 
-size_t blocked_floats(uint32_t M, uint32_t K) {
-  size_t blocks = (M + 63) / 64;
-  return blocks * 64 * (size_t)K;
+size_t blocked_floats(uint32_t M, uint32_t K, uint32_t R) {
+  size_t blocks = (M + R - 1) / R;
+  return blocks * R * (size_t)K;
 }
 
 // ---------------------------------------------------------------------------
@@ -29,14 +29,15 @@ struct GemvArgs {
 
 __device__ __forceinline__ float gemv_chain(const float* __restrict__ Wb,
                                             const float* __restrict__ x, uint32_t K,
-                                            uint32_t lane) {
-  const float4* __restrict__ wp = reinterpret_cast<const float4*>(Wb) + lane;
+                                            uint32_t R, uint32_t lane) {
+  const float4* __restrict__ wp =
+      reinterpret_cast<const float4*>(Wb) + (lane < R ? lane : R - 1);
   const float4* __restrict__ xp = reinterpret_cast<const float4*>(x);
   const uint32_t KG = K >> 2;
   float acc = 0.0f;
 #pragma unroll 8
   for (uint32_t g = 0; g < KG; ++g) {
-    float4 w = wp[(size_t)g * 64];
+    float4 w = wp[(size_t)g * R];
     float4 xv = xp[g];
     float p;
     p = w.x * xv.x; acc = acc + p;
@@ -54,10 +55,10 @@ __global__ __launch_bounds__(64) void k_gemv(GemvArgs a) {
   const GemvSeg g = a.seg[s];
   b -= a.blk_start[s];
   const uint32_t lane = threadIdx.x;
-  const float* Wb = g.W + (size_t)b * 64 * g.K;
-  float acc = gemv_chain(Wb, g.x, g.K, lane);
-  uint32_t row = b * 64 + lane;
-  if (row < g.M) {
+  const float* Wb = g.W + (size_t)b * g.R * g.K;
+  float acc = gemv_chain(Wb, g.x, g.K, g.R, lane);
+  uint32_t row = b * g.R + lane;
+  if (lane < g.R && row < g.M) {
     float r = acc;
     if (g.add) r = g.add_first ? (g.add[row] + acc) : (acc + g.add[row]);
     g.y[row] = r;
@@ -69,10 +70,11 @@ hipError_t launch_gemv(const GemvSeg* segs, int nseg, hipStream_t s) {
   GemvArgs a;
   uint32_t total = 0;
   for (int i = 0; i < nseg; ++i) {
-    if (segs[i].K % 4 != 0 || segs[i].M == 0) return hipErrorInvalidValue;
+    if (segs[i].K % 4 != 0 || segs[i].M == 0 || segs[i].R == 0 || segs[i].R > 64)
+      return hipErrorInvalidValue;
     a.seg[i] = segs[i];
     a.blk_start[i] = total;
-    total += (segs[i].M + 63) / 64;
+    total += (segs[i].M + segs[i].R - 1) / segs[i].R;
   }
   a.blk_start[nseg] = total;
   a.nseg = nseg;
@@ -86,18 +88,18 @@ __global__ __launch_bounds__(128) void k_gate_up_silu(const float* __restrict__ 
                                                       const float* __restrict__ Wu,
                                                       const float* __restrict__ x,
                                                       float* gate, float* up, float* hid,
-                                                      uint32_t I, uint32_t H) {
+                                                      uint32_t I, uint32_t H, uint32_t R) {
   __shared__ float sg[64];
   const uint32_t b = blockIdx.x, w = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const float* Wb = (w ? Wu : Wg) + (size_t)b * 64 * H;
-  float acc = gemv_chain(Wb, x, H, lane);
-  const uint32_t row = b * 64 + lane;
+  const float* Wb = (w ? Wu : Wg) + (size_t)b * R * H;
+  float acc = gemv_chain(Wb, x, H, R, lane);
+  const uint32_t row = b * R + lane;
   if (w == 0) {
     sg[lane] = acc;
-    if (row < I) gate[row] = acc;
+    if (lane < R && row < I) gate[row] = acc;
   }
   __syncthreads();
-  if (w == 1 && row < I) {
+  if (w == 1 && lane < R && row < I) {
     up[row] = acc;
     float sgl = silu_pinned(sg[lane]);
     hid[row] = sgl * acc;
@@ -106,31 +108,32 @@ __global__ __launch_bounds__(128) void k_gate_up_silu(const float* __restrict__ 
 
 hipError_t launch_gate_up_silu(const float* Wg, const float* Wu, const float* x,
                                float* gate, float* up, float* hid, uint32_t I,
-                               uint32_t H, hipStream_t s) {
-  if (H % 4 != 0) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_gate_up_silu, dim3((I + 63) / 64), dim3(128), 0, s, Wg, Wu, x,
-                     gate, up, hid, I, H);
+                               uint32_t H, uint32_t R, hipStream_t s) {
+  if (H % 4 != 0 || R == 0 || R > 64) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_gate_up_silu, dim3((I + R - 1) / R), dim3(128), 0, s, Wg, Wu, x,
+                     gate, up, hid, I, H, R);
   return hipGetLastError();
 }
 
 __global__ void k_relayout(const float* __restrict__ src, float* __restrict__ dst,
-                           uint32_t M, uint32_t K, size_t total) {
+                           uint32_t M, uint32_t K, uint32_t R, size_t total) {
   size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
   const size_t stride = (size_t)gridDim.x * blockDim.x;
   const size_t KG = K / 4;
   for (; i < total; i += stride) {
-    size_t j = i & 3, lane = (i >> 2) & 63, rest = i >> 8;
+    size_t j = i & 3, q = i >> 2;
+    size_t lane = q % R, rest = q / R;
     size_t g = rest % KG, b = rest / KG;
-    size_t row = b * 64 + lane;
+    size_t row = b * R + lane;
     dst[i] = row < M ? src[row * K + 4 * g + j] : 0.0f;
   }
 }
 
-hipError_t launch_relayout(const float* src, float* dst, uint32_t M, uint32_t K,
+hipError_t launch_relayout(const float* src, float* dst, uint32_t M, uint32_t K, uint32_t R,
                            hipStream_t s) {
-  if (K % 4 != 0) return hipErrorInvalidValue;
-  size_t total = blocked_floats(M, K);
-  hipLaunchKernelGGL(k_relayout, dim3(2048), dim3(256), 0, s, src, dst, M, K, total);
+  if (K % 4 != 0 || R == 0 || R > 64) return hipErrorInvalidValue;
+  size_t total = blocked_floats(M, K, R);
+  hipLaunchKernelGGL(k_relayout, dim3(2048), dim3(256), 0, s, src, dst, M, K, R, total);
   return hipGetLastError();
 }
 

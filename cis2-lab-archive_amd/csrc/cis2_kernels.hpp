@@ -8,12 +8,13 @@
 namespace cis2 {
 
 // GEMV weight layout in HBM ("row-block interleaved"): rows are grouped in
-// blocks of 64 (one wavefront, one row per lane); inside a block the matrix
-// is stored k-group-major with 4 consecutive k per lane, so one wave-wide
-// 16-byte load per lane reads 1 KiB contiguous:
-//   W_blk[((b * (K/4) + g) * 64 + lane) * 4 + j] = W[b*64 + lane][4*g + j]
+// blocks of R <= 64 (one row per lane of a wavefront); inside a block the
+// matrix is stored k-group-major with 4 consecutive k per lane, so a
+// wave-wide 16-byte load per lane reads R*16 contiguous bytes and a block is
+// one contiguous R*K run (what a workgroup copies into its LDS):
+//   W_blk[((b * (K/4) + g) * R + lane) * 4 + j] = W[b*R + lane][4*g + j]
 // Rows past M in the last block are zero.  K must be a multiple of 4.
-size_t blocked_floats(uint32_t M, uint32_t K);
+size_t blocked_floats(uint32_t M, uint32_t K, uint32_t R);
 
 // One output segment of a multi-segment GEMV launch.
 struct GemvSeg {
@@ -23,6 +24,7 @@ struct GemvSeg {
   float* y;            // output [M]
   uint32_t M, K;
   uint32_t add_first;  // 1: y = add[i] + acc (residual); 0: y = acc + add[i] (bias)
+  uint32_t R;          // rows per block of W's layout (1..64)
 };
 
 // Strict left-to-right per-row GEMV over up to 4 segments in one launch.
@@ -30,9 +32,9 @@ hipError_t launch_gemv(const GemvSeg* segs, int nseg, hipStream_t s);
 // Gate/up pair fused with hid = silu(gate) * up.
 hipError_t launch_gate_up_silu(const float* Wg, const float* Wu, const float* x,
                                float* gate, float* up, float* hid, uint32_t I,
-                               uint32_t H, hipStream_t s);
+                               uint32_t H, uint32_t R, hipStream_t s);
 // Relayout a row-major [M,K] f32 matrix (device) into the blocked layout.
-hipError_t launch_relayout(const float* src, float* dst, uint32_t M, uint32_t K,
+hipError_t launch_relayout(const float* src, float* dst, uint32_t M, uint32_t K, uint32_t R,
                            hipStream_t s);
 // Exact BF16 -> F32 widening (bits << 16).
 hipError_t launch_widen(const uint16_t* src, float* dst, uint64_t n, hipStream_t s);

@@ -2,11 +2,13 @@
 // tensor upload, the per-token kernel sequence, the greedy decode loop with
 // the pipelined witness fold, tracing, and the standalone GEMV plan.
 #include "cis2_amd.h"
+#include "cis2_decode.hpp"
 #include "cis2_kernels.hpp"
 #include "cis2_sha256.hpp"
 
 #include <hip/hip_runtime.h>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include <map>
@@ -40,7 +42,7 @@ struct Slot {
   float** ptr;
   uint64_t count;
   Kind kind;
-  uint32_t M, K;
+  uint32_t M, K, R;  // R: rows per block of the blocked GEMV layout
   bool required;
 };
 
@@ -57,6 +59,7 @@ struct Session {
   bool active = false;
   uint32_t seq = 0, n_prompt = 0, max_steps = 0;
   uint32_t enqueued = 0, folded = 0;
+  bool fast = false;  // persistent kernel (argmax fused) vs per-op kernels
   Sha256 w;
   std::vector<uint32_t> ids;
   std::vector<uint8_t> step_dig;
@@ -90,6 +93,18 @@ struct cis2_ctx {
   uint32_t* ring_tok = nullptr;
   hipEvent_t ring_ev[kRing];
   Session sess;
+  // persistent decode kernel state
+  uint32_t Rq = 0, Ro = 0, Rg = 0, Rd = 0, Rl = 0;
+  bool fast_ok = false;      // this configuration fits the persistent kernel
+  bool force_ops = false;    // CIS2_PATH=ops: per-op kernels only
+  uint32_t ncu = 0;
+  LayerW* d_layers = nullptr;
+  bool layers_dirty = true;
+  float* act = nullptr;
+  uint32_t* counters = nullptr;
+  uint32_t* cand = nullptr;
+  uint32_t epoch = 0, lm_epoch = 0;
+  DecodeArgs dargs;
   std::vector<void*> allocs;
 };
 
@@ -123,8 +138,8 @@ float* dalloc(cis2_ctx* c, size_t nfloats) {
 }
 
 void add_slot(cis2_ctx* c, const std::string& name, float** ptr, uint64_t count, Kind kind,
-              uint32_t M, uint32_t K, bool required) {
-  c->slots[name] = Slot{ptr, count, kind, M, K, required};
+              uint32_t M, uint32_t K, bool required, uint32_t R = 64) {
+  c->slots[name] = Slot{ptr, count, kind, M, K, R, required};
 }
 
 // Checkpoint tensor names as the reference loader reads them
@@ -133,9 +148,10 @@ void add_slot(cis2_ctx* c, const std::string& name, float** ptr, uint64_t count,
 void build_registry(cis2_ctx* c) {
   const cis2_config& f = c->cfg;
   const uint32_t H = f.hidden, I = f.inter, V = f.vocab, QD = c->qd, KV = c->kvd;
-  add_slot(c, "model.embed_tokens.weight", &c->embed, (uint64_t)V * H, EMBED, V, H, true);
+  add_slot(c, "model.embed_tokens.weight", &c->embed, (uint64_t)V * H, EMBED, V, H, true, c->Rl);
   add_slot(c, "model.norm.weight", &c->final_norm, H, VEC, 0, 0, true);
-  if (!f.tied) add_slot(c, "lm_head.weight", &c->lm_head, (uint64_t)V * H, LMHEAD, V, H, true);
+  if (!f.tied)
+    add_slot(c, "lm_head.weight", &c->lm_head, (uint64_t)V * H, LMHEAD, V, H, true, c->Rl);
   for (uint32_t l = 0; l < f.n_layers; ++l) {
     Layer& Ly = c->L[l];
     char p[64];
@@ -143,13 +159,13 @@ void build_registry(cis2_ctx* c) {
     std::string s(p);
     add_slot(c, s + "input_layernorm.weight", &Ly.ln1, H, VEC, 0, 0, true);
     add_slot(c, s + "post_attention_layernorm.weight", &Ly.ln2, H, VEC, 0, 0, true);
-    add_slot(c, s + "self_attn.q_proj.weight", &Ly.wq, (uint64_t)QD * H, GEMV, QD, H, true);
-    add_slot(c, s + "self_attn.k_proj.weight", &Ly.wk, (uint64_t)KV * H, GEMV, KV, H, true);
-    add_slot(c, s + "self_attn.v_proj.weight", &Ly.wv, (uint64_t)KV * H, GEMV, KV, H, true);
-    add_slot(c, s + "self_attn.o_proj.weight", &Ly.wo, (uint64_t)H * QD, GEMV, H, QD, true);
-    add_slot(c, s + "mlp.gate_proj.weight", &Ly.wg, (uint64_t)I * H, GEMV, I, H, true);
-    add_slot(c, s + "mlp.up_proj.weight", &Ly.wu, (uint64_t)I * H, GEMV, I, H, true);
-    add_slot(c, s + "mlp.down_proj.weight", &Ly.wd, (uint64_t)H * I, GEMV, H, I, true);
+    add_slot(c, s + "self_attn.q_proj.weight", &Ly.wq, (uint64_t)QD * H, GEMV, QD, H, true, c->Rq);
+    add_slot(c, s + "self_attn.k_proj.weight", &Ly.wk, (uint64_t)KV * H, GEMV, KV, H, true, c->Rq);
+    add_slot(c, s + "self_attn.v_proj.weight", &Ly.wv, (uint64_t)KV * H, GEMV, KV, H, true, c->Rq);
+    add_slot(c, s + "self_attn.o_proj.weight", &Ly.wo, (uint64_t)H * QD, GEMV, H, QD, true, c->Ro);
+    add_slot(c, s + "mlp.gate_proj.weight", &Ly.wg, (uint64_t)I * H, GEMV, I, H, true, c->Rg);
+    add_slot(c, s + "mlp.up_proj.weight", &Ly.wu, (uint64_t)I * H, GEMV, I, H, true, c->Rg);
+    add_slot(c, s + "mlp.down_proj.weight", &Ly.wd, (uint64_t)H * I, GEMV, H, I, true, c->Rd);
     add_slot(c, s + "self_attn.q_proj.bias", &Ly.bq, QD, VEC, 0, 0, false);
     add_slot(c, s + "self_attn.k_proj.bias", &Ly.bk, KV, VEC, 0, 0, false);
     add_slot(c, s + "self_attn.v_proj.bias", &Ly.bv, KV, VEC, 0, 0, false);
@@ -201,9 +217,9 @@ int forward_one(cis2_ctx* c, uint32_t seq, uint32_t pos, const uint32_t* d_tokp,
     float* vc = vcache(c, seq, l);
     LAUNCH(launch_rmsnorm(c->h, Ly.ln1, f.eps, H, 1, c->x, s), "norm1");
     EMIT(pos, l, "norm1", c->x, H);
-    GemvSeg qkv[3] = {{Ly.wq, c->x, Ly.bq, c->q, QD, H, 0},
-                      {Ly.wk, c->x, Ly.bk, c->k, KV, H, 0},
-                      {Ly.wv, c->x, Ly.bv, c->v, KV, H, 0}};
+    GemvSeg qkv[3] = {{Ly.wq, c->x, Ly.bq, c->q, QD, H, 0, c->Rq},
+                      {Ly.wk, c->x, Ly.bk, c->k, KV, H, 0, c->Rq},
+                      {Ly.wv, c->x, Ly.bv, c->v, KV, H, 0, c->Rq}};
     LAUNCH(launch_gemv(qkv, 3, s), "qkv");
     EMIT(pos, l, "q", c->q, QD);
     EMIT(pos, l, "k", c->k, KV);
@@ -228,9 +244,9 @@ int forward_one(cis2_ctx* c, uint32_t seq, uint32_t pos, const uint32_t* d_tokp,
     EMIT(pos, l, "scores", c->scores, (size_t)f.n_heads * (pos + 1));
     EMIT(pos, l, "softmax", c->probs, (size_t)f.n_heads * (pos + 1));
     EMIT(pos, l, "attn_out", c->att, QD);
-    GemvSeg os[1] = {{Ly.wo, c->att, c->h, c->h2, H, QD, 1}};
+    GemvSeg os[1] = {{Ly.wo, c->att, c->h, c->h2, H, QD, 1, c->Ro}};
     if (tr) {  // the trace needs o_proj on its own
-      GemvSeg ot[1] = {{Ly.wo, c->att, nullptr, c->o, H, QD, 0}};
+      GemvSeg ot[1] = {{Ly.wo, c->att, nullptr, c->o, H, QD, 0, c->Ro}};
       LAUNCH(launch_gemv(ot, 1, s), "o_proj");
       EMIT(pos, l, "o_proj", c->o, H);
     }
@@ -239,16 +255,16 @@ int forward_one(cis2_ctx* c, uint32_t seq, uint32_t pos, const uint32_t* d_tokp,
     EMIT(pos, l, "resid1", c->h, H);
     LAUNCH(launch_rmsnorm(c->h, Ly.ln2, f.eps, H, 1, c->x, s), "norm2");
     EMIT(pos, l, "norm2", c->x, H);
-    LAUNCH(launch_gate_up_silu(Ly.wg, Ly.wu, c->x, c->g, c->u, c->hid, I, H, s), "gate_up");
+    LAUNCH(launch_gate_up_silu(Ly.wg, Ly.wu, c->x, c->g, c->u, c->hid, I, H, c->Rg, s), "gate_up");
     EMIT(pos, l, "gate", c->g, I);
     EMIT(pos, l, "up", c->u, I);
     EMIT(pos, l, "silu_mul", c->hid, I);
     if (tr) {
-      GemvSeg dt[1] = {{Ly.wd, c->hid, nullptr, c->dn, H, I, 0}};
+      GemvSeg dt[1] = {{Ly.wd, c->hid, nullptr, c->dn, H, I, 0, c->Rd}};
       LAUNCH(launch_gemv(dt, 1, s), "down");
       EMIT(pos, l, "down", c->dn, H);
     }
-    GemvSeg ds[1] = {{Ly.wd, c->hid, c->h, c->h2, H, I, 1}};
+    GemvSeg ds[1] = {{Ly.wd, c->hid, c->h, c->h2, H, I, 1, c->Rd}};
     LAUNCH(launch_gemv(ds, 1, s), "down+resid");
     std::swap(c->h, c->h2);
     EMIT(pos, l, "resid2", c->h, H);
@@ -256,7 +272,7 @@ int forward_one(cis2_ctx* c, uint32_t seq, uint32_t pos, const uint32_t* d_tokp,
   if (want_logits || tr) {
     LAUNCH(launch_rmsnorm(c->h, c->final_norm, f.eps, H, 1, c->x, s), "final_norm");
     EMIT(pos, -1, "final_norm", c->x, H);
-    GemvSeg lm[1] = {{c->lm_head, c->x, nullptr, c->logits, f.vocab, H, 0}};
+    GemvSeg lm[1] = {{c->lm_head, c->x, nullptr, c->logits, f.vocab, H, 0, c->Rl}};
     LAUNCH(launch_gemv(lm, 1, s), "lm_head");
     EMIT(pos, -1, "logits", c->logits, f.vocab);
   }
@@ -268,10 +284,60 @@ int check_err_flag(cis2_ctx* c) {
   HIPCHK(c, hipMemcpy(&e, c->d_err, 4, hipMemcpyDeviceToHost), "error flag");
   if (e) {
     (void)hipMemset(c->d_err, 0, 4);
+    if (e & 2u)
+      return fail(c, CIS2_E_DEVICE,
+                  "persistent decode kernel: a phase wait hit its spin cap "
+                  "(workgroups not co-resident)");
     return fail(c, CIS2_E_RANGE, "token id out of range on the device");
   }
   return CIS2_OK;
 }
+
+// Fills the persistent-kernel arguments once the weights are in place.
+int prepare_fast(cis2_ctx* c) {
+  if (!c->layers_dirty) return CIS2_OK;
+  const cis2_config& f = c->cfg;
+  std::vector<LayerW> hl(f.n_layers);
+  for (uint32_t l = 0; l < f.n_layers; ++l) {
+    const Layer& L = c->L[l];
+    hl[l] = LayerW{L.ln1, L.ln2, L.wq, L.wk, L.wv, L.wo, L.wg, L.wu, L.wd,
+                   L.bq, L.bk, L.bv, L.qn, L.kn};
+  }
+  HIPCHK(c, hipMemcpy(c->d_layers, hl.data(), hl.size() * sizeof(LayerW), hipMemcpyHostToDevice),
+         "layer table");
+  DecodeArgs& a = c->dargs;
+  a.layers = c->d_layers;
+  a.embed = c->embed;
+  a.lm = c->lm_head;
+  a.fnorm = c->final_norm;
+  c->layers_dirty = false;
+  return CIS2_OK;
+}
+
+// One position through the persistent kernel; the token is read from
+// *tokp on the device and the argmax is written to c->d_tok[0].
+int forward_fast(cis2_ctx* c, uint32_t seq, uint32_t pos, uint32_t* tokp, bool want_logits) {
+  int r = prepare_fast(c);
+  if (r) return r;
+  DecodeArgs& a = c->dargs;
+  const size_t per_layer = (size_t)2 * c->kvd * c->cfg.max_pos;
+  a.kc0 = c->kv + (size_t)seq * c->cfg.n_layers * per_layer;
+  a.vc0 = a.kc0 + (size_t)c->kvd * c->cfg.max_pos;
+  a.tok_in = tokp;
+  a.tok_out = c->d_tok;
+  a.pos = pos;
+  a.epoch = ++c->epoch;
+  if (want_logits) ++c->lm_epoch;
+  a.lm_epoch = c->lm_epoch;
+  a.want_logits = want_logits ? 1u : 0u;
+  LAUNCH(launch_decode(a, c->st), "decode kernel");
+  return CIS2_OK;
+}
+
+// The path a step takes: the persistent kernel, or the per-op kernels when
+// tracing (every op's output is observed) or when the configuration does
+// not fit the persistent kernel.
+bool use_fast(const cis2_ctx* c) { return c->fast_ok && !c->force_ops && !c->trace; }
 
 }  // namespace
 
@@ -399,6 +465,74 @@ int cis2_ctx_create(const cis2_config* cfg, cis2_ctx** out) {
       cis2_ctx_destroy(c);
       return CIS2_E_DEVICE;
     }
+  // Row-block sizes of the blocked GEMV layout (shared by both paths).
+  c->Rq = rows_per_block(H);
+  c->Ro = rows_per_block(c->qd);
+  c->Rg = rows_per_block(H) / 2 > 0 ? rows_per_block(H) / 2 : 1;
+  c->Rd = rows_per_block(I);
+  c->Rl = rows_per_block(H);
+  // Persistent decode kernel: task counts, workgroup roles, scratch.
+  {
+    int dev = 0, ncu = 0, lds = 0;
+    (void)hipGetDevice(&dev);
+    (void)hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev);
+    (void)hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor, dev);
+    c->ncu = (uint32_t)ncu;
+    const char* pe = getenv("CIS2_PATH");
+    c->force_ops = pe && !strcmp(pe, "ops");
+    DecodeArgs& a = c->dargs;
+    memset(&a, 0, sizeof a);
+    a.H = H; a.I = I; a.V = V; a.L = f.n_layers; a.nh = f.n_heads; a.nkv = f.n_kv_heads;
+    a.hd = f.head_dim; a.qd = c->qd; a.kvd = c->kvd; a.max_pos = f.max_pos;
+    a.Rq = c->Rq; a.Ro = c->Ro; a.Rg = c->Rg; a.Rd = c->Rd; a.Rl = c->Rl;
+    a.nq_q = (c->qd + a.Rq - 1) / a.Rq;
+    a.nq_k = (c->kvd + a.Rq - 1) / a.Rq;
+    a.nq = a.nq_q + 2 * a.nq_k;
+    a.no = (H + a.Ro - 1) / a.Ro;
+    a.ng = (I + a.Rg - 1) / a.Rg;
+    a.nd = (H + a.Rd - 1) / a.Rd;
+    a.nl = (V + a.Rl - 1) / a.Rl;
+    a.base_q = 0;
+    a.base_a = a.base_q + a.nq;
+    a.base_o = a.base_a + a.nh;
+    a.base_g = a.base_o + a.no;
+    a.base_d = a.base_g + a.ng;
+    a.nwg = c->ncu;
+    a.cache_stride = (uint64_t)2 * c->kvd * f.max_pos;
+    a.eps = f.eps;
+    a.scale = c->scale;
+    a.rope_cs = c->rope_cs;
+    a.logits = c->logits;
+    a.err = c->d_err;
+    const size_t need_lds = decode_lds_bytes(a);
+    c->fast_ok = (a.base_d + a.nd <= c->ncu) && lds > 0 && need_lds <= (size_t)lds &&
+                 need_lds <= 160 * 1024;
+    void* p = nullptr;
+    const size_t act_f = (size_t)f.n_layers * decode_act_floats(H, I, c->qd, c->kvd);
+    const size_t cnt_n = ((size_t)f.n_layers + 1) * kCountersPerLayer;
+    if (!(c->act = dalloc(c, act_f)) || hipMalloc(&p, cnt_n * 4) != hipSuccess) {
+      cis2_ctx_destroy(c);
+      return CIS2_E_OOM;
+    }
+    c->allocs.push_back(p);
+    c->counters = static_cast<uint32_t*>(p);
+    (void)hipMemset(c->counters, 0, cnt_n * 4);
+    if (hipMalloc(&p, ((size_t)2 * a.nl + 4) * 4) != hipSuccess) {
+      cis2_ctx_destroy(c);
+      return CIS2_E_OOM;
+    }
+    c->allocs.push_back(p);
+    c->cand = static_cast<uint32_t*>(p);
+    if (hipMalloc(&p, (size_t)f.n_layers * sizeof(LayerW)) != hipSuccess) {
+      cis2_ctx_destroy(c);
+      return CIS2_E_OOM;
+    }
+    c->allocs.push_back(p);
+    c->d_layers = static_cast<LayerW*>(p);
+    a.act = c->act;
+    a.cnt = c->counters;
+    a.cand = c->cand;
+  }
   build_registry(c);
   *out = c;
   return CIS2_OK;
@@ -425,12 +559,13 @@ int cis2_upload_bf16(cis2_ctx* c, const char* name, const uint16_t* bf16, uint64
     if (!dst && !(dst = dalloc(c, n))) e = hipErrorOutOfMemory;
     if (e == hipSuccess) e = hipMemcpyAsync(dst, wide, n * sizeof(float), hipMemcpyDeviceToDevice, c->st);
     if (e == hipSuccess && c->cfg.tied) {
-      if (!c->lm_head && !(c->lm_head = dalloc(c, blocked_floats(s.M, s.K)))) e = hipErrorOutOfMemory;
-      if (e == hipSuccess) e = launch_relayout(wide, c->lm_head, s.M, s.K, c->st);
+      if (!c->lm_head && !(c->lm_head = dalloc(c, blocked_floats(s.M, s.K, s.R))))
+        e = hipErrorOutOfMemory;
+      if (e == hipSuccess) e = launch_relayout(wide, c->lm_head, s.M, s.K, s.R, c->st);
     }
   } else if (e == hipSuccess) {  // GEMV / LMHEAD: blocked layout
-    if (!dst && !(dst = dalloc(c, blocked_floats(s.M, s.K)))) e = hipErrorOutOfMemory;
-    if (e == hipSuccess) e = launch_relayout(wide, dst, s.M, s.K, c->st);
+    if (!dst && !(dst = dalloc(c, blocked_floats(s.M, s.K, s.R)))) e = hipErrorOutOfMemory;
+    if (e == hipSuccess) e = launch_relayout(wide, dst, s.M, s.K, s.R, c->st);
   }
   if (e == hipSuccess) e = hipStreamSynchronize(c->st);
   (void)hipFree(stage);
@@ -438,6 +573,7 @@ int cis2_upload_bf16(cis2_ctx* c, const char* name, const uint16_t* bf16, uint64
   if (e != hipSuccess) return hipfail(c, e, "upload");
   *s.ptr = dst;
   c->present[name] = true;
+  c->layers_dirty = true;
   return CIS2_OK;
 }
 
@@ -482,9 +618,16 @@ int cis2_forward(cis2_ctx* c, uint32_t n, const uint32_t* seq, const uint32_t* p
     if (pos[i] >= c->cfg.max_pos) return fail(c, CIS2_E_RANGE, "position beyond max_pos");
     if (tok[i] >= c->cfg.vocab) return fail(c, CIS2_E_RANGE, "token id >= vocab");
     HIPCHK(c, hipMemcpyAsync(c->d_tok, &tok[i], 4, hipMemcpyHostToDevice, c->st), "token");
-    r = forward_one(c, seq[i], pos[i], c->d_tok, true);
-    if (r) return r;
-    if (argmax_out) LAUNCH(launch_argmax(c->logits, c->cfg.vocab, c->d_tok + 1, c->st), "argmax");
+    if (use_fast(c)) {
+      r = forward_fast(c, seq[i], pos[i], c->d_tok, true);
+      if (r) return r;
+      HIPCHK(c, hipMemcpyAsync(c->d_tok + 1, c->d_tok, 4, hipMemcpyDeviceToDevice, c->st),
+             "argmax copy");
+    } else {
+      r = forward_one(c, seq[i], pos[i], c->d_tok, true);
+      if (r) return r;
+      if (argmax_out) LAUNCH(launch_argmax(c->logits, c->cfg.vocab, c->d_tok + 1, c->st), "argmax");
+    }
     HIPCHK(c, hipStreamSynchronize(c->st), "forward sync");
     if (logits_host)
       HIPCHK(c, hipMemcpy(logits_host + (size_t)i * c->cfg.vocab, c->logits,
@@ -543,8 +686,10 @@ int cis2_decode_begin(cis2_ctx* c, uint32_t seq, const uint32_t* prompt, uint32_
   // Prefill: every prompt position; only the last needs its logits.
   HIPCHK(c, hipMemcpy(c->d_prompt, prompt, (size_t)n_prompt * 4, hipMemcpyHostToDevice),
          "prompt upload");
+  S.fast = use_fast(c);
   for (uint32_t p = 0; p < n_prompt; ++p) {
-    r = forward_one(c, seq, p, c->d_prompt + p, p + 1 == n_prompt);
+    r = S.fast ? forward_fast(c, seq, p, c->d_prompt + p, p + 1 == n_prompt)
+               : forward_one(c, seq, p, c->d_prompt + p, p + 1 == n_prompt);
     if (r) return r;
   }
   HIPCHK(c, hipStreamSynchronize(c->st), "prefill sync");
@@ -567,14 +712,16 @@ int cis2_decode_steps(cis2_ctx* c, uint32_t n) {
       r = fold_step(c);
       if (r) return r;
     }
-    LAUNCH(launch_argmax(c->logits, V, c->d_tok, s), "argmax");
+    // the persistent kernel already left the argmax of these logits in d_tok
+    if (!S.fast) LAUNCH(launch_argmax(c->logits, V, c->d_tok, s), "argmax");
     HIPCHK(c, hipMemcpyAsync(c->ring + (size_t)slot * V, c->logits, (size_t)V * sizeof(float),
                              hipMemcpyDeviceToHost, s),
            "logits d2h");
     HIPCHK(c, hipMemcpyAsync(c->ring_tok + slot * 2, c->d_tok, 4, hipMemcpyDeviceToHost, s),
            "token d2h");
     HIPCHK(c, hipEventRecord(c->ring_ev[slot], s), "ring event");
-    r = forward_one(c, S.seq, S.n_prompt + step, c->d_tok, true);
+    r = S.fast ? forward_fast(c, S.seq, S.n_prompt + step, c->d_tok, true)
+               : forward_one(c, S.seq, S.n_prompt + step, c->d_tok, true);
     if (r) return r;
     S.enqueued++;
   }
@@ -641,7 +788,7 @@ int cis2_gemv_plan_create(uint32_t M, uint32_t K, uint32_t copies, const float* 
   if (!W || !out || M == 0 || K == 0 || K % 4 || copies == 0) return CIS2_E_ARG;
   cis2_gemv_plan* p = new cis2_gemv_plan();
   p->M = M; p->K = K; p->copies = copies;
-  const size_t per = blocked_floats(M, K);
+  const size_t per = blocked_floats(M, K, 64);
   float* rowmajor = nullptr;
   hipError_t e = hipStreamCreateWithFlags(&p->st, hipStreamNonBlocking);
   if (e == hipSuccess) e = hipMalloc(&p->W, per * copies * sizeof(float));
@@ -650,7 +797,7 @@ int cis2_gemv_plan_create(uint32_t M, uint32_t K, uint32_t copies, const float* 
   if (e == hipSuccess) e = hipMalloc(&rowmajor, (size_t)M * K * sizeof(float));
   if (e == hipSuccess) e = hipMemcpy(rowmajor, W, (size_t)M * K * sizeof(float), hipMemcpyHostToDevice);
   for (uint32_t i = 0; e == hipSuccess && i < copies; ++i)
-    e = launch_relayout(rowmajor, p->W + per * i, M, K, p->st);
+    e = launch_relayout(rowmajor, p->W + per * i, M, K, 64, p->st);
   if (e == hipSuccess) e = hipStreamSynchronize(p->st);
   if (e == hipSuccess) e = hipEventCreate(&p->e0);
   if (e == hipSuccess) e = hipEventCreate(&p->e1);
@@ -666,7 +813,7 @@ int cis2_gemv_plan_create(uint32_t M, uint32_t K, uint32_t copies, const float* 
 int cis2_gemv_plan_run(cis2_gemv_plan* p, const float* x, float* y) {
   if (!p || !x || !y) return CIS2_E_ARG;
   hipError_t e = hipMemcpyAsync(p->x, x, (size_t)p->K * sizeof(float), hipMemcpyHostToDevice, p->st);
-  GemvSeg sg[1] = {{p->W, p->x, nullptr, p->y, p->M, p->K, 0}};
+  GemvSeg sg[1] = {{p->W, p->x, nullptr, p->y, p->M, p->K, 0, 64}};
   if (e == hipSuccess) e = launch_gemv(sg, 1, p->st);
   if (e == hipSuccess) e = hipMemcpyAsync(y, p->y, (size_t)p->M * sizeof(float), hipMemcpyDeviceToHost, p->st);
   if (e == hipSuccess) e = hipStreamSynchronize(p->st);
@@ -675,15 +822,15 @@ int cis2_gemv_plan_run(cis2_gemv_plan* p, const float* x, float* y) {
 
 int cis2_gemv_plan_time(cis2_gemv_plan* p, uint32_t iters, float* ms) {
   if (!p || !ms || iters == 0) return CIS2_E_ARG;
-  const size_t per = blocked_floats(p->M, p->K);
+  const size_t per = blocked_floats(p->M, p->K, 64);
   hipError_t e = hipSuccess;
   for (uint32_t i = 0; e == hipSuccess && i < p->copies; ++i) {  // warm-up pass
-    GemvSeg sg[1] = {{p->W + per * i, p->x, nullptr, p->y, p->M, p->K, 0}};
+    GemvSeg sg[1] = {{p->W + per * i, p->x, nullptr, p->y, p->M, p->K, 0, 64}};
     e = launch_gemv(sg, 1, p->st);
   }
   if (e == hipSuccess) e = hipEventRecord(p->e0, p->st);
   for (uint32_t i = 0; e == hipSuccess && i < iters; ++i) {
-    GemvSeg sg[1] = {{p->W + per * (i % p->copies), p->x, nullptr, p->y, p->M, p->K, 0}};
+    GemvSeg sg[1] = {{p->W + per * (i % p->copies), p->x, nullptr, p->y, p->M, p->K, 0, 64}};
     e = launch_gemv(sg, 1, p->st);
   }
   if (e == hipSuccess) e = hipEventRecord(p->e1, p->st);
