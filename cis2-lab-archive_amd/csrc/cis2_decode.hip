@@ -42,6 +42,21 @@ struct Act {
   float *q, *k, *v, *att, *h1, *hid, *hout;
 };
 
+// Bytes of the LDS region that holds a task's weight block, or the
+// attention task's scores and cached K/V (up to the LDS budget).
+__host__ __device__ inline size_t decode_wregion_bytes(const DecodeArgs& a) {
+  size_t q = (size_t)a.Rq * a.H, o = (size_t)a.Ro * a.qd, g = 2 * (size_t)a.Rg * a.H,
+         d = (size_t)a.Rd * a.I;
+  size_t m = q > o ? q : o;
+  m = m > g ? m : g;
+  m = m > d ? m : d;
+  size_t att = (size_t)a.max_pos + 64 + 2 * (size_t)a.hd * (((size_t)a.max_pos + 3) & ~(size_t)3);
+  const size_t cap = 38400;  // 150 KiB in floats: what LDS can give this region
+  if (att > cap) att = m > (size_t)a.max_pos + 64 ? m : (size_t)a.max_pos + 64;
+  m = m > att ? m : att;
+  return ((m * 4 + 255) / 256) * 256;
+}
+
 __host__ __device__ inline size_t layer_stride(uint32_t H, uint32_t I, uint32_t qd,
                                                uint32_t kvd) {
   size_t s = 2 * (size_t)qd + 2 * (size_t)kvd + 2 * (size_t)H + I;
@@ -72,6 +87,12 @@ __device__ __forceinline__ void st_ag(float* p, float v) {
 }
 __device__ __forceinline__ void st_ag(uint32_t* p, uint32_t v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ void stamp(const DecodeArgs& a, uint32_t l, uint32_t ph, uint32_t t,
+                                      uint32_t slot) {
+  if (a.tline && threadIdx.x == 0 && t < kTimelineTasks)
+    a.tline[(((size_t)l * 6 + ph) * kTimelineTasks + t) * 4 + slot] = __builtin_amdgcn_s_memrealtime();
 }
 
 __device__ void wait_ge(uint32_t* ctr, uint32_t target, uint32_t* err) {
@@ -275,7 +296,9 @@ __device__ void run_qkv(const DecodeArgs& a, uint32_t l, uint32_t t, Lds& s, uin
   uint32_t M, blk;
   float* out;
   qkv_task_geom(a, Lw, t, &W, &bias, &M, &blk, &out, ac);
+  stamp(a, l, C_QKV, t, 0);
   if (l > 0) wait_ge(a.cnt + (size_t)(l - 1) * kCountersPerLayer + C_D, a.epoch * a.nd, a.err);
+  stamp(a, l, C_QKV, t, 1);
   float* x = s.v;
   float* ln = s.v + a.H;
   float* s_inv = s.v + 2 * a.H;
@@ -291,20 +314,65 @@ __device__ void run_qkv(const DecodeArgs& a, uint32_t l, uint32_t t, Lds& s, uin
     }
   }
   signal_add(a.cnt + (size_t)l * kCountersPerLayer + C_QKV, 1);
+  stamp(a, l, C_QKV, t, 2);
+}
+
+// LDS floats the attention task needs to hold `pos` cached positions of one
+// kv head (K as [hd][pos4], V as [pos][hd]) plus the scores.
+__host__ __device__ inline size_t att_lds_floats(uint32_t hd, uint32_t pos, uint32_t max_pos) {
+  size_t pos4 = (pos + 3) & ~3u;
+  return (size_t)max_pos + 64 + (size_t)hd * pos4 + (size_t)pos * hd;
+}
+
+// Copies the cached K/V of positions [0, pos) of one kv head into LDS
+// (before the phase wait: those positions were written by earlier launches).
+__device__ void prefetch_kv(const DecodeArgs& a, uint32_t l, uint32_t kvh, float* kl, float* vl) {
+  const uint32_t hd = a.hd, pos = a.pos, pos4 = (pos + 3) & ~3u, mp4 = a.max_pos >> 2;
+  const float4* kc = reinterpret_cast<const float4*>(a.kc0 + (size_t)l * a.cache_stride) +
+                     (size_t)kvh * hd * mp4;
+  const float4* vc = reinterpret_cast<const float4*>(a.vc0 + (size_t)l * a.cache_stride +
+                                                     (size_t)kvh * a.max_pos * hd);
+  const uint32_t kq = pos4 >> 2, nk = hd * kq, nv = (pos * hd) >> 2;
+  float4* kl4 = reinterpret_cast<float4*>(kl);
+  float4* vl4 = reinterpret_cast<float4*>(vl);
+  constexpr int B = 8;
+  uint32_t i = threadIdx.x;
+  for (; i + (B - 1) * kThreads < nk; i += B * kThreads) {
+    float4 t[B];
+#pragma unroll
+    for (int u = 0; u < B; ++u) {
+      uint32_t e = i + u * kThreads, d = e / kq, q = e - d * kq;
+      t[u] = kc[(size_t)d * mp4 + q];
+    }
+#pragma unroll
+    for (int u = 0; u < B; ++u) kl4[i + u * kThreads] = t[u];
+  }
+  for (; i < nk; i += kThreads) {
+    uint32_t d = i / kq, q = i - d * kq;
+    kl4[i] = kc[(size_t)d * mp4 + q];
+  }
+  copy_block_to_lds(vl4, vc, nv);
 }
 
 // Attention for query head h (code/cis2-fp/src/main.rs:415-467).
-__device__ void run_att(const DecodeArgs& a, uint32_t l, uint32_t h, Lds& s) {
+__device__ void run_att(const DecodeArgs& a, uint32_t l, uint32_t h, Lds& s, size_t wfloats) {
   const LayerW& Lw = a.layers[l];
   const Act ac = act_of(a, l);
   const uint32_t hd = a.hd, group = a.nh / a.nkv, kvh = h / group, len = a.pos + 1;
+  const uint32_t pos4 = (a.pos + 3) & ~3u;
   float* qv = s.v;
   float* kv = qv + hd;
   float* vv = kv + hd;
   float* tmp = vv + hd;
-  float* misc = tmp + hd;  // [0] inv, [1] den, [2..] reduction scratch
+  float* misc = tmp + hd;  // [0] inv, [1] den, [4..] reduction scratch
   float* ss = s.w;         // scores / probabilities, len floats
+  float* kl = ss + a.max_pos + 64;
+  float* vl = kl + (size_t)hd * pos4;
+  const bool in_lds = att_lds_floats(hd, a.pos, a.max_pos) <= wfloats;
+  stamp(a, l, C_ATT, h, 0);
+  if (in_lds) prefetch_kv(a, l, kvh, kl, vl);
   wait_ge(a.cnt + (size_t)l * kCountersPerLayer + C_QKV, a.epoch * a.nq, a.err);
+  stamp(a, l, C_ATT, h, 1);
   for (uint32_t d = threadIdx.x; d < hd; d += kThreads) {
     qv[d] = ld_ag(ac.q + (size_t)h * hd + d);
     kv[d] = ld_ag(ac.k + (size_t)kvh * hd + d);
@@ -342,12 +410,24 @@ __device__ void run_att(const DecodeArgs& a, uint32_t l, uint32_t h, Lds& s) {
   }
   // scores_j = dot_seq(q, k_j) * scale (main.rs:440-445)
   const float* kb = kc + (size_t)kvh * hd * a.max_pos;
+  const float4* q4 = reinterpret_cast<const float4*>(qv);
   for (uint32_t j = threadIdx.x; j < len; j += kThreads) {
     float acc = 0.0f;
     if (j == a.pos) {
       for (uint32_t d = 0; d < hd; ++d) {
         float p = qv[d] * kv[d];
         acc = acc + p;
+      }
+    } else if (in_lds) {
+#pragma unroll 4
+      for (uint32_t d4 = 0; d4 < hd / 4; ++d4) {
+        float4 qq = q4[d4];
+        const float* kr = kl + (size_t)(4 * d4) * pos4 + j;
+        float p;
+        p = qq.x * kr[0]; acc = acc + p;
+        p = qq.y * kr[pos4]; acc = acc + p;
+        p = qq.z * kr[2 * pos4]; acc = acc + p;
+        p = qq.w * kr[3 * pos4]; acc = acc + p;
       }
     } else {
 #pragma unroll 8
@@ -400,7 +480,7 @@ __device__ void run_att(const DecodeArgs& a, uint32_t l, uint32_t h, Lds& s) {
   }
   __syncthreads();
   // V mix out_d = fold_j (p_j * v_j[d]) (main.rs:454-463)
-  const float* vb = vc + (size_t)kvh * a.max_pos * hd;
+  const float* vb = in_lds ? vl : vc + (size_t)kvh * a.max_pos * hd;
   for (uint32_t d = threadIdx.x; d < hd; d += kThreads) {
     float acc = 0.0f;
     const uint32_t np = a.pos;  // cached positions; position pos from LDS
@@ -414,6 +494,7 @@ __device__ void run_att(const DecodeArgs& a, uint32_t l, uint32_t h, Lds& s) {
     st_ag(ac.att + (size_t)h * hd + d, acc);
   }
   signal_add(a.cnt + (size_t)l * kCountersPerLayer + C_ATT, 1);
+  stamp(a, l, C_ATT, h, 2);
 }
 
 __device__ void prefetch_rows(const float* W, uint32_t R, uint32_t K, uint32_t blk, float* dst) {
@@ -425,7 +506,9 @@ __device__ void prefetch_rows(const float* W, uint32_t R, uint32_t K, uint32_t b
 // o_proj block + residual h1 = h + o (main.rs:470-472).
 __device__ void run_o(const DecodeArgs& a, uint32_t l, uint32_t t, Lds& s, uint32_t tok) {
   const Act ac = act_of(a, l);
+  stamp(a, l, C_O, t, 0);
   wait_ge(a.cnt + (size_t)l * kCountersPerLayer + C_ATT, a.epoch * a.nh, a.err);
+  stamp(a, l, C_O, t, 1);
   float* x = s.v;
   load_vec(x, ac.att, a.qd, true);
   __syncthreads();
@@ -439,6 +522,7 @@ __device__ void run_o(const DecodeArgs& a, uint32_t l, uint32_t t, Lds& s, uint3
     }
   }
   signal_add(a.cnt + (size_t)l * kCountersPerLayer + C_O, 1);
+  stamp(a, l, C_O, t, 2);
 }
 
 // gate/up block (wave 0 gate rows, wave 1 up rows) after
@@ -446,7 +530,9 @@ __device__ void run_o(const DecodeArgs& a, uint32_t l, uint32_t t, Lds& s, uint3
 __device__ void run_gu(const DecodeArgs& a, uint32_t l, uint32_t t, Lds& s) {
   const LayerW& Lw = a.layers[l];
   const Act ac = act_of(a, l);
+  stamp(a, l, C_GU, t, 0);
   wait_ge(a.cnt + (size_t)l * kCountersPerLayer + C_O, a.epoch * a.no, a.err);
+  stamp(a, l, C_GU, t, 1);
   float* x = s.v;
   float* ln = x + a.H;
   float* gx = ln + a.H;  // 64 floats: gate results
@@ -468,12 +554,15 @@ __device__ void run_gu(const DecodeArgs& a, uint32_t l, uint32_t t, Lds& s) {
     }
   }
   signal_add(a.cnt + (size_t)l * kCountersPerLayer + C_GU, 1);
+  stamp(a, l, C_GU, t, 2);
 }
 
 // down block + residual h_next = h1 + down (main.rs:489-491).
 __device__ void run_d(const DecodeArgs& a, uint32_t l, uint32_t t, Lds& s) {
   const Act ac = act_of(a, l);
+  stamp(a, l, C_D, t, 0);
   wait_ge(a.cnt + (size_t)l * kCountersPerLayer + C_GU, a.epoch * a.ng, a.err);
+  stamp(a, l, C_D, t, 1);
   float* x = s.v;
   load_vec(x, ac.hid, a.I, true);
   __syncthreads();
@@ -483,13 +572,16 @@ __device__ void run_d(const DecodeArgs& a, uint32_t l, uint32_t t, Lds& s) {
     if (threadIdx.x < a.Rd && row < a.H) st_ag(ac.hout + row, ld_ag(ac.h1 + row) + acc);
   }
   signal_add(a.cnt + (size_t)l * kCountersPerLayer + C_D, 1);
+  stamp(a, l, C_D, t, 2);
 }
 
 // Final norm, LM-head rows (4 waves = 4 blocks at a time), per-block argmax
 // candidates; the last workgroup to finish reduces them.
 __device__ void run_lm(const DecodeArgs& a, Lds& s) {
   const uint32_t L = a.L;
+  stamp(a, L - 1, 5, blockIdx.x, 0);
   wait_ge(a.cnt + (size_t)(L - 1) * kCountersPerLayer + C_D, a.epoch * a.nd, a.err);
+  stamp(a, L - 1, 5, blockIdx.x, 1);
   float* x = s.v;
   float* hn = x + a.H;
   float* misc = hn + a.H;
@@ -519,6 +611,7 @@ __device__ void run_lm(const DecodeArgs& a, Lds& s) {
     }
     done += (base < a.nl) ? min(4u, a.nl - base) : 0u;
   }
+  stamp(a, L - 1, 5, blockIdx.x, 2);
   // ticket: the workgroup whose blocks complete the set reduces them
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
@@ -545,23 +638,14 @@ __device__ void run_lm(const DecodeArgs& a, Lds& s) {
     uint32_t first_nan = ld_ag(a.cand + 2 * a.nl);
     *a.tok_out = (first_nan || r.i == UINT32_MAX) ? 0u : r.i;
   }
+  stamp(a, L - 1, 5, blockIdx.x, 3);
 }
 
 __global__ __launch_bounds__(256) void k_decode(DecodeArgs a) {
   extern __shared__ float4 lds4[];
   Lds s;
   s.w = reinterpret_cast<float*>(lds4);
-  size_t wbytes = 0;
-  {
-    size_t q = (size_t)a.Rq * a.H, o = (size_t)a.Ro * a.qd, g = 2 * (size_t)a.Rg * a.H,
-           d = (size_t)a.Rd * a.I;
-    size_t m = q > o ? q : o;
-    m = m > g ? m : g;
-    m = m > d ? m : d;
-    size_t att = (size_t)a.max_pos + 64;
-    m = m > att ? m : att;
-    wbytes = ((m * 4 + 255) / 256) * 256;
-  }
+  const size_t wbytes = decode_wregion_bytes(a);
   s.v = reinterpret_cast<float*>(reinterpret_cast<char*>(lds4) + wbytes);
   const uint32_t wg = blockIdx.x;
   // role of this workgroup in every layer
@@ -590,7 +674,7 @@ __global__ __launch_bounds__(256) void k_decode(DecodeArgs a) {
         run_qkv(a, l, t, s, tok);
         break;
       case C_ATT:
-        run_att(a, l, t, s);
+        run_att(a, l, t, s, wbytes / 4);
         break;
       case C_O:
         prefetch_rows(Lw.wo, a.Ro, a.qd, t, s.w);
@@ -624,14 +708,7 @@ size_t decode_act_floats(uint32_t H, uint32_t I, uint32_t qd, uint32_t kvd) {
 }
 
 size_t decode_lds_bytes(const DecodeArgs& a) {
-  size_t q = (size_t)a.Rq * a.H, o = (size_t)a.Ro * a.qd, g = 2 * (size_t)a.Rg * a.H,
-         d = (size_t)a.Rd * a.I;
-  size_t m = q > o ? q : o;
-  m = m > g ? m : g;
-  m = m > d ? m : d;
-  size_t att = (size_t)a.max_pos + 64;
-  m = m > att ? m : att;
-  size_t wbytes = ((m * 4 + 255) / 256) * 256;
+  size_t wbytes = decode_wregion_bytes(a);
   size_t vec = 2 * (size_t)a.H + 64 + 64;
   size_t vi = a.I, vq = a.qd, va = 4 * (size_t)a.hd + 64;
   vec = vec > vi ? vec : vi;

@@ -35,6 +35,9 @@ struct DecodeArgs {
   uint32_t* tok_in;      // token of this position
   uint32_t* tok_out;     // argmax written here (may alias tok_in)
   uint32_t* err;
+  // Optional per-task timestamps (s_memrealtime, 100 MHz), null when off:
+  // [(l * 6 + phase) * 64 + task] * 4 words: wait start, wait end, done.
+  uint64_t* tline;
   uint64_t cache_stride;
   uint32_t H, I, V, L, nh, nkv, hd, qd, kvd, max_pos;
   uint32_t Rq, Ro, Rg, Rd, Rl;
@@ -49,6 +52,7 @@ struct DecodeArgs {
 // Floats of per-layer activation storage, and counters per layer.
 size_t decode_act_floats(uint32_t H, uint32_t I, uint32_t qd, uint32_t kvd);
 constexpr uint32_t kCountersPerLayer = 8;
+constexpr uint32_t kTimelineTasks = 64;
 // Dynamic LDS bytes the kernel needs for this configuration.
 size_t decode_lds_bytes(const DecodeArgs& a);
 hipError_t launch_decode(const DecodeArgs& a, hipStream_t s);

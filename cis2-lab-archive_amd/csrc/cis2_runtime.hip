@@ -105,6 +105,8 @@ struct cis2_ctx {
   uint32_t* cand = nullptr;
   uint32_t epoch = 0, lm_epoch = 0;
   DecodeArgs dargs;
+  uint64_t* tline = nullptr;  // CIS2_TIMELINE=<file>: per-task timestamps of every launch
+  FILE* tline_file = nullptr;
   std::vector<void*> allocs;
 };
 
@@ -330,7 +332,17 @@ int forward_fast(cis2_ctx* c, uint32_t seq, uint32_t pos, uint32_t* tokp, bool w
   if (want_logits) ++c->lm_epoch;
   a.lm_epoch = c->lm_epoch;
   a.want_logits = want_logits ? 1u : 0u;
+  a.tline = c->tline;
   LAUNCH(launch_decode(a, c->st), "decode kernel");
+  if (c->tline_file) {  // profiling mode: synchronous, one record per launch
+    const size_t n = (size_t)c->cfg.n_layers * 6 * kTimelineTasks * 4;
+    std::vector<uint64_t> hbuf(n);
+    HIPCHK(c, hipStreamSynchronize(c->st), "timeline sync");
+    HIPCHK(c, hipMemcpy(hbuf.data(), c->tline, n * 8, hipMemcpyDeviceToHost), "timeline copy");
+    uint32_t hdr[4] = {pos, c->cfg.n_layers, kTimelineTasks, want_logits ? 1u : 0u};
+    fwrite(hdr, sizeof hdr, 1, c->tline_file);
+    fwrite(hbuf.data(), 8, n, c->tline_file);
+  }
   return CIS2_OK;
 }
 
@@ -365,6 +377,7 @@ void cis2_ctx_destroy(cis2_ctx* c) {
   if (!c) return;
   if (c->st) (void)hipStreamSynchronize(c->st);
   for (void* p : c->allocs) (void)hipFree(p);
+  if (c->tline_file) fclose(c->tline_file);
   if (c->ring) (void)hipHostFree(c->ring);
   if (c->ring_tok) (void)hipHostFree(c->ring_tok);
   for (int i = 0; i < kRing; ++i)
@@ -376,7 +389,7 @@ void cis2_ctx_destroy(cis2_ctx* c) {
 int cis2_ctx_create(const cis2_config* cfg, cis2_ctx** out) {
   if (!cfg || !out) return CIS2_E_ARG;
   *out = nullptr;
-  const cis2_config f = *cfg;
+  cis2_config f = *cfg;
   if (f.hidden == 0 || f.inter == 0 || f.n_layers == 0 || f.n_heads == 0 || f.n_kv_heads == 0 ||
       f.head_dim == 0 || f.vocab == 0 || f.max_pos == 0 || f.max_seqs == 0)
     return CIS2_E_ARG;
@@ -384,6 +397,8 @@ int cis2_ctx_create(const cis2_config* cfg, cis2_ctx** out) {
   if (f.n_heads % f.n_kv_heads || f.head_dim % 2 || f.hidden % 4 || f.inter % 4 ||
       (f.n_heads * f.head_dim) % 4 || f.max_pos > 16384 || f.head_dim > 1024)
     return CIS2_E_UNSUPPORTED;
+  // capacity rounded up to 4 positions: the K cache rows are copied as float4
+  f.max_pos = (f.max_pos + 3u) & ~3u;
   cis2_ctx* c = new cis2_ctx();
   memset(c->ring_ev, 0, sizeof c->ring_ev);
   c->cfg = f;
@@ -532,6 +547,15 @@ int cis2_ctx_create(const cis2_config* cfg, cis2_ctx** out) {
     a.act = c->act;
     a.cnt = c->counters;
     a.cand = c->cand;
+    if (const char* tl = getenv("CIS2_TIMELINE")) {
+      const size_t n = (size_t)f.n_layers * 6 * kTimelineTasks * 4;
+      if (hipMalloc(&p, n * 8) == hipSuccess) {
+        c->allocs.push_back(p);
+        c->tline = static_cast<uint64_t*>(p);
+        (void)hipMemset(c->tline, 0, n * 8);
+        c->tline_file = fopen(tl, "wb");
+      }
+    }
   }
   build_registry(c);
   *out = c;
