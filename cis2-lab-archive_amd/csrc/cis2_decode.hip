@@ -3,11 +3,11 @@
 // One launch computes one position of one sequence: all layers, the LM head
 // and the greedy argmax (code/cis2-fp/src/main.rs:355-529 and :1161-1169;
 // C++ mirror code/cis2-fp/gpu/cis2_model.h:685-774).  Every workgroup owns
-// one fixed task per layer phase, so the weights a task needs for the next
-// layer are copied into its LDS while it waits, and phases hand over through
-// per-layer counters instead of kernel boundaries:
+// one fixed task per layer phase, copies the weights that task needs into
+// its LDS while it waits, and consumes the previous phase's outputs as soon
+// as they are written:
 //
-//   QKV  row blocks of q/k/v (+ RMSNorm input_layernorm, recomputed per task)
+//   QKV  row blocks of q/k/v (+ input_layernorm, recomputed per task)
 //   ATT  one workgroup per query head: optional QK-norm, RoPE, KV store,
 //        scores, softmax, V mix
 //   O    row blocks of o_proj, + residual
@@ -17,15 +17,22 @@
 //   LM   final norm, LM-head rows, per-block argmax candidates; the last
 //        workgroup to finish reduces them to the next token id.
 //
-// Arithmetic order is exactly the per-op kernels' (cis2_kernels.hip): one
-// lane owns an output and folds its terms left to right from 0.
+// Arithmetic order is the per-op kernels' (cis2_kernels.hip): one lane owns
+// an output and folds its terms left to right from 0.  Dot products are
+// split into two passes: every wave forms the rounded products (one
+// rounding each, so any order gives the same bits) in LDS, then the owning
+// lane adds them strictly in order, one add per step.
 //
-// Cross-workgroup data within a launch is written and read with agent-scope
-// (sc1) accesses; a counter is incremented only after the writer's stores
-// completed (s_waitcnt vmcnt(0)) and a reader loads the data only after it
-// saw the counter.  Counters grow monotonically: a launch with epoch e
-// waits for e * (task count).  Every wait has a spin cap that raises an
-// error flag instead of hanging.
+// Hand-over: every value that crosses workgroups is one 64-bit word
+// {f32 bits, launch epoch} written with a single agent-scope (sc1) store;
+// the consumer re-reads (sc1) the words it needs until all carry the
+// current epoch.  An aligned 64-bit store is single-copy atomic, so a
+// matching tag implies the matching value: no counters, fences or cache
+// maintenance between phases.  Waits have a spin cap that raises an error
+// flag instead of hanging, and stop early once any task raised it.
+//
+// Pointers carry their address space (LDS = 3, global = 1) so that every
+// access is a ds_* or global_* instruction, never flat_*.
 #include "cis2_decode.hpp"
 #include "cis2_device_math.hpp"
 
@@ -33,38 +40,38 @@ namespace cis2 {
 
 namespace {
 
+#define AS_LDS __attribute__((address_space(3)))
+#define AS_GLB __attribute__((address_space(1)))
+typedef float f4 __attribute__((ext_vector_type(4)));
+typedef unsigned long long u64;
+typedef AS_LDS float lf;
+typedef AS_LDS f4 lf4;
+typedef const AS_GLB float gf;
+typedef const AS_GLB f4 gf4;
+typedef AS_GLB u64 gw;
+
+__device__ __forceinline__ gf* G(const float* p) { return (gf*)p; }
+__device__ __forceinline__ gf4* G4(const float* p) { return (gf4*)p; }
+__device__ __forceinline__ AS_GLB float* GW(float* p) { return (AS_GLB float*)p; }
+__device__ __forceinline__ AS_GLB uint32_t* GU(uint32_t* p) { return (AS_GLB uint32_t*)p; }
+
 constexpr uint32_t kThreads = 256;
 constexpr uint32_t kSpinCap = 1u << 24;  // ~0.5 s of s_sleep(1)
 
-enum { C_QKV = 0, C_ATT = 1, C_O = 2, C_GU = 3, C_D = 4 };
+enum { P_QKV = 0, P_ATT = 1, P_O = 2, P_GU = 3, P_D = 4, P_LM = 5 };
 
+// Per-layer tagged activations.
 struct Act {
-  float *q, *k, *v, *att, *h1, *hid, *hout;
+  gw *q, *k, *v, *att, *h1, *hid, *hout;
 };
 
-// Bytes of the LDS region that holds a task's weight block, or the
-// attention task's scores and cached K/V (up to the LDS budget).
-__host__ __device__ inline size_t decode_wregion_bytes(const DecodeArgs& a) {
-  size_t q = (size_t)a.Rq * a.H, o = (size_t)a.Ro * a.qd, g = 2 * (size_t)a.Rg * a.H,
-         d = (size_t)a.Rd * a.I;
-  size_t m = q > o ? q : o;
-  m = m > g ? m : g;
-  m = m > d ? m : d;
-  size_t att = (size_t)a.max_pos + 64 + 2 * (size_t)a.hd * (((size_t)a.max_pos + 3) & ~(size_t)3);
-  const size_t cap = 38400;  // 150 KiB in floats: what LDS can give this region
-  if (att > cap) att = m > (size_t)a.max_pos + 64 ? m : (size_t)a.max_pos + 64;
-  m = m > att ? m : att;
-  return ((m * 4 + 255) / 256) * 256;
-}
-
-__host__ __device__ inline size_t layer_stride(uint32_t H, uint32_t I, uint32_t qd,
-                                               uint32_t kvd) {
+__host__ __device__ inline size_t layer_words(uint32_t H, uint32_t I, uint32_t qd, uint32_t kvd) {
   size_t s = 2 * (size_t)qd + 2 * (size_t)kvd + 2 * (size_t)H + I;
   return (s + 63) & ~(size_t)63;
 }
 
 __device__ __forceinline__ Act act_of(const DecodeArgs& a, uint32_t l) {
-  float* b = a.act + (size_t)l * layer_stride(a.H, a.I, a.qd, a.kvd);
+  gw* b = (gw*)a.act + (size_t)l * layer_words(a.H, a.I, a.qd, a.kvd);
   Act r;
   r.q = b;
   r.k = r.q + a.qd;
@@ -76,139 +83,367 @@ __device__ __forceinline__ Act act_of(const DecodeArgs& a, uint32_t l) {
   return r;
 }
 
-__device__ __forceinline__ float ld_ag(const float* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+// Row stride (floats) of the attention task's LDS copies of K and V for a
+// position count: the least value >= pos rounded up to 4 that is 4 mod 32,
+// so that 64 lanes reading 16 bytes each from 64 rows hit distinct banks.
+__host__ __device__ inline uint32_t att_row_stride(uint32_t pos) {
+  const uint32_t p4 = (pos + 3) & ~3u;
+  return p4 + ((36u - (p4 & 31u)) & 31u);
 }
+
+// LDS floats of the attention task: scores (max_pos + 64) and K, V rows.
+__host__ __device__ inline size_t att_lds_floats(uint32_t hd, uint32_t pos, uint32_t max_pos) {
+  return (size_t)max_pos + 64 + 2 * (size_t)hd * att_row_stride(pos);
+}
+
+// Bytes of the LDS region that holds a task's weight block(s), or the
+// attention task's scores and cached K/V (up to what LDS can give).
+__host__ __device__ inline size_t decode_wregion_bytes(const DecodeArgs& a) {
+  size_t q = (size_t)a.Rq * a.H, o = (size_t)a.Ro * a.qd, g = 2 * (size_t)a.Rg * a.H,
+         d = (size_t)a.Rd * a.I, lm = (size_t)a.Rl * a.H;
+  size_t m = q > o ? q : o;
+  m = m > g ? m : g;
+  m = m > d ? m : d;
+  m = m > lm ? m : lm;
+  // Attention: scores always in LDS; K/V rows in LDS for the positions that
+  // fit in 150 KiB, read from HBM beyond that.
+  size_t att = att_lds_floats(a.hd, a.max_pos, a.max_pos);
+  size_t cap = 38400;
+  if (cap < (size_t)a.max_pos + 64) cap = (size_t)a.max_pos + 64;
+  if (att > cap) att = cap;
+  m = m > att ? m : att;
+  return ((m * 4 + 255) / 256) * 256;
+}
+
 __device__ __forceinline__ uint32_t ld_ag(const uint32_t* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void st_ag(float* p, float v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return __hip_atomic_load((const AS_GLB uint32_t*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ void st_ag(uint32_t* p, uint32_t v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_store(GU(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void raise_err(uint32_t* err, uint32_t bit) {
+  __hip_atomic_fetch_or(GU(err), bit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ u64 get_word(const gw* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void put_word(gw* p, float v, uint32_t epoch) {
+  __hip_atomic_store(p, ((u64)epoch << 32) | (u64)__float_as_uint(v), __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
 }
 
 __device__ __forceinline__ void stamp(const DecodeArgs& a, uint32_t l, uint32_t ph, uint32_t t,
                                       uint32_t slot) {
   if (a.tline && threadIdx.x == 0 && t < kTimelineTasks)
-    a.tline[(((size_t)l * 6 + ph) * kTimelineTasks + t) * 4 + slot] = __builtin_amdgcn_s_memrealtime();
+    ((AS_GLB uint64_t*)a.tline)[(((size_t)l * 6 + ph) * kTimelineTasks + t) * 4 + slot] =
+        __builtin_amdgcn_s_memrealtime();
 }
 
-__device__ void wait_ge(uint32_t* ctr, uint32_t target, uint32_t* err) {
-  if (threadIdx.x == 0) {
+// Waits until the n tagged words addr(0..n-1) carry `epoch` and copies their
+// values to dst[0..n-1].  Up to 12 words in flight per thread; longer
+// vectors are gathered in slices.
+template <class F>
+__device__ __forceinline__ void gather(lf* dst, uint32_t n, uint32_t epoch, uint32_t* err,
+                                       F addr) {
+  constexpr int M = 12;
+  for (uint32_t base = 0; base < n; base += M * kThreads) {
+    u64 w[M];
     uint32_t spins = 0;
-    while ((int32_t)(ld_ag(ctr) - target) < 0) {
+    while (true) {
+#pragma unroll
+      for (int u = 0; u < M; ++u) {
+        const uint32_t i = base + threadIdx.x + u * kThreads;
+        if (i < n) w[u] = get_word(addr(i));
+      }
+      bool ok = true;
+#pragma unroll
+      for (int u = 0; u < M; ++u) {
+        const uint32_t i = base + threadIdx.x + u * kThreads;
+        if (i < n && (uint32_t)(w[u] >> 32) != epoch) ok = false;
+      }
+      if (ok) break;
       __builtin_amdgcn_s_sleep(1);
-      if ((++spins & 255u) == 0 && ld_ag(err) != 0u) break;  // another task failed
+      ++spins;
+      if ((spins & 255u) == 0 && ld_ag(err) != 0u) break;  // another task failed
       if (spins > kSpinCap) {
-        atomicOr(err, 2u);
+        raise_err(err, 2u);
         break;
       }
     }
+#pragma unroll
+    for (int u = 0; u < M; ++u) {
+      const uint32_t i = base + threadIdx.x + u * kThreads;
+      if (i < n) dst[i] = __uint_as_float((uint32_t)w[u]);
+    }
   }
   __syncthreads();
 }
 
-// All of this workgroup's stores are complete before the counter moves.
-__device__ void signal_add(uint32_t* ctr, uint32_t n) {
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __syncthreads();
-  if (threadIdx.x == 0) __hip_atomic_fetch_add(ctr, n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+__device__ __forceinline__ void gather_vec(lf* dst, const gw* src, uint32_t n,
+                                           const DecodeArgs& a) {
+  gather(dst, n, a.epoch, a.err, [=](uint32_t i) { return src + i; });
 }
 
-// Copies n4 float4 from global memory into LDS with 12 loads in flight per
-// thread.
-__device__ void copy_block_to_lds(float4* dst, const float4* __restrict__ src, uint32_t n4) {
-  uint32_t i = threadIdx.x;
-  constexpr int B = 12;
-  for (; i + (B - 1) * kThreads < n4; i += B * kThreads) {
-    float4 t[B];
+// Copies n4 f4 (element i from src(i), global memory) to dst[i] with up to
+// 36 loads in flight per thread: a 144 KiB block in one round trip per
+// workgroup.
+template <class F>
+__device__ __forceinline__ void copy_to_lds(lf4* dst, uint32_t n4, F src) {
+  constexpr uint32_t B = 36;
+  for (uint32_t i = threadIdx.x; i < n4; i += B * kThreads) {
+    f4 t[B];
 #pragma unroll
-    for (int u = 0; u < B; ++u) t[u] = src[i + u * kThreads];
+    for (uint32_t u = 0; u < B; ++u)
+      if (i + u * kThreads < n4) t[u] = *src(i + u * kThreads);
 #pragma unroll
-    for (int u = 0; u < B; ++u) dst[i + u * kThreads] = t[u];
+    for (uint32_t u = 0; u < B; ++u)
+      if (i + u * kThreads < n4) dst[i + u * kThreads] = t[u];
   }
-  for (; i < n4; i += kThreads) dst[i] = src[i];
 }
 
-// Strict left-to-right chain over K for row `lane` of an LDS block laid out
-// [K/4][R][4]; x is the LDS input vector.  Lanes >= R read row R-1 (their
-// result is discarded).
-__device__ __forceinline__ float chain_lds(const float* W, uint32_t R, const float* x, uint32_t K,
-                                           uint32_t lane) {
-  const uint32_t ln = lane < R ? lane : R - 1;
-  const float4* wp = reinterpret_cast<const float4*>(W) + ln;
-  const float4* xp = reinterpret_cast<const float4*>(x);
-  const uint32_t KG = K >> 2;
-  float acc = 0.0f;
-#pragma unroll 8
-  for (uint32_t g = 0; g < KG; ++g) {
-    float4 w = wp[(size_t)g * R];
-    float4 xv = xp[g];
-    float p;
-    p = w.x * xv.x; acc = acc + p;
-    p = w.y * xv.y; acc = acc + p;
-    p = w.z * xv.z; acc = acc + p;
-    p = w.w * xv.w; acc = acc + p;
+// Row block blk ([K/4][R][4] floats) of a blocked matrix into LDS.
+__device__ __forceinline__ void prefetch_rows(const float* W, uint32_t R, uint32_t K, uint32_t blk,
+                                              lf* dst) {
+  const size_t blkf = (size_t)R * K;
+  gf4* src = G4(W + blk * blkf);
+  copy_to_lds((lf4*)dst, (uint32_t)(blkf / 4), [=](uint32_t i) { return src + i; });
+}
+
+// Row block blk of two matrices of the same shape, back to back in LDS.
+__device__ __forceinline__ void prefetch_rows2(const float* A, const float* B, uint32_t R,
+                                               uint32_t K, uint32_t blk, lf* dst) {
+  const size_t blkf = (size_t)R * K;
+  const uint32_t n4 = (uint32_t)(blkf / 4);
+  gf4* sa = G4(A + blk * blkf);
+  gf4* sb = G4(B + blk * blkf);
+  copy_to_lds((lf4*)dst, 2 * n4, [=](uint32_t i) { return i < n4 ? sa + i : sb + (i - n4); });
+}
+
+// ---------------------------------------------------------------------------
+// Strict chains over LDS with reads kept in flight
+// ---------------------------------------------------------------------------
+
+// acc + p[0].x + p[0].y + ... + p[n-1].w (element i at p[i * st]), strictly
+// left to right.  A ring of D reads stays in flight, so a step costs its four
+// adds rather than an LDS round trip.  The ring is filled unconditionally
+// (n >= D) and each slot is refilled right after its adds, in an order the
+// scheduler may not change: that lets the wait before each step be
+// lgkmcnt(D-1) instead of a full drain.
+template <uint32_t D = 8>
+__device__ __forceinline__ float chain4(const lf4* p, uint32_t n, uint32_t st, float acc) {
+  if (n < D) {
+    for (uint32_t g = 0; g < n; ++g) {
+      const f4 v = p[(size_t)g * st];
+      acc = acc + v.x;
+      acc = acc + v.y;
+      acc = acc + v.z;
+      acc = acc + v.w;
+    }
+    return acc;
   }
-  return acc;
-}
-
-// Same chain with the block streamed from global memory; `D` float4 loads
-// are kept in flight per lane.
-__device__ __forceinline__ float chain_global(const float* __restrict__ W, uint32_t R,
-                                              const float* x, uint32_t K, uint32_t lane) {
-  const uint32_t ln = lane < R ? lane : R - 1;
-  const float4* __restrict__ wp = reinterpret_cast<const float4*>(W) + ln;
-  const float4* xp = reinterpret_cast<const float4*>(x);
-  const uint32_t KG = K >> 2;
-  constexpr uint32_t D = 16;
-  float4 buf[D];
+  f4 ring[D];
 #pragma unroll
-  for (uint32_t u = 0; u < D; ++u) buf[u] = u < KG ? wp[(size_t)u * R] : make_float4(0, 0, 0, 0);
-  float acc = 0.0f;
-  for (uint32_t g0 = 0; g0 < KG; g0 += D) {
+  for (uint32_t u = 0; u < D; ++u) ring[u] = p[(size_t)u * st];
+  uint32_t g = 0;
+  for (; g + 2 * D <= n; g += D) {
 #pragma unroll
     for (uint32_t u = 0; u < D; ++u) {
-      const uint32_t g = g0 + u;
-      if (g < KG) {
-        float4 w = buf[u];
-        if (g + D < KG) buf[u] = wp[(size_t)(g + D) * R];
-        float4 xv = xp[g];
-        float p;
-        p = w.x * xv.x; acc = acc + p;
-        p = w.y * xv.y; acc = acc + p;
-        p = w.z * xv.z; acc = acc + p;
-        p = w.w * xv.w; acc = acc + p;
-      }
+      const f4 v = ring[u];
+      acc = acc + v.x;
+      acc = acc + v.y;
+      acc = acc + v.z;
+      acc = acc + v.w;
+      ring[u] = p[(size_t)(g + u + D) * st];
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  // ring holds [g, g + D) and D <= n - g < 2D
+#pragma unroll
+  for (uint32_t u = 0; u < D; ++u) {
+    const f4 v = ring[u];
+    acc = acc + v.x;
+    acc = acc + v.y;
+    acc = acc + v.z;
+    acc = acc + v.w;
+    if (g + u + D < n) ring[u] = p[(size_t)(g + u + D) * st];
+  }
+  g += D;
+#pragma unroll
+  for (uint32_t u = 0; u < D; ++u) {
+    if (g + u < n) {
+      const f4 v = ring[u];
+      acc = acc + v.x;
+      acc = acc + v.y;
+      acc = acc + v.z;
+      acc = acc + v.w;
     }
   }
   return acc;
+}
+
+// acc + p[0] + p[st] + ... + p[(n-1)*st], strictly in order, same ring scheme.
+template <uint32_t D = 12>
+__device__ __forceinline__ float chain1(const lf* p, uint32_t n, uint32_t st, float acc) {
+  if (n < D) {
+    for (uint32_t g = 0; g < n; ++g) acc = acc + p[(size_t)g * st];
+    return acc;
+  }
+  float ring[D];
+#pragma unroll
+  for (uint32_t u = 0; u < D; ++u) ring[u] = p[(size_t)u * st];
+  uint32_t g = 0;
+  for (; g + 2 * D <= n; g += D) {
+#pragma unroll
+    for (uint32_t u = 0; u < D; ++u) {
+      acc = acc + ring[u];
+      ring[u] = p[(size_t)(g + u + D) * st];
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+#pragma unroll
+  for (uint32_t u = 0; u < D; ++u) {
+    acc = acc + ring[u];
+    if (g + u + D < n) ring[u] = p[(size_t)(g + u + D) * st];
+  }
+  g += D;
+#pragma unroll
+  for (uint32_t u = 0; u < D; ++u)
+    if (g + u < n) acc = acc + ring[u];
+  return acc;
+}
+
+// Strict sum of n contiguous LDS floats (16-byte aligned).
+__device__ __forceinline__ float chain_vec(const lf* p, uint32_t n, float acc) {
+  acc = chain4(reinterpret_cast<const lf4*>(p), n >> 2, 1, acc);
+  for (uint32_t i = n & ~3u; i < n; ++i) acc = acc + p[i];
+  return acc;
+}
+
+// ---------------------------------------------------------------------------
+// GEMV on LDS-resident row blocks ([K/4][R][4] floats per block)
+// ---------------------------------------------------------------------------
+
+// In place W[g][r][j] *= x[4g+j] over groups [g0, g1) of nb blocks (block b
+// at W4 + b*bf4), by threads tid = 0..nt-1.
+// Reads are batched (B weight and B input reads before the B writes): the
+// in-place writes would otherwise order every read behind the previous write.
+template <uint32_t R>
+__device__ __forceinline__ void prod_range(lf4* W4, const lf4* x4, uint32_t bf4, uint32_t nb,
+                                           uint32_t g0, uint32_t g1, uint32_t tid, uint32_t nt) {
+  constexpr uint32_t B = 6;
+  const uint32_t per = (g1 - g0) * R;
+  for (uint32_t b = 0; b < nb; ++b) {
+    lf4* base = W4 + (size_t)b * bf4 + (size_t)g0 * R;
+    const lf4* xb = x4 + g0;
+    for (uint32_t i0 = tid; i0 < per; i0 += B * nt) {
+      f4 w[B], xv[B];
+#pragma unroll
+      for (uint32_t u = 0; u < B; ++u) {
+        const uint32_t i = i0 + u * nt;
+        if (i < per) {
+          w[u] = base[i];
+          xv[u] = xb[i / R];
+        }
+      }
+#pragma unroll
+      for (uint32_t u = 0; u < B; ++u) {
+        const uint32_t i = i0 + u * nt;
+        if (i < per) {
+          f4 v = w[u];
+          v.x = v.x * xv[u].x;
+          v.y = v.y * xv[u].y;
+          v.z = v.z * xv[u].z;
+          v.w = v.w * xv[u].w;
+          base[i] = v;
+        }
+      }
+    }
+  }
+}
+
+// acc + strict left-to-right sum of row r's products over groups [g0, g1).
+template <uint32_t R>
+__device__ __forceinline__ float chain_range(const lf4* P4, uint32_t g0, uint32_t g1, uint32_t r,
+                                             float acc) {
+  return chain4(P4 + (size_t)g0 * R + r, g1 - g0, R, acc);
+}
+
+// y[r] = fold_k (W[r][k] * x[k]) for nb LDS blocks (block b at W + b*R*K).
+// K is cut into 4 chunks: all waves form the products of chunk 0, then
+// waves [0, nb) add chunk c while the other waves form chunk c+1.  Returns
+// row `lane` of block `wave` in waves < nb (lanes >= R: row R-1).
+template <uint32_t R>
+__device__ __forceinline__ float gemv_lds_t(lf* W, const lf* x, uint32_t K, uint32_t nb) {
+  constexpr uint32_t NC = 4;
+  const uint32_t KG = K >> 2, wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  lf4* W4 = (lf4*)W;
+  const lf4* x4 = (const lf4*)x;
+  const uint32_t bf4 = KG * R;
+  const uint32_t r = lane < R ? lane : R - 1;
+  prod_range<R>(W4, x4, bf4, nb, 0, KG / NC, threadIdx.x, kThreads);
+  __syncthreads();
+  float acc = 0.0f;
+  for (uint32_t c = 0; c < NC; ++c) {
+    const uint32_t g0 = (KG * c) / NC, g1 = (KG * (c + 1)) / NC;
+    if (wv < nb) {
+      acc = chain_range<R>(W4 + (size_t)wv * bf4, g0, g1, r, acc);
+    } else if (c + 1 < NC) {
+      prod_range<R>(W4, x4, bf4, nb, g1, (KG * (c + 2)) / NC, threadIdx.x - nb * 64,
+                    kThreads - nb * 64);
+    }
+    __syncthreads();
+  }
+  return acc;
+}
+
+// Same order for any other block height (runtime stride, no overlap).
+__device__ float gemv_lds_any(uint32_t R, lf* W, const lf* x, uint32_t K, uint32_t nb) {
+  const uint32_t KG = K >> 2, wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  lf4* W4 = (lf4*)W;
+  const lf4* x4 = (const lf4*)x;
+  const uint32_t bf4 = KG * R;
+  for (uint32_t i = threadIdx.x; i < nb * bf4; i += kThreads) {
+    const f4 xv = x4[(i % bf4) / R];
+    f4 w = W4[i];
+    w.x = w.x * xv.x;
+    w.y = w.y * xv.y;
+    w.z = w.z * xv.z;
+    w.w = w.w * xv.w;
+    W4[i] = w;
+  }
+  __syncthreads();
+  float acc = 0.0f;
+  if (wv < nb) acc = chain4(W4 + (size_t)wv * bf4 + (lane < R ? lane : R - 1), KG, R, 0.0f);
+  __syncthreads();
+  return acc;
+}
+
+__device__ __noinline__ float gemv_lds(uint32_t R, lf* W, const lf* x, uint32_t K, uint32_t nb) {
+  switch (R) {
+    case 64: return gemv_lds_t<64>(W, x, K, nb);
+    case 48: return gemv_lds_t<48>(W, x, K, nb);
+    case 36: return gemv_lds_t<36>(W, x, K, nb);
+    case 32: return gemv_lds_t<32>(W, x, K, nb);
+    case 24: return gemv_lds_t<24>(W, x, K, nb);
+    case 18: return gemv_lds_t<18>(W, x, K, nb);
+    case 12: return gemv_lds_t<12>(W, x, K, nb);
+    default: return gemv_lds_any(R, W, x, K, nb);
+  }
 }
 
 // RMSNorm of an LDS vector (code/cis2-fp/src/main.rs:245-260): squares
 // into `tmp`, one strict chain in wave 0, mean by a true divide,
-// inv = 1/sqrt(mean + eps), out = (x*inv)*w.  `out` may alias `tmp` (not x).
-__device__ void rmsnorm_lds(const float* x, const float* __restrict__ w, float eps, uint32_t n,
-                            float* tmp, float* out, float* s_inv) {
+// inv = 1/sqrt(mean + eps), out = (x*inv)*w.  `out` may alias `tmp` or x.
+__device__ __forceinline__ void rmsnorm_lds(const lf* x, const float* w_, float eps, uint32_t n,
+                                            lf* tmp, lf* out, lf* s_inv) {
+  gf* w = G(w_);
   for (uint32_t i = threadIdx.x; i < n; i += kThreads) {
     float v = x[i];
     tmp[i] = v * v;
   }
   __syncthreads();
   if (threadIdx.x < 64) {
-    const float4* p = reinterpret_cast<const float4*>(tmp);
-    float acc = 0.0f;
-#pragma unroll 8
-    for (uint32_t i = 0; i < (n >> 2); ++i) {
-      float4 v = p[i];
-      acc = acc + v.x;
-      acc = acc + v.y;
-      acc = acc + v.z;
-      acc = acc + v.w;
-    }
-    for (uint32_t i = n & ~3u; i < n; ++i) acc = acc + tmp[i];
+    const float acc = chain_vec(tmp, n, 0.0f);
     float mean = acc / (float)n;
     float arg = mean + eps;
     float inv = rsqrt_cr(arg);
@@ -243,151 +478,138 @@ __device__ __forceinline__ Cand cand_wave(Cand x) {
   }
   return x;
 }
+// Block-wide pick over the 4 waves' candidates (scratch: 8 words in LDS).
+__device__ __forceinline__ Cand cand_block(Cand c, AS_LDS uint32_t* red) {
+  c = cand_wave(c);
+  if ((threadIdx.x & 63) == 0) {
+    red[2 * (threadIdx.x >> 6)] = __float_as_uint(c.v);
+    red[2 * (threadIdx.x >> 6) + 1] = c.i;
+  }
+  __syncthreads();
+  Cand b = {__uint_as_float(red[0]), red[1]};
+  for (uint32_t i = 1; i < kThreads / 64; ++i)
+    b = cand_pick(b, Cand{__uint_as_float(red[2 * i]), red[2 * i + 1]});
+  __syncthreads();
+  return b;
+}
 
-// LDS layout: [weights | vec region].  The vec region holds the task's
-// input vector and scratch.
+// LDS layout: [weights | vectors].
 struct Lds {
-  float* w;
-  float* v;
+  lf* w;  // weight block(s); attention: scores, K rows, V rows
+  lf* v;  // the task's input vector(s) and scratch
 };
-
-__device__ const float* hin_of(const DecodeArgs& a, uint32_t l, uint32_t tok) {
-  return l == 0 ? a.embed + (size_t)tok * a.H : act_of(a, l - 1).hout;
-}
-
-// Loads n floats of a layer input into LDS: the embedding row (weights, plain
-// loads) for layer 0, otherwise the previous layer's output (agent scope).
-__device__ void load_vec(float* dst, const float* src, uint32_t n, bool shared) {
-  for (uint32_t i = threadIdx.x; i < n; i += kThreads) dst[i] = shared ? ld_ag(src + i) : src[i];
-}
 
 // ---------------------------------------------------------------------------
 // Phase tasks
 // ---------------------------------------------------------------------------
 
-// QKV task t: which matrix and block.
-__device__ void qkv_task_geom(const DecodeArgs& a, const LayerW& Lw, uint32_t t, const float** W,
-                              const float** bias, uint32_t* M, uint32_t* blk, float** out,
-                              const Act& ac) {
-  if (t < a.nq_q) {
-    *W = Lw.wq; *bias = Lw.bq; *M = a.qd; *blk = t; *out = ac.q;
-  } else if (t < a.nq_q + a.nq_k) {
-    *W = Lw.wk; *bias = Lw.bk; *M = a.kvd; *blk = t - a.nq_q; *out = ac.k;
-  } else {
-    *W = Lw.wv; *bias = Lw.bv; *M = a.kvd; *blk = t - a.nq_q - a.nq_k; *out = ac.v;
-  }
-}
-
-__device__ void prefetch_qkv(const DecodeArgs& a, uint32_t l, uint32_t t, Lds& s) {
-  const LayerW& Lw = a.layers[l];
-  const float *W, *bias;
+struct QkvGeom {
+  const float* W;
+  const float* bias;
+  gw* out;
   uint32_t M, blk;
-  float* out;
-  qkv_task_geom(a, Lw, t, &W, &bias, &M, &blk, &out, act_of(a, l));
-  const size_t blkf = (size_t)a.Rq * a.H;
-  copy_block_to_lds(reinterpret_cast<float4*>(s.w),
-                    reinterpret_cast<const float4*>(W + blk * blkf), (uint32_t)(blkf / 4));
+};
+__device__ __forceinline__ QkvGeom qkv_geom(const DecodeArgs& a, const LayerW& Lw, const Act& ac,
+                                            uint32_t t) {
+  if (t < a.nq_q) return QkvGeom{Lw.wq, Lw.bq, ac.q, a.qd, t};
+  if (t < a.nq_q + a.nq_k) return QkvGeom{Lw.wk, Lw.bk, ac.k, a.kvd, t - a.nq_q};
+  return QkvGeom{Lw.wv, Lw.bv, ac.v, a.kvd, t - a.nq_q - a.nq_k};
 }
 
-__device__ void run_qkv(const DecodeArgs& a, uint32_t l, uint32_t t, Lds& s, uint32_t tok) {
-  const LayerW& Lw = a.layers[l];
+// One row block of q, k or v: input_layernorm, GEMV, bias (main.rs:405-413).
+__device__ __forceinline__ void run_qkv(const DecodeArgs& a, uint32_t l, uint32_t t, const Lds& s,
+                                       uint32_t tok) {
+  const LayerW Lw = a.layers[l];
   const Act ac = act_of(a, l);
-  const float *W, *bias;
-  uint32_t M, blk;
-  float* out;
-  qkv_task_geom(a, Lw, t, &W, &bias, &M, &blk, &out, ac);
-  stamp(a, l, C_QKV, t, 0);
-  if (l > 0) wait_ge(a.cnt + (size_t)(l - 1) * kCountersPerLayer + C_D, a.epoch * a.nd, a.err);
-  stamp(a, l, C_QKV, t, 1);
-  float* x = s.v;
-  float* ln = s.v + a.H;
-  float* s_inv = s.v + 2 * a.H;
-  load_vec(x, hin_of(a, l, tok), a.H, l > 0);
-  __syncthreads();
+  const QkvGeom g = qkv_geom(a, Lw, ac, t);
+  lf* x = s.v;
+  lf* ln = s.v + a.H;
+  lf* s_inv = s.v + 2 * a.H;
+  prefetch_rows(g.W, a.Rq, a.H, g.blk, s.w);
+  stamp(a, l, P_QKV, t, 0);
+  if (l == 0) {
+    gf* e = G(a.embed) + (size_t)tok * a.H;
+    for (uint32_t i = threadIdx.x; i < a.H; i += kThreads) x[i] = e[i];
+    __syncthreads();
+  } else {
+    gather_vec(x, act_of(a, l - 1).hout, a.H, a);
+  }
+  stamp(a, l, P_QKV, t, 1);
   rmsnorm_lds(x, Lw.ln1, a.eps, a.H, ln, ln, s_inv);
-  if (threadIdx.x < 64) {
-    float acc = chain_lds(s.w, a.Rq, ln, a.H, threadIdx.x);
-    uint32_t row = blk * a.Rq + threadIdx.x;
-    if (threadIdx.x < a.Rq && row < M) {
-      float r = bias ? acc + bias[row] : acc;
-      st_ag(out + row, r);
-    }
+  const float acc = gemv_lds(a.Rq, s.w, ln, a.H, 1);
+  const uint32_t row = g.blk * a.Rq + threadIdx.x;
+  if (threadIdx.x < a.Rq && row < g.M) {
+    const float r = g.bias ? acc + G(g.bias)[row] : acc;
+    put_word(g.out + row, r, a.epoch);
   }
-  signal_add(a.cnt + (size_t)l * kCountersPerLayer + C_QKV, 1);
-  stamp(a, l, C_QKV, t, 2);
+  stamp(a, l, P_QKV, t, 2);
 }
 
-// LDS floats the attention task needs to hold `pos` cached positions of one
-// kv head (K as [hd][pos4], V as [pos][hd]) plus the scores.
-__host__ __device__ inline size_t att_lds_floats(uint32_t hd, uint32_t pos, uint32_t max_pos) {
-  size_t pos4 = (pos + 3) & ~3u;
-  return (size_t)max_pos + 64 + (size_t)hd * pos4 + (size_t)pos * hd;
-}
-
-// Copies the cached K/V of positions [0, pos) of one kv head into LDS
-// (before the phase wait: those positions were written by earlier launches).
-__device__ void prefetch_kv(const DecodeArgs& a, uint32_t l, uint32_t kvh, float* kl, float* vl) {
-  const uint32_t hd = a.hd, pos = a.pos, pos4 = (pos + 3) & ~3u, mp4 = a.max_pos >> 2;
-  const float4* kc = reinterpret_cast<const float4*>(a.kc0 + (size_t)l * a.cache_stride) +
-                     (size_t)kvh * hd * mp4;
-  const float4* vc = reinterpret_cast<const float4*>(a.vc0 + (size_t)l * a.cache_stride +
-                                                     (size_t)kvh * a.max_pos * hd);
-  const uint32_t kq = pos4 >> 2, nk = hd * kq, nv = (pos * hd) >> 2;
-  float4* kl4 = reinterpret_cast<float4*>(kl);
-  float4* vl4 = reinterpret_cast<float4*>(vl);
-  constexpr int B = 8;
-  uint32_t i = threadIdx.x;
-  for (; i + (B - 1) * kThreads < nk; i += B * kThreads) {
-    float4 t[B];
+// Copies positions [0, pos) of one kv head's cached K and V (both
+// [hd][max_pos] in HBM, written by earlier launches) into LDS rows of
+// stride S: K rows 0..hd-1, then V rows.  Positions up to pos rounded to 4
+// are copied; the ones >= pos are never used.
+__device__ __forceinline__ void prefetch_kv(const DecodeArgs& a, uint32_t l, uint32_t kvh, lf* kl,
+                                            uint32_t S) {
+  const uint32_t hd = a.hd, kq = (a.pos + 3) >> 2, mp4 = a.max_pos >> 2, nrow = 2 * hd;
+  gf4* kc = G4(a.kc0 + (size_t)l * a.cache_stride);
+  gf4* kb = kc + (size_t)kvh * hd * mp4;
+  gf4* vb = kc + (size_t)a.kvd * mp4 + (size_t)kvh * hd * mp4;
+  lf4* dst = (lf4*)kl;
+  const uint32_t s4 = S >> 2, wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  constexpr uint32_t B = 16;
+  for (uint32_t q = lane; q < kq; q += 64) {
+    uint32_t r = wv;
+    for (; r + 4 * (B - 1) < nrow; r += 4 * B) {
+      f4 t[B];
 #pragma unroll
-    for (int u = 0; u < B; ++u) {
-      uint32_t e = i + u * kThreads, d = e / kq, q = e - d * kq;
-      t[u] = kc[(size_t)d * mp4 + q];
+      for (uint32_t u = 0; u < B; ++u) {
+        const uint32_t rr = r + 4 * u;
+        t[u] = rr < hd ? kb[(size_t)rr * mp4 + q] : vb[(size_t)(rr - hd) * mp4 + q];
+      }
+#pragma unroll
+      for (uint32_t u = 0; u < B; ++u) dst[(size_t)(r + 4 * u) * s4 + q] = t[u];
     }
-#pragma unroll
-    for (int u = 0; u < B; ++u) kl4[i + u * kThreads] = t[u];
+    for (; r < nrow; r += 4)
+      dst[(size_t)r * s4 + q] = r < hd ? kb[(size_t)r * mp4 + q] : vb[(size_t)(r - hd) * mp4 + q];
   }
-  for (; i < nk; i += kThreads) {
-    uint32_t d = i / kq, q = i - d * kq;
-    kl4[i] = kc[(size_t)d * mp4 + q];
-  }
-  copy_block_to_lds(vl4, vc, nv);
 }
 
 // Attention for query head h (code/cis2-fp/src/main.rs:415-467).
-__device__ void run_att(const DecodeArgs& a, uint32_t l, uint32_t h, Lds& s, size_t wfloats) {
-  const LayerW& Lw = a.layers[l];
+__device__ __forceinline__ void run_att(const DecodeArgs& a, uint32_t l, uint32_t h, const Lds& s,
+                        size_t wfloats) {
+  const LayerW Lw = a.layers[l];
   const Act ac = act_of(a, l);
-  const uint32_t hd = a.hd, group = a.nh / a.nkv, kvh = h / group, len = a.pos + 1;
-  const uint32_t pos4 = (a.pos + 3) & ~3u;
-  float* qv = s.v;
-  float* kv = qv + hd;
-  float* vv = kv + hd;
-  float* tmp = vv + hd;
-  float* misc = tmp + hd;  // [0] inv, [1] den, [4..] reduction scratch
-  float* ss = s.w;         // scores / probabilities, len floats
-  float* kl = ss + a.max_pos + 64;
-  float* vl = kl + (size_t)hd * pos4;
-  const bool in_lds = att_lds_floats(hd, a.pos, a.max_pos) <= wfloats;
-  stamp(a, l, C_ATT, h, 0);
-  if (in_lds) prefetch_kv(a, l, kvh, kl, vl);
-  wait_ge(a.cnt + (size_t)l * kCountersPerLayer + C_QKV, a.epoch * a.nq, a.err);
-  stamp(a, l, C_ATT, h, 1);
-  for (uint32_t d = threadIdx.x; d < hd; d += kThreads) {
-    qv[d] = ld_ag(ac.q + (size_t)h * hd + d);
-    kv[d] = ld_ag(ac.k + (size_t)kvh * hd + d);
-    vv[d] = ld_ag(ac.v + (size_t)kvh * hd + d);
-  }
-  __syncthreads();
+  const uint32_t hd = a.hd, group = a.nh / a.nkv, kvh = h / group, pos = a.pos, len = pos + 1;
+  const uint32_t wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  lf* qv = s.v;
+  lf* kv = qv + hd;
+  lf* vv = kv + hd;
+  lf* tmp = vv + hd;
+  lf* misc = tmp + hd;  // [0] inv, [1] den, [4..] reduction scratch
+  AS_LDS uint32_t* red = (AS_LDS uint32_t*)(misc + 4);
+  lf* ss = s.w;  // scores / probabilities
+  lf* kl = ss + a.max_pos + 64;
+  const uint32_t S = att_row_stride(pos);
+  lf* vl = kl + (size_t)hd * S;
+  const bool in_lds = att_lds_floats(hd, pos, a.max_pos) <= wfloats;
+  stamp(a, l, P_ATT, h, 0);
+  if (in_lds) prefetch_kv(a, l, kvh, kl, S);
+  gather(qv, 3 * hd, a.epoch, a.err, [=](uint32_t i) {
+    const uint32_t seg = i >= hd ? (i >= 2 * hd ? 2u : 1u) : 0u, d = i - seg * hd;
+    return seg == 0 ? ac.q + (size_t)h * hd + d
+                    : (seg == 1 ? ac.k : ac.v) + (size_t)kvh * hd + d;
+  });
+  stamp(a, l, P_ATT, h, 1);
   // Qwen3 per-head QK-norm, after bias and before RoPE
   // (labs/w1x-qwen3/scripts/qwen3-port.diff:66-80).
   if (Lw.qn) rmsnorm_lds(qv, Lw.qn, a.eps, hd, tmp, qv, misc);
   if (Lw.kn) rmsnorm_lds(kv, Lw.kn, a.eps, hd, tmp, kv, misc);
   // RoPE rotate-half (main.rs:285-307): o1 = x1*c + (-x2)*s, o2 = x2*c + x1*s.
   const uint32_t half = hd / 2;
-  const float* cs = a.rope_cs + (size_t)a.pos * half * 2;
+  gf* cs = G(a.rope_cs) + (size_t)pos * half * 2;
   for (uint32_t idx = threadIdx.x; idx < 2 * half; idx += kThreads) {
-    float* hv = idx < half ? qv : kv;
+    lf* hv = idx < half ? qv : kv;
     uint32_t i = idx < half ? idx : idx - half;
     float c = cs[2 * i], sn = cs[2 * i + 1];
     float x1 = hv[i], x2 = hv[i + half];
@@ -400,43 +622,72 @@ __device__ void run_att(const DecodeArgs& a, uint32_t l, uint32_t h, Lds& s, siz
     hv[i + half] = t3 + t4;
   }
   __syncthreads();
-  float* kc = a.kc0 + (size_t)l * a.cache_stride;
-  float* vc = a.vc0 + (size_t)l * a.cache_stride;
+  AS_GLB float* kc = GW(a.kc0 + (size_t)l * a.cache_stride);
+  AS_GLB float* vc = GW(a.vc0 + (size_t)l * a.cache_stride);
   if (h % group == 0) {  // one writer per kv head; the others use their own copy
     for (uint32_t d = threadIdx.x; d < hd; d += kThreads) {
-      kc[((size_t)kvh * hd + d) * a.max_pos + a.pos] = kv[d];
-      vc[((size_t)kvh * a.max_pos + a.pos) * hd + d] = vv[d];
+      kc[((size_t)kvh * hd + d) * a.max_pos + pos] = kv[d];
+      vc[((size_t)kvh * hd + d) * a.max_pos + pos] = vv[d];
     }
   }
   // scores_j = dot_seq(q, k_j) * scale (main.rs:440-445)
-  const float* kb = kc + (size_t)kvh * hd * a.max_pos;
-  const float4* q4 = reinterpret_cast<const float4*>(qv);
-  for (uint32_t j = threadIdx.x; j < len; j += kThreads) {
-    float acc = 0.0f;
-    if (j == a.pos) {
-      for (uint32_t d = 0; d < hd; ++d) {
-        float p = qv[d] * kv[d];
-        acc = acc + p;
-      }
-    } else if (in_lds) {
-#pragma unroll 4
-      for (uint32_t d4 = 0; d4 < hd / 4; ++d4) {
-        float4 qq = q4[d4];
-        const float* kr = kl + (size_t)(4 * d4) * pos4 + j;
-        float p;
-        p = qq.x * kr[0]; acc = acc + p;
-        p = qq.y * kr[pos4]; acc = acc + p;
-        p = qq.z * kr[2 * pos4]; acc = acc + p;
-        p = qq.w * kr[3 * pos4]; acc = acc + p;
-      }
-    } else {
-#pragma unroll 8
-      for (uint32_t d = 0; d < hd; ++d) {
-        float p = qv[d] * kb[(size_t)d * a.max_pos + j];
-        acc = acc + p;
+  if (in_lds) {
+    // products q[d] * k_j[d] in place (row d scaled by q[d]); tmp = q * k_pos
+    const uint32_t kq = (pos + 3) >> 2, s4 = S >> 2;
+    lf4* k4 = (lf4*)kl;
+    constexpr uint32_t B = 8;  // rows per batch: all reads before the writes
+    for (uint32_t q = lane; q < kq; q += 64) {
+      for (uint32_t d0 = wv; d0 < hd; d0 += 4 * B) {
+        f4 v[B];
+        float qd[B];
+#pragma unroll
+        for (uint32_t u = 0; u < B; ++u) {
+          const uint32_t d = d0 + 4 * u;
+          if (d < hd) {
+            v[u] = k4[(size_t)d * s4 + q];
+            qd[u] = qv[d];
+          }
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < B; ++u) {
+          const uint32_t d = d0 + 4 * u;
+          if (d < hd) {
+            f4 w = v[u];
+            w.x = qd[u] * w.x;
+            w.y = qd[u] * w.y;
+            w.z = qd[u] * w.z;
+            w.w = qd[u] * w.w;
+            k4[(size_t)d * s4 + q] = w;
+          }
+        }
       }
     }
-    ss[j] = acc * a.scale;
+    for (uint32_t d = threadIdx.x; d < hd; d += kThreads) tmp[d] = qv[d] * kv[d];
+    __syncthreads();
+    for (uint32_t j = threadIdx.x; j < len; j += kThreads) {
+      const lf* p = j < pos ? kl + j : tmp;
+      const uint32_t st = j < pos ? S : 1u;
+      const float acc = chain1(p, hd, st, 0.0f);
+      ss[j] = acc * a.scale;
+    }
+  } else {
+    const AS_GLB float* kb = kc + (size_t)kvh * hd * a.max_pos;
+    for (uint32_t j = threadIdx.x; j < len; j += kThreads) {
+      float acc = 0.0f;
+      if (j == pos) {
+        for (uint32_t d = 0; d < hd; ++d) {
+          float p = qv[d] * kv[d];
+          acc = acc + p;
+        }
+      } else {
+#pragma unroll 8
+        for (uint32_t d = 0; d < hd; ++d) {
+          float p = qv[d] * kb[(size_t)d * a.max_pos + j];
+          acc = acc + p;
+        }
+      }
+      ss[j] = acc * a.scale;
+    }
   }
   __syncthreads();
   // softmax_seq (math.rs:425-442): first-wins max, pinned exp, strict-chain
@@ -446,30 +697,15 @@ __device__ void run_att(const DecodeArgs& a, uint32_t l, uint32_t h, Lds& s, siz
     float v = ss[j];
     if (v == v) best = cand_pick(best, Cand{v, j});
   }
-  best = cand_wave(best);
-  Cand* red = reinterpret_cast<Cand*>(misc + 4);
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = best;
-  __syncthreads();
-  Cand b = red[0];
-  for (uint32_t i = 1; i < kThreads / 64; ++i) b = cand_pick(b, red[i]);
+  const Cand b = cand_block(best, red);
   const float mx = (ss[0] != ss[0]) ? ss[0] : b.v;
-  __syncthreads();
   for (uint32_t j = threadIdx.x; j < len; j += kThreads) {
     float dlt = ss[j] - mx;
     ss[j] = exp_pinned(dlt);
   }
   __syncthreads();
   if (threadIdx.x < 64) {
-    float acc = 0.0f;
-    uint32_t j = 0;
-    for (; j + 4 <= len; j += 4) {
-      float4 e = *reinterpret_cast<const float4*>(ss + j);
-      acc = acc + e.x;
-      acc = acc + e.y;
-      acc = acc + e.z;
-      acc = acc + e.w;
-    }
-    for (; j < len; ++j) acc = acc + ss[j];
+    const float acc = chain_vec(ss, len, 0.0f);
     if (threadIdx.x == 0) misc[1] = acc;
   }
   __syncthreads();
@@ -480,124 +716,158 @@ __device__ void run_att(const DecodeArgs& a, uint32_t l, uint32_t h, Lds& s, siz
   }
   __syncthreads();
   // V mix out_d = fold_j (p_j * v_j[d]) (main.rs:454-463)
-  const float* vb = in_lds ? vl : vc + (size_t)kvh * a.max_pos * hd;
-  for (uint32_t d = threadIdx.x; d < hd; d += kThreads) {
-    float acc = 0.0f;
-    const uint32_t np = a.pos;  // cached positions; position pos from LDS
-#pragma unroll 8
-    for (uint32_t j = 0; j < np; ++j) {
-      float p = ss[j] * vb[(size_t)j * hd + d];
-      acc = acc + p;
+  if (in_lds) {
+    const uint32_t kq = (pos + 3) >> 2, s4 = S >> 2;
+    lf4* v4 = (lf4*)vl;
+    const lf4* p4 = (const lf4*)ss;
+    constexpr uint32_t B = 8;  // rows per batch: all reads before the writes
+    for (uint32_t q = lane; q < kq; q += 64) {
+      const f4 p = p4[q];
+      for (uint32_t d0 = wv; d0 < hd; d0 += 4 * B) {
+        f4 v[B];
+#pragma unroll
+        for (uint32_t u = 0; u < B; ++u)
+          if (d0 + 4 * u < hd) v[u] = v4[(size_t)(d0 + 4 * u) * s4 + q];
+#pragma unroll
+        for (uint32_t u = 0; u < B; ++u) {
+          if (d0 + 4 * u < hd) {
+            f4 w = v[u];
+            w.x = p.x * w.x;
+            w.y = p.y * w.y;
+            w.z = p.z * w.z;
+            w.w = p.w * w.w;
+            v4[(size_t)(d0 + 4 * u) * s4 + q] = w;
+          }
+        }
+      }
     }
-    float p = ss[np] * vv[d];
-    acc = acc + p;
-    st_ag(ac.att + (size_t)h * hd + d, acc);
+    __syncthreads();
+    for (uint32_t d = threadIdx.x; d < hd; d += kThreads) {
+      float acc = chain_vec(vl + (size_t)d * S, pos, 0.0f);
+      float p = ss[pos] * vv[d];
+      acc = acc + p;
+      put_word(ac.att + (size_t)h * hd + d, acc, a.epoch);
+    }
+  } else {
+    const AS_GLB float* vb = vc + (size_t)kvh * hd * a.max_pos;
+    for (uint32_t d = threadIdx.x; d < hd; d += kThreads) {
+      float acc = 0.0f;
+#pragma unroll 8
+      for (uint32_t j = 0; j < pos; ++j) {
+        float p = ss[j] * vb[(size_t)d * a.max_pos + j];
+        acc = acc + p;
+      }
+      float p = ss[pos] * vv[d];
+      acc = acc + p;
+      put_word(ac.att + (size_t)h * hd + d, acc, a.epoch);
+    }
   }
-  signal_add(a.cnt + (size_t)l * kCountersPerLayer + C_ATT, 1);
-  stamp(a, l, C_ATT, h, 2);
-}
-
-__device__ void prefetch_rows(const float* W, uint32_t R, uint32_t K, uint32_t blk, float* dst) {
-  const size_t blkf = (size_t)R * K;
-  copy_block_to_lds(reinterpret_cast<float4*>(dst), reinterpret_cast<const float4*>(W + blk * blkf),
-                    (uint32_t)(blkf / 4));
+  __syncthreads();
+  stamp(a, l, P_ATT, h, 2);
 }
 
 // o_proj block + residual h1 = h + o (main.rs:470-472).
-__device__ void run_o(const DecodeArgs& a, uint32_t l, uint32_t t, Lds& s, uint32_t tok) {
+__device__ __forceinline__ void run_o(const DecodeArgs& a, uint32_t l, uint32_t t, const Lds& s,
+                                     uint32_t tok) {
+  const LayerW Lw = a.layers[l];
   const Act ac = act_of(a, l);
-  stamp(a, l, C_O, t, 0);
-  wait_ge(a.cnt + (size_t)l * kCountersPerLayer + C_ATT, a.epoch * a.nh, a.err);
-  stamp(a, l, C_O, t, 1);
-  float* x = s.v;
-  load_vec(x, ac.att, a.qd, true);
-  __syncthreads();
-  if (threadIdx.x < 64) {
-    float acc = chain_lds(s.w, a.Ro, x, a.qd, threadIdx.x);
-    uint32_t row = t * a.Ro + threadIdx.x;
-    if (threadIdx.x < a.Ro && row < a.H) {
-      const float* hp = hin_of(a, l, tok);
-      float hv = l > 0 ? ld_ag(hp + row) : hp[row];
-      st_ag(ac.h1 + row, hv + acc);
-    }
+  const uint32_t qd = a.qd, r0 = t * a.Ro, nr = min(a.Ro, a.H - r0);
+  lf* x = s.v;        // attention output [qd]
+  lf* hres = x + qd;  // this block's residual rows [nr]
+  prefetch_rows(Lw.wo, a.Ro, qd, t, s.w);
+  stamp(a, l, P_O, t, 0);
+  if (l == 0) {
+    gf* e = G(a.embed) + (size_t)tok * a.H + r0;
+    for (uint32_t i = threadIdx.x; i < nr; i += kThreads) hres[i] = e[i];
+    gather_vec(x, ac.att, qd, a);
+  } else {
+    const gw* hin = act_of(a, l - 1).hout + r0;
+    const gw* att = ac.att;
+    gather(x, qd + nr, a.epoch, a.err,
+           [=](uint32_t i) { return i < qd ? att + i : hin + (i - qd); });
   }
-  signal_add(a.cnt + (size_t)l * kCountersPerLayer + C_O, 1);
-  stamp(a, l, C_O, t, 2);
+  stamp(a, l, P_O, t, 1);
+  const float acc = gemv_lds(a.Ro, s.w, x, qd, 1);
+  if (threadIdx.x < nr) put_word(ac.h1 + r0 + threadIdx.x, hres[threadIdx.x] + acc, a.epoch);
+  stamp(a, l, P_O, t, 2);
 }
 
 // gate/up block (wave 0 gate rows, wave 1 up rows) after
 // post_attention_layernorm; hid = silu(gate) * up (main.rs:478-487).
-__device__ void run_gu(const DecodeArgs& a, uint32_t l, uint32_t t, Lds& s) {
-  const LayerW& Lw = a.layers[l];
+__device__ __forceinline__ void run_gu(const DecodeArgs& a, uint32_t l, uint32_t t, const Lds& s) {
+  const LayerW Lw = a.layers[l];
   const Act ac = act_of(a, l);
-  stamp(a, l, C_GU, t, 0);
-  wait_ge(a.cnt + (size_t)l * kCountersPerLayer + C_O, a.epoch * a.no, a.err);
-  stamp(a, l, C_GU, t, 1);
-  float* x = s.v;
-  float* ln = x + a.H;
-  float* gx = ln + a.H;  // 64 floats: gate results
-  float* s_inv = gx + 64;
-  load_vec(x, ac.h1, a.H, true);
-  __syncthreads();
+  lf* x = s.v;
+  lf* ln = x + a.H;
+  lf* gx = ln + a.H;  // 64 floats: gate results
+  lf* s_inv = gx + 64;
+  prefetch_rows2(Lw.wg, Lw.wu, a.Rg, a.H, t, s.w);
+  stamp(a, l, P_GU, t, 0);
+  gather_vec(x, ac.h1, a.H, a);
+  stamp(a, l, P_GU, t, 1);
   rmsnorm_lds(x, Lw.ln2, a.eps, a.H, ln, ln, s_inv);
+  const float acc = gemv_lds(a.Rg, s.w, ln, a.H, 2);
   const uint32_t wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const size_t blkf = (size_t)a.Rg * a.H;
-  float acc = 0.0f;
-  if (wv < 2) acc = chain_lds(s.w + wv * blkf, a.Rg, ln, a.H, lane);
   if (wv == 0) gx[lane] = acc;
   __syncthreads();
   if (wv == 1) {
-    uint32_t row = t * a.Rg + lane;
+    const uint32_t row = t * a.Rg + lane;
     if (lane < a.Rg && row < a.I) {
-      float sg = silu_pinned(gx[lane]);
-      st_ag(ac.hid + row, sg * acc);
+      const float sg = silu_pinned(gx[lane]);
+      put_word(ac.hid + row, sg * acc, a.epoch);
     }
   }
-  signal_add(a.cnt + (size_t)l * kCountersPerLayer + C_GU, 1);
-  stamp(a, l, C_GU, t, 2);
+  stamp(a, l, P_GU, t, 2);
 }
 
 // down block + residual h_next = h1 + down (main.rs:489-491).
-__device__ void run_d(const DecodeArgs& a, uint32_t l, uint32_t t, Lds& s) {
+__device__ __forceinline__ void run_d(const DecodeArgs& a, uint32_t l, uint32_t t, const Lds& s) {
+  const LayerW Lw = a.layers[l];
   const Act ac = act_of(a, l);
-  stamp(a, l, C_D, t, 0);
-  wait_ge(a.cnt + (size_t)l * kCountersPerLayer + C_GU, a.epoch * a.ng, a.err);
-  stamp(a, l, C_D, t, 1);
-  float* x = s.v;
-  load_vec(x, ac.hid, a.I, true);
-  __syncthreads();
-  if (threadIdx.x < 64) {
-    float acc = chain_lds(s.w, a.Rd, x, a.I, threadIdx.x);
-    uint32_t row = t * a.Rd + threadIdx.x;
-    if (threadIdx.x < a.Rd && row < a.H) st_ag(ac.hout + row, ld_ag(ac.h1 + row) + acc);
-  }
-  signal_add(a.cnt + (size_t)l * kCountersPerLayer + C_D, 1);
-  stamp(a, l, C_D, t, 2);
+  const uint32_t I = a.I, r0 = t * a.Rd, nr = min(a.Rd, a.H - r0);
+  lf* x = s.v;       // hid [I]
+  lf* hres = x + I;  // residual rows [nr]
+  prefetch_rows(Lw.wd, a.Rd, I, t, s.w);
+  stamp(a, l, P_D, t, 0);
+  const gw* h1 = ac.h1 + r0;
+  const gw* hid = ac.hid;
+  gather(x, I + nr, a.epoch, a.err,
+         [=](uint32_t i) { return i < I ? hid + i : h1 + (i - I); });
+  stamp(a, l, P_D, t, 1);
+  const float acc = gemv_lds(a.Rd, s.w, x, I, 1);
+  if (threadIdx.x < nr) put_word(ac.hout + r0 + threadIdx.x, hres[threadIdx.x] + acc, a.epoch);
+  stamp(a, l, P_D, t, 2);
 }
 
-// Final norm, LM-head rows (4 waves = 4 blocks at a time), per-block argmax
-// candidates; the last workgroup to finish reduces them.
-__device__ void run_lm(const DecodeArgs& a, Lds& s) {
-  const uint32_t L = a.L;
-  stamp(a, L - 1, 5, blockIdx.x, 0);
-  wait_ge(a.cnt + (size_t)(L - 1) * kCountersPerLayer + C_D, a.epoch * a.nd, a.err);
-  stamp(a, L - 1, 5, blockIdx.x, 1);
-  float* x = s.v;
-  float* hn = x + a.H;
-  float* misc = hn + a.H;
-  load_vec(x, act_of(a, L - 1).hout, a.H, true);
-  __syncthreads();
-  rmsnorm_lds(x, a.fnorm, a.eps, a.H, hn, hn, misc);
+// Final norm, LM-head row blocks (one LDS block at a time; the first is
+// copied before the wait), per-block argmax candidates; the workgroup whose
+// blocks complete the set reduces the candidates to the next token id
+// (strict >, first maximum wins, NaN at index 0 wins; main.rs:1161-1169).
+__device__ __forceinline__ void run_lm(const DecodeArgs& a, const Lds& s) {
+  const uint32_t L = a.L, wg = blockIdx.x;
   const uint32_t wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  lf* x = s.v;
+  lf* hn = x + a.H;
+  lf* misc = hn + a.H;
+  AS_LDS uint32_t* red = (AS_LDS uint32_t*)(misc + 4);
+  if (wg < a.nl) prefetch_rows(a.lm, a.Rl, a.H, wg, s.w);
+  stamp(a, L - 1, P_LM, wg, 0);
+  gather_vec(x, act_of(a, L - 1).hout, a.H, a);
+  stamp(a, L - 1, P_LM, wg, 1);
+  rmsnorm_lds(x, a.fnorm, a.eps, a.H, hn, hn, misc);
+  AS_GLB float* logits = GW(a.logits);
   uint32_t done = 0;
-  for (uint32_t base = blockIdx.x * 4; base < a.nl; base += a.nwg * 4) {
-    const uint32_t b = base + wv;
-    if (b < a.nl) {
-      float acc = chain_global(a.lm + (size_t)b * a.Rl * a.H, a.Rl, hn, a.H, lane);
+  for (uint32_t b = wg; b < a.nl; b += a.nwg) {
+    if (b != wg) {
+      prefetch_rows(a.lm, a.Rl, a.H, b, s.w);
+      __syncthreads();
+    }
+    const float acc = gemv_lds(a.Rl, s.w, hn, a.H, 1);
+    if (wv == 0) {
       const uint32_t row = b * a.Rl + lane;
       Cand c = {0.0f, UINT32_MAX};
       if (lane < a.Rl && row < a.V) {
-        a.logits[row] = acc;
+        logits[row] = acc;
         if (acc == acc) c = Cand{acc, row};
       }
       c = cand_wave(c);
@@ -605,20 +875,20 @@ __device__ void run_lm(const DecodeArgs& a, Lds& s) {
         st_ag(a.cand + 2 * b, __float_as_uint(c.v));
         st_ag(a.cand + 2 * b + 1, c.i);
       }
-      if (b == 0 && lane == 0) {  // NaN at index 0 wins outright (strict > scan)
-        st_ag(a.cand + 2 * a.nl, acc != acc ? 1u : 0u);
-      }
+      if (b == 0 && lane == 0) st_ag(a.cand + 2 * a.nl, acc != acc ? 1u : 0u);
     }
-    done += (base < a.nl) ? min(4u, a.nl - base) : 0u;
+    ++done;
+    __syncthreads();
   }
-  stamp(a, L - 1, 5, blockIdx.x, 2);
-  // ticket: the workgroup whose blocks complete the set reduces them
+  stamp(a, L - 1, P_LM, wg, 2);
+  if (done == 0) return;  // no blocks here (fewer blocks than workgroups)
+  // ticket: all candidate stores are complete before the ticket moves
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
-  uint32_t* ticket = a.cnt + (size_t)L * kCountersPerLayer;
   __shared__ uint32_t s_last;
   if (threadIdx.x == 0) {
-    uint32_t before = __hip_atomic_fetch_add(ticket, done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    uint32_t before =
+        __hip_atomic_fetch_add(GU(a.cnt), done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     s_last = (before + done == a.lm_epoch * a.nl) ? 1u : 0u;
   }
   __syncthreads();
@@ -628,73 +898,51 @@ __device__ void run_lm(const DecodeArgs& a, Lds& s) {
     Cand o = {__uint_as_float(ld_ag(a.cand + 2 * b)), ld_ag(a.cand + 2 * b + 1)};
     c = cand_pick(c, o);
   }
-  c = cand_wave(c);
-  Cand* red = reinterpret_cast<Cand*>(misc + 4);
-  if (lane == 0) red[wv] = c;
-  __syncthreads();
+  const Cand r = cand_block(c, red);
   if (threadIdx.x == 0) {
-    Cand r = red[0];
-    for (uint32_t i = 1; i < kThreads / 64; ++i) r = cand_pick(r, red[i]);
-    uint32_t first_nan = ld_ag(a.cand + 2 * a.nl);
-    *a.tok_out = (first_nan || r.i == UINT32_MAX) ? 0u : r.i;
+    const uint32_t first_nan = ld_ag(a.cand + 2 * a.nl);
+    *GU(a.tok_out) = (first_nan || r.i == UINT32_MAX) ? 0u : r.i;
   }
-  stamp(a, L - 1, 5, blockIdx.x, 3);
+  stamp(a, L - 1, P_LM, wg, 3);
 }
 
-__global__ __launch_bounds__(256) void k_decode(DecodeArgs a) {
-  extern __shared__ float4 lds4[];
+// One 256-thread workgroup per CU (the LDS footprint allows no second one),
+// so one wave per SIMD: the compiler may use the whole register file.
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void k_decode(DecodeArgs a) {
+  // 16-byte element type: the dynamic region follows the static LDS variables
+  // (s_last) at a 16-byte boundary, so every ds_read/write_b128 is aligned
+  // (a misaligned b128 access is split and runs several times slower).
+  extern __shared__ f4 lds_dyn[];
   Lds s;
-  s.w = reinterpret_cast<float*>(lds4);
+  s.w = (lf*)lds_dyn;
   const size_t wbytes = decode_wregion_bytes(a);
-  s.v = reinterpret_cast<float*>(reinterpret_cast<char*>(lds4) + wbytes);
+  s.v = s.w + wbytes / 4;
   const uint32_t wg = blockIdx.x;
   // role of this workgroup in every layer
   int role = -1;
   uint32_t t = 0;
-  if (wg >= a.base_q && wg < a.base_q + a.nq) { role = C_QKV; t = wg - a.base_q; }
-  else if (wg >= a.base_a && wg < a.base_a + a.nh) { role = C_ATT; t = wg - a.base_a; }
-  else if (wg >= a.base_o && wg < a.base_o + a.no) { role = C_O; t = wg - a.base_o; }
-  else if (wg >= a.base_g && wg < a.base_g + a.ng) { role = C_GU; t = wg - a.base_g; }
-  else if (wg >= a.base_d && wg < a.base_d + a.nd) { role = C_D; t = wg - a.base_d; }
-
+  if (wg >= a.base_q && wg < a.base_q + a.nq) { role = P_QKV; t = wg - a.base_q; }
+  else if (wg >= a.base_a && wg < a.base_a + a.nh) { role = P_ATT; t = wg - a.base_a; }
+  else if (wg >= a.base_o && wg < a.base_o + a.no) { role = P_O; t = wg - a.base_o; }
+  else if (wg >= a.base_g && wg < a.base_g + a.ng) { role = P_GU; t = wg - a.base_g; }
+  else if (wg >= a.base_d && wg < a.base_d + a.nd) { role = P_D; t = wg - a.base_d; }
   uint32_t tok = 0;
-  if (role == C_QKV || role == C_O) {  // the layer-0 tasks that read the embedding row
-    tok = *a.tok_in;
+  if (role == P_QKV || role == P_O) {  // the layer-0 tasks that read the embedding row
+    tok = *(const AS_GLB uint32_t*)a.tok_in;
     if (tok >= a.V) {
-      if (threadIdx.x == 0) atomicOr(a.err, 1u);
+      if (threadIdx.x == 0) raise_err(a.err, 1u);
       tok = 0;
     }
   }
   for (uint32_t l = 0; l < a.L; ++l) {
-    const LayerW& Lw = a.layers[l];
     switch (role) {
-      case C_QKV:
-        prefetch_qkv(a, l, t, s);
-        __syncthreads();
-        run_qkv(a, l, t, s, tok);
-        break;
-      case C_ATT:
-        run_att(a, l, t, s, wbytes / 4);
-        break;
-      case C_O:
-        prefetch_rows(Lw.wo, a.Ro, a.qd, t, s.w);
-        __syncthreads();
-        run_o(a, l, t, s, tok);
-        break;
-      case C_GU: {
-        prefetch_rows(Lw.wg, a.Rg, a.H, t, s.w);
-        prefetch_rows(Lw.wu, a.Rg, a.H, t, s.w + (size_t)a.Rg * a.H);
-        __syncthreads();
-        run_gu(a, l, t, s);
-        break;
-      }
-      case C_D:
-        prefetch_rows(Lw.wd, a.Rd, a.I, t, s.w);
-        __syncthreads();
-        run_d(a, l, t, s);
-        break;
-      default:
-        break;
+      case P_QKV: run_qkv(a, l, t, s, tok); break;
+      case P_ATT: run_att(a, l, t, s, wbytes / 4); break;
+      case P_O: run_o(a, l, t, s, tok); break;
+      case P_GU: run_gu(a, l, t, s); break;
+      case P_D: run_d(a, l, t, s); break;
+      default: break;
     }
     __syncthreads();
   }
@@ -704,15 +952,16 @@ __global__ __launch_bounds__(256) void k_decode(DecodeArgs a) {
 }  // namespace
 
 size_t decode_act_floats(uint32_t H, uint32_t I, uint32_t qd, uint32_t kvd) {
-  return layer_stride(H, I, qd, kvd);
+  return 2 * layer_words(H, I, qd, kvd);
 }
 
 size_t decode_lds_bytes(const DecodeArgs& a) {
-  size_t wbytes = decode_wregion_bytes(a);
-  size_t vec = 2 * (size_t)a.H + 64 + 64;
-  size_t vi = a.I, vq = a.qd, va = 4 * (size_t)a.hd + 64;
-  vec = vec > vi ? vec : vi;
-  vec = vec > vq ? vec : vq;
+  const size_t wbytes = decode_wregion_bytes(a);
+  size_t vec = 2 * (size_t)a.H + 64 + 64;                          // QKV, GU, LM
+  const size_t vo = (size_t)a.qd + a.Ro, vd = (size_t)a.I + a.Rd;  // O, D
+  const size_t va = 4 * (size_t)a.hd + 64;                         // ATT
+  vec = vec > vo ? vec : vo;
+  vec = vec > vd ? vec : vd;
   vec = vec > va ? vec : va;
   return wbytes + vec * 4 + 256;
 }

@@ -28,8 +28,8 @@ struct DecodeArgs {
   const float* rope_cs;  // [max_pos][hd/2][2]
   float* kc0;            // this sequence's caches: layer l at kc0 + l*cache_stride
   float* vc0;
-  float* act;            // per-layer activations
-  uint32_t* cnt;         // per-layer phase counters
+  float* act;            // per-layer activations as 64-bit {f32 bits, epoch} words (zeroed at start)
+  uint32_t* cnt;         // [0]: LM-head ticket (blocks completed, all launches)
   float* logits;         // [V]
   uint32_t* cand;        // [nl][2] (value bits, index) per LM block
   uint32_t* tok_in;      // token of this position
@@ -49,9 +49,8 @@ struct DecodeArgs {
   uint32_t pos, epoch, lm_epoch, want_logits;
 };
 
-// Floats of per-layer activation storage, and counters per layer.
+// Floats (4-byte units) of one layer's tagged activation storage.
 size_t decode_act_floats(uint32_t H, uint32_t I, uint32_t qd, uint32_t kvd);
-constexpr uint32_t kCountersPerLayer = 8;
 constexpr uint32_t kTimelineTasks = 64;
 // Dynamic LDS bytes the kernel needs for this configuration.
 size_t decode_lds_bytes(const DecodeArgs& a);

@@ -246,7 +246,7 @@ __global__ __launch_bounds__(256) void k_rope_store(float* q, float* k, const fl
   }
   for (uint32_t idx = threadIdx.x; idx < nkv * hd; idx += blockDim.x) {
     uint32_t kvh = idx / hd, d = idx - kvh * hd;
-    vc[((size_t)kvh * max_pos + pos) * hd + d] = v[idx];
+    vc[((size_t)kvh * hd + d) * max_pos + pos] = v[idx];
   }
 }
 
@@ -352,11 +352,11 @@ __global__ __launch_bounds__(256) void k_attention(const float* __restrict__ q,
     if (probs_out) probs_out[(size_t)qh * len + j] = pj;
   }
   __syncthreads();
-  const float* vb = vc + (size_t)kvh * max_pos * hd;
+  const float* vb = vc + (size_t)kvh * hd * max_pos;
   for (uint32_t d = threadIdx.x; d < hd; d += blockDim.x) {
     float acc = 0.0f;
     for (uint32_t j = 0; j < len; ++j) {
-      float p = ss[j] * vb[(size_t)j * hd + d];
+      float p = ss[j] * vb[(size_t)d * max_pos + j];
       acc = acc + p;
     }
     att_out[(size_t)qh * hd + d] = acc;

@@ -48,7 +48,7 @@ hipError_t launch_rmsnorm(const float* x, const float* w, float eps, uint32_t n,
                           uint32_t nvec, float* out, hipStream_t s);
 // RoPE on q (nh heads) and k (nkv heads) in place from the per-position
 // table, then store rotated k and raw v into the caches at pos.
-// Caches: K as [kvh][hd][max_pos], V as [kvh][max_pos][hd].
+// Caches: K and V both as [kvh][hd][max_pos] (one row per head dimension).
 hipError_t launch_rope_store(float* q, float* k, const float* v, const float* rope_cs,
                              uint32_t pos, uint32_t nh, uint32_t nkv, uint32_t hd,
                              uint32_t max_pos, float* kc, float* vc, hipStream_t s);

@@ -328,6 +328,15 @@ int forward_fast(cis2_ctx* c, uint32_t seq, uint32_t pos, uint32_t* tokp, bool w
   a.tok_in = tokp;
   a.tok_out = c->d_tok;
   a.pos = pos;
+  if (c->epoch == UINT32_MAX) {  // tags would repeat: clear them and restart at 1
+    HIPCHK(c, hipMemsetAsync(c->act, 0,
+                             (size_t)c->cfg.n_layers *
+                                 decode_act_floats(c->cfg.hidden, c->cfg.inter, c->qd,
+                                                   c->kvd) * sizeof(float),
+                             c->st),
+           "tag reset");
+    c->epoch = 0;
+  }
   a.epoch = ++c->epoch;
   if (want_logits) ++c->lm_epoch;
   a.lm_epoch = c->lm_epoch;
@@ -524,7 +533,7 @@ int cis2_ctx_create(const cis2_config* cfg, cis2_ctx** out) {
                  need_lds <= 160 * 1024;
     void* p = nullptr;
     const size_t act_f = (size_t)f.n_layers * decode_act_floats(H, I, c->qd, c->kvd);
-    const size_t cnt_n = ((size_t)f.n_layers + 1) * kCountersPerLayer;
+    const size_t cnt_n = 64;
     if (!(c->act = dalloc(c, act_f)) || hipMalloc(&p, cnt_n * 4) != hipSuccess) {
       cis2_ctx_destroy(c);
       return CIS2_E_OOM;
@@ -532,6 +541,7 @@ int cis2_ctx_create(const cis2_config* cfg, cis2_ctx** out) {
     c->allocs.push_back(p);
     c->counters = static_cast<uint32_t*>(p);
     (void)hipMemset(c->counters, 0, cnt_n * 4);
+    (void)hipMemset(c->act, 0, act_f * sizeof(float));  // tag 0: never a launch epoch
     if (hipMalloc(&p, ((size_t)2 * a.nl + 4) * 4) != hipSuccess) {
       cis2_ctx_destroy(c);
       return CIS2_E_OOM;
