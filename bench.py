@@ -10,6 +10,13 @@ weights ~N(0,0.02)); `--warmup` steps run first, then `--steps` are timed.
 When warmup + steps == 256 the run's witness digest is checked against the
 reference driver's digest for the same inputs (tests/golden).
 
+The roofline object is the persistent decode kernel's (one launch computes one
+position: all layers, LM head, argmax): algorithmic bytes per launch are the
+fp32 GEMV weights, the norm weights and the K/V rows read at that position,
+divided by the launch's device time from HIP events on the library's own
+stream (cis2_profile), summed over the timed steps.  `traffic` is the HBM
+bytes per launch from the committed rocprofv3 counter summary, when present.
+
 Prints ONE JSON line on stdout.
 """
 import argparse
@@ -30,6 +37,32 @@ SEED = 20261201
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
+
+
+# Algorithmic bytes of one SmolLM2-135M decode launch at position p: fp32 GEMV
+# weights (30 layers x 3,538,944 + LM head 49152 x 576 floats), 61 norm vectors
+# of 576 floats, and the cached K and V rows of positions 0..p (2 x 192 floats
+# per layer per position).
+GEMV_WEIGHT_BYTES = 4 * (30 * 3538944 + 49152 * 576)
+NORM_BYTES = 4 * 61 * 576
+KV_BYTES_PER_POS = 4 * 2 * 192 * 30
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "k_decode_smollm2_pmc.txt")
+
+
+def decode_bytes(pos):
+    return GEMV_WEIGHT_BYTES + NORM_BYTES + KV_BYTES_PER_POS * (int(pos) + 1)
+
+
+def measured_traffic():
+    """HBM bytes per decode launch (FETCH_SIZE + WRITE_SIZE, copy-calibrated)
+    from the committed counter summary, or None."""
+    try:
+        for line in open(TRAFFIC_FILE):
+            if line.startswith("traffic_bytes_per_launch="):
+                return int(line.split("=", 1)[1].split()[0])
+    except OSError:
+        pass
+    return None
 
 
 def gemv_roofline(M=1536, K=576, copies=128, iters=4096):
@@ -83,7 +116,21 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-roofline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a plain 512 MiB device-to-device copy (counter calibration)")
     a = ap.parse_args()
+    if a.copy_calibration:
+        import torch
+        n = 128 << 20  # floats: 512 MiB per buffer
+        src = torch.ones(n, dtype=torch.float32, device="cuda:0")
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log("copied 3 x %d bytes" % (4 * n))
+        print(json.dumps({"copy_bytes": 4 * n, "copies": 3}), flush=True)
+        return
     if a.gpus != 1:
         print("bench.py: this build runs on one GPU only (the pinned-order decode does not shard "
               "across GPUs here); use --gpus 1", file=sys.stderr)
@@ -99,10 +146,13 @@ def main():
     t = time.perf_counter()
     model.begin(prompt, total)
     prefill_s = time.perf_counter() - t
-    model.steps(a.warmup)
+    model.steps(a.warmup)  # returns with the stream drained
+    model.profile(True)
     t0 = time.perf_counter()
-    model.steps(a.steps)
+    model.steps(a.steps)   # blocks until every step is folded and the stream drained
     t1 = time.perf_counter()
+    model.profile(False)
+    launches, kernel_ms, positions = model.profile_read()
     res = model.end(total)
     dt = t1 - t0
     value = a.steps / dt
@@ -115,6 +165,17 @@ def main():
                           [int(v) for v in res["ids"]] == rec["tokens"])
     log("decode: %d steps in %.3fs -> %.1f tok/s; prefill 32 tokens %.3fs; witness_ok=%s"
         % (a.steps, dt, value, prefill_s, witness_ok))
+    roof = None
+    if launches:
+        algo = sum(decode_bytes(p) for p in positions)
+        achieved = algo / (kernel_ms * 1e-3) / 1e9
+        roof = {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
+                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                "traffic": measured_traffic(),
+                "kernel": "k_decode (persistent: 30 layers + LM head + argmax per launch)",
+                "launches": launches, "us_per_launch": round(kernel_ms * 1e3 / launches, 2),
+                "algorithmic_bytes_per_launch": int(round(algo / launches))}
+        log("decode kernel roofline:", roof)
     model.close()
     out = {
         "metric": METRIC, "value": round(value, 3), "unit": "tok/s", "n_gpus": 1,
@@ -126,9 +187,11 @@ def main():
                    "global_batch": 1, "seq_len": len(prompt) + total, "parallelism": "none"},
         "witness_bit_exact": witness_ok, "witness": res["witness"],
     }
+    if roof is not None:
+        out["roofline"] = roof
     if not a.no_roofline:
-        out["roofline"] = gemv_roofline()
-        log("gemv roofline:", out["roofline"])
+        out["gemv_config1"] = gemv_roofline()
+        log("standalone GEMV 1536x576:", out["gemv_config1"])
     if not a.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(spec, weights, prompt, a.cpu_seconds)
         log("cpu baseline:", out["cpu_baseline"])

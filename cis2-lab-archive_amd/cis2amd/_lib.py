@@ -62,6 +62,9 @@ SIGNATURES = {
     "cis2_decode_batch": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_uint32, c_u32p, c_u32p,
                                          ctypes.c_uint32, c_u8p, c_u32p, c_u8p, c_u8p]),
     "cis2_trace_enable": (ctypes.c_int, [ctypes.c_void_p, TRACE_FN, ctypes.c_void_p]),
+    "cis2_profile": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int]),
+    "cis2_profile_read": (ctypes.c_int, [ctypes.c_void_p, c_u64p, ctypes.POINTER(ctypes.c_double),
+                                         c_u32p, ctypes.c_uint64]),
     "cis2_gemv_plan_create": (ctypes.c_int, [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32,
                                              c_fp, ctypes.POINTER(ctypes.c_void_p)]),
     "cis2_gemv_plan_run": (ctypes.c_int, [ctypes.c_void_p, c_fp, c_fp]),

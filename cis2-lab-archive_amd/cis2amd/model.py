@@ -63,6 +63,20 @@ class Cis2Model:
     def reset(self, seq=0):
         check(_lib.lib().cis2_reset_seq(self.ctx, seq), self.ctx)
 
+    def profile(self, on):
+        """Starts (clearing the record) or stops event timing of every
+        persistent-decode kernel launch (cis2_profile)."""
+        check(_lib.lib().cis2_profile(self.ctx, 1 if on else 0), self.ctx)
+
+    def profile_read(self, cap=65536):
+        """(launches, summed device ms, positions computed) since profile(True)."""
+        n = (ctypes.c_uint64 * 1)()
+        ms = (ctypes.c_double * 1)()
+        pos = np.zeros(cap, dtype=np.uint32)
+        check(_lib.lib().cis2_profile_read(self.ctx, n, ms, _ptr(pos, _lib.c_u32p), cap), self.ctx)
+        k = int(n[0])
+        return k, float(ms[0]), pos[:min(k, cap)].copy()
+
     def forward_token(self, pos, tok, seq=0):
         """One forward pass; returns (logits float32[vocab], argmax id)."""
         V = self.spec.vocab

@@ -107,8 +107,14 @@ struct cis2_ctx {
   DecodeArgs dargs;
   uint64_t* tline = nullptr;  // CIS2_TIMELINE=<file>: per-task timestamps of every launch
   FILE* tline_file = nullptr;
+  // cis2_profile: event pairs around decode-kernel launches
+  bool prof_on = false;
+  std::vector<hipEvent_t> prof_ev;  // [2 * kProfMax], created on first use
+  std::vector<uint32_t> prof_pos;
   std::vector<void*> allocs;
 };
+
+constexpr size_t kProfMax = 65536;
 
 struct cis2_gemv_plan {
   uint32_t M, K, copies;
@@ -342,7 +348,14 @@ int forward_fast(cis2_ctx* c, uint32_t seq, uint32_t pos, uint32_t* tokp, bool w
   a.lm_epoch = c->lm_epoch;
   a.want_logits = want_logits ? 1u : 0u;
   a.tline = c->tline;
+  const size_t pi = c->prof_pos.size();
+  const bool prof = c->prof_on && pi < kProfMax;
+  if (prof) HIPCHK(c, hipEventRecord(c->prof_ev[2 * pi], c->st), "profile event");
   LAUNCH(launch_decode(a, c->st), "decode kernel");
+  if (prof) {
+    HIPCHK(c, hipEventRecord(c->prof_ev[2 * pi + 1], c->st), "profile event");
+    c->prof_pos.push_back(pos);
+  }
   if (c->tline_file) {  // profiling mode: synchronous, one record per launch
     const size_t n = (size_t)c->cfg.n_layers * 6 * kTimelineTasks * 4;
     std::vector<uint64_t> hbuf(n);
@@ -387,6 +400,8 @@ void cis2_ctx_destroy(cis2_ctx* c) {
   if (c->st) (void)hipStreamSynchronize(c->st);
   for (void* p : c->allocs) (void)hipFree(p);
   if (c->tline_file) fclose(c->tline_file);
+  for (hipEvent_t e : c->prof_ev)
+    if (e) (void)hipEventDestroy(e);
   if (c->ring) (void)hipHostFree(c->ring);
   if (c->ring_tok) (void)hipHostFree(c->ring_tok);
   for (int i = 0; i < kRing; ++i)
@@ -632,6 +647,34 @@ int cis2_reset_seq(cis2_ctx* c, uint32_t seq) {
   size_t per = (size_t)c->cfg.n_layers * 2 * c->kvd * c->cfg.max_pos;
   HIPCHK(c, hipMemsetAsync(c->kv + seq * per, 0, per * sizeof(float), c->st), "reset");
   HIPCHK(c, hipStreamSynchronize(c->st), "reset sync");
+  return CIS2_OK;
+}
+
+int cis2_profile(cis2_ctx* c, int on) {
+  if (!c) return CIS2_E_ARG;
+  if (on && c->prof_ev.empty()) {
+    c->prof_ev.assign(2 * kProfMax, nullptr);
+    for (auto& e : c->prof_ev) HIPCHK(c, hipEventCreate(&e), "profile events");
+  }
+  if (on) c->prof_pos.clear();
+  c->prof_on = on != 0;
+  return CIS2_OK;
+}
+
+int cis2_profile_read(cis2_ctx* c, uint64_t* launches, double* total_ms, uint32_t* positions,
+                      uint64_t cap) {
+  if (!c || !launches || !total_ms) return CIS2_E_ARG;
+  const size_t n = c->prof_pos.size();
+  double tot = 0.0;
+  if (n) HIPCHK(c, hipEventSynchronize(c->prof_ev[2 * n - 1]), "profile sync");
+  for (size_t i = 0; i < n; ++i) {
+    float ms = 0.0f;
+    HIPCHK(c, hipEventElapsedTime(&ms, c->prof_ev[2 * i], c->prof_ev[2 * i + 1]), "profile time");
+    tot += ms;
+    if (positions && i < cap) positions[i] = c->prof_pos[i];
+  }
+  *launches = n;
+  *total_ms = tot;
   return CIS2_OK;
 }
 

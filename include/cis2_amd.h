@@ -152,6 +152,17 @@ int cis2_decode_batch(cis2_ctx *ctx, uint32_t nseq, const uint32_t *prompts,
  * op, so it is a verification mode, not a fast path. */
 int cis2_trace_enable(cis2_ctx *ctx, cis2_trace_fn fn, void *user);
 
+/* ---- Kernel timing (measurement; no counterpart in the reference) --------
+ * While on, every launch of the persistent decode kernel is bracketed by a
+ * pair of HIP events on the library's stream (at most 65536 launches are
+ * kept).  cis2_profile(ctx, 1) also clears the record.
+ * cis2_profile_read waits for the recorded launches and returns their count
+ * and summed device time; positions[i] (optional, `cap` entries) receive the
+ * position each launch computed. */
+int cis2_profile(cis2_ctx *ctx, int on);
+int cis2_profile_read(cis2_ctx *ctx, uint64_t *launches, double *total_ms, uint32_t *positions,
+                      uint64_t cap);
+
 /* ---- Standalone pinned-order GEMV (the 4-row-interleaved reference kernel
  * of labs/rust-5, whose bits equal matvec/dot_seq: src/main.rs:228-243,
  * math.rs:40-48) --------------------------------------------------------- */
