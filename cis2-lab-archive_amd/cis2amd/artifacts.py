@@ -195,3 +195,25 @@ class Weights:
 def prompt_ids(seed, vocab, n, ordinal=1 << 40):
     """n prompt ids uniform in [0, vocab)."""
     return gen_uniform(seed, ordinal, 0, vocab - 1, n)
+
+
+def set_prompt(seed, idx, vocab, lo, hi, stream):
+    """Prompt idx of a seeded prompt set: length uniform in [lo, hi], ids
+    uniform in [0, vocab).  stream separates sets drawn from one seed."""
+    n = int(gen_uniform(seed, (stream << 40) + (1 << 39) + idx, lo, hi, 1)[0])
+    return gen_uniform(seed, (stream << 40) + idx, 0, vocab - 1, n)
+
+
+# The llama-160m prompt set: 300 prompts of 8..64 tokens, 128 generated each.
+LLAMA_SET = {"spec": "llama-160m", "seed": 160, "count": 300, "lo": 8, "hi": 64,
+             "stream": 3, "gen_toks": 128}
+# The batch-stress set on the SmolLM2-135M shape: 64 sequences with prompts of
+# 16..512 tokens, 256 generated each; a batch of B uses sequences 0..B-1.
+BATCH_SET = {"spec": "smollm2-135m", "seed": 20261201, "count": 64, "lo": 16, "hi": 512,
+             "stream": 4, "gen_toks": 256}
+
+
+def set_prompts(pset):
+    spec = SPECS[pset["spec"]]
+    return [set_prompt(pset["seed"], i, spec.vocab, pset["lo"], pset["hi"], pset["stream"])
+            for i in range(pset["count"])]

@@ -115,6 +115,18 @@ __host__ __device__ inline size_t decode_wregion_bytes(const DecodeArgs& a) {
   return ((m * 4 + 255) / 256) * 256;
 }
 
+// Floats of the vector region (input vectors and scratch of every role),
+// rounded up to 16 bytes.
+__host__ __device__ inline size_t decode_vec_floats(const DecodeArgs& a) {
+  size_t vec = 2 * (size_t)a.H + 64 + 64;                          // QKV, GU, LM
+  const size_t vo = (size_t)a.qd + a.Ro, vd = (size_t)a.I + a.Rd;  // O, D
+  const size_t va = 4 * (size_t)a.hd + 64;                         // ATT
+  vec = vec > vo ? vec : vo;
+  vec = vec > vd ? vec : vd;
+  vec = vec > va ? vec : va;
+  return (vec + 3) & ~(size_t)3;
+}
+
 __device__ __forceinline__ uint32_t ld_ag(const uint32_t* p) {
   return __hip_atomic_load((const AS_GLB uint32_t*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -229,7 +241,7 @@ __device__ __forceinline__ void prefetch_rows2(const float* A, const float* B, u
 // (n >= D) and each slot is refilled right after its adds, in an order the
 // scheduler may not change: that lets the wait before each step be
 // lgkmcnt(D-1) instead of a full drain.
-template <uint32_t D = 8>
+template <uint32_t D = 15>
 __device__ __forceinline__ float chain4(const lf4* p, uint32_t n, uint32_t st, float acc) {
   if (n < D) {
     for (uint32_t g = 0; g < n; ++g) {
@@ -323,73 +335,85 @@ __device__ __forceinline__ float chain_vec(const lf* p, uint32_t n, float acc) {
 // GEMV on LDS-resident row blocks ([K/4][R][4] floats per block)
 // ---------------------------------------------------------------------------
 
-// In place W[g][r][j] *= x[4g+j] over groups [g0, g1) of nb blocks (block b
-// at W4 + b*bf4), by threads tid = 0..nt-1.
-// Reads are batched (B weight and B input reads before the B writes): the
-// in-place writes would otherwise order every read behind the previous write.
+// Product pass over wave instructions [i0, i1) of nb blocks (block b at
+// W4 + b*bf4): instruction `ins` covers groups [ins*GP, ins*GP + GP)
+// (GP = 64/R), lane l forming W[g][r] *= x4[g] for g = ins*GP + l/R,
+// r = l%R.  Lanes past GP*R, or past the last group, read and write their
+// own slot of `pad` instead, so no lane is ever masked off.  Waves w, w+nw,
+// ... (w wave-uniform) take turns over the instructions; the reads of B
+// instructions are issued before their writes (in-place writes would
+// otherwise order every read behind the previous write).
+#ifndef PROD_BATCH
+#define PROD_BATCH 12
+#endif
 template <uint32_t R>
-__device__ __forceinline__ void prod_range(lf4* W4, const lf4* x4, uint32_t bf4, uint32_t nb,
-                                           uint32_t g0, uint32_t g1, uint32_t tid, uint32_t nt) {
-  constexpr uint32_t B = 6;
-  const uint32_t per = (g1 - g0) * R;
+__device__ __forceinline__ void prod_ins(lf4* W4, const lf4* x4, uint32_t bf4, uint32_t nb,
+                                         uint32_t KG, uint32_t i0, uint32_t i1, uint32_t w,
+                                         uint32_t nw, lf4* pad) {
+  constexpr uint32_t GP = 64 / R, B = PROD_BATCH;
+  const uint32_t lane = threadIdx.x & 63;
+  const uint32_t lg = lane / R, lr = lane - (lane / R) * R;
+  const bool live = lane < GP * R;
   for (uint32_t b = 0; b < nb; ++b) {
-    lf4* base = W4 + (size_t)b * bf4 + (size_t)g0 * R;
-    const lf4* xb = x4 + g0;
-    for (uint32_t i0 = tid; i0 < per; i0 += B * nt) {
-      f4 w[B], xv[B];
+    lf4* base = W4 + (size_t)b * bf4;
+    for (uint32_t ins = i0 + w; ins < i1; ins += B * nw) {
+      lf4* dst[B];
+      f4 wv[B], xv[B];
 #pragma unroll
       for (uint32_t u = 0; u < B; ++u) {
-        const uint32_t i = i0 + u * nt;
-        if (i < per) {
-          w[u] = base[i];
-          xv[u] = xb[i / R];
+        const uint32_t ii = ins + u * nw;
+        const uint32_t g = ii * GP + lg;
+        const bool ok = live && g < KG;
+        dst[u] = ok ? base + (size_t)g * R + lr : pad + lane;
+        const lf4* xs = ok ? x4 + g : (const lf4*)(pad + lane);
+        if (ii < i1) {
+          wv[u] = *dst[u];
+          xv[u] = *xs;
         }
       }
 #pragma unroll
       for (uint32_t u = 0; u < B; ++u) {
-        const uint32_t i = i0 + u * nt;
-        if (i < per) {
-          f4 v = w[u];
+        if (ins + u * nw < i1) {
+          f4 v = wv[u];
           v.x = v.x * xv[u].x;
           v.y = v.y * xv[u].y;
           v.z = v.z * xv[u].z;
           v.w = v.w * xv[u].w;
-          base[i] = v;
+          *dst[u] = v;
         }
       }
     }
   }
 }
 
-// acc + strict left-to-right sum of row r's products over groups [g0, g1).
-template <uint32_t R>
-__device__ __forceinline__ float chain_range(const lf4* P4, uint32_t g0, uint32_t g1, uint32_t r,
-                                             float acc) {
-  return chain4(P4 + (size_t)g0 * R + r, g1 - g0, R, acc);
-}
-
 // y[r] = fold_k (W[r][k] * x[k]) for nb LDS blocks (block b at W + b*R*K).
-// K is cut into 4 chunks: all waves form the products of chunk 0, then
-// waves [0, nb) add chunk c while the other waves form chunk c+1.  Returns
-// row `lane` of block `wave` in waves < nb (lanes >= R: row R-1).
+// The product pass is cut into NC chunks of wave instructions: all waves
+// form chunk 0, then waves [0, nb) add chunk c (a strict chain per lane,
+// reads kept in flight) while the other waves form chunk c+1.  Returns row
+// `lane` of block `wave` in waves < nb (lanes >= R: row R-1).
 template <uint32_t R>
-__device__ __forceinline__ float gemv_lds_t(lf* W, const lf* x, uint32_t K, uint32_t nb) {
-  constexpr uint32_t NC = 4;
-  const uint32_t KG = K >> 2, wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
+__device__ __forceinline__ float gemv_lds_t(lf* W, const lf* x, uint32_t K, uint32_t nb,
+                                            lf4* pad) {
+  constexpr uint32_t NC = 4, GP = 64 / R;
+  // sizes are wave-uniform: keep them (and every bound derived from them) scalar
+  const uint32_t KG = __builtin_amdgcn_readfirstlane(K >> 2), lane = threadIdx.x & 63;
+  nb = __builtin_amdgcn_readfirstlane(nb);
+  const uint32_t wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   lf4* W4 = (lf4*)W;
   const lf4* x4 = (const lf4*)x;
-  const uint32_t bf4 = KG * R;
+  const uint32_t bf4 = KG * R, nins = (KG + GP - 1) / GP;
   const uint32_t r = lane < R ? lane : R - 1;
-  prod_range<R>(W4, x4, bf4, nb, 0, KG / NC, threadIdx.x, kThreads);
+  prod_ins<R>(W4, x4, bf4, nb, KG, 0, nins / NC, wv, kThreads / 64, pad);
   __syncthreads();
   float acc = 0.0f;
   for (uint32_t c = 0; c < NC; ++c) {
-    const uint32_t g0 = (KG * c) / NC, g1 = (KG * (c + 1)) / NC;
+    const uint32_t i0 = nins * c / NC, i1 = nins * (c + 1) / NC;
     if (wv < nb) {
-      acc = chain_range<R>(W4 + (size_t)wv * bf4, g0, g1, r, acc);
+      const uint32_t g0 = i0 * GP, g1 = min(i1 * GP, KG);
+      acc = chain4<8>(W4 + (size_t)wv * bf4 + (size_t)g0 * R + r, g1 - g0, R, acc);
     } else if (c + 1 < NC) {
-      prod_range<R>(W4, x4, bf4, nb, g1, (KG * (c + 2)) / NC, threadIdx.x - nb * 64,
-                    kThreads - nb * 64);
+      prod_ins<R>(W4, x4, bf4, nb, KG, i1, nins * (c + 2) / NC, wv - nb, kThreads / 64 - nb,
+                  pad);
     }
     __syncthreads();
   }
@@ -418,25 +442,50 @@ __device__ float gemv_lds_any(uint32_t R, lf* W, const lf* x, uint32_t K, uint32
   return acc;
 }
 
-__device__ __noinline__ float gemv_lds(uint32_t R, lf* W, const lf* x, uint32_t K, uint32_t nb) {
-  switch (R) {
-    case 64: return gemv_lds_t<64>(W, x, K, nb);
-    case 48: return gemv_lds_t<48>(W, x, K, nb);
-    case 36: return gemv_lds_t<36>(W, x, K, nb);
-    case 32: return gemv_lds_t<32>(W, x, K, nb);
-    case 24: return gemv_lds_t<24>(W, x, K, nb);
-    case 18: return gemv_lds_t<18>(W, x, K, nb);
-    case 12: return gemv_lds_t<12>(W, x, K, nb);
-    default: return gemv_lds_any(R, W, x, K, nb);
+__device__ __noinline__ float gemv_lds_generic(uint32_t R, lf* W, const lf* x, uint32_t K,
+                                               uint32_t nb) {
+  return gemv_lds_any(R, W, x, K, nb);
+}
+
+// Inlined GEMV for the block heights a call site can see (the persistent
+// kernel's layouts: R = min(32, 36864/K), gate/up R/2); any other height
+// takes the generic out-of-line path.
+template <uint32_t R0, uint32_t... Rs>
+__device__ __forceinline__ float gemv_lds(uint32_t R, lf* W, const lf* x, uint32_t K, uint32_t nb,
+                                          lf4* pad) {
+  if (R == R0) return gemv_lds_t<R0>(W, x, K, nb, pad);
+  if constexpr (sizeof...(Rs) > 0) {
+    return gemv_lds<Rs...>(R, W, x, K, nb, pad);
+  } else {
+    return gemv_lds_generic(R, W, x, K, nb);
   }
 }
 
 // RMSNorm of an LDS vector (code/cis2-fp/src/main.rs:245-260): squares
 // into `tmp`, one strict chain in wave 0, mean by a true divide,
 // inv = 1/sqrt(mean + eps), out = (x*inv)*w.  `out` may alias `tmp` or x.
-__device__ __forceinline__ void rmsnorm_lds(const lf* x, const float* w_, float eps, uint32_t n,
-                                            lf* tmp, lf* out, lf* s_inv) {
+// The norm weights a thread scales with (elements threadIdx.x + 256u) are
+// loaded into registers before the input is waited for (load_normw), so the
+// scaling pass after the chain reads no global memory (n <= 1024; longer
+// vectors read the tail from global memory).
+constexpr uint32_t kNormRegs = 4;
+struct NormW {
+  float v[kNormRegs];
+  const float* g;
+};
+__device__ __forceinline__ NormW load_normw(const float* w_, uint32_t n) {
+  NormW r;
+  r.g = w_;
   gf* w = G(w_);
+#pragma unroll
+  for (uint32_t u = 0; u < kNormRegs; ++u) {
+    const uint32_t i = threadIdx.x + u * kThreads;
+    r.v[u] = i < n ? w[i] : 0.0f;
+  }
+  return r;
+}
+__device__ __forceinline__ void rmsnorm_lds(const lf* x, const NormW& w, float eps, uint32_t n,
+                                            lf* tmp, lf* out, lf* s_inv) {
   for (uint32_t i = threadIdx.x; i < n; i += kThreads) {
     float v = x[i];
     tmp[i] = v * v;
@@ -451,9 +500,17 @@ __device__ __forceinline__ void rmsnorm_lds(const lf* x, const float* w_, float 
   }
   __syncthreads();
   const float inv = *s_inv;
-  for (uint32_t i = threadIdx.x; i < n; i += kThreads) {
+#pragma unroll
+  for (uint32_t u = 0; u < kNormRegs; ++u) {
+    const uint32_t i = threadIdx.x + u * kThreads;
+    if (i < n) {
+      float sx = x[i] * inv;
+      out[i] = sx * w.v[u];
+    }
+  }
+  for (uint32_t i = threadIdx.x + kNormRegs * kThreads; i < n; i += kThreads) {
     float sx = x[i] * inv;
-    out[i] = sx * w[i];
+    out[i] = sx * G(w.g)[i];
   }
   __syncthreads();
 }
@@ -495,8 +552,9 @@ __device__ __forceinline__ Cand cand_block(Cand c, AS_LDS uint32_t* red) {
 
 // LDS layout: [weights | vectors].
 struct Lds {
-  lf* w;  // weight block(s); attention: scores, K rows, V rows
-  lf* v;  // the task's input vector(s) and scratch
+  lf* w;     // weight block(s); attention: scores, K rows, V rows
+  lf* v;     // the task's input vector(s) and scratch
+  lf4* pad;  // 64 slots the product pass's idle lanes write instead
 };
 
 // ---------------------------------------------------------------------------
@@ -526,6 +584,7 @@ __device__ __forceinline__ void run_qkv(const DecodeArgs& a, uint32_t l, uint32_
   lf* ln = s.v + a.H;
   lf* s_inv = s.v + 2 * a.H;
   prefetch_rows(g.W, a.Rq, a.H, g.blk, s.w);
+  const NormW nw = load_normw(Lw.ln1, a.H);
   stamp(a, l, P_QKV, t, 0);
   if (l == 0) {
     gf* e = G(a.embed) + (size_t)tok * a.H;
@@ -535,8 +594,9 @@ __device__ __forceinline__ void run_qkv(const DecodeArgs& a, uint32_t l, uint32_
     gather_vec(x, act_of(a, l - 1).hout, a.H, a);
   }
   stamp(a, l, P_QKV, t, 1);
-  rmsnorm_lds(x, Lw.ln1, a.eps, a.H, ln, ln, s_inv);
-  const float acc = gemv_lds(a.Rq, s.w, ln, a.H, 1);
+  rmsnorm_lds(x, nw, a.eps, a.H, ln, ln, s_inv);
+  stamp(a, l, P_QKV, t, 3);
+  const float acc = gemv_lds<32>(a.Rq, s.w, ln, a.H, 1, s.pad);
   const uint32_t row = g.blk * a.Rq + threadIdx.x;
   if (threadIdx.x < a.Rq && row < g.M) {
     const float r = g.bias ? acc + G(g.bias)[row] : acc;
@@ -595,6 +655,18 @@ __device__ __forceinline__ void run_att(const DecodeArgs& a, uint32_t l, uint32_
   const bool in_lds = att_lds_floats(hd, pos, a.max_pos) <= wfloats;
   stamp(a, l, P_ATT, h, 0);
   if (in_lds) prefetch_kv(a, l, kvh, kl, S);
+  NormW nq, nk;
+  if (Lw.qn) nq = load_normw(Lw.qn, hd);
+  if (Lw.kn) nk = load_normw(Lw.kn, hd);
+  // cos/sin of this position for the pair this thread rotates (hd <= 256)
+  const uint32_t half = hd / 2;
+  float rc = 0.0f, rsn = 0.0f;
+  if (threadIdx.x < 2 * half) {
+    const uint32_t i = threadIdx.x < half ? threadIdx.x : threadIdx.x - half;
+    gf* cs = G(a.rope_cs) + (size_t)pos * half * 2;
+    rc = cs[2 * i];
+    rsn = cs[2 * i + 1];
+  }
   gather(qv, 3 * hd, a.epoch, a.err, [=](uint32_t i) {
     const uint32_t seg = i >= hd ? (i >= 2 * hd ? 2u : 1u) : 0u, d = i - seg * hd;
     return seg == 0 ? ac.q + (size_t)h * hd + d
@@ -603,15 +675,14 @@ __device__ __forceinline__ void run_att(const DecodeArgs& a, uint32_t l, uint32_
   stamp(a, l, P_ATT, h, 1);
   // Qwen3 per-head QK-norm, after bias and before RoPE
   // (labs/w1x-qwen3/scripts/qwen3-port.diff:66-80).
-  if (Lw.qn) rmsnorm_lds(qv, Lw.qn, a.eps, hd, tmp, qv, misc);
-  if (Lw.kn) rmsnorm_lds(kv, Lw.kn, a.eps, hd, tmp, kv, misc);
+  if (Lw.qn) rmsnorm_lds(qv, nq, a.eps, hd, tmp, qv, misc);
+  if (Lw.kn) rmsnorm_lds(kv, nk, a.eps, hd, tmp, kv, misc);
   // RoPE rotate-half (main.rs:285-307): o1 = x1*c + (-x2)*s, o2 = x2*c + x1*s.
-  const uint32_t half = hd / 2;
-  gf* cs = G(a.rope_cs) + (size_t)pos * half * 2;
-  for (uint32_t idx = threadIdx.x; idx < 2 * half; idx += kThreads) {
+  if (threadIdx.x < 2 * half) {
+    const uint32_t idx = threadIdx.x;
     lf* hv = idx < half ? qv : kv;
     uint32_t i = idx < half ? idx : idx - half;
-    float c = cs[2 * i], sn = cs[2 * i + 1];
+    float c = rc, sn = rsn;
     float x1 = hv[i], x2 = hv[i + half];
     float t1 = x1 * c;
     float nx2 = -x2;
@@ -715,6 +786,7 @@ __device__ __forceinline__ void run_att(const DecodeArgs& a, uint32_t l, uint32_
     ss[j] = pj;
   }
   __syncthreads();
+  stamp(a, l, P_ATT, h, 3);
   // V mix out_d = fold_j (p_j * v_j[d]) (main.rs:454-463)
   if (in_lds) {
     const uint32_t kq = (pos + 3) >> 2, s4 = S >> 2;
@@ -787,7 +859,8 @@ __device__ __forceinline__ void run_o(const DecodeArgs& a, uint32_t l, uint32_t 
            [=](uint32_t i) { return i < qd ? att + i : hin + (i - qd); });
   }
   stamp(a, l, P_O, t, 1);
-  const float acc = gemv_lds(a.Ro, s.w, x, qd, 1);
+  const float acc = gemv_lds<32, 18>(a.Ro, s.w, x, qd, 1, s.pad);
+  stamp(a, l, P_O, t, 3);
   if (threadIdx.x < nr) put_word(ac.h1 + r0 + threadIdx.x, hres[threadIdx.x] + acc, a.epoch);
   stamp(a, l, P_O, t, 2);
 }
@@ -802,11 +875,13 @@ __device__ __forceinline__ void run_gu(const DecodeArgs& a, uint32_t l, uint32_t
   lf* gx = ln + a.H;  // 64 floats: gate results
   lf* s_inv = gx + 64;
   prefetch_rows2(Lw.wg, Lw.wu, a.Rg, a.H, t, s.w);
+  const NormW nw = load_normw(Lw.ln2, a.H);
   stamp(a, l, P_GU, t, 0);
   gather_vec(x, ac.h1, a.H, a);
   stamp(a, l, P_GU, t, 1);
-  rmsnorm_lds(x, Lw.ln2, a.eps, a.H, ln, ln, s_inv);
-  const float acc = gemv_lds(a.Rg, s.w, ln, a.H, 2);
+  rmsnorm_lds(x, nw, a.eps, a.H, ln, ln, s_inv);
+  stamp(a, l, P_GU, t, 3);
+  const float acc = gemv_lds<16>(a.Rg, s.w, ln, a.H, 2, s.pad);
   const uint32_t wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
   if (wv == 0) gx[lane] = acc;
   __syncthreads();
@@ -834,7 +909,8 @@ __device__ __forceinline__ void run_d(const DecodeArgs& a, uint32_t l, uint32_t 
   gather(x, I + nr, a.epoch, a.err,
          [=](uint32_t i) { return i < I ? hid + i : h1 + (i - I); });
   stamp(a, l, P_D, t, 1);
-  const float acc = gemv_lds(a.Rd, s.w, x, I, 1);
+  const float acc = gemv_lds<32, 24, 12>(a.Rd, s.w, x, I, 1, s.pad);
+  stamp(a, l, P_D, t, 3);
   if (threadIdx.x < nr) put_word(ac.hout + r0 + threadIdx.x, hres[threadIdx.x] + acc, a.epoch);
   stamp(a, l, P_D, t, 2);
 }
@@ -851,10 +927,11 @@ __device__ __forceinline__ void run_lm(const DecodeArgs& a, const Lds& s) {
   lf* misc = hn + a.H;
   AS_LDS uint32_t* red = (AS_LDS uint32_t*)(misc + 4);
   if (wg < a.nl) prefetch_rows(a.lm, a.Rl, a.H, wg, s.w);
+  const NormW nw = load_normw(a.fnorm, a.H);
   stamp(a, L - 1, P_LM, wg, 0);
   gather_vec(x, act_of(a, L - 1).hout, a.H, a);
   stamp(a, L - 1, P_LM, wg, 1);
-  rmsnorm_lds(x, a.fnorm, a.eps, a.H, hn, hn, misc);
+  rmsnorm_lds(x, nw, a.eps, a.H, hn, hn, misc);
   AS_GLB float* logits = GW(a.logits);
   uint32_t done = 0;
   for (uint32_t b = wg; b < a.nl; b += a.nwg) {
@@ -862,7 +939,7 @@ __device__ __forceinline__ void run_lm(const DecodeArgs& a, const Lds& s) {
       prefetch_rows(a.lm, a.Rl, a.H, b, s.w);
       __syncthreads();
     }
-    const float acc = gemv_lds(a.Rl, s.w, hn, a.H, 1);
+    const float acc = gemv_lds<32>(a.Rl, s.w, hn, a.H, 1, s.pad);
     if (wv == 0) {
       const uint32_t row = b * a.Rl + lane;
       Cand c = {0.0f, UINT32_MAX};
@@ -918,6 +995,7 @@ void k_decode(DecodeArgs a) {
   s.w = (lf*)lds_dyn;
   const size_t wbytes = decode_wregion_bytes(a);
   s.v = s.w + wbytes / 4;
+  s.pad = (lf4*)(s.v + decode_vec_floats(a));
   const uint32_t wg = blockIdx.x;
   // role of this workgroup in every layer
   int role = -1;
@@ -956,14 +1034,8 @@ size_t decode_act_floats(uint32_t H, uint32_t I, uint32_t qd, uint32_t kvd) {
 }
 
 size_t decode_lds_bytes(const DecodeArgs& a) {
-  const size_t wbytes = decode_wregion_bytes(a);
-  size_t vec = 2 * (size_t)a.H + 64 + 64;                          // QKV, GU, LM
-  const size_t vo = (size_t)a.qd + a.Ro, vd = (size_t)a.I + a.Rd;  // O, D
-  const size_t va = 4 * (size_t)a.hd + 64;                         // ATT
-  vec = vec > vo ? vec : vo;
-  vec = vec > vd ? vec : vd;
-  vec = vec > va ? vec : va;
-  return wbytes + vec * 4 + 256;
+  // weight region | vectors | product-pass pad (64 x 16 B) | slack
+  return decode_wregion_bytes(a) + decode_vec_floats(a) * 4 + 64 * 16 + 256;
 }
 
 hipError_t launch_decode(const DecodeArgs& a, hipStream_t s) {

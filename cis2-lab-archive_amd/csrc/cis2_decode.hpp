@@ -14,10 +14,12 @@ struct LayerW {
 };
 
 // Rows per GEMV row block for a reduction length K: the block (R x K
-// floats) of one task fits the 144 KiB LDS weight budget.
-inline uint32_t rows_per_block(uint32_t K) {
+// floats) of one task fits the 144 KiB LDS weight budget, and R <= cap.
+// The persistent kernel uses cap 32 where its roles fit the device (two
+// k-groups per product instruction); the per-op kernels use cap 64.
+inline uint32_t rows_per_block(uint32_t K, uint32_t cap = 64) {
   uint32_t r = 36864u / K;
-  return r > 64 ? 64 : (r < 1 ? 1 : r);
+  return r > cap ? cap : (r < 1 ? 1 : r);
 }
 
 struct DecodeArgs {
@@ -36,7 +38,9 @@ struct DecodeArgs {
   uint32_t* tok_out;     // argmax written here (may alias tok_in)
   uint32_t* err;
   // Optional per-task timestamps (s_memrealtime, 100 MHz), null when off:
-  // [(l * 6 + phase) * 64 + task] * 4 words: wait start, wait end, done.
+  // [(l * 6 + phase) * 64 + task] * 4 words: wait start, wait end, done,
+  // and a mid-point (after RMSNorm for QKV/GU, after the GEMV for O/D,
+  // after the softmax for ATT, the argmax reduction for LM).
   uint64_t* tline;
   uint64_t cache_stride;
   uint32_t H, I, V, L, nh, nkv, hd, qd, kvd, max_pos;

@@ -504,13 +504,9 @@ int cis2_ctx_create(const cis2_config* cfg, cis2_ctx** out) {
       cis2_ctx_destroy(c);
       return CIS2_E_DEVICE;
     }
-  // Row-block sizes of the blocked GEMV layout (shared by both paths).
-  c->Rq = rows_per_block(H);
-  c->Ro = rows_per_block(c->qd);
-  c->Rg = rows_per_block(H) / 2 > 0 ? rows_per_block(H) / 2 : 1;
-  c->Rd = rows_per_block(I);
-  c->Rl = rows_per_block(H);
-  // Persistent decode kernel: task counts, workgroup roles, scratch.
+  // Persistent decode kernel: row-block sizes, task counts, workgroup roles.
+  // The GEMV layout's row-block sizes are shared by both paths: R <= 32 when
+  // the persistent kernel fits with them, else R <= 64.
   {
     int dev = 0, ncu = 0, lds = 0;
     (void)hipGetDevice(&dev);
@@ -520,32 +516,41 @@ int cis2_ctx_create(const cis2_config* cfg, cis2_ctx** out) {
     const char* pe = getenv("CIS2_PATH");
     c->force_ops = pe && !strcmp(pe, "ops");
     DecodeArgs& a = c->dargs;
-    memset(&a, 0, sizeof a);
-    a.H = H; a.I = I; a.V = V; a.L = f.n_layers; a.nh = f.n_heads; a.nkv = f.n_kv_heads;
-    a.hd = f.head_dim; a.qd = c->qd; a.kvd = c->kvd; a.max_pos = f.max_pos;
-    a.Rq = c->Rq; a.Ro = c->Ro; a.Rg = c->Rg; a.Rd = c->Rd; a.Rl = c->Rl;
-    a.nq_q = (c->qd + a.Rq - 1) / a.Rq;
-    a.nq_k = (c->kvd + a.Rq - 1) / a.Rq;
-    a.nq = a.nq_q + 2 * a.nq_k;
-    a.no = (H + a.Ro - 1) / a.Ro;
-    a.ng = (I + a.Rg - 1) / a.Rg;
-    a.nd = (H + a.Rd - 1) / a.Rd;
-    a.nl = (V + a.Rl - 1) / a.Rl;
-    a.base_q = 0;
-    a.base_a = a.base_q + a.nq;
-    a.base_o = a.base_a + a.nh;
-    a.base_g = a.base_o + a.no;
-    a.base_d = a.base_g + a.ng;
-    a.nwg = c->ncu;
-    a.cache_stride = (uint64_t)2 * c->kvd * f.max_pos;
-    a.eps = f.eps;
-    a.scale = c->scale;
-    a.rope_cs = c->rope_cs;
-    a.logits = c->logits;
-    a.err = c->d_err;
-    const size_t need_lds = decode_lds_bytes(a);
-    c->fast_ok = (a.base_d + a.nd <= c->ncu) && lds > 0 && need_lds <= (size_t)lds &&
-                 need_lds <= 160 * 1024;
+    auto plan = [&](uint32_t cap) {
+      memset(&a, 0, sizeof a);
+      a.H = H; a.I = I; a.V = V; a.L = f.n_layers; a.nh = f.n_heads; a.nkv = f.n_kv_heads;
+      a.hd = f.head_dim; a.qd = c->qd; a.kvd = c->kvd; a.max_pos = f.max_pos;
+      a.Rq = rows_per_block(H, cap);
+      a.Ro = rows_per_block(c->qd, cap);
+      a.Rg = rows_per_block(H, cap) / 2 > 0 ? rows_per_block(H, cap) / 2 : 1;
+      a.Rd = rows_per_block(I, cap);
+      a.Rl = rows_per_block(H, cap);
+      a.nq_q = (c->qd + a.Rq - 1) / a.Rq;
+      a.nq_k = (c->kvd + a.Rq - 1) / a.Rq;
+      a.nq = a.nq_q + 2 * a.nq_k;
+      a.no = (H + a.Ro - 1) / a.Ro;
+      a.ng = (I + a.Rg - 1) / a.Rg;
+      a.nd = (H + a.Rd - 1) / a.Rd;
+      a.nl = (V + a.Rl - 1) / a.Rl;
+      a.base_q = 0;
+      a.base_a = a.base_q + a.nq;
+      a.base_o = a.base_a + a.nh;
+      a.base_g = a.base_o + a.no;
+      a.base_d = a.base_g + a.ng;
+      a.nwg = c->ncu;
+      a.cache_stride = (uint64_t)2 * c->kvd * f.max_pos;
+      a.eps = f.eps;
+      a.scale = c->scale;
+      a.rope_cs = c->rope_cs;
+      a.logits = c->logits;
+      a.err = c->d_err;
+      // dynamic LDS plus the kernel's static LDS (a few words) within one CU
+      const size_t need_lds = decode_lds_bytes(a) + 64;
+      return (a.base_d + a.nd <= c->ncu) && lds > 0 && need_lds <= (size_t)lds &&
+             need_lds <= 160 * 1024 && a.hd <= 256;  // RoPE: one pair per thread
+    };
+    c->fast_ok = plan(32) || plan(64);
+    c->Rq = a.Rq; c->Ro = a.Ro; c->Rg = a.Rg; c->Rd = a.Rd; c->Rl = a.Rl;
     void* p = nullptr;
     const size_t act_f = (size_t)f.n_layers * decode_act_floats(H, I, c->qd, c->kvd);
     const size_t cnt_n = 64;

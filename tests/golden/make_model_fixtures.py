@@ -9,7 +9,7 @@ list, the table / inv_freq digests, and the sha256 of its --trace file.
 Only these small results are committed; the artifacts are regenerated from
 their seeds wherever a test needs them.
 
-Usage: python tests/golden/make_model_fixtures.py [case ...] [--jobs N]
+Usage: python tests/golden/make_model_fixtures.py [case ...] [--jobs N] [--out FILE]
 """
 import argparse
 import hashlib
@@ -39,6 +39,8 @@ CASES = {
     "llama-160m-p0": ("llama-160m", 160, ("llama", 0), 128, False),
     "llama-160m-p1": ("llama-160m", 160, ("llama", 1), 128, False),
     "llama-160m-p2": ("llama-160m", 160, ("llama", 2), 128, False),
+    # Qwen3-0.6B shape: 4096-token prompt, 256 generated tokens (positions 0..4351)
+    "qwen3-0.6b-4096": ("qwen3-0.6b", 6, 4096, 256, False),
 }
 
 
@@ -93,14 +95,16 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("cases", nargs="*")
     ap.add_argument("--jobs", type=int, default=4)
+    ap.add_argument("--out", default=OUT)
     a = ap.parse_args()
     names = a.cases or list(CASES)
-    doc = json.load(open(OUT)) if os.path.exists(OUT) else {}
+    out = a.out
+    doc = json.load(open(out)) if os.path.exists(out) else {}
     with ThreadPoolExecutor(a.jobs) as ex:
         for name, rec in ex.map(run_case, names):
             doc[name] = rec
             print(name, rec["witness"], flush=True)
-            with open(OUT, "w") as f:
+            with open(out, "w") as f:
                 json.dump(doc, f, indent=1, sort_keys=True)
 
 
