@@ -1027,7 +1027,72 @@ void k_decode(DecodeArgs a) {
   if (a.want_logits) run_lm(a, s);
 }
 
+// ---------------------------------------------------------------------------
+// Standalone strict-order GEMV y = W x (the per-row dot_seq of
+// code/cis2-fp/src/main.rs:228-243) on the blocked layout: one workgroup
+// per R-row block copies the block and x into LDS in one round trip, then
+// runs the same pipelined product pass and strict chains as the decode
+// kernel.
+// ---------------------------------------------------------------------------
+template <uint32_t R>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void k_gemv_blk(const float* __restrict__ W, const float* __restrict__ x, float* y, uint32_t M,
+                uint32_t K) {
+  extern __shared__ f4 lds_dyn[];
+  lf* w = (lf*)lds_dyn;
+  lf* xs = w + (size_t)R * K;
+  lf4* pad = (lf4*)(xs + K);
+  const uint32_t b = blockIdx.x;
+  const size_t blkf = (size_t)R * K;
+  gf4* src = G4(W + b * blkf);
+  gf4* x4 = G4(x);
+  const uint32_t n4 = (uint32_t)(blkf / 4), k4 = K >> 2;
+  copy_to_lds((lf4*)w, n4 + k4, [=](uint32_t i) { return i < n4 ? src + i : x4 + (i - n4); });
+  __syncthreads();
+  const float acc = gemv_lds_t<R>(w, xs, K, 1, pad);
+  const uint32_t row = b * R + threadIdx.x;
+  if (threadIdx.x < R && row < M) GW(y)[row] = acc;
+}
+
 }  // namespace
+
+size_t gemv_blk_lds_bytes(uint32_t K, uint32_t R) {
+  return ((size_t)R * K + K) * 4 + 64 * 16;
+}
+
+hipError_t launch_gemv_blk(const float* W, const float* x, float* y, uint32_t M, uint32_t K,
+                           uint32_t R, hipStream_t s) {
+  const size_t lds = gemv_blk_lds_bytes(K, R);
+  if (K % 4 || lds > 160 * 1024 - 64) return hipErrorInvalidValue;
+  const dim3 grid((M + R - 1) / R);
+  switch (R) {
+    case 16: {
+      static size_t configured = 0;
+      if (lds > configured) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemv_blk<16>),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return e;
+        configured = lds;
+      }
+      hipLaunchKernelGGL(k_gemv_blk<16>, grid, dim3(kThreads), lds, s, W, x, y, M, K);
+      break;
+    }
+    case 32: {
+      static size_t configured = 0;
+      if (lds > configured) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemv_blk<32>),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return e;
+        configured = lds;
+      }
+      hipLaunchKernelGGL(k_gemv_blk<32>, grid, dim3(kThreads), lds, s, W, x, y, M, K);
+      break;
+    }
+    default:
+      return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
 
 size_t decode_act_floats(uint32_t H, uint32_t I, uint32_t qd, uint32_t kvd) {
   return 2 * layer_words(H, I, qd, kvd);

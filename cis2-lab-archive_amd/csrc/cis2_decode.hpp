@@ -60,4 +60,10 @@ constexpr uint32_t kTimelineTasks = 64;
 size_t decode_lds_bytes(const DecodeArgs& a);
 hipError_t launch_decode(const DecodeArgs& a, hipStream_t s);
 
+// Standalone strict-order GEMV y = W x on the blocked layout with R rows per
+// block (R = 16 or 32): one workgroup per block, block and x staged in LDS.
+size_t gemv_blk_lds_bytes(uint32_t K, uint32_t R);
+hipError_t launch_gemv_blk(const float* W, const float* x, float* y, uint32_t M, uint32_t K,
+                           uint32_t R, hipStream_t s);
+
 }  // namespace cis2

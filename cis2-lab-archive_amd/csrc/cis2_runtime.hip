@@ -115,6 +115,8 @@ struct cis2_ctx {
 };
 
 constexpr size_t kProfMax = 65536;
+// Rows per block of the standalone GEMV plan's layout (one workgroup each).
+constexpr uint32_t kPlanR = 16;
 
 struct cis2_gemv_plan {
   uint32_t M, K, copies;
@@ -868,9 +870,10 @@ int cis2_decode_batch(cis2_ctx* c, uint32_t nseq, const uint32_t* prompts,
 int cis2_gemv_plan_create(uint32_t M, uint32_t K, uint32_t copies, const float* W,
                           cis2_gemv_plan** out) {
   if (!W || !out || M == 0 || K == 0 || K % 4 || copies == 0) return CIS2_E_ARG;
+  if (gemv_blk_lds_bytes(K, kPlanR) > 160 * 1024 - 64) return CIS2_E_UNSUPPORTED;
   cis2_gemv_plan* p = new cis2_gemv_plan();
   p->M = M; p->K = K; p->copies = copies;
-  const size_t per = blocked_floats(M, K, 64);
+  const size_t per = blocked_floats(M, K, kPlanR);
   float* rowmajor = nullptr;
   hipError_t e = hipStreamCreateWithFlags(&p->st, hipStreamNonBlocking);
   if (e == hipSuccess) e = hipMalloc(&p->W, per * copies * sizeof(float));
@@ -879,7 +882,7 @@ int cis2_gemv_plan_create(uint32_t M, uint32_t K, uint32_t copies, const float* 
   if (e == hipSuccess) e = hipMalloc(&rowmajor, (size_t)M * K * sizeof(float));
   if (e == hipSuccess) e = hipMemcpy(rowmajor, W, (size_t)M * K * sizeof(float), hipMemcpyHostToDevice);
   for (uint32_t i = 0; e == hipSuccess && i < copies; ++i)
-    e = launch_relayout(rowmajor, p->W + per * i, M, K, 64, p->st);
+    e = launch_relayout(rowmajor, p->W + per * i, M, K, kPlanR, p->st);
   if (e == hipSuccess) e = hipStreamSynchronize(p->st);
   if (e == hipSuccess) e = hipEventCreate(&p->e0);
   if (e == hipSuccess) e = hipEventCreate(&p->e1);
@@ -895,8 +898,7 @@ int cis2_gemv_plan_create(uint32_t M, uint32_t K, uint32_t copies, const float* 
 int cis2_gemv_plan_run(cis2_gemv_plan* p, const float* x, float* y) {
   if (!p || !x || !y) return CIS2_E_ARG;
   hipError_t e = hipMemcpyAsync(p->x, x, (size_t)p->K * sizeof(float), hipMemcpyHostToDevice, p->st);
-  GemvSeg sg[1] = {{p->W, p->x, nullptr, p->y, p->M, p->K, 0, 64}};
-  if (e == hipSuccess) e = launch_gemv(sg, 1, p->st);
+  if (e == hipSuccess) e = launch_gemv_blk(p->W, p->x, p->y, p->M, p->K, kPlanR, p->st);
   if (e == hipSuccess) e = hipMemcpyAsync(y, p->y, (size_t)p->M * sizeof(float), hipMemcpyDeviceToHost, p->st);
   if (e == hipSuccess) e = hipStreamSynchronize(p->st);
   return e == hipSuccess ? CIS2_OK : CIS2_E_DEVICE;
@@ -904,17 +906,13 @@ int cis2_gemv_plan_run(cis2_gemv_plan* p, const float* x, float* y) {
 
 int cis2_gemv_plan_time(cis2_gemv_plan* p, uint32_t iters, float* ms) {
   if (!p || !ms || iters == 0) return CIS2_E_ARG;
-  const size_t per = blocked_floats(p->M, p->K, 64);
+  const size_t per = blocked_floats(p->M, p->K, kPlanR);
   hipError_t e = hipSuccess;
-  for (uint32_t i = 0; e == hipSuccess && i < p->copies; ++i) {  // warm-up pass
-    GemvSeg sg[1] = {{p->W + per * i, p->x, nullptr, p->y, p->M, p->K, 0, 64}};
-    e = launch_gemv(sg, 1, p->st);
-  }
+  for (uint32_t i = 0; e == hipSuccess && i < p->copies; ++i)  // warm-up pass
+    e = launch_gemv_blk(p->W + per * i, p->x, p->y, p->M, p->K, kPlanR, p->st);
   if (e == hipSuccess) e = hipEventRecord(p->e0, p->st);
-  for (uint32_t i = 0; e == hipSuccess && i < iters; ++i) {
-    GemvSeg sg[1] = {{p->W + per * (i % p->copies), p->x, nullptr, p->y, p->M, p->K, 0, 64}};
-    e = launch_gemv(sg, 1, p->st);
-  }
+  for (uint32_t i = 0; e == hipSuccess && i < iters; ++i)
+    e = launch_gemv_blk(p->W + per * (i % p->copies), p->x, p->y, p->M, p->K, kPlanR, p->st);
   if (e == hipSuccess) e = hipEventRecord(p->e1, p->st);
   if (e == hipSuccess) e = hipEventSynchronize(p->e1);
   float t = 0.0f;
