@@ -58,7 +58,8 @@ __device__ __forceinline__ AS_GLB uint32_t* GU(uint32_t* p) { return (AS_GLB uin
 constexpr uint32_t kThreads = 256;
 constexpr uint32_t kSpinCap = 1u << 24;  // ~0.5 s of s_sleep(1)
 
-enum { P_QKV = 0, P_ATT = 1, P_O = 2, P_GU = 3, P_D = 4, P_LM = 5 };
+enum { P_QKV = kPhaseQKV, P_ATT = kPhaseATT, P_O = kPhaseO, P_GU = kPhaseGU, P_D = kPhaseD,
+       P_LM = 5 };
 
 // Per-layer tagged activations.
 struct Act {
@@ -96,6 +97,18 @@ __host__ __device__ inline size_t att_lds_floats(uint32_t hd, uint32_t pos, uint
   return (size_t)max_pos + 64 + 2 * (size_t)hd * att_row_stride(pos);
 }
 
+// Floats of the vector region (input vectors and scratch of every role),
+// rounded up to 16 bytes.
+__host__ __device__ inline size_t decode_vec_floats(const DecodeArgs& a) {
+  size_t vec = 2 * (size_t)a.H + 64 + 64;                          // QKV, GU, LM
+  const size_t vo = (size_t)a.qd + a.Ro, vd = (size_t)a.I + a.Rd;  // O, D
+  const size_t va = 4 * (size_t)a.hd + 64;                         // ATT
+  vec = vec > vo ? vec : vo;
+  vec = vec > vd ? vec : vd;
+  vec = vec > va ? vec : va;
+  return (vec + 3) & ~(size_t)3;
+}
+
 // Bytes of the LDS region that holds a task's weight block(s), or the
 // attention task's scores and cached K/V (up to what LDS can give).
 __host__ __device__ inline size_t decode_wregion_bytes(const DecodeArgs& a) {
@@ -108,23 +121,14 @@ __host__ __device__ inline size_t decode_wregion_bytes(const DecodeArgs& a) {
   // Attention: scores always in LDS; K/V rows in LDS for the positions that
   // fit in 150 KiB, read from HBM beyond that.
   size_t att = att_lds_floats(a.hd, a.max_pos, a.max_pos);
-  size_t cap = 38400;
+  // what LDS leaves after the vectors, the product pad, slack and static LDS
+  const size_t rest = decode_vec_floats(a) * 4 + 64 * 16 + 256 + 64;
+  size_t cap = rest < 160 * 1024 ? (160 * 1024 - rest) / 4 : 0;
+  cap &= ~(size_t)63;
   if (cap < (size_t)a.max_pos + 64) cap = (size_t)a.max_pos + 64;
   if (att > cap) att = cap;
   m = m > att ? m : att;
   return ((m * 4 + 255) / 256) * 256;
-}
-
-// Floats of the vector region (input vectors and scratch of every role),
-// rounded up to 16 bytes.
-__host__ __device__ inline size_t decode_vec_floats(const DecodeArgs& a) {
-  size_t vec = 2 * (size_t)a.H + 64 + 64;                          // QKV, GU, LM
-  const size_t vo = (size_t)a.qd + a.Ro, vd = (size_t)a.I + a.Rd;  // O, D
-  const size_t va = 4 * (size_t)a.hd + 64;                         // ATT
-  vec = vec > vo ? vec : vo;
-  vec = vec > vd ? vec : vd;
-  vec = vec > va ? vec : va;
-  return (vec + 3) & ~(size_t)3;
 }
 
 __device__ __forceinline__ uint32_t ld_ag(const uint32_t* p) {
@@ -997,16 +1001,21 @@ void k_decode(DecodeArgs a) {
   s.v = s.w + wbytes / 4;
   s.pad = (lf4*)(s.v + decode_vec_floats(a));
   const uint32_t wg = blockIdx.x;
-  // role of this workgroup in every layer
-  int role = -1;
-  uint32_t t = 0;
-  if (wg >= a.base_q && wg < a.base_q + a.nq) { role = P_QKV; t = wg - a.base_q; }
-  else if (wg >= a.base_a && wg < a.base_a + a.nh) { role = P_ATT; t = wg - a.base_a; }
-  else if (wg >= a.base_o && wg < a.base_o + a.no) { role = P_O; t = wg - a.base_o; }
-  else if (wg >= a.base_g && wg < a.base_g + a.ng) { role = P_GU; t = wg - a.base_g; }
-  else if (wg >= a.base_d && wg < a.base_d + a.nd) { role = P_D; t = wg - a.base_d; }
+  // this workgroup's tasks (the same in every layer), in phase order
+  uint32_t task[kMaxTasks];
+  uint32_t ntask = 0;
+  bool reads_tok = false;
+#pragma unroll
+  for (uint32_t i = 0; i < kMaxTasks; ++i) {
+    task[i] = __builtin_amdgcn_readfirstlane(((const AS_GLB uint16_t*)a.wg_tasks)[wg * kMaxTasks + i]);
+    if (task[i] != kNoTask) {
+      ntask = i + 1;
+      const uint32_t ph = task[i] >> 12;
+      reads_tok |= ph == P_QKV || ph == P_O;  // the layer-0 tasks that read the embedding row
+    }
+  }
   uint32_t tok = 0;
-  if (role == P_QKV || role == P_O) {  // the layer-0 tasks that read the embedding row
+  if (reads_tok) {
     tok = *(const AS_GLB uint32_t*)a.tok_in;
     if (tok >= a.V) {
       if (threadIdx.x == 0) raise_err(a.err, 1u);
@@ -1014,15 +1023,18 @@ void k_decode(DecodeArgs a) {
     }
   }
   for (uint32_t l = 0; l < a.L; ++l) {
-    switch (role) {
-      case P_QKV: run_qkv(a, l, t, s, tok); break;
-      case P_ATT: run_att(a, l, t, s, wbytes / 4); break;
-      case P_O: run_o(a, l, t, s, tok); break;
-      case P_GU: run_gu(a, l, t, s); break;
-      case P_D: run_d(a, l, t, s); break;
-      default: break;
+    for (uint32_t i = 0; i < ntask; ++i) {
+      const uint32_t ph = task[i] >> 12, t = task[i] & 0xFFFu;
+      switch (ph) {
+        case P_QKV: run_qkv(a, l, t, s, tok); break;
+        case P_ATT: run_att(a, l, t, s, wbytes / 4); break;
+        case P_O: run_o(a, l, t, s, tok); break;
+        case P_GU: run_gu(a, l, t, s); break;
+        case P_D: run_d(a, l, t, s); break;
+        default: break;
+      }
+      __syncthreads();
     }
-    __syncthreads();
   }
   if (a.want_logits) run_lm(a, s);
 }

@@ -47,7 +47,9 @@ struct DecodeArgs {
   uint32_t Rq, Ro, Rg, Rd, Rl;
   uint32_t nq_q, nq_k, nq;  // QKV tasks: q blocks, k blocks, total (q + k + v)
   uint32_t no, ng, nd, nl;  // O, gate/up, down, LM-head task counts
-  uint32_t base_q, base_a, base_o, base_g, base_d;  // first workgroup of each phase
+  // Tasks of each workgroup, in the order it runs them within a layer:
+  // wg_tasks[wg * kMaxTasks + i] = phase << 12 | task (kNoTask ends a list).
+  const uint16_t* wg_tasks;
   uint32_t nwg;
   float eps, scale;
   uint32_t pos, epoch, lm_epoch, want_logits;
@@ -56,6 +58,10 @@ struct DecodeArgs {
 // Floats (4-byte units) of one layer's tagged activation storage.
 size_t decode_act_floats(uint32_t H, uint32_t I, uint32_t qd, uint32_t kvd);
 constexpr uint32_t kTimelineTasks = 64;
+constexpr uint32_t kMaxTasks = 4;       // tasks per workgroup per layer
+constexpr uint16_t kNoTask = 0xFFFF;
+// Phases of a layer, in dependency order.
+enum { kPhaseQKV = 0, kPhaseATT = 1, kPhaseO = 2, kPhaseGU = 3, kPhaseD = 4, kPhases = 5 };
 // Dynamic LDS bytes the kernel needs for this configuration.
 size_t decode_lds_bytes(const DecodeArgs& a);
 hipError_t launch_decode(const DecodeArgs& a, hipStream_t s);

@@ -107,6 +107,7 @@ struct cis2_ctx {
   DecodeArgs dargs;
   uint64_t* tline = nullptr;  // CIS2_TIMELINE=<file>: per-task timestamps of every launch
   FILE* tline_file = nullptr;
+  std::vector<uint16_t> wg_tasks;  // [nwg][kMaxTasks] task table of the persistent kernel
   // cis2_profile: event pairs around decode-kernel launches
   bool prof_on = false;
   std::vector<hipEvent_t> prof_ev;  // [2 * kProfMax], created on first use
@@ -377,6 +378,37 @@ bool use_fast(const cis2_ctx* c) { return c->fast_ok && !c->force_ops && !c->tra
 
 }  // namespace
 
+// Spreads the tasks of every phase over the workgroups: each task goes to a
+// workgroup with the fewest tasks so far, preferring one whose last task is
+// not in the phase just before (so its next weight copy has a phase of time
+// to land).  Every list is in phase order, which makes the waits acyclic: a
+// task only waits for tasks of earlier (layer, phase).  False when some
+// workgroup would need more than kMaxTasks or a task index exceeds 12 bits.
+static bool assign_tasks(const DecodeArgs& a, std::vector<uint16_t>& table) {
+  const uint32_t n[kPhases] = {a.nq, a.nh, a.no, a.ng, a.nd};
+  const uint32_t W = a.nwg;
+  table.assign((size_t)W * kMaxTasks, kNoTask);
+  std::vector<uint32_t> cnt(W, 0);
+  std::vector<int> last(W, -2);
+  for (uint32_t p = 0; p < kPhases; ++p) {
+    if (n[p] >= 4096) return false;
+    for (uint32_t t = 0; t < n[p]; ++t) {
+      uint32_t best = W;
+      for (uint32_t w = 0; w < W; ++w) {
+        if (cnt[w] >= kMaxTasks || last[w] == (int)p) continue;
+        if (best == W) { best = w; continue; }
+        const bool adj_w = last[w] == (int)p - 1, adj_b = last[best] == (int)p - 1;
+        if (cnt[w] < cnt[best] || (cnt[w] == cnt[best] && !adj_w && adj_b)) best = w;
+      }
+      if (best == W) return false;
+      table[(size_t)best * kMaxTasks + cnt[best]] = (uint16_t)(p << 12 | t);
+      ++cnt[best];
+      last[best] = (int)p;
+    }
+  }
+  return true;
+}
+
 extern "C" {
 
 const char* cis2_strerror(int code) {
@@ -534,11 +566,6 @@ int cis2_ctx_create(const cis2_config* cfg, cis2_ctx** out) {
       a.ng = (I + a.Rg - 1) / a.Rg;
       a.nd = (H + a.Rd - 1) / a.Rd;
       a.nl = (V + a.Rl - 1) / a.Rl;
-      a.base_q = 0;
-      a.base_a = a.base_q + a.nq;
-      a.base_o = a.base_a + a.nh;
-      a.base_g = a.base_o + a.no;
-      a.base_d = a.base_g + a.ng;
       a.nwg = c->ncu;
       a.cache_stride = (uint64_t)2 * c->kvd * f.max_pos;
       a.eps = f.eps;
@@ -548,12 +575,20 @@ int cis2_ctx_create(const cis2_config* cfg, cis2_ctx** out) {
       a.err = c->d_err;
       // dynamic LDS plus the kernel's static LDS (a few words) within one CU
       const size_t need_lds = decode_lds_bytes(a) + 64;
-      return (a.base_d + a.nd <= c->ncu) && lds > 0 && need_lds <= (size_t)lds &&
+      return assign_tasks(a, c->wg_tasks) && lds > 0 && need_lds <= (size_t)lds &&
              need_lds <= 160 * 1024 && a.hd <= 256;  // RoPE: one pair per thread
     };
     c->fast_ok = plan(32) || plan(64);
     c->Rq = a.Rq; c->Ro = a.Ro; c->Rg = a.Rg; c->Rd = a.Rd; c->Rl = a.Rl;
     void* p = nullptr;
+    if (hipMalloc(&p, c->wg_tasks.size() * sizeof(uint16_t)) != hipSuccess) {
+      cis2_ctx_destroy(c);
+      return CIS2_E_OOM;
+    }
+    c->allocs.push_back(p);
+    (void)hipMemcpy(p, c->wg_tasks.data(), c->wg_tasks.size() * sizeof(uint16_t),
+                    hipMemcpyHostToDevice);
+    a.wg_tasks = static_cast<const uint16_t*>(p);
     const size_t act_f = (size_t)f.n_layers * decode_act_floats(H, I, c->qd, c->kvd);
     const size_t cnt_n = 64;
     if (!(c->act = dalloc(c, act_f)) || hipMalloc(&p, cnt_n * 4) != hipSuccess) {

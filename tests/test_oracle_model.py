@@ -47,3 +47,30 @@ def test_smollm2_135m_256_tokens_matches_reference(model_fixtures):
     _, _, res, _ = run(rec)
     assert list(res["ids"]) == rec["tokens"]
     assert res["witness"] == rec["witness"]
+
+
+def _set_cases(fname, pset):
+    import json
+    import os
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", fname)
+    if not os.path.exists(path):
+        pytest.skip("fixture %s not generated" % fname)
+    doc = json.load(open(path))
+    assert doc["set"] == pset
+    return doc["cases"]
+
+
+@pytest.mark.slow
+def test_llama160m_set_fixture_matches_oracle():
+    """The 300-prompt llama-160m fixture is complete and the oracle
+    reproduces the reference driver's digests on prompts from it."""
+    pset = artifacts.LLAMA_SET
+    cases = _set_cases("llama160m_set.json", pset)
+    assert sorted(int(k) for k in cases) == list(range(pset["count"]))
+    spec = artifacts.SPECS[pset["spec"]]
+    prompts = artifacts.set_prompts(pset)
+    w = artifacts.Weights(spec, pset["seed"])
+    for i in (0, 157):
+        m = O.OracleModel(spec, w, max_pos=len(prompts[i]) + pset["gen_toks"], threads=8)
+        r = m.decode(prompts[i], pset["gen_toks"])
+        assert [r["witness"], r["argmax_digest"]] == cases[str(i)], i
