@@ -87,6 +87,10 @@ SPECS = {
     "tiny-qwen2": ModelSpec("tiny-qwen2", 64, 128, 2, 4, 1, 256, 1e-6, 1000000.0, True,
                             qkv_bias=True),
     "smollm2-4l": ModelSpec("smollm2-4l", 576, 1536, 4, 9, 3, 49152, 1e-5, 100000.0, True),
+    # Qwen3-style head geometry (head_dim 128, QK-norm, GQA 2:1) at a small
+    # size: long prompts run the streamed-attention path in few seconds.
+    "tiny-wide": ModelSpec("tiny-wide", 256, 256, 2, 2, 1, 512, 1e-6, 1000000.0, True,
+                           head_dim=128, qk_norm=True),
 }
 
 TOKENIZER_JSON = (json.dumps({"version": "1.0", "model": {"type": "synthetic-ids"},

@@ -97,6 +97,19 @@ __host__ __device__ inline size_t att_lds_floats(uint32_t hd, uint32_t pos, uint
   return (size_t)max_pos + 64 + 2 * (size_t)hd * att_row_stride(pos);
 }
 
+// Positions per tile when a head's cached K/V do not fit in LDS: the
+// largest multiple of 32 whose [hd][TP+4] tile fits beside the scores (row
+// stride TP+4 is 4 mod 32: conflict-free 16-byte row reads); 0 if < 32.
+__host__ __device__ inline uint32_t att_tile_positions(uint32_t hd, uint32_t max_pos,
+                                                       size_t wfloats) {
+  const size_t room = wfloats > (size_t)max_pos + 64 ? wfloats - max_pos - 64 : 0;
+  const size_t per = room / hd;
+  if (per < 36) return 0;
+  size_t tp = (per - 4) & ~(size_t)31;
+  if (tp > 1024) tp = 1024;
+  return (uint32_t)tp;
+}
+
 // Floats of the vector region (input vectors and scratch of every role),
 // rounded up to 16 bytes.
 __host__ __device__ inline size_t decode_vec_floats(const DecodeArgs& a) {
@@ -214,6 +227,66 @@ __device__ __forceinline__ void copy_to_lds(lf4* dst, uint32_t n4, F src) {
 #pragma unroll
     for (uint32_t u = 0; u < B; ++u)
       if (i + u * kThreads < n4) dst[i + u * kThreads] = t[u];
+  }
+}
+
+// n4 16-byte elements from src(i) (global) to dst(i) (LDS), up to 16 loads
+// in flight per thread.
+template <class F, class G>
+__device__ __forceinline__ void copy_map(uint32_t n4, F src, G dst) {
+  constexpr uint32_t B = 16;
+  for (uint32_t i = threadIdx.x; i < n4; i += B * kThreads) {
+    f4 t[B];
+#pragma unroll
+    for (uint32_t u = 0; u < B; ++u)
+      if (i + u * kThreads < n4) t[u] = *src(i + u * kThreads);
+#pragma unroll
+    for (uint32_t u = 0; u < B; ++u)
+      if (i + u * kThreads < n4) *dst(i + u * kThreads) = t[u];
+  }
+}
+
+// Positions [j0, j0 + n) of the hd rows of one kv head's cache ([hd][max_pos]
+// at `rows`) into LDS rows of stride TS; n is rounded up to 4 (the extra
+// positions stay inside max_pos and are never used).
+__device__ __forceinline__ void copy_cache_tile(lf* dst, const float* rows, uint32_t max_pos,
+                                                uint32_t hd, uint32_t j0, uint32_t n,
+                                                uint32_t TS) {
+  const uint32_t nq = (n + 3) >> 2, mp4 = max_pos >> 2, ts4 = TS >> 2, j04 = j0 >> 2;
+  gf4* r4 = G4(rows);
+  lf4* d4 = (lf4*)dst;
+  copy_map(hd * nq,
+           [=](uint32_t i) {
+             const uint32_t d = i / nq, q = i - d * nq;
+             return r4 + (size_t)d * mp4 + j04 + q;
+           },
+           [=](uint32_t i) {
+             const uint32_t d = i / nq, q = i - d * nq;
+             return d4 + (size_t)d * ts4 + q;
+           });
+}
+
+// In place rows[d][q] *= scale(d, q) (16-byte groups q < nq of rows d < nrows,
+// row stride s4 groups): waves take rows wv, wv+4, ..., lanes the groups;
+// 8 rows' reads are issued before their writes.
+template <class F>
+__device__ __forceinline__ void scale_rows(lf4* rows, uint32_t s4, uint32_t nrows, uint32_t nq,
+                                           F scale) {
+  const uint32_t wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  constexpr uint32_t B = 8;
+  for (uint32_t q = lane; q < nq; q += 64) {
+    for (uint32_t d0 = wv; d0 < nrows; d0 += 4 * B) {
+      f4 v[B];
+#pragma unroll
+      for (uint32_t u = 0; u < B; ++u)
+        if (d0 + 4 * u < nrows) v[u] = rows[(size_t)(d0 + 4 * u) * s4 + q];
+#pragma unroll
+      for (uint32_t u = 0; u < B; ++u) {
+        if (d0 + 4 * u < nrows) {
+          rows[(size_t)(d0 + 4 * u) * s4 + q] = scale(d0 + 4 * u, q, v[u]);
+        }
+      }
+    }
   }
 }
 
@@ -709,34 +782,14 @@ __device__ __forceinline__ void run_att(const DecodeArgs& a, uint32_t l, uint32_
   if (in_lds) {
     // products q[d] * k_j[d] in place (row d scaled by q[d]); tmp = q * k_pos
     const uint32_t kq = (pos + 3) >> 2, s4 = S >> 2;
-    lf4* k4 = (lf4*)kl;
-    constexpr uint32_t B = 8;  // rows per batch: all reads before the writes
-    for (uint32_t q = lane; q < kq; q += 64) {
-      for (uint32_t d0 = wv; d0 < hd; d0 += 4 * B) {
-        f4 v[B];
-        float qd[B];
-#pragma unroll
-        for (uint32_t u = 0; u < B; ++u) {
-          const uint32_t d = d0 + 4 * u;
-          if (d < hd) {
-            v[u] = k4[(size_t)d * s4 + q];
-            qd[u] = qv[d];
-          }
-        }
-#pragma unroll
-        for (uint32_t u = 0; u < B; ++u) {
-          const uint32_t d = d0 + 4 * u;
-          if (d < hd) {
-            f4 w = v[u];
-            w.x = qd[u] * w.x;
-            w.y = qd[u] * w.y;
-            w.z = qd[u] * w.z;
-            w.w = qd[u] * w.w;
-            k4[(size_t)d * s4 + q] = w;
-          }
-        }
-      }
-    }
+    scale_rows((lf4*)kl, s4, hd, kq, [=](uint32_t d, uint32_t, f4 v) {
+      const float qd = qv[d];
+      v.x = qd * v.x;
+      v.y = qd * v.y;
+      v.z = qd * v.z;
+      v.w = qd * v.w;
+      return v;
+    });
     for (uint32_t d = threadIdx.x; d < hd; d += kThreads) tmp[d] = qv[d] * kv[d];
     __syncthreads();
     for (uint32_t j = threadIdx.x; j < len; j += kThreads) {
@@ -746,23 +799,32 @@ __device__ __forceinline__ void run_att(const DecodeArgs& a, uint32_t l, uint32_
       ss[j] = acc * a.scale;
     }
   } else {
-    const AS_GLB float* kb = kc + (size_t)kvh * hd * a.max_pos;
-    for (uint32_t j = threadIdx.x; j < len; j += kThreads) {
-      float acc = 0.0f;
-      if (j == pos) {
-        for (uint32_t d = 0; d < hd; ++d) {
-          float p = qv[d] * kv[d];
-          acc = acc + p;
-        }
-      } else {
-#pragma unroll 8
-        for (uint32_t d = 0; d < hd; ++d) {
-          float p = qv[d] * kb[(size_t)d * a.max_pos + j];
-          acc = acc + p;
-        }
-      }
-      ss[j] = acc * a.scale;
+    // The cached K/V do not fit in LDS: stream tiles of TP positions.  Per
+    // tile, the products q[d] * k_j[d] are formed in place and each
+    // position's lane adds its hd products in order.
+    const uint32_t TP = att_tile_positions(hd, a.max_pos, wfloats), TS = TP + 4;
+    const float* kb = a.kc0 + (size_t)l * a.cache_stride + (size_t)kvh * hd * a.max_pos;
+    lf* kt = ss + a.max_pos + 64;
+    for (uint32_t j0 = 0; j0 < pos; j0 += TP) {
+      const uint32_t n = min(TP, pos - j0);
+      copy_cache_tile(kt, kb, a.max_pos, hd, j0, n, TS);
+      __syncthreads();
+      scale_rows((lf4*)kt, TS >> 2, hd, (n + 3) >> 2, [=](uint32_t d, uint32_t, f4 v) {
+        const float qd = qv[d];
+        v.x = qd * v.x;
+        v.y = qd * v.y;
+        v.z = qd * v.z;
+        v.w = qd * v.w;
+        return v;
+      });
+      __syncthreads();
+      for (uint32_t jj = threadIdx.x; jj < n; jj += kThreads)
+        ss[j0 + jj] = chain1(kt + jj, hd, TS, 0.0f) * a.scale;
+      __syncthreads();
     }
+    for (uint32_t d = threadIdx.x; d < hd; d += kThreads) tmp[d] = qv[d] * kv[d];
+    __syncthreads();
+    if (threadIdx.x == 0) ss[pos] = chain1(tmp, hd, 1, 0.0f) * a.scale;
   }
   __syncthreads();
   // softmax_seq (math.rs:425-442): first-wins max, pinned exp, strict-chain
@@ -796,27 +858,14 @@ __device__ __forceinline__ void run_att(const DecodeArgs& a, uint32_t l, uint32_
     const uint32_t kq = (pos + 3) >> 2, s4 = S >> 2;
     lf4* v4 = (lf4*)vl;
     const lf4* p4 = (const lf4*)ss;
-    constexpr uint32_t B = 8;  // rows per batch: all reads before the writes
-    for (uint32_t q = lane; q < kq; q += 64) {
+    scale_rows(v4, s4, hd, kq, [=](uint32_t, uint32_t q, f4 v) {
       const f4 p = p4[q];
-      for (uint32_t d0 = wv; d0 < hd; d0 += 4 * B) {
-        f4 v[B];
-#pragma unroll
-        for (uint32_t u = 0; u < B; ++u)
-          if (d0 + 4 * u < hd) v[u] = v4[(size_t)(d0 + 4 * u) * s4 + q];
-#pragma unroll
-        for (uint32_t u = 0; u < B; ++u) {
-          if (d0 + 4 * u < hd) {
-            f4 w = v[u];
-            w.x = p.x * w.x;
-            w.y = p.y * w.y;
-            w.z = p.z * w.z;
-            w.w = p.w * w.w;
-            v4[(size_t)(d0 + 4 * u) * s4 + q] = w;
-          }
-        }
-      }
-    }
+      v.x = p.x * v.x;
+      v.y = p.y * v.y;
+      v.z = p.z * v.z;
+      v.w = p.w * v.w;
+      return v;
+    });
     __syncthreads();
     for (uint32_t d = threadIdx.x; d < hd; d += kThreads) {
       float acc = chain_vec(vl + (size_t)d * S, pos, 0.0f);
@@ -825,14 +874,31 @@ __device__ __forceinline__ void run_att(const DecodeArgs& a, uint32_t l, uint32_
       put_word(ac.att + (size_t)h * hd + d, acc, a.epoch);
     }
   } else {
-    const AS_GLB float* vb = vc + (size_t)kvh * hd * a.max_pos;
-    for (uint32_t d = threadIdx.x; d < hd; d += kThreads) {
-      float acc = 0.0f;
-#pragma unroll 8
-      for (uint32_t j = 0; j < pos; ++j) {
-        float p = ss[j] * vb[(size_t)d * a.max_pos + j];
-        acc = acc + p;
-      }
+    // Tiles of TP positions: products p_j * v_j[d] in place, then lane d
+    // continues its one left-to-right chain over the tile.
+    const uint32_t TP = att_tile_positions(hd, a.max_pos, wfloats), TS = TP + 4;
+    const float* vb = a.vc0 + (size_t)l * a.cache_stride + (size_t)kvh * hd * a.max_pos;
+    lf* vt = ss + a.max_pos + 64;
+    float acc = 0.0f;
+    for (uint32_t j0 = 0; j0 < pos; j0 += TP) {
+      const uint32_t n = min(TP, pos - j0);
+      copy_cache_tile(vt, vb, a.max_pos, hd, j0, n, TS);
+      __syncthreads();
+      const lf4* p4 = (const lf4*)(ss + j0);
+      scale_rows((lf4*)vt, TS >> 2, hd, (n + 3) >> 2, [=](uint32_t, uint32_t q, f4 v) {
+        const f4 p = p4[q];
+        v.x = p.x * v.x;
+        v.y = p.y * v.y;
+        v.z = p.z * v.z;
+        v.w = p.w * v.w;
+        return v;
+      });
+      __syncthreads();
+      if (threadIdx.x < hd) acc = chain_vec(vt + (size_t)threadIdx.x * TS, n, acc);
+      __syncthreads();
+    }
+    if (threadIdx.x < hd) {
+      const uint32_t d = threadIdx.x;
       float p = ss[pos] * vv[d];
       acc = acc + p;
       put_word(ac.att + (size_t)h * hd + d, acc, a.epoch);
@@ -1108,6 +1174,12 @@ hipError_t launch_gemv_blk(const float* W, const float* x, float* y, uint32_t M,
 
 size_t decode_act_floats(uint32_t H, uint32_t I, uint32_t qd, uint32_t kvd) {
   return 2 * layer_words(H, I, qd, kvd);
+}
+
+bool decode_att_ok(const DecodeArgs& a) {
+  const size_t wfloats = decode_wregion_bytes(a) / 4;
+  return att_lds_floats(a.hd, a.max_pos, a.max_pos) <= wfloats ||
+         att_tile_positions(a.hd, a.max_pos, wfloats) >= 32;
 }
 
 size_t decode_lds_bytes(const DecodeArgs& a) {

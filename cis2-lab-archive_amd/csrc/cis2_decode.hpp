@@ -64,6 +64,9 @@ constexpr uint16_t kNoTask = 0xFFFF;
 enum { kPhaseQKV = 0, kPhaseATT = 1, kPhaseO = 2, kPhaseGU = 3, kPhaseD = 4, kPhases = 5 };
 // Dynamic LDS bytes the kernel needs for this configuration.
 size_t decode_lds_bytes(const DecodeArgs& a);
+// True when attention fits the configuration: every cached position in LDS,
+// or tiles of at least 32 positions beside the scores.
+bool decode_att_ok(const DecodeArgs& a);
 hipError_t launch_decode(const DecodeArgs& a, hipStream_t s);
 
 // Standalone strict-order GEMV y = W x on the blocked layout with R rows per

@@ -576,7 +576,8 @@ int cis2_ctx_create(const cis2_config* cfg, cis2_ctx** out) {
       // dynamic LDS plus the kernel's static LDS (a few words) within one CU
       const size_t need_lds = decode_lds_bytes(a) + 64;
       return assign_tasks(a, c->wg_tasks) && lds > 0 && need_lds <= (size_t)lds &&
-             need_lds <= 160 * 1024 && a.hd <= 256;  // RoPE: one pair per thread
+             need_lds <= 160 * 1024 && a.hd <= 256 &&  // RoPE: one pair per thread
+             decode_att_ok(a);
     };
     c->fast_ok = plan(32) || plan(64);
     c->Rq = a.Rq; c->Ro = a.Ro; c->Rg = a.Rg; c->Rd = a.Rd; c->Rl = a.Rl;

@@ -144,3 +144,20 @@ def test_error_paths(model_fixtures):
     with pytest.raises(Cis2Error) as e:
         Cis2Model(spec, w4, max_pos=8)
     assert e.value.code == -5
+
+
+def test_long_context_streamed_attention_matches_oracle():
+    """Positions whose cached K/V no longer fit in LDS take the streamed
+    attention path (tiles of 288 positions at head_dim 128); every step's
+    logits digest and the witness must equal the oracle's."""
+    spec = artifacts.SPECS["tiny-wide"]
+    w = artifacts.Weights(spec, 77)
+    prompt = artifacts.prompt_ids(77, spec.vocab, 1180)
+    gen = 20
+    m = Cis2Model(spec, w, max_pos=len(prompt) + gen)
+    r = m.decode(prompt, gen)
+    o = O.OracleModel(spec, w, max_pos=len(prompt) + gen, threads=8)
+    ro = o.decode(prompt, gen)
+    assert r["step_digests"] == ro["step_digests"]
+    assert r["witness"] == ro["witness"]
+    assert list(r["ids"]) == list(ro["ids"])
