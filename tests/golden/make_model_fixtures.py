@@ -28,7 +28,7 @@ from cis2amd import artifacts  # noqa: E402
 OUT = os.path.join(ROOT, "tests", "golden", "model_fixtures.json")
 REF = os.path.join(ROOT, "oracle", "_ref")
 
-# name: (spec, seed, prompt_len or list, gen_toks, trace)
+# name: (spec, seed, prompt_len or list, gen_toks, trace[, tree reduction])
 CASES = {
     "tiny-llama": ("tiny-llama", 1, 5, 12, True),
     "tiny-untied": ("tiny-untied", 2, 7, 10, True),
@@ -41,6 +41,13 @@ CASES = {
     "llama-160m-p2": ("llama-160m", 160, ("llama", 2), 128, False),
     # Qwen3-0.6B shape: 4096-token prompt, 256 generated tokens (positions 0..4351)
     "qwen3-0.6b-4096": ("qwen3-0.6b", 6, 4096, 256, False),
+    # v0.4 tree reduction order (reference built with -DCIS2_REDUCTION_TREE)
+    "tiny-llama-tree": ("tiny-llama", 1, 5, 12, True, True),
+    "tiny-untied-tree": ("tiny-untied", 2, 7, 10, True, True),
+    "tiny-qwen3-tree": ("tiny-qwen3", 3, 6, 10, True, True),
+    "tiny-qwen2-tree": ("tiny-qwen2", 4, 4, 8, True, True),
+    "tiny-wide-tree": ("tiny-wide", 77, 1180, 20, False, True),
+    "smollm2-135m-tree": ("smollm2-135m", 20261201, 32, 256, False, True),
 }
 
 
@@ -57,11 +64,13 @@ def case_prompt(spec, seed, p):
 
 
 def run_case(name):
-    spec_name, seed, p, gen, trace = CASES[name]
+    spec_name, seed, p, gen, trace = CASES[name][:5]
+    tree = len(CASES[name]) > 5 and CASES[name][5]
     spec = artifacts.SPECS[spec_name]
     prompt = case_prompt(spec, seed, p)
     w = artifacts.Weights(spec, seed)
-    binary = os.path.join(REF, "cis2_host_qwen3" if spec.qk_norm or spec.head_dim else "cis2_host")
+    binary = os.path.join(REF, ("cis2_host_qwen3" if spec.qk_norm or spec.head_dim else "cis2_host")
+                          + ("_tree" if tree else ""))
     with tempfile.TemporaryDirectory(prefix="cis2fx_") as d:
         w.write_dir(d)
         ids = os.path.join(d, "ids.txt")
@@ -76,7 +85,8 @@ def run_case(name):
             raise RuntimeError("%s failed: %s" % (name, r.stderr[-2000:]))
         out = r.stdout
         rec = {"spec": spec_name, "seed": seed, "prompt": prompt, "gen_toks": gen,
-               "reference_binary": os.path.basename(binary)}
+               "reference_binary": os.path.basename(binary),
+               "reduction": re.search(r"reduction_mode=(\w+)", out).group(1)}
         for key in ["weights_sha256", "tokenizer_sha256", "config_sha256", "table_digest",
                     "inv_freq_table_digest"]:
             rec[key] = re.search(key + r"=([0-9a-f]{64})", out).group(1)

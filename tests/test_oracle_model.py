@@ -74,3 +74,37 @@ def test_llama160m_set_fixture_matches_oracle():
         m = O.OracleModel(spec, w, max_pos=len(prompts[i]) + pset["gen_toks"], threads=8)
         r = m.decode(prompts[i], pset["gen_toks"])
         assert [r["witness"], r["argmax_digest"]] == cases[str(i)], i
+
+
+TREE = ["tiny-llama-tree", "tiny-untied-tree", "tiny-qwen3-tree", "tiny-qwen2-tree"]
+
+
+def run_tree(rec, trace=False):
+    spec = artifacts.SPECS[rec["spec"]]
+    w = artifacts.Weights(spec, rec["seed"])
+    m = O.OracleModel(spec, w, max_pos=len(rec["prompt"]) + rec["gen_toks"], threads=8,
+                      reduction=1)
+    lines = [] if trace else None
+    return m.decode(rec["prompt"], rec["gen_toks"], trace=lines), lines
+
+
+@pytest.mark.parametrize("name", TREE)
+def test_tree_mode_tiny_models_match_reference(name, model_fixtures):
+    """The oracle's v0.4 tree order against the reference driver built with
+    -DCIS2_REDUCTION_TREE (witness, argmax digest, tokens, --trace hash)."""
+    rec = model_fixtures[name]
+    assert rec["reduction"] == "tree"
+    res, lines = run_tree(rec, trace=True)
+    assert list(res["ids"]) == rec["tokens"]
+    assert res["argmax_digest"] == rec["argmax_digest"]
+    assert res["witness"] == rec["witness"]
+    assert hashlib.sha256(("\n".join(lines) + "\n").encode()).hexdigest() == rec["trace_sha256"]
+
+
+@pytest.mark.slow
+@pytest.mark.parametrize("name", ["tiny-wide-tree", "smollm2-135m-tree"])
+def test_tree_mode_models_match_reference(name, model_fixtures):
+    rec = model_fixtures[name]
+    res, _ = run_tree(rec)
+    assert list(res["ids"]) == rec["tokens"]
+    assert res["witness"] == rec["witness"]
