@@ -26,7 +26,9 @@ def _ptr(arr, ctype):
 
 
 class Cis2Model:
-    def __init__(self, spec, weights, max_pos, max_seqs=1):
+    def __init__(self, spec, weights, max_pos, max_seqs=1, reduction_mode=0):
+        """reduction_mode 0: sequential order (v0.3b); 1: the v0.4-candidate
+        tree order (code/cis2-fp/src/math.rs:60-125, CIS2_REDUCTION_TREE)."""
         L = _lib.lib()
         self.spec = spec
         self.weights = weights
@@ -34,12 +36,13 @@ class Cis2Model:
             hidden=spec.hidden, inter=spec.inter, n_layers=spec.n_layers,
             n_heads=spec.n_heads, n_kv_heads=spec.n_kv_heads, head_dim=spec.hd,
             vocab=spec.vocab, tied=1 if spec.tied else 0, max_pos=max_pos,
-            max_seqs=max_seqs, reduction_mode=0, eps=spec.eps, rope_theta=spec.rope_theta)
+            max_seqs=max_seqs, reduction_mode=reduction_mode, eps=spec.eps, rope_theta=spec.rope_theta)
         h = ctypes.c_void_p()
         check(L.cis2_ctx_create(ctypes.byref(cfg), ctypes.byref(h)))
         self.ctx = h
         self.max_pos = max_pos
         self.max_seqs = max_seqs
+        self.reduction_mode = reduction_mode
         for name, _shape, arr in weights.tensors:
             arr = np.ascontiguousarray(arr, dtype=np.uint16)
             check(L.cis2_upload_bf16(self.ctx, name.encode(), _ptr(arr, _lib.c_u16p), arr.size),

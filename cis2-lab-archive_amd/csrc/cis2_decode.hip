@@ -538,6 +538,102 @@ __device__ __forceinline__ float gemv_lds(uint32_t R, lf* W, const lf* x, uint32
   }
 }
 
+// Tree order (v0.4 candidate, code/cis2-fp/src/math.rs:60-125) on LDS row
+// blocks: after the product pass, item (block b, k block kb, row r) reduces
+// its row's 32 products k in [32kb, 32kb + 32) by tree32 (+0 past K) and
+// leaves the result in the first product slot; lane r of wave b then folds
+// its row's block results from 0.  R = 0: height given at run time (Rr).
+template <uint32_t R>
+__device__ __forceinline__ float gemv_tree_t(uint32_t Rr, lf* W, const lf* x, uint32_t K,
+                                             uint32_t nb, lf4* pad) {
+  const uint32_t Rv = R ? R : Rr;
+  const uint32_t KG = __builtin_amdgcn_readfirstlane(K >> 2), lane = threadIdx.x & 63;
+  nb = __builtin_amdgcn_readfirstlane(nb);
+  const uint32_t wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  lf4* W4 = (lf4*)W;
+  const lf4* x4 = (const lf4*)x;
+  const uint32_t bf4 = KG * Rv;
+  if constexpr (R != 0) {
+    constexpr uint32_t GP = 64 / R;
+    prod_ins<R>(W4, x4, bf4, nb, KG, 0, (KG + GP - 1) / GP, wv, kThreads / 64, pad);
+  } else {
+    for (uint32_t i = threadIdx.x; i < nb * bf4; i += kThreads) {
+      const f4 xv = x4[(i % bf4) / Rv];
+      f4 w = W4[i];
+      w.x = w.x * xv.x;
+      w.y = w.y * xv.y;
+      w.z = w.z * xv.z;
+      w.w = w.w * xv.w;
+      W4[i] = w;
+    }
+  }
+  __syncthreads();
+  const uint32_t KB = (KG + 7) / 8, items = nb * KB * Rv;
+  for (uint32_t it = threadIdx.x; it < items; it += kThreads) {
+    const uint32_t r = it % Rv, q = it / Rv, kb = q % KB, b = q / KB;
+    lf4* p = W4 + (size_t)b * bf4 + (size_t)kb * 8 * Rv + r;
+    float lv[32];
+#pragma unroll
+    for (uint32_t j = 0; j < 8; ++j) {
+      f4 v = {0.0f, 0.0f, 0.0f, 0.0f};
+      if (kb * 8 + j < KG) v = p[(size_t)j * Rv];
+      lv[4 * j] = v.x;
+      lv[4 * j + 1] = v.y;
+      lv[4 * j + 2] = v.z;
+      lv[4 * j + 3] = v.w;
+    }
+    ((lf*)p)[0] = tree32(lv);
+  }
+  __syncthreads();
+  float acc = 0.0f;
+  if (wv < nb)
+    acc = chain1((const lf*)(W4 + (size_t)wv * bf4 + (lane < Rv ? lane : Rv - 1)), KB, 32 * Rv,
+                 0.0f);
+  __syncthreads();
+  return acc;
+}
+
+__device__ __noinline__ float gemv_tree_generic(uint32_t R, lf* W, const lf* x, uint32_t K,
+                                                uint32_t nb, lf4* pad) {
+  return gemv_tree_t<0>(R, W, x, K, nb, pad);
+}
+
+template <uint32_t R0, uint32_t... Rs>
+__device__ __forceinline__ float gemv_tree(uint32_t R, lf* W, const lf* x, uint32_t K,
+                                           uint32_t nb, lf4* pad) {
+  if (R == R0) return gemv_tree_t<R0>(R, W, x, K, nb, pad);
+  if constexpr (sizeof...(Rs) > 0) {
+    return gemv_tree<Rs...>(R, W, x, K, nb, pad);
+  } else {
+    return gemv_tree_generic(R, W, x, K, nb, pad);
+  }
+}
+
+// The GEMV of a call site in the reduction order TR selects.
+template <bool TR, uint32_t... Rs>
+__device__ __forceinline__ float gemv_sel(uint32_t R, lf* W, const lf* x, uint32_t K,
+                                          uint32_t nb, lf4* pad) {
+  if constexpr (TR) {
+    return gemv_tree<Rs...>(R, W, x, K, nb, pad);
+  } else {
+    return gemv_lds<Rs...>(R, W, x, K, nb, pad);
+  }
+}
+
+// tree32 over the LDS values p[i * st], i < min(n, 32) (+0 past n).
+__device__ __forceinline__ float tree_part(const lf* p, uint32_t n, uint32_t st) {
+  float lv[32];
+#pragma unroll
+  for (uint32_t i = 0; i < 32; ++i) lv[i] = i < n ? p[(size_t)i * st] : 0.0f;
+  return tree32(lv);
+}
+// Tree-order sum over n strided LDS values p[i * st] (scores: one column of
+// products): 32-value blocks by tree32, the block results folded from acc.
+__device__ __forceinline__ float tree_col(const lf* p, uint32_t n, uint32_t st, float acc) {
+  for (uint32_t i0 = 0; i0 < n; i0 += 32) acc = acc + tree_part(p + (size_t)i0 * st, n - i0, st);
+  return acc;
+}
+
 // RMSNorm of an LDS vector (code/cis2-fp/src/main.rs:245-260): squares
 // into `tmp`, one strict chain in wave 0, mean by a true divide,
 // inv = 1/sqrt(mean + eps), out = (x*inv)*w.  `out` may alias `tmp` or x.
@@ -561,15 +657,31 @@ __device__ __forceinline__ NormW load_normw(const float* w_, uint32_t n) {
   }
   return r;
 }
+// Tree order (TR): the squares of block t of 32 are reduced by tree32 into
+// tmp[t], and the block results folded from 0.
+template <bool TR>
 __device__ __forceinline__ void rmsnorm_lds(const lf* x, const NormW& w, float eps, uint32_t n,
                                             lf* tmp, lf* out, lf* s_inv) {
-  for (uint32_t i = threadIdx.x; i < n; i += kThreads) {
-    float v = x[i];
-    tmp[i] = v * v;
+  const uint32_t nb = (n + 31) / 32;
+  if constexpr (TR) {
+    for (uint32_t t = threadIdx.x; t < nb; t += kThreads) {
+      float lv[32];
+#pragma unroll
+      for (uint32_t i = 0; i < 32; ++i) {
+        const float v = 32 * t + i < n ? x[32 * t + i] : 0.0f;
+        lv[i] = v * v;
+      }
+      tmp[t] = tree32(lv);
+    }
+  } else {
+    for (uint32_t i = threadIdx.x; i < n; i += kThreads) {
+      float v = x[i];
+      tmp[i] = v * v;
+    }
   }
   __syncthreads();
   if (threadIdx.x < 64) {
-    const float acc = chain_vec(tmp, n, 0.0f);
+    const float acc = TR ? chain1(tmp, nb, 1, 0.0f) : chain_vec(tmp, n, 0.0f);
     float mean = acc / (float)n;
     float arg = mean + eps;
     float inv = rsqrt_cr(arg);
@@ -652,6 +764,7 @@ __device__ __forceinline__ QkvGeom qkv_geom(const DecodeArgs& a, const LayerW& L
 }
 
 // One row block of q, k or v: input_layernorm, GEMV, bias (main.rs:405-413).
+template <bool TR>
 __device__ __forceinline__ void run_qkv(const DecodeArgs& a, uint32_t l, uint32_t t, const Lds& s,
                                        uint32_t tok) {
   const LayerW Lw = a.layers[l];
@@ -671,9 +784,9 @@ __device__ __forceinline__ void run_qkv(const DecodeArgs& a, uint32_t l, uint32_
     gather_vec(x, act_of(a, l - 1).hout, a.H, a);
   }
   stamp(a, l, P_QKV, t, 1);
-  rmsnorm_lds(x, nw, a.eps, a.H, ln, ln, s_inv);
+  rmsnorm_lds<TR>(x, nw, a.eps, a.H, ln, ln, s_inv);
   stamp(a, l, P_QKV, t, 3);
-  const float acc = gemv_lds<32>(a.Rq, s.w, ln, a.H, 1, s.pad);
+  const float acc = gemv_sel<TR, 32>(a.Rq, s.w, ln, a.H, 1, s.pad);
   const uint32_t row = g.blk * a.Rq + threadIdx.x;
   if (threadIdx.x < a.Rq && row < g.M) {
     const float r = g.bias ? acc + G(g.bias)[row] : acc;
@@ -713,6 +826,7 @@ __device__ __forceinline__ void prefetch_kv(const DecodeArgs& a, uint32_t l, uin
 }
 
 // Attention for query head h (code/cis2-fp/src/main.rs:415-467).
+template <bool TR>
 __device__ __forceinline__ void run_att(const DecodeArgs& a, uint32_t l, uint32_t h, const Lds& s,
                         size_t wfloats) {
   const LayerW Lw = a.layers[l];
@@ -752,8 +866,8 @@ __device__ __forceinline__ void run_att(const DecodeArgs& a, uint32_t l, uint32_
   stamp(a, l, P_ATT, h, 1);
   // Qwen3 per-head QK-norm, after bias and before RoPE
   // (labs/w1x-qwen3/scripts/qwen3-port.diff:66-80).
-  if (Lw.qn) rmsnorm_lds(qv, nq, a.eps, hd, tmp, qv, misc);
-  if (Lw.kn) rmsnorm_lds(kv, nk, a.eps, hd, tmp, kv, misc);
+  if (Lw.qn) rmsnorm_lds<TR>(qv, nq, a.eps, hd, tmp, qv, misc);
+  if (Lw.kn) rmsnorm_lds<TR>(kv, nk, a.eps, hd, tmp, kv, misc);
   // RoPE rotate-half (main.rs:285-307): o1 = x1*c + (-x2)*s, o2 = x2*c + x1*s.
   if (threadIdx.x < 2 * half) {
     const uint32_t idx = threadIdx.x;
@@ -795,7 +909,7 @@ __device__ __forceinline__ void run_att(const DecodeArgs& a, uint32_t l, uint32_
     for (uint32_t j = threadIdx.x; j < len; j += kThreads) {
       const lf* p = j < pos ? kl + j : tmp;
       const uint32_t st = j < pos ? S : 1u;
-      const float acc = chain1(p, hd, st, 0.0f);
+      const float acc = TR ? tree_col(p, hd, st, 0.0f) : chain1(p, hd, st, 0.0f);
       ss[j] = acc * a.scale;
     }
   } else {
@@ -819,12 +933,14 @@ __device__ __forceinline__ void run_att(const DecodeArgs& a, uint32_t l, uint32_
       });
       __syncthreads();
       for (uint32_t jj = threadIdx.x; jj < n; jj += kThreads)
-        ss[j0 + jj] = chain1(kt + jj, hd, TS, 0.0f) * a.scale;
+        ss[j0 + jj] = (TR ? tree_col(kt + jj, hd, TS, 0.0f) : chain1(kt + jj, hd, TS, 0.0f)) *
+                      a.scale;
       __syncthreads();
     }
     for (uint32_t d = threadIdx.x; d < hd; d += kThreads) tmp[d] = qv[d] * kv[d];
     __syncthreads();
-    if (threadIdx.x == 0) ss[pos] = chain1(tmp, hd, 1, 0.0f) * a.scale;
+    if (threadIdx.x == 0)
+      ss[pos] = (TR ? tree_col(tmp, hd, 1, 0.0f) : chain1(tmp, hd, 1, 0.0f)) * a.scale;
   }
   __syncthreads();
   // softmax_seq (math.rs:425-442): first-wins max, pinned exp, strict-chain
@@ -841,7 +957,19 @@ __device__ __forceinline__ void run_att(const DecodeArgs& a, uint32_t l, uint32_
     ss[j] = exp_pinned(dlt);
   }
   __syncthreads();
-  if (threadIdx.x < 64) {
+  if constexpr (TR) {
+    // softmax_tree (math.rs:448-465): block results of the exp values in
+    // the (now unused) K region, folded from 0
+    lf* part = ss + a.max_pos + 64;
+    const uint32_t nbk = (len + 31) / 32;
+    for (uint32_t t = threadIdx.x; t < nbk; t += kThreads)
+      part[t] = tree_part(ss + 32 * t, len - 32 * t, 1);
+    __syncthreads();
+    if (threadIdx.x < 64) {
+      const float acc = chain1(part, nbk, 1, 0.0f);
+      if (threadIdx.x == 0) misc[1] = acc;
+    }
+  } else if (threadIdx.x < 64) {
     const float acc = chain_vec(ss, len, 0.0f);
     if (threadIdx.x == 0) misc[1] = acc;
   }
@@ -909,6 +1037,7 @@ __device__ __forceinline__ void run_att(const DecodeArgs& a, uint32_t l, uint32_
 }
 
 // o_proj block + residual h1 = h + o (main.rs:470-472).
+template <bool TR>
 __device__ __forceinline__ void run_o(const DecodeArgs& a, uint32_t l, uint32_t t, const Lds& s,
                                      uint32_t tok) {
   const LayerW Lw = a.layers[l];
@@ -929,7 +1058,7 @@ __device__ __forceinline__ void run_o(const DecodeArgs& a, uint32_t l, uint32_t 
            [=](uint32_t i) { return i < qd ? att + i : hin + (i - qd); });
   }
   stamp(a, l, P_O, t, 1);
-  const float acc = gemv_lds<32, 18>(a.Ro, s.w, x, qd, 1, s.pad);
+  const float acc = gemv_sel<TR, 32, 18>(a.Ro, s.w, x, qd, 1, s.pad);
   stamp(a, l, P_O, t, 3);
   if (threadIdx.x < nr) put_word(ac.h1 + r0 + threadIdx.x, hres[threadIdx.x] + acc, a.epoch);
   stamp(a, l, P_O, t, 2);
@@ -937,6 +1066,7 @@ __device__ __forceinline__ void run_o(const DecodeArgs& a, uint32_t l, uint32_t 
 
 // gate/up block (wave 0 gate rows, wave 1 up rows) after
 // post_attention_layernorm; hid = silu(gate) * up (main.rs:478-487).
+template <bool TR>
 __device__ __forceinline__ void run_gu(const DecodeArgs& a, uint32_t l, uint32_t t, const Lds& s) {
   const LayerW Lw = a.layers[l];
   const Act ac = act_of(a, l);
@@ -949,9 +1079,9 @@ __device__ __forceinline__ void run_gu(const DecodeArgs& a, uint32_t l, uint32_t
   stamp(a, l, P_GU, t, 0);
   gather_vec(x, ac.h1, a.H, a);
   stamp(a, l, P_GU, t, 1);
-  rmsnorm_lds(x, nw, a.eps, a.H, ln, ln, s_inv);
+  rmsnorm_lds<TR>(x, nw, a.eps, a.H, ln, ln, s_inv);
   stamp(a, l, P_GU, t, 3);
-  const float acc = gemv_lds<16>(a.Rg, s.w, ln, a.H, 2, s.pad);
+  const float acc = gemv_sel<TR, 16>(a.Rg, s.w, ln, a.H, 2, s.pad);
   const uint32_t wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
   if (wv == 0) gx[lane] = acc;
   __syncthreads();
@@ -966,6 +1096,7 @@ __device__ __forceinline__ void run_gu(const DecodeArgs& a, uint32_t l, uint32_t
 }
 
 // down block + residual h_next = h1 + down (main.rs:489-491).
+template <bool TR>
 __device__ __forceinline__ void run_d(const DecodeArgs& a, uint32_t l, uint32_t t, const Lds& s) {
   const LayerW Lw = a.layers[l];
   const Act ac = act_of(a, l);
@@ -979,7 +1110,7 @@ __device__ __forceinline__ void run_d(const DecodeArgs& a, uint32_t l, uint32_t 
   gather(x, I + nr, a.epoch, a.err,
          [=](uint32_t i) { return i < I ? hid + i : h1 + (i - I); });
   stamp(a, l, P_D, t, 1);
-  const float acc = gemv_lds<32, 24, 12>(a.Rd, s.w, x, I, 1, s.pad);
+  const float acc = gemv_sel<TR, 32, 24, 12>(a.Rd, s.w, x, I, 1, s.pad);
   stamp(a, l, P_D, t, 3);
   if (threadIdx.x < nr) put_word(ac.hout + r0 + threadIdx.x, hres[threadIdx.x] + acc, a.epoch);
   stamp(a, l, P_D, t, 2);
@@ -989,6 +1120,7 @@ __device__ __forceinline__ void run_d(const DecodeArgs& a, uint32_t l, uint32_t 
 // copied before the wait), per-block argmax candidates; the workgroup whose
 // blocks complete the set reduces the candidates to the next token id
 // (strict >, first maximum wins, NaN at index 0 wins; main.rs:1161-1169).
+template <bool TR>
 __device__ __forceinline__ void run_lm(const DecodeArgs& a, const Lds& s) {
   const uint32_t L = a.L, wg = blockIdx.x;
   const uint32_t wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -1001,7 +1133,7 @@ __device__ __forceinline__ void run_lm(const DecodeArgs& a, const Lds& s) {
   stamp(a, L - 1, P_LM, wg, 0);
   gather_vec(x, act_of(a, L - 1).hout, a.H, a);
   stamp(a, L - 1, P_LM, wg, 1);
-  rmsnorm_lds(x, nw, a.eps, a.H, hn, hn, misc);
+  rmsnorm_lds<TR>(x, nw, a.eps, a.H, hn, hn, misc);
   AS_GLB float* logits = GW(a.logits);
   uint32_t done = 0;
   for (uint32_t b = wg; b < a.nl; b += a.nwg) {
@@ -1009,7 +1141,7 @@ __device__ __forceinline__ void run_lm(const DecodeArgs& a, const Lds& s) {
       prefetch_rows(a.lm, a.Rl, a.H, b, s.w);
       __syncthreads();
     }
-    const float acc = gemv_lds<32>(a.Rl, s.w, hn, a.H, 1, s.pad);
+    const float acc = gemv_sel<TR, 32>(a.Rl, s.w, hn, a.H, 1, s.pad);
     if (wv == 0) {
       const uint32_t row = b * a.Rl + lane;
       Cand c = {0.0f, UINT32_MAX};
@@ -1055,6 +1187,7 @@ __device__ __forceinline__ void run_lm(const DecodeArgs& a, const Lds& s) {
 
 // One 256-thread workgroup per CU (the LDS footprint allows no second one),
 // so one wave per SIMD: the compiler may use the whole register file.
+template <bool TR>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void k_decode(DecodeArgs a) {
   // 16-byte element type: the dynamic region follows the static LDS variables
@@ -1092,17 +1225,17 @@ void k_decode(DecodeArgs a) {
     for (uint32_t i = 0; i < ntask; ++i) {
       const uint32_t ph = task[i] >> 12, t = task[i] & 0xFFFu;
       switch (ph) {
-        case P_QKV: run_qkv(a, l, t, s, tok); break;
-        case P_ATT: run_att(a, l, t, s, wbytes / 4); break;
-        case P_O: run_o(a, l, t, s, tok); break;
-        case P_GU: run_gu(a, l, t, s); break;
-        case P_D: run_d(a, l, t, s); break;
+        case P_QKV: run_qkv<TR>(a, l, t, s, tok); break;
+        case P_ATT: run_att<TR>(a, l, t, s, wbytes / 4); break;
+        case P_O: run_o<TR>(a, l, t, s, tok); break;
+        case P_GU: run_gu<TR>(a, l, t, s); break;
+        case P_D: run_d<TR>(a, l, t, s); break;
         default: break;
       }
       __syncthreads();
     }
   }
-  if (a.want_logits) run_lm(a, s);
+  if (a.want_logits) run_lm<TR>(a, s);
 }
 
 // ---------------------------------------------------------------------------
@@ -1187,17 +1320,22 @@ size_t decode_lds_bytes(const DecodeArgs& a) {
   return decode_wregion_bytes(a) + decode_vec_floats(a) * 4 + 64 * 16 + 256;
 }
 
-hipError_t launch_decode(const DecodeArgs& a, hipStream_t s) {
+template <bool TR>
+hipError_t launch_decode_t(const DecodeArgs& a, hipStream_t s) {
   const size_t lds = decode_lds_bytes(a);
   static size_t configured = 0;
   if (lds > configured) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_decode),
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_decode<TR>),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
     configured = lds;
   }
-  hipLaunchKernelGGL(k_decode, dim3(a.nwg), dim3(kThreads), lds, s, a);
+  hipLaunchKernelGGL(k_decode<TR>, dim3(a.nwg), dim3(kThreads), lds, s, a);
   return hipGetLastError();
+}
+
+hipError_t launch_decode(const DecodeArgs& a, hipStream_t s) {
+  return a.tree ? launch_decode_t<true>(a, s) : launch_decode_t<false>(a, s);
 }
 
 }  // namespace cis2

@@ -53,6 +53,7 @@ struct DecodeArgs {
   uint32_t nwg;
   float eps, scale;
   uint32_t pos, epoch, lm_epoch, want_logits;
+  uint32_t tree;  // 1: v0.4-candidate tree reduction order, 0: sequential
 };
 
 // Floats (4-byte units) of one layer's tagged activation storage.

@@ -259,4 +259,16 @@ __device__ __forceinline__ float silu_pinned(float x) {
   return x / d;
 }
 
+// v0.4-candidate tree order for one 32-leaf block (code/cis2-fp/src/math.rs:
+// 60-125): five in-place rounds leaf[i] = leaf[2i] + leaf[2i+1]; leaves past
+// the data are +0.  The caller folds the block results left to right from 0.
+__device__ __forceinline__ float tree32(float (&l)[32]) {
+#pragma unroll
+  for (int w = 32; w > 1; w >>= 1) {
+#pragma unroll
+    for (int i = 0; i < w / 2; ++i) l[i] = l[2 * i] + l[2 * i + 1];
+  }
+  return l[0];
+}
+
 }  // namespace cis2

@@ -63,6 +63,7 @@ uint32_t num_key(const JValue& cfg, const char* k) {
 int main(int argc, char** argv) {
   std::string weights_dir = "weights", ids_path, trace_path;
   int gen_toks = 16, prompt_idx = 0;
+  uint32_t reduction = 0;  // --reduction sequential|tree (code/cis2-fp/src/main.rs:775-782)
   for (int i = 1; i < argc; ++i) {
     std::string a = argv[i];
     if (a == "--weights-dir" && i + 1 < argc) weights_dir = argv[++i];
@@ -70,6 +71,16 @@ int main(int argc, char** argv) {
     else if (a == "--gen-toks" && i + 1 < argc) gen_toks = atoi(argv[++i]);
     else if (a == "--trace" && i + 1 < argc) trace_path = argv[++i];
     else if (a == "--prompt-idx" && i + 1 < argc) prompt_idx = atoi(argv[++i]);
+    else if (a == "--reduction" && i + 1 < argc) {
+      std::string r = argv[++i];
+      if (r == "sequential") reduction = 0;
+      else if (r == "tree") reduction = 1;
+      else {
+        fprintf(stderr, "FATAL: --reduction: expected 'sequential' or 'tree', got %s\n",
+                r.c_str());
+        return 2;
+      }
+    }
     else { fprintf(stderr, "FATAL: unknown CLI argument: %s\n", a.c_str()); return 2; }
   }
   if (ids_path.empty()) fatal("--ids FILE is required");
@@ -106,7 +117,7 @@ int main(int argc, char** argv) {
   std::vector<uint32_t> prompt = read_ids(ids_path);
   cfg.max_pos = (uint32_t)(prompt.size() + gen_toks);
   cfg.max_seqs = 1;
-  cfg.reduction_mode = 0;
+  cfg.reduction_mode = reduction;
 
   cis2_ctx* ctx = nullptr;
   int rc = cis2_ctx_create(&cfg, &ctx);
@@ -184,10 +195,11 @@ int main(int argc, char** argv) {
   printf("prompt_idx=%d run1_tokens=%s\n", prompt_idx, ids_list(ids).c_str());
   printf("prompt_idx=%d run1_witness_digest=%s\n", prompt_idx, hex(wit, 32).c_str());
   printf("prompt_idx=%d run1_argmax_digest=%s\n", prompt_idx, hex(adig, 32).c_str());
-  printf("prompt_idx=%d reduction_mode=sequential\n", prompt_idx);
+  const char* mode = reduction ? "tree" : "sequential";
+  printf("prompt_idx=%d reduction_mode=%s\n", prompt_idx, mode);
   printf("CIS2_REF digest=%s prompt_idx=%d prompt_toks=%zu gen_toks=%d dtype=fp32 "
-         "reduction_mode=sequential\n",
-         hex(wit, 32).c_str(), prompt_idx, prompt.size(), gen_toks);
+         "reduction_mode=%s\n",
+         hex(wit, 32).c_str(), prompt_idx, prompt.size(), gen_toks, mode);
   cis2_ctx_destroy(ctx);
   return 0;
 }

@@ -25,7 +25,37 @@ struct GemvArgs {
   GemvSeg seg[4];
   uint32_t blk_start[5];
   int nseg;
+  uint32_t tree;
 };
+
+// Tree order (code/cis2-fp/src/math.rs:60-125): per 32-wide k block the
+// products are reduced by tree32, the block results folded from 0.
+__device__ __forceinline__ float gemv_tree(const float* __restrict__ Wb,
+                                           const float* __restrict__ x, uint32_t K, uint32_t R,
+                                           uint32_t lane) {
+  const float4* __restrict__ wp =
+      reinterpret_cast<const float4*>(Wb) + (lane < R ? lane : R - 1);
+  const float4* __restrict__ xp = reinterpret_cast<const float4*>(x);
+  const uint32_t KG = K >> 2;
+  float acc = 0.0f;
+  for (uint32_t g0 = 0; g0 < KG; g0 += 8) {
+    float l[32];
+#pragma unroll
+    for (uint32_t j = 0; j < 8; ++j) {
+      float4 w = make_float4(0.0f, 0.0f, 0.0f, 0.0f), xv = w;
+      if (g0 + j < KG) {
+        w = wp[(size_t)(g0 + j) * R];
+        xv = xp[g0 + j];
+      }
+      l[4 * j] = w.x * xv.x;
+      l[4 * j + 1] = w.y * xv.y;
+      l[4 * j + 2] = w.z * xv.z;
+      l[4 * j + 3] = w.w * xv.w;
+    }
+    acc = acc + tree32(l);
+  }
+  return acc;
+}
 
 __device__ __forceinline__ float gemv_chain(const float* __restrict__ Wb,
                                             const float* __restrict__ x, uint32_t K,
@@ -56,7 +86,7 @@ __global__ __launch_bounds__(64) void k_gemv(GemvArgs a) {
   b -= a.blk_start[s];
   const uint32_t lane = threadIdx.x;
   const float* Wb = g.W + (size_t)b * g.R * g.K;
-  float acc = gemv_chain(Wb, g.x, g.K, g.R, lane);
+  float acc = a.tree ? gemv_tree(Wb, g.x, g.K, g.R, lane) : gemv_chain(Wb, g.x, g.K, g.R, lane);
   uint32_t row = b * g.R + lane;
   if (lane < g.R && row < g.M) {
     float r = acc;
@@ -65,9 +95,10 @@ __global__ __launch_bounds__(64) void k_gemv(GemvArgs a) {
   }
 }
 
-hipError_t launch_gemv(const GemvSeg* segs, int nseg, hipStream_t s) {
+hipError_t launch_gemv(const GemvSeg* segs, int nseg, hipStream_t s, bool tree) {
   if (nseg < 1 || nseg > 4) return hipErrorInvalidValue;
   GemvArgs a;
+  a.tree = tree ? 1u : 0u;
   uint32_t total = 0;
   for (int i = 0; i < nseg; ++i) {
     if (segs[i].K % 4 != 0 || segs[i].M == 0 || segs[i].R == 0 || segs[i].R > 64)
@@ -88,11 +119,12 @@ __global__ __launch_bounds__(128) void k_gate_up_silu(const float* __restrict__ 
                                                       const float* __restrict__ Wu,
                                                       const float* __restrict__ x,
                                                       float* gate, float* up, float* hid,
-                                                      uint32_t I, uint32_t H, uint32_t R) {
+                                                      uint32_t I, uint32_t H, uint32_t R,
+                                                      uint32_t tree) {
   __shared__ float sg[64];
   const uint32_t b = blockIdx.x, w = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const float* Wb = (w ? Wu : Wg) + (size_t)b * R * H;
-  float acc = gemv_chain(Wb, x, H, R, lane);
+  float acc = tree ? gemv_tree(Wb, x, H, R, lane) : gemv_chain(Wb, x, H, R, lane);
   const uint32_t row = b * R + lane;
   if (w == 0) {
     sg[lane] = acc;
@@ -108,10 +140,10 @@ __global__ __launch_bounds__(128) void k_gate_up_silu(const float* __restrict__ 
 
 hipError_t launch_gate_up_silu(const float* Wg, const float* Wu, const float* x,
                                float* gate, float* up, float* hid, uint32_t I,
-                               uint32_t H, uint32_t R, hipStream_t s) {
+                               uint32_t H, uint32_t R, hipStream_t s, bool tree) {
   if (H % 4 != 0 || R == 0 || R > 64) return hipErrorInvalidValue;
   hipLaunchKernelGGL(k_gate_up_silu, dim3((I + R - 1) / R), dim3(128), 0, s, Wg, Wu, x,
-                     gate, up, hid, I, H, R);
+                     gate, up, hid, I, H, R, tree ? 1u : 0u);
   return hipGetLastError();
 }
 
@@ -179,7 +211,8 @@ hipError_t launch_embed(const float* E, const uint32_t* tok, float* h, uint32_t 
 // value; the other work is lane-parallel.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void k_rmsnorm(const float* x, const float* __restrict__ w,
-                                                 float eps, uint32_t n, float* out) {
+                                                 float eps, uint32_t n, float* out,
+                                                 uint32_t tree) {
   extern __shared__ float sq[];
   __shared__ float s_inv;
   const float* xv = x + (size_t)blockIdx.x * n;
@@ -189,9 +222,25 @@ __global__ __launch_bounds__(256) void k_rmsnorm(const float* x, const float* __
     sq[i] = v * v;
   }
   __syncthreads();
+  const uint32_t nb = (n + 31) / 32;
+  if (tree) {
+    // block partials by tree32 (code/cis2-fp/src/math.rs:60-125), stored
+    // after the squares; thread t owns block t
+    for (uint32_t t = threadIdx.x; t < nb; t += blockDim.x) {
+      float l[32];
+#pragma unroll
+      for (uint32_t i = 0; i < 32; ++i) l[i] = 32 * t + i < n ? sq[32 * t + i] : 0.0f;
+      sq[n + t] = tree32(l);
+    }
+    __syncthreads();
+  }
   if (threadIdx.x < 64) {
     float acc = 0.0f;
-    for (uint32_t i = 0; i < n; ++i) acc = acc + sq[i];
+    if (tree) {
+      for (uint32_t t = 0; t < nb; ++t) acc = acc + sq[n + t];
+    } else {
+      for (uint32_t i = 0; i < n; ++i) acc = acc + sq[i];
+    }
     float mean = acc / (float)n;
     float arg = mean + eps;
     float inv = rsqrt_cr(arg);
@@ -206,10 +255,11 @@ __global__ __launch_bounds__(256) void k_rmsnorm(const float* x, const float* __
 }
 
 hipError_t launch_rmsnorm(const float* x, const float* w, float eps, uint32_t n,
-                          uint32_t nvec, float* out, hipStream_t s) {
-  if (n == 0 || n > 8192) return hipErrorInvalidValue;  // LDS: n floats + scalars
-  hipLaunchKernelGGL(k_rmsnorm, dim3(nvec), dim3(256), n * sizeof(float), s, x, w, eps, n,
-                     out);
+                          uint32_t nvec, float* out, hipStream_t s, bool tree) {
+  if (n == 0 || n > 8192) return hipErrorInvalidValue;  // LDS: squares, partials, scalars
+  const size_t shmem = (n + (n + 31) / 32) * sizeof(float);
+  hipLaunchKernelGGL(k_rmsnorm, dim3(nvec), dim3(256), shmem, s, x, w, eps, n, out,
+                     tree ? 1u : 0u);
   return hipGetLastError();
 }
 
@@ -306,7 +356,7 @@ __global__ __launch_bounds__(256) void k_attention(const float* __restrict__ q,
                                                    uint32_t nh, uint32_t nkv, uint32_t hd,
                                                    uint32_t max_pos, float scale,
                                                    float* att_out, float* scores_out,
-                                                   float* probs_out) {
+                                                   float* probs_out, uint32_t tree) {
   extern __shared__ float sh[];
   __shared__ VI red[4];
   __shared__ float s_den;
@@ -318,9 +368,19 @@ __global__ __launch_bounds__(256) void k_attention(const float* __restrict__ q,
   const float* kb = kc + (size_t)kvh * hd * max_pos;
   for (uint32_t j = threadIdx.x; j < len; j += blockDim.x) {
     float acc = 0.0f;
-    for (uint32_t d = 0; d < hd; ++d) {
-      float p = sq[d] * kb[(size_t)d * max_pos + j];
-      acc = acc + p;
+    if (tree) {  // dot_tree (code/cis2-fp/src/math.rs:60-125)
+      for (uint32_t d0 = 0; d0 < hd; d0 += 32) {
+        float l[32];
+#pragma unroll
+        for (uint32_t i = 0; i < 32; ++i)
+          l[i] = d0 + i < hd ? sq[d0 + i] * kb[(size_t)(d0 + i) * max_pos + j] : 0.0f;
+        acc = acc + tree32(l);
+      }
+    } else {
+      for (uint32_t d = 0; d < hd; ++d) {
+        float p = sq[d] * kb[(size_t)d * max_pos + j];
+        acc = acc + p;
+      }
     }
     float sc = acc * scale;
     ss[j] = sc;
@@ -339,9 +399,24 @@ __global__ __launch_bounds__(256) void k_attention(const float* __restrict__ q,
     ss[j] = exp_pinned(dlt);
   }
   __syncthreads();
+  const uint32_t nb = (len + 31) / 32;
+  float* part = ss + len;  // tree: block partials of the denominator
+  if (tree) {  // softmax_tree's sum (code/cis2-fp/src/math.rs:448-465)
+    for (uint32_t t = threadIdx.x; t < nb; t += blockDim.x) {
+      float l[32];
+#pragma unroll
+      for (uint32_t i = 0; i < 32; ++i) l[i] = 32 * t + i < len ? ss[32 * t + i] : 0.0f;
+      part[t] = tree32(l);
+    }
+    __syncthreads();
+  }
   if (threadIdx.x < 64) {
     float acc = 0.0f;
-    for (uint32_t j = 0; j < len; ++j) acc = acc + ss[j];
+    if (tree) {
+      for (uint32_t t = 0; t < nb; ++t) acc = acc + part[t];
+    } else {
+      for (uint32_t j = 0; j < len; ++j) acc = acc + ss[j];
+    }
     if (threadIdx.x == 0) s_den = acc;
   }
   __syncthreads();
@@ -366,12 +441,13 @@ __global__ __launch_bounds__(256) void k_attention(const float* __restrict__ q,
 hipError_t launch_attention(const float* q, const float* kc, const float* vc,
                             uint32_t pos, uint32_t nh, uint32_t nkv, uint32_t hd,
                             uint32_t max_pos, float scale, float* att_out,
-                            float* scores_out, float* probs_out, hipStream_t s) {
+                            float* scores_out, float* probs_out, hipStream_t s, bool tree) {
   if (pos >= max_pos || nkv == 0 || nh % nkv) return hipErrorInvalidValue;
-  size_t shmem = (size_t)(hd + pos + 1) * sizeof(float);
+  // q, scores, and the denominator's block partials
+  size_t shmem = (size_t)(hd + pos + 1 + (pos + 32) / 32) * sizeof(float);
   if (shmem > 60 * 1024) return hipErrorInvalidValue;  // leaves room for static LDS
   hipLaunchKernelGGL(k_attention, dim3(nh), dim3(256), shmem, s, q, kc, vc, pos, nh, nkv, hd,
-                     max_pos, scale, att_out, scores_out, probs_out);
+                     max_pos, scale, att_out, scores_out, probs_out, tree ? 1u : 0u);
   return hipGetLastError();
 }
 

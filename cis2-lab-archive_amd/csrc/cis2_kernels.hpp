@@ -27,12 +27,15 @@ struct GemvSeg {
   uint32_t R;          // rows per block of W's layout (1..64)
 };
 
-// Strict left-to-right per-row GEMV over up to 4 segments in one launch.
-hipError_t launch_gemv(const GemvSeg* segs, int nseg, hipStream_t s);
+// Per-row GEMV over up to 4 segments in one launch: strict left-to-right
+// products, or (tree) 32-product blocks by tree32 folded left to right.
+// The RMSNorm sum and the attention scores / softmax denominator take the
+// same `tree` switch; the V mix is sequential in both orders.
+hipError_t launch_gemv(const GemvSeg* segs, int nseg, hipStream_t s, bool tree = false);
 // Gate/up pair fused with hid = silu(gate) * up.
 hipError_t launch_gate_up_silu(const float* Wg, const float* Wu, const float* x,
                                float* gate, float* up, float* hid, uint32_t I,
-                               uint32_t H, uint32_t R, hipStream_t s);
+                               uint32_t H, uint32_t R, hipStream_t s, bool tree = false);
 // Relayout a row-major [M,K] f32 matrix (device) into the blocked layout.
 hipError_t launch_relayout(const float* src, float* dst, uint32_t M, uint32_t K, uint32_t R,
                            hipStream_t s);
@@ -45,7 +48,7 @@ hipError_t launch_embed(const float* E, const uint32_t* tok, float* h, uint32_t 
 // out = RMSNorm(x) * w over n elements; `nvec` independent vectors of
 // length n at stride n (the per-head QK-norm uses nvec = heads).
 hipError_t launch_rmsnorm(const float* x, const float* w, float eps, uint32_t n,
-                          uint32_t nvec, float* out, hipStream_t s);
+                          uint32_t nvec, float* out, hipStream_t s, bool tree = false);
 // RoPE on q (nh heads) and k (nkv heads) in place from the per-position
 // table, then store rotated k and raw v into the caches at pos.
 // Caches: K and V both as [kvh][hd][max_pos] (one row per head dimension).
@@ -57,7 +60,8 @@ hipError_t launch_rope_store(float* q, float* k, const float* v, const float* ro
 hipError_t launch_attention(const float* q, const float* kc, const float* vc,
                             uint32_t pos, uint32_t nh, uint32_t nkv, uint32_t hd,
                             uint32_t max_pos, float scale, float* att_out,
-                            float* scores_out, float* probs_out, hipStream_t s);
+                            float* scores_out, float* probs_out, hipStream_t s,
+                            bool tree = false);
 // Greedy argmax (strict >, first maximum wins) -> *tok_out.
 hipError_t launch_argmax(const float* logits, uint32_t n, uint32_t* tok_out,
                          hipStream_t s);

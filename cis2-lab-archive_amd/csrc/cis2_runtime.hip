@@ -220,27 +220,28 @@ int forward_one(cis2_ctx* c, uint32_t seq, uint32_t pos, const uint32_t* d_tokp,
   const uint32_t H = f.hidden, I = f.inter, hd = f.head_dim, QD = c->qd, KV = c->kvd;
   hipStream_t s = c->st;
   const bool tr = c->trace != nullptr;
+  const bool tree = c->cfg.reduction_mode == 1;
   LAUNCH(launch_embed(c->embed, d_tokp, c->h, H, f.vocab, c->d_err, s), "embed");
   EMIT(pos, -1, "embedding", c->h, H);
   for (uint32_t l = 0; l < f.n_layers; ++l) {
     const Layer& Ly = c->L[l];
     float* kc = kcache(c, seq, l);
     float* vc = vcache(c, seq, l);
-    LAUNCH(launch_rmsnorm(c->h, Ly.ln1, f.eps, H, 1, c->x, s), "norm1");
+    LAUNCH(launch_rmsnorm(c->h, Ly.ln1, f.eps, H, 1, c->x, s, tree), "norm1");
     EMIT(pos, l, "norm1", c->x, H);
     GemvSeg qkv[3] = {{Ly.wq, c->x, Ly.bq, c->q, QD, H, 0, c->Rq},
                       {Ly.wk, c->x, Ly.bk, c->k, KV, H, 0, c->Rq},
                       {Ly.wv, c->x, Ly.bv, c->v, KV, H, 0, c->Rq}};
-    LAUNCH(launch_gemv(qkv, 3, s), "qkv");
+    LAUNCH(launch_gemv(qkv, 3, s, tree), "qkv");
     EMIT(pos, l, "q", c->q, QD);
     EMIT(pos, l, "k", c->k, KV);
     EMIT(pos, l, "v", c->v, KV);
     if (Ly.qn) {
-      LAUNCH(launch_rmsnorm(c->q, Ly.qn, f.eps, hd, f.n_heads, c->q, s), "q_norm");
+      LAUNCH(launch_rmsnorm(c->q, Ly.qn, f.eps, hd, f.n_heads, c->q, s, tree), "q_norm");
       EMIT(pos, l, "q_norm", c->q, QD);
     }
     if (Ly.kn) {
-      LAUNCH(launch_rmsnorm(c->k, Ly.kn, f.eps, hd, f.n_kv_heads, c->k, s), "k_norm");
+      LAUNCH(launch_rmsnorm(c->k, Ly.kn, f.eps, hd, f.n_kv_heads, c->k, s, tree), "k_norm");
       EMIT(pos, l, "k_norm", c->k, KV);
     }
     LAUNCH(launch_rope_store(c->q, c->k, c->v, c->rope_cs, pos, f.n_heads, f.n_kv_heads, hd,
@@ -250,7 +251,7 @@ int forward_one(cis2_ctx* c, uint32_t seq, uint32_t pos, const uint32_t* d_tokp,
     EMIT(pos, l, "rope_k", c->k, KV);
     LAUNCH(launch_attention(c->q, kc, vc, pos, f.n_heads, f.n_kv_heads, hd, f.max_pos,
                             c->scale, c->att, tr ? c->scores : nullptr,
-                            tr ? c->probs : nullptr, s),
+                            tr ? c->probs : nullptr, s, tree),
            "attention");
     EMIT(pos, l, "scores", c->scores, (size_t)f.n_heads * (pos + 1));
     EMIT(pos, l, "softmax", c->probs, (size_t)f.n_heads * (pos + 1));
@@ -258,33 +259,34 @@ int forward_one(cis2_ctx* c, uint32_t seq, uint32_t pos, const uint32_t* d_tokp,
     GemvSeg os[1] = {{Ly.wo, c->att, c->h, c->h2, H, QD, 1, c->Ro}};
     if (tr) {  // the trace needs o_proj on its own
       GemvSeg ot[1] = {{Ly.wo, c->att, nullptr, c->o, H, QD, 0, c->Ro}};
-      LAUNCH(launch_gemv(ot, 1, s), "o_proj");
+      LAUNCH(launch_gemv(ot, 1, s, tree), "o_proj");
       EMIT(pos, l, "o_proj", c->o, H);
     }
-    LAUNCH(launch_gemv(os, 1, s), "o_proj+resid");
+    LAUNCH(launch_gemv(os, 1, s, tree), "o_proj+resid");
     std::swap(c->h, c->h2);
     EMIT(pos, l, "resid1", c->h, H);
-    LAUNCH(launch_rmsnorm(c->h, Ly.ln2, f.eps, H, 1, c->x, s), "norm2");
+    LAUNCH(launch_rmsnorm(c->h, Ly.ln2, f.eps, H, 1, c->x, s, tree), "norm2");
     EMIT(pos, l, "norm2", c->x, H);
-    LAUNCH(launch_gate_up_silu(Ly.wg, Ly.wu, c->x, c->g, c->u, c->hid, I, H, c->Rg, s), "gate_up");
+    LAUNCH(launch_gate_up_silu(Ly.wg, Ly.wu, c->x, c->g, c->u, c->hid, I, H, c->Rg, s, tree),
+           "gate_up");
     EMIT(pos, l, "gate", c->g, I);
     EMIT(pos, l, "up", c->u, I);
     EMIT(pos, l, "silu_mul", c->hid, I);
     if (tr) {
       GemvSeg dt[1] = {{Ly.wd, c->hid, nullptr, c->dn, H, I, 0, c->Rd}};
-      LAUNCH(launch_gemv(dt, 1, s), "down");
+      LAUNCH(launch_gemv(dt, 1, s, tree), "down");
       EMIT(pos, l, "down", c->dn, H);
     }
     GemvSeg ds[1] = {{Ly.wd, c->hid, c->h, c->h2, H, I, 1, c->Rd}};
-    LAUNCH(launch_gemv(ds, 1, s), "down+resid");
+    LAUNCH(launch_gemv(ds, 1, s, tree), "down+resid");
     std::swap(c->h, c->h2);
     EMIT(pos, l, "resid2", c->h, H);
   }
   if (want_logits || tr) {
-    LAUNCH(launch_rmsnorm(c->h, c->final_norm, f.eps, H, 1, c->x, s), "final_norm");
+    LAUNCH(launch_rmsnorm(c->h, c->final_norm, f.eps, H, 1, c->x, s, tree), "final_norm");
     EMIT(pos, -1, "final_norm", c->x, H);
     GemvSeg lm[1] = {{c->lm_head, c->x, nullptr, c->logits, f.vocab, H, 0, c->Rl}};
-    LAUNCH(launch_gemv(lm, 1, s), "lm_head");
+    LAUNCH(launch_gemv(lm, 1, s, tree), "lm_head");
     EMIT(pos, -1, "logits", c->logits, f.vocab);
   }
   return CIS2_OK;
@@ -451,7 +453,7 @@ int cis2_ctx_create(const cis2_config* cfg, cis2_ctx** out) {
   if (f.hidden == 0 || f.inter == 0 || f.n_layers == 0 || f.n_heads == 0 || f.n_kv_heads == 0 ||
       f.head_dim == 0 || f.vocab == 0 || f.max_pos == 0 || f.max_seqs == 0)
     return CIS2_E_ARG;
-  if (f.reduction_mode != 0) return CIS2_E_UNSUPPORTED;
+  if (f.reduction_mode > 1) return CIS2_E_UNSUPPORTED;
   if (f.n_heads % f.n_kv_heads || f.head_dim % 2 || f.hidden % 4 || f.inter % 4 ||
       (f.n_heads * f.head_dim) % 4 || f.max_pos > 16384 || f.head_dim > 1024)
     return CIS2_E_UNSUPPORTED;
@@ -570,6 +572,7 @@ int cis2_ctx_create(const cis2_config* cfg, cis2_ctx** out) {
       a.cache_stride = (uint64_t)2 * c->kvd * f.max_pos;
       a.eps = f.eps;
       a.scale = c->scale;
+      a.tree = f.reduction_mode;
       a.rope_cs = c->rope_cs;
       a.logits = c->logits;
       a.err = c->d_err;

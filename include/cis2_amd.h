@@ -22,8 +22,10 @@
  *     synchronous ops do).
  *   - Numerics: IEEE binary32, round to nearest even, FTZ/DAZ, no FMA
  *     contraction, pinned exp/sin/cos/ln, strict left-to-right reductions
- *     (CIS-2 v0.3b, reduction_mode 0).  Results are bit-identical to the
- *     reference CPU path.
+ *     (CIS-2 v0.3b, reduction_mode 0) or the v0.4-candidate tree order
+ *     (reduction_mode 1: 32-leaf pairwise blocks folded left to right,
+ *     code/cis2-fp/src/math.rs:60-125).  Results are bit-identical to the
+ *     reference CPU path in either mode.
  */
 #ifndef CIS2_AMD_H
 #define CIS2_AMD_H
@@ -66,7 +68,7 @@ typedef struct {
   uint32_t tied;            /* tie_word_embeddings (1: LM head = embedding)  */
   uint32_t max_pos;         /* KV-cache capacity per sequence (<= 16384)     */
   uint32_t max_seqs;        /* independent sequences (KV caches), >= 1       */
-  uint32_t reduction_mode;  /* 0 sequential (v0.3b); 1 tree: CIS2_E_UNSUPPORTED */
+  uint32_t reduction_mode;  /* 0 sequential (v0.3b); 1 tree (v0.4 candidate)  */
   float eps;                /* (float)rms_norm_eps, narrowed once            */
   double rope_theta;        /* rope_theta as parsed (narrowed on use)        */
 } cis2_config;

@@ -16,7 +16,7 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 CLI = os.path.join(ROOT, "cis2-lab-archive_amd", "bin", "cis2_host")
 
 
-@pytest.mark.parametrize("name", ["tiny-llama", "tiny-qwen3", "tiny-untied"])
+@pytest.mark.parametrize("name", ["tiny-llama", "tiny-qwen3", "tiny-untied", "tiny-qwen3-tree"])
 def test_cli_matches_reference_lines_and_trace(name, model_fixtures, tmp_path):
     rec = model_fixtures[name]
     w = artifacts.Weights(artifacts.SPECS[rec["spec"]], rec["seed"])
@@ -24,14 +24,15 @@ def test_cli_matches_reference_lines_and_trace(name, model_fixtures, tmp_path):
     ids = tmp_path / "ids.txt"
     ids.write_text("\n".join(str(t) for t in rec["prompt"]) + "\n")
     trace = tmp_path / "trace.txt"
+    mode = rec.get("reduction", "sequential")
     r = subprocess.run([CLI, "--weights-dir", str(tmp_path), "--ids", str(ids), "--gen-toks",
-                        str(rec["gen_toks"]), "--trace", str(trace)],
+                        str(rec["gen_toks"]), "--trace", str(trace), "--reduction", mode],
                        capture_output=True, text=True, timeout=120)
     assert r.returncode == 0, r.stderr[-2000:]
     out = r.stdout
     assert re.search(r"^CIS2_REF digest=%s prompt_idx=0 prompt_toks=%d gen_toks=%d dtype=fp32 "
-                     r"reduction_mode=sequential$" % (rec["witness"], len(rec["prompt"]),
-                                                      rec["gen_toks"]), out, re.M)
+                     r"reduction_mode=%s$" % (rec["witness"], len(rec["prompt"]),
+                                              rec["gen_toks"], mode), out, re.M)
     assert "run1_argmax_digest=%s" % rec["argmax_digest"] in out
     assert "table_digest=%s" % rec["table_digest"] in out
     assert "inv_freq_table_digest=%s" % rec["inv_freq_table_digest"] in out

@@ -11,16 +11,20 @@ from cis2amd import Cis2Error, Cis2Model, artifacts
 pytestmark = pytest.mark.gpu
 
 TINY = ["tiny-llama", "tiny-untied", "tiny-qwen3", "tiny-qwen2"]
+# the same cases in the v0.4-candidate tree order (reference built with
+# -DCIS2_REDUCTION_TREE)
+TINY_TREE = [n + "-tree" for n in TINY]
 
 
 def build(rec, max_seqs=1, extra_pos=0):
     spec = artifacts.SPECS[rec["spec"]]
     w = artifacts.Weights(spec, rec["seed"])
+    mode = 1 if rec.get("reduction") == "tree" else 0
     return Cis2Model(spec, w, max_pos=len(rec["prompt"]) + rec["gen_toks"] + extra_pos,
-                     max_seqs=max_seqs), w
+                     max_seqs=max_seqs, reduction_mode=mode), w
 
 
-@pytest.mark.parametrize("name", TINY)
+@pytest.mark.parametrize("name", TINY + TINY_TREE)
 def test_tiny_decode_and_trace_match_reference(name, model_fixtures):
     rec = model_fixtures[name]
     m, _ = build(rec)
@@ -36,12 +40,13 @@ def test_tiny_decode_and_trace_match_reference(name, model_fixtures):
     assert fast["witness"] == rec["witness"]
 
 
-@pytest.mark.parametrize("name", TINY)
+@pytest.mark.parametrize("name", TINY + TINY_TREE)
 def test_tiny_step_digests_match_oracle(name, model_fixtures):
     rec = model_fixtures[name]
     m, w = build(rec)
     spec = artifacts.SPECS[rec["spec"]]
-    o = O.OracleModel(spec, w, max_pos=len(rec["prompt"]) + rec["gen_toks"])
+    o = O.OracleModel(spec, w, max_pos=len(rec["prompt"]) + rec["gen_toks"],
+                      reduction=m.reduction_mode)
     a = m.decode(rec["prompt"], rec["gen_toks"])
     b = o.decode(rec["prompt"], rec["gen_toks"])
     assert a["step_digests"] == b["step_digests"]
@@ -144,6 +149,10 @@ def test_error_paths(model_fixtures):
     with pytest.raises(Cis2Error) as e:
         Cis2Model(spec, w4, max_pos=8)
     assert e.value.code == -5
+    # reduction orders other than sequential (0) and tree (1)
+    with pytest.raises(Cis2Error) as e:
+        Cis2Model(spec, w, max_pos=8, reduction_mode=2)
+    assert e.value.code == -2
 
 
 def test_long_context_streamed_attention_matches_oracle():
@@ -161,3 +170,25 @@ def test_long_context_streamed_attention_matches_oracle():
     assert r["step_digests"] == ro["step_digests"]
     assert r["witness"] == ro["witness"]
     assert list(r["ids"]) == list(ro["ids"])
+
+
+def test_tree_mode_smollm2_135m_32_prompt_256_tokens(model_fixtures):
+    """The headline shape in the tree order: persistent kernel with tree
+    GEMVs, tree RMSNorm sums, tree scores and softmax denominators."""
+    rec = model_fixtures["smollm2-135m-tree"]
+    assert rec["reduction"] == "tree"
+    m, _ = build(rec)
+    r = m.decode(rec["prompt"], rec["gen_toks"], step_digests=False)
+    assert list(r["ids"]) == rec["tokens"]
+    assert r["argmax_digest"] == rec["argmax_digest"]
+    assert r["witness"] == rec["witness"]
+
+
+def test_tree_mode_long_context_streamed_attention(model_fixtures):
+    """Tree order on the streamed-attention path (1180 prompt positions at
+    head_dim 128): the reference's witness for the same run."""
+    rec = model_fixtures["tiny-wide-tree"]
+    m, _ = build(rec)
+    r = m.decode(rec["prompt"], rec["gen_toks"], step_digests=False)
+    assert list(r["ids"]) == rec["tokens"]
+    assert r["witness"] == rec["witness"]
