@@ -61,6 +61,9 @@ SIGNATURES = {
     "cis2_decode_end": (ctypes.c_int, [ctypes.c_void_p, c_u32p, c_u8p, c_u8p, c_u8p]),
     "cis2_decode_batch": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_uint32, c_u32p, c_u32p,
                                          ctypes.c_uint32, c_u8p, c_u32p, c_u8p, c_u8p]),
+    "cis2_verify_prefill": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_uint32, c_u32p, ctypes.c_uint32,
+                                           c_u32p, ctypes.c_uint32, c_u8p, c_u32p, c_u8p, c_u8p,
+                                           ctypes.POINTER(ctypes.c_int64), c_fp]),
     "cis2_trace_enable": (ctypes.c_int, [ctypes.c_void_p, TRACE_FN, ctypes.c_void_p]),
     "cis2_profile": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int]),
     "cis2_profile_read": (ctypes.c_int, [ctypes.c_void_p, c_u64p, ctypes.POINTER(ctypes.c_double),

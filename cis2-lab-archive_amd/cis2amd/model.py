@@ -151,6 +151,43 @@ class Cis2Model:
             off += int(n) + gen_toks
         return rows
 
+    def forward_rows(self, seq, pos, tok, want_logits=True):
+        """One row-batched pass over rows (seq[i], pos[i], tok[i]); returns
+        (logits float32[n][vocab] or None, argmax ids uint32[n])."""
+        seq = np.ascontiguousarray(seq, dtype=np.uint32)
+        pos = np.ascontiguousarray(pos, dtype=np.uint32)
+        tok = np.ascontiguousarray(tok, dtype=np.uint32)
+        n = seq.size
+        logits = np.empty((n, self.spec.vocab), dtype=np.float32) if want_logits else None
+        am = np.zeros(n, dtype=np.uint32)
+        check(_lib.lib().cis2_forward(self.ctx, n, _ptr(seq, _lib.c_u32p), _ptr(pos, _lib.c_u32p),
+                                      _ptr(tok, _lib.c_u32p),
+                                      _ptr(logits, _lib.c_fp) if want_logits else None,
+                                      _ptr(am, _lib.c_u32p)), self.ctx)
+        return logits, am
+
+    def verify_prefill(self, prompt, claimed, seq=0, want_logits=False):
+        """Teacher-forced check of a claimed continuation in one pass
+        (cis2_verify_prefill): ids argmax'd at each claimed position, the
+        witness / argmax digest they give, and the first mismatch (-1)."""
+        prompt = np.ascontiguousarray(prompt, dtype=np.uint32)
+        claimed = np.ascontiguousarray(claimed, dtype=np.uint32)
+        n_gen = claimed.size
+        gen = np.zeros(max(n_gen, 1), dtype=np.uint32)
+        wit, adg = _u8buf(32), _u8buf(32)
+        fm = ctypes.c_int64()
+        logits = np.empty((n_gen, self.spec.vocab), dtype=np.float32) if want_logits else None
+        hdr = (ctypes.c_uint8 * 96).from_buffer_copy(self.hdr)
+        check(_lib.lib().cis2_verify_prefill(
+            self.ctx, seq, _ptr(prompt, _lib.c_u32p), prompt.size, _ptr(claimed, _lib.c_u32p),
+            n_gen, hdr, _ptr(gen, _lib.c_u32p), wit, adg, ctypes.byref(fm),
+            _ptr(logits, _lib.c_fp) if want_logits else None), self.ctx)
+        out = {"generated": gen[:n_gen].copy(), "witness": bytes(wit).hex(),
+               "argmax_digest": bytes(adg).hex(), "first_mismatch": int(fm.value)}
+        if want_logits:
+            out["logits"] = logits
+        return out
+
     def trace(self, prompt, gen_toks):
         """Decode with per-op tracing; returns (decode result, trace lines in
         the reference's `pos=.. layer=.. op=.. sha256=..` format)."""

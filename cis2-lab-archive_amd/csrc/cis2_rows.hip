@@ -1,0 +1,386 @@
+// cis2_rows.hip — gfx950 kernels of the row-batched forward pass (several
+// sequences per step, or every position of one sequence).  Each output is
+// computed by one lane in the order the single-row kernels use
+// (code/cis2-fp/src/main.rs:355-529), so a row's results do not depend on
+// which other rows share the launch (batch invariance).
+#include "cis2_device_math.hpp"
+#include "cis2_rows.hpp"
+
+#include <algorithm>
+
+namespace cis2 {
+namespace {
+
+constexpr uint32_t kT = 256;
+// LDS per batched-GEMM workgroup: two workgroups fit one CU.
+constexpr uint32_t kBgemmLds = 78 * 1024;
+
+// ---------------------------------------------------------------------------
+// Batched GEMM.  A workgroup owns one R-row block of W and TB = 256 / R batch
+// rows: thread t computes output (row b0 + t / R, column blk * R + t % R).
+// K runs in chunks of KC: the block's [KC/4][R] float4 slice (contiguous in
+// the blocked layout) and the TB input rows' KC floats are staged in LDS,
+// then each thread continues its own chain acc = acc + W[m][k] * X[b][k],
+// k ascending (code/cis2-fp/src/main.rs:228-243, math.rs:40-48); in tree
+// mode the chain adds one tree32 block result per 32 k (math.rs:60-125).
+// ---------------------------------------------------------------------------
+struct BgemmArgs {
+  BgemmSeg s;
+  uint32_t n, TB, KC, tree;
+};
+
+__global__ __launch_bounds__(256) void k_bgemm(BgemmArgs a) {
+  extern __shared__ float4 sm[];
+  const BgemmSeg& g = a.s;
+  const uint32_t R = g.R, TB = a.TB, KC = a.KC, K = g.K;
+  const uint32_t blk = blockIdx.x, b0 = blockIdx.y * TB, t = threadIdx.x;
+  const uint32_t r = t % R, bb = t / R;
+  const bool live = t < R * TB;
+  const uint32_t qmax = KC / 4, xs4 = qmax + 1;  // padded X rows: no bank aliasing
+  float4* Ws = sm;
+  float4* Xs = sm + (size_t)qmax * R;
+  const float4* Wg = reinterpret_cast<const float4*>(g.W + (size_t)blk * R * K);
+  float acc = 0.0f;
+  for (uint32_t k0 = 0; k0 < K; k0 += KC) {
+    const uint32_t q4 = std::min(KC, K - k0) / 4, g0 = k0 / 4;
+    for (uint32_t i = t; i < q4 * R; i += kT) Ws[i] = Wg[(size_t)g0 * R + i];
+    for (uint32_t i = t; i < TB * q4; i += kT) {
+      const uint32_t bx = i / q4, q = i - bx * q4;
+      const uint32_t row = std::min(b0 + bx, a.n - 1);
+      Xs[bx * xs4 + q] = reinterpret_cast<const float4*>(g.X + (size_t)row * g.ldx)[g0 + q];
+    }
+    __syncthreads();
+    if (live) {
+      const float4* wp = Ws + r;
+      const float4* xp = Xs + bb * xs4;
+      if (a.tree) {
+        for (uint32_t q = 0; q < q4; q += 8) {
+          float l[32];
+#pragma unroll
+          for (uint32_t j = 0; j < 8; ++j) {
+            float4 w = make_float4(0.0f, 0.0f, 0.0f, 0.0f), x = w;
+            if (q + j < q4) {
+              w = wp[(size_t)(q + j) * R];
+              x = xp[q + j];
+            }
+            l[4 * j] = w.x * x.x;
+            l[4 * j + 1] = w.y * x.y;
+            l[4 * j + 2] = w.z * x.z;
+            l[4 * j + 3] = w.w * x.w;
+          }
+          acc = acc + tree32(l);
+        }
+      } else {
+#pragma unroll 4
+        for (uint32_t q = 0; q < q4; ++q) {
+          const float4 w = wp[(size_t)q * R], x = xp[q];
+          float p;
+          p = w.x * x.x; acc = acc + p;
+          p = w.y * x.y; acc = acc + p;
+          p = w.z * x.z; acc = acc + p;
+          p = w.w * x.w; acc = acc + p;
+        }
+      }
+    }
+    __syncthreads();
+  }
+  const uint32_t row = b0 + bb, m = blk * R + r;
+  if (live && row < a.n && m < g.M) {
+    float y = acc;
+    if (g.epi == kEpiBias) y = acc + g.add[m];
+    else if (g.epi == kEpiResidual) y = g.add[(size_t)row * g.ldadd + m] + acc;
+    g.Y[(size_t)row * g.ldy + m] = y;
+  }
+}
+
+// (value, index) pick of a strict-> scan from index 0 (first maximum wins;
+// a NaN wins only at index 0, handled by the caller).
+struct Pick {
+  float v;
+  uint32_t i;  // UINT32_MAX: none
+};
+__device__ __forceinline__ Pick pick2(Pick a, Pick b) {
+  if (b.i == UINT32_MAX) return a;
+  if (a.i == UINT32_MAX) return b;
+  if (b.v > a.v) return b;
+  if (a.v > b.v) return a;
+  return b.i < a.i ? b : a;
+}
+__device__ Pick pick_block(Pick x, Pick* scratch) {
+  for (int off = 32; off > 0; off >>= 1) {
+    Pick o;
+    o.v = __shfl_xor(x.v, off, 64);
+    o.i = __shfl_xor(x.i, off, 64);
+    x = pick2(x, o);
+  }
+  const uint32_t wv = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  if ((threadIdx.x & 63) == 0) scratch[wv] = x;
+  __syncthreads();
+  Pick r = scratch[0];
+  for (uint32_t i = 1; i < nw; ++i) r = pick2(r, scratch[i]);
+  __syncthreads();
+  return r;
+}
+
+__global__ void k_embed_rows(const float* __restrict__ E, RowsDesc rows, uint32_t H,
+                             uint32_t vocab, float* h, uint32_t* err) {
+  const uint32_t r = blockIdx.x;
+  uint32_t tok = rows.tok[r];
+  if (tok >= vocab) {
+    if (threadIdx.x == 0) atomicOr(err, 1u);
+    tok = 0;
+  }
+  const float* src = E + (size_t)tok * H;
+  for (uint32_t i = threadIdx.x; i < H; i += blockDim.x) h[(size_t)r * H + i] = src[i];
+}
+
+// RoPE rotate-half (main.rs:285-307): o1 = x1*c + (-x2)*s, o2 = x2*c + x1*s.
+__global__ __launch_bounds__(256) void k_rope_store_rows(float* q, float* k, const float* v,
+                                                         const float* __restrict__ cs,
+                                                         RowsDesc rows, uint32_t nh,
+                                                         uint32_t nkv, uint32_t hd,
+                                                         uint32_t max_pos, float* kc, float* vc,
+                                                         uint64_t seq_stride) {
+  const uint32_t r = blockIdx.x, pos = rows.pos[r], half = hd / 2;
+  const size_t sb = (size_t)rows.seq[r] * seq_stride;
+  float* qr = q + (size_t)r * nh * hd;
+  float* kr = k + (size_t)r * nkv * hd;
+  const float* vr = v + (size_t)r * nkv * hd;
+  const float* c = cs + (size_t)pos * half * 2;
+  const uint32_t total = (nh + nkv) * half;
+  for (uint32_t idx = threadIdx.x; idx < total; idx += blockDim.x) {
+    const uint32_t head = idx / half, i = idx - head * half;
+    float* hv = head < nh ? qr + (size_t)head * hd : kr + (size_t)(head - nh) * hd;
+    const float cv = c[2 * i], sv = c[2 * i + 1];
+    const float x1 = hv[i], x2 = hv[i + half];
+    float t1 = x1 * cv;
+    float nx2 = -x2;
+    float t2 = nx2 * sv;
+    float t3 = x2 * cv;
+    float t4 = x1 * sv;
+    const float o1 = t1 + t2, o2 = t3 + t4;
+    hv[i] = o1;
+    hv[i + half] = o2;
+    if (head >= nh) {
+      const size_t base = (size_t)(head - nh) * hd;
+      kc[sb + (base + i) * max_pos + pos] = o1;
+      kc[sb + (base + i + half) * max_pos + pos] = o2;
+    }
+  }
+  for (uint32_t idx = threadIdx.x; idx < nkv * hd; idx += blockDim.x)
+    vc[sb + (size_t)idx * max_pos + pos] = vr[idx];
+}
+
+// One workgroup per (query head, row): scores_j = dot(q, k_j) * scale
+// (dot_seq, or dot_tree), softmax (first-wins max, pinned exp, strict or
+// tree denominator, true divide), then out_d = fold_j (p_j * v_j[d]) in
+// position order (code/cis2-fp/src/main.rs:429-467; math.rs:425-465).
+__global__ __launch_bounds__(256) void k_attention_rows(const float* __restrict__ q,
+                                                        const float* __restrict__ kc,
+                                                        const float* __restrict__ vc,
+                                                        RowsDesc rows, uint32_t nh, uint32_t nkv,
+                                                        uint32_t hd, uint32_t max_pos,
+                                                        uint64_t seq_stride, float scale,
+                                                        float* out, uint32_t tree) {
+  extern __shared__ float sh[];
+  __shared__ Pick red[4];
+  __shared__ float s_den;
+  const uint32_t qh = blockIdx.x, r = blockIdx.y;
+  const uint32_t group = nh / nkv, kvh = qh / group, pos = rows.pos[r], len = pos + 1;
+  const size_t sb = (size_t)rows.seq[r] * seq_stride;
+  float* sq = sh;
+  float* ss = sh + hd;
+  float* part = ss + len;
+  const float* qv = q + (size_t)r * nh * hd + (size_t)qh * hd;
+  for (uint32_t d = threadIdx.x; d < hd; d += blockDim.x) sq[d] = qv[d];
+  __syncthreads();
+  const float* kb = kc + sb + (size_t)kvh * hd * max_pos;
+  for (uint32_t j = threadIdx.x; j < len; j += blockDim.x) {
+    float acc = 0.0f;
+    if (tree) {
+      for (uint32_t d0 = 0; d0 < hd; d0 += 32) {
+        float l[32];
+#pragma unroll
+        for (uint32_t i = 0; i < 32; ++i)
+          l[i] = d0 + i < hd ? sq[d0 + i] * kb[(size_t)(d0 + i) * max_pos + j] : 0.0f;
+        acc = acc + tree32(l);
+      }
+    } else {
+      for (uint32_t d = 0; d < hd; ++d) {
+        float p = sq[d] * kb[(size_t)d * max_pos + j];
+        acc = acc + p;
+      }
+    }
+    ss[j] = acc * scale;
+  }
+  __syncthreads();
+  Pick best = {0.0f, UINT32_MAX};
+  for (uint32_t j = threadIdx.x; j < len; j += blockDim.x) {
+    const float v = ss[j];
+    if (v == v) best = pick2(best, Pick{v, j});
+  }
+  best = pick_block(best, red);
+  const float mx = (ss[0] != ss[0]) ? ss[0] : best.v;
+  for (uint32_t j = threadIdx.x; j < len; j += blockDim.x) {
+    float dlt = ss[j] - mx;
+    ss[j] = exp_pinned(dlt);
+  }
+  __syncthreads();
+  const uint32_t nb = (len + 31) / 32;
+  if (tree) {
+    for (uint32_t t = threadIdx.x; t < nb; t += blockDim.x) {
+      float l[32];
+#pragma unroll
+      for (uint32_t i = 0; i < 32; ++i) l[i] = 32 * t + i < len ? ss[32 * t + i] : 0.0f;
+      part[t] = tree32(l);
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x < 64) {
+    float acc = 0.0f;
+    if (tree) {
+      for (uint32_t t = 0; t < nb; ++t) acc = acc + part[t];
+    } else {
+      for (uint32_t j = 0; j < len; ++j) acc = acc + ss[j];
+    }
+    if (threadIdx.x == 0) s_den = acc;
+  }
+  __syncthreads();
+  const float den = s_den;
+  for (uint32_t j = threadIdx.x; j < len; j += blockDim.x) {
+    float pj = ss[j] / den;
+    ss[j] = pj;
+  }
+  __syncthreads();
+  const float* vb = vc + sb + (size_t)kvh * hd * max_pos;
+  float* o = out + (size_t)r * nh * hd + (size_t)qh * hd;
+  for (uint32_t d = threadIdx.x; d < hd; d += blockDim.x) {
+    const float* vr = vb + (size_t)d * max_pos;
+    float acc = 0.0f;
+    for (uint32_t j = 0; j < len; ++j) {
+      float p = ss[j] * vr[j];
+      acc = acc + p;
+    }
+    o[d] = acc;
+  }
+}
+
+__global__ void k_silu_mul(const float* __restrict__ g, const float* __restrict__ u,
+                           float* hid, uint64_t n) {
+  uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+  for (; i < n; i += stride) {
+    float sg = silu_pinned(g[i]);
+    hid[i] = sg * u[i];
+  }
+}
+
+__global__ void k_gather_rows(const float* __restrict__ src, const uint32_t* __restrict__ idx,
+                              uint32_t width, float* dst) {
+  const uint32_t r = blockIdx.x;
+  const float* s = src + (size_t)idx[r] * width;
+  for (uint32_t i = threadIdx.x; i < width; i += blockDim.x) dst[(size_t)r * width + i] = s[i];
+}
+
+__global__ __launch_bounds__(1024) void k_argmax_rows(const float* __restrict__ v,
+                                                      uint32_t width, uint32_t* out) {
+  __shared__ Pick red[16];
+  const float* row = v + (size_t)blockIdx.x * width;
+  Pick best = {0.0f, UINT32_MAX};
+  for (uint32_t i = threadIdx.x; i < width; i += blockDim.x) {
+    const float x = row[i];
+    if (x == x) best = pick2(best, Pick{x, i});
+  }
+  best = pick_block(best, red);
+  if (threadIdx.x == 0) {
+    const float v0 = row[0];
+    out[blockIdx.x] = (v0 != v0 || best.i == UINT32_MAX) ? 0u : best.i;
+  }
+}
+
+}  // namespace
+
+hipError_t launch_bgemm(const BgemmSeg& s, uint32_t n, bool tree, hipStream_t st) {
+  if (n == 0) return hipSuccess;
+  if (s.K % 4 || s.ldx % 4 || s.R == 0 || s.R > kT || s.M == 0) return hipErrorInvalidValue;
+  BgemmArgs a;
+  a.s = s;
+  a.n = n;
+  a.TB = kT / s.R;
+  a.tree = tree ? 1u : 0u;
+  // largest chunk (a multiple of 32 k) whose W slice and X rows fit the budget
+  const uint32_t q_fit = (kBgemmLds / 16 - a.TB) / (s.R + a.TB);
+  uint32_t KC = (q_fit * 4) & ~31u;
+  if (KC == 0) return hipErrorInvalidValue;
+  const uint32_t K32 = (s.K + 31) & ~31u;
+  if (KC > K32) KC = K32;
+  a.KC = KC;
+  const size_t lds = ((size_t)(KC / 4) * s.R + (size_t)a.TB * (KC / 4 + 1)) * 16;
+  static bool configured = false;
+  if (!configured) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_bgemm),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)kBgemmLds);
+    if (e != hipSuccess) return e;
+    configured = true;
+  }
+  const dim3 grid((s.M + s.R - 1) / s.R, (n + a.TB - 1) / a.TB);
+  hipLaunchKernelGGL(k_bgemm, grid, dim3(kT), lds, st, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_embed_rows(const float* E, RowsDesc rows, uint32_t H, uint32_t vocab,
+                             float* h, uint32_t* err, hipStream_t st) {
+  if (rows.n == 0) return hipSuccess;
+  hipLaunchKernelGGL(k_embed_rows, dim3(rows.n), dim3(kT), 0, st, E, rows, H, vocab, h, err);
+  return hipGetLastError();
+}
+
+hipError_t launch_rope_store_rows(float* q, float* k, const float* v, const float* rope_cs,
+                                  RowsDesc rows, uint32_t nh, uint32_t nkv, uint32_t hd,
+                                  uint32_t max_pos, float* kc, float* vc, uint64_t seq_stride,
+                                  hipStream_t st) {
+  if (rows.n == 0) return hipSuccess;
+  if (hd % 2) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_rope_store_rows, dim3(rows.n), dim3(kT), 0, st, q, k, v, rope_cs, rows,
+                     nh, nkv, hd, max_pos, kc, vc, seq_stride);
+  return hipGetLastError();
+}
+
+hipError_t launch_attention_rows(const float* q, const float* kc, const float* vc,
+                                 RowsDesc rows, uint32_t max_len, uint32_t nh, uint32_t nkv,
+                                 uint32_t hd, uint32_t max_pos, uint64_t seq_stride, float scale,
+                                 float* out, bool tree, hipStream_t st) {
+  if (rows.n == 0) return hipSuccess;
+  if (nkv == 0 || nh % nkv || max_len == 0 || max_len > max_pos) return hipErrorInvalidValue;
+  // q, scores, and the denominator's block partials
+  const size_t shmem = ((size_t)hd + max_len + (max_len + 31) / 32) * sizeof(float);
+  if (shmem > 60 * 1024) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_attention_rows, dim3(nh, rows.n), dim3(kT), shmem, st, q, kc, vc, rows,
+                     nh, nkv, hd, max_pos, seq_stride, scale, out, tree ? 1u : 0u);
+  return hipGetLastError();
+}
+
+hipError_t launch_silu_mul(const float* g, const float* u, float* hid, uint64_t n,
+                           hipStream_t st) {
+  if (n == 0) return hipSuccess;
+  const uint64_t blocks = std::min<uint64_t>((n + kT - 1) / kT, 4096);
+  hipLaunchKernelGGL(k_silu_mul, dim3((uint32_t)blocks), dim3(kT), 0, st, g, u, hid, n);
+  return hipGetLastError();
+}
+
+hipError_t launch_gather_rows(const float* src, const uint32_t* idx, uint32_t n, uint32_t width,
+                              float* dst, hipStream_t st) {
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(k_gather_rows, dim3(n), dim3(kT), 0, st, src, idx, width, dst);
+  return hipGetLastError();
+}
+
+hipError_t launch_argmax_rows(const float* v, uint32_t n, uint32_t width, uint32_t* out,
+                              hipStream_t st) {
+  if (n == 0) return hipSuccess;
+  if (width == 0) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_argmax_rows, dim3(n), dim3(1024), 0, st, v, width, out);
+  return hipGetLastError();
+}
+
+}  // namespace cis2

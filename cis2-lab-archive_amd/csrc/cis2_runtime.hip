@@ -4,6 +4,7 @@
 #include "cis2_amd.h"
 #include "cis2_decode.hpp"
 #include "cis2_kernels.hpp"
+#include "cis2_rows.hpp"
 #include "cis2_sha256.hpp"
 
 #include <hip/hip_runtime.h>
@@ -11,8 +12,10 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <algorithm>
 #include <map>
 #include <string>
+#include <thread>
 #include <vector>
 
 using namespace cis2;
@@ -65,6 +68,17 @@ struct Session {
   std::vector<uint8_t> step_dig;
 };
 
+// Device buffers of the row-batched forward pass (grown on demand).
+struct RowsBuf {
+  uint32_t cap = 0, lcap = 0;  // rows / logit rows allocated
+  float *h = nullptr, *h2 = nullptr, *x = nullptr, *q = nullptr, *k = nullptr, *v = nullptr,
+        *att = nullptr, *g = nullptr, *u = nullptr, *hid = nullptr;  // [cap][width]
+  float *lx = nullptr, *logits = nullptr;                            // [lcap][H], [lcap][V]
+  uint32_t *seq = nullptr, *pos = nullptr, *tok = nullptr;           // [cap]
+  uint32_t *lrows = nullptr, *arg = nullptr;                         // [lcap]
+  std::vector<void*> mem, lmem;
+};
+
 }  // namespace
 
 struct cis2_ctx {
@@ -97,6 +111,7 @@ struct cis2_ctx {
   uint32_t Rq = 0, Ro = 0, Rg = 0, Rd = 0, Rl = 0;
   bool fast_ok = false;      // this configuration fits the persistent kernel
   bool force_ops = false;    // CIS2_PATH=ops: per-op kernels only
+  bool seq_prefill = false;  // CIS2_PREFILL=seq: prefill position by position
   uint32_t ncu = 0;
   LayerW* d_layers = nullptr;
   bool layers_dirty = true;
@@ -112,6 +127,7 @@ struct cis2_ctx {
   bool prof_on = false;
   std::vector<hipEvent_t> prof_ev;  // [2 * kProfMax], created on first use
   std::vector<uint32_t> prof_pos;
+  RowsBuf rows;
   std::vector<void*> allocs;
 };
 
@@ -378,6 +394,166 @@ int forward_fast(cis2_ctx* c, uint32_t seq, uint32_t pos, uint32_t* tokp, bool w
 // not fit the persistent kernel.
 bool use_fast(const cis2_ctx* c) { return c->fast_ok && !c->force_ops && !c->trace; }
 
+// ---- row-batched forward pass ----------------------------------------------
+
+template <class T>
+T* rows_alloc(std::vector<void*>& mem, size_t n) {
+  void* p = nullptr;
+  if (hipMalloc(&p, n * sizeof(T) + 16) != hipSuccess) return nullptr;
+  mem.push_back(p);
+  return static_cast<T*>(p);
+}
+
+// Row buffers for n rows and nl logit rows.
+int rows_reserve(cis2_ctx* c, uint32_t n, uint32_t nl) {
+  RowsBuf& b = c->rows;
+  const cis2_config& f = c->cfg;
+  if (n > b.cap) {
+    HIPCHK(c, hipStreamSynchronize(c->st), "rows sync");
+    for (void* p : b.mem) (void)hipFree(p);
+    b.mem.clear();
+    b.cap = 0;
+    const size_t H = f.hidden, I = f.inter, QD = c->qd, KV = c->kvd;
+    bool ok = (b.h = rows_alloc<float>(b.mem, n * H)) && (b.h2 = rows_alloc<float>(b.mem, n * H)) &&
+              (b.x = rows_alloc<float>(b.mem, n * H)) && (b.q = rows_alloc<float>(b.mem, n * QD)) &&
+              (b.k = rows_alloc<float>(b.mem, n * KV)) && (b.v = rows_alloc<float>(b.mem, n * KV)) &&
+              (b.att = rows_alloc<float>(b.mem, n * QD)) && (b.g = rows_alloc<float>(b.mem, n * I)) &&
+              (b.u = rows_alloc<float>(b.mem, n * I)) && (b.hid = rows_alloc<float>(b.mem, n * I)) &&
+              (b.seq = rows_alloc<uint32_t>(b.mem, n)) && (b.pos = rows_alloc<uint32_t>(b.mem, n)) &&
+              (b.tok = rows_alloc<uint32_t>(b.mem, n));
+    if (!ok) return fail(c, CIS2_E_OOM, "row buffers");
+    b.cap = n;
+  }
+  if (nl > b.lcap) {
+    HIPCHK(c, hipStreamSynchronize(c->st), "rows sync");
+    for (void* p : b.lmem) (void)hipFree(p);
+    b.lmem.clear();
+    b.lcap = 0;
+    bool ok = (b.lx = rows_alloc<float>(b.lmem, (size_t)nl * f.hidden)) &&
+              (b.logits = rows_alloc<float>(b.lmem, (size_t)nl * f.vocab)) &&
+              (b.lrows = rows_alloc<uint32_t>(b.lmem, nl)) &&
+              (b.arg = rows_alloc<uint32_t>(b.lmem, nl));
+    if (!ok) return fail(c, CIS2_E_OOM, "logit row buffers");
+    b.lcap = nl;
+  }
+  return CIS2_OK;
+}
+
+// The forward pass of n rows whose descriptors are already in c->rows
+// (seq, pos, and the token of row r at tok[r]), every op over all rows
+// before the next (code/cis2-fp/src/main.rs:355-529): K and V of every row
+// reach the caches before any row's attention, so rows of one sequence see
+// each other causally.  max_len = 1 + the largest position.  The final
+// norm, LM head and argmax run for the nl rows listed in rows.lrows:
+// logits[i] and arg[i] belong to row lrows[i].
+int forward_rows(cis2_ctx* c, uint32_t n, const uint32_t* d_tok, uint32_t max_len, uint32_t nl) {
+  const cis2_config& f = c->cfg;
+  RowsBuf& b = c->rows;
+  const uint32_t H = f.hidden, I = f.inter, hd = f.head_dim, QD = c->qd, KV = c->kvd;
+  const bool tree = f.reduction_mode == 1;
+  hipStream_t s = c->st;
+  const RowsDesc rd{b.seq, b.pos, d_tok, n};
+  const size_t per = (size_t)KV * f.max_pos;           // one layer's K (or V) of one sequence
+  const uint64_t seq_stride = (uint64_t)f.n_layers * 2 * per;
+  LAUNCH(launch_embed_rows(c->embed, rd, H, f.vocab, b.h, c->d_err, s), "rows embed");
+  for (uint32_t l = 0; l < f.n_layers; ++l) {
+    const Layer& Ly = c->L[l];
+    float* kc = c->kv + (size_t)l * 2 * per;
+    float* vc = kc + per;
+    LAUNCH(launch_rmsnorm(b.h, Ly.ln1, f.eps, H, n, b.x, s, tree), "rows norm1");
+    const BgemmSeg sq{Ly.wq, QD, H, c->Rq, b.x, H, b.q, QD, Ly.bq, 0, Ly.bq ? kEpiBias : kEpiNone};
+    const BgemmSeg sk{Ly.wk, KV, H, c->Rq, b.x, H, b.k, KV, Ly.bk, 0, Ly.bk ? kEpiBias : kEpiNone};
+    const BgemmSeg sv{Ly.wv, KV, H, c->Rq, b.x, H, b.v, KV, Ly.bv, 0, Ly.bv ? kEpiBias : kEpiNone};
+    LAUNCH(launch_bgemm(sq, n, tree, s), "rows q");
+    LAUNCH(launch_bgemm(sk, n, tree, s), "rows k");
+    LAUNCH(launch_bgemm(sv, n, tree, s), "rows v");
+    if (Ly.qn) LAUNCH(launch_rmsnorm(b.q, Ly.qn, f.eps, hd, n * f.n_heads, b.q, s, tree), "rows q_norm");
+    if (Ly.kn) LAUNCH(launch_rmsnorm(b.k, Ly.kn, f.eps, hd, n * f.n_kv_heads, b.k, s, tree), "rows k_norm");
+    LAUNCH(launch_rope_store_rows(b.q, b.k, b.v, c->rope_cs, rd, f.n_heads, f.n_kv_heads, hd,
+                                  f.max_pos, kc, vc, seq_stride, s),
+           "rows rope");
+    LAUNCH(launch_attention_rows(b.q, kc, vc, rd, max_len, f.n_heads, f.n_kv_heads, hd,
+                                 f.max_pos, seq_stride, c->scale, b.att, tree, s),
+           "rows attention");
+    const BgemmSeg so{Ly.wo, H, QD, c->Ro, b.att, QD, b.h2, H, b.h, H, kEpiResidual};
+    LAUNCH(launch_bgemm(so, n, tree, s), "rows o_proj");
+    std::swap(b.h, b.h2);
+    LAUNCH(launch_rmsnorm(b.h, Ly.ln2, f.eps, H, n, b.x, s, tree), "rows norm2");
+    const BgemmSeg sg{Ly.wg, I, H, c->Rg, b.x, H, b.g, I, nullptr, 0, kEpiNone};
+    const BgemmSeg su{Ly.wu, I, H, c->Rg, b.x, H, b.u, I, nullptr, 0, kEpiNone};
+    LAUNCH(launch_bgemm(sg, n, tree, s), "rows gate");
+    LAUNCH(launch_bgemm(su, n, tree, s), "rows up");
+    LAUNCH(launch_silu_mul(b.g, b.u, b.hid, (uint64_t)n * I, s), "rows silu");
+    const BgemmSeg sd{Ly.wd, H, I, c->Rd, b.hid, I, b.h2, H, b.h, H, kEpiResidual};
+    LAUNCH(launch_bgemm(sd, n, tree, s), "rows down");
+    std::swap(b.h, b.h2);
+  }
+  if (nl) {
+    LAUNCH(launch_gather_rows(b.h, b.lrows, nl, H, b.lx, s), "rows gather");
+    LAUNCH(launch_rmsnorm(b.lx, c->final_norm, f.eps, H, nl, b.lx, s, tree), "rows final_norm");
+    const BgemmSeg sl{c->lm_head, f.vocab, H, c->Rl, b.lx, H, b.logits, f.vocab, nullptr, 0,
+                      kEpiNone};
+    LAUNCH(launch_bgemm(sl, nl, tree, s), "rows lm_head");
+    LAUNCH(launch_argmax_rows(b.logits, nl, f.vocab, b.arg, s), "rows argmax");
+  }
+  return CIS2_OK;
+}
+
+// Uploads row descriptors (and the logit-row list) and runs forward_rows.
+int forward_rows_host(cis2_ctx* c, uint32_t n, const uint32_t* seq, const uint32_t* pos,
+                      const uint32_t* tok, uint32_t nl, const uint32_t* lrows) {
+  int r = rows_reserve(c, n, nl);
+  if (r) return r;
+  RowsBuf& b = c->rows;
+  uint32_t max_len = 0;
+  for (uint32_t i = 0; i < n; ++i) max_len = std::max(max_len, pos[i] + 1);
+  HIPCHK(c, hipMemcpyAsync(b.seq, seq, (size_t)n * 4, hipMemcpyHostToDevice, c->st), "rows seq");
+  HIPCHK(c, hipMemcpyAsync(b.pos, pos, (size_t)n * 4, hipMemcpyHostToDevice, c->st), "rows pos");
+  HIPCHK(c, hipMemcpyAsync(b.tok, tok, (size_t)n * 4, hipMemcpyHostToDevice, c->st), "rows tok");
+  if (nl)
+    HIPCHK(c, hipMemcpyAsync(b.lrows, lrows, (size_t)nl * 4, hipMemcpyHostToDevice, c->st),
+           "rows lrows");
+  return forward_rows(c, n, b.tok, max_len, nl);
+}
+
+// Checks a row set: sequence and position ranges, token ranges, and no two
+// rows at the same (sequence, position).
+int check_rows(cis2_ctx* c, uint32_t n, const uint32_t* seq, const uint32_t* pos,
+               const uint32_t* tok) {
+  std::vector<uint64_t> keys(n);
+  for (uint32_t i = 0; i < n; ++i) {
+    if (seq[i] >= c->cfg.max_seqs) return fail(c, CIS2_E_ARG, "sequence index out of range");
+    if (pos[i] >= c->cfg.max_pos) return fail(c, CIS2_E_RANGE, "position beyond max_pos");
+    if (tok && tok[i] >= c->cfg.vocab) return fail(c, CIS2_E_RANGE, "token id >= vocab");
+    keys[i] = (uint64_t)seq[i] << 32 | pos[i];
+  }
+  std::sort(keys.begin(), keys.end());
+  if (std::adjacent_find(keys.begin(), keys.end()) != keys.end())
+    return fail(c, CIS2_E_ARG, "two rows at the same sequence and position");
+  return CIS2_OK;
+}
+
+// Folds `rows` logit rows into their witness streams on up to 16 host
+// threads: for row i, the V logit bit patterns (u32 LE) then next id.
+void fold_rows(std::vector<Sha256>& w, const float* logits, const uint32_t* ids, uint32_t rows,
+               uint32_t V) {
+  const uint32_t nt = std::max(1u, std::min<uint32_t>(rows, std::min(16u, std::max(
+                                                           1u, std::thread::hardware_concurrency()))));
+  auto job = [&](uint32_t t) {
+    for (uint32_t i = t; i < rows; i += nt) {
+      w[i].update(logits + (size_t)i * V, (size_t)V * sizeof(float));
+      w[i].update_u32le(ids[i]);
+    }
+  };
+  if (nt == 1) {
+    job(0);
+    return;
+  }
+  std::vector<std::thread> th;
+  for (uint32_t t = 0; t < nt; ++t) th.emplace_back(job, t);
+  for (auto& x : th) x.join();
+}
+
 }  // namespace
 
 // Spreads the tasks of every phase over the workgroups: each task goes to a
@@ -435,6 +611,8 @@ void cis2_ctx_destroy(cis2_ctx* c) {
   if (!c) return;
   if (c->st) (void)hipStreamSynchronize(c->st);
   for (void* p : c->allocs) (void)hipFree(p);
+  for (void* p : c->rows.mem) (void)hipFree(p);
+  for (void* p : c->rows.lmem) (void)hipFree(p);
   if (c->tline_file) fclose(c->tline_file);
   for (hipEvent_t e : c->prof_ev)
     if (e) (void)hipEventDestroy(e);
@@ -551,6 +729,8 @@ int cis2_ctx_create(const cis2_config* cfg, cis2_ctx** out) {
     c->ncu = (uint32_t)ncu;
     const char* pe = getenv("CIS2_PATH");
     c->force_ops = pe && !strcmp(pe, "ops");
+    const char* pf = getenv("CIS2_PREFILL");
+    c->seq_prefill = pf && !strcmp(pf, "seq");
     DecodeArgs& a = c->dargs;
     auto plan = [&](uint32_t cap) {
       memset(&a, 0, sizeof a);
@@ -736,6 +916,23 @@ int cis2_forward(cis2_ctx* c, uint32_t n, const uint32_t* seq, const uint32_t* p
   if (!c || !seq || !pos || !tok) return CIS2_E_ARG;
   int r = cis2_check_ready(c);
   if (r) return r;
+  if (n > 1 && !c->trace) {  // all rows in one row-batched pass
+    r = check_rows(c, n, seq, pos, tok);
+    if (r) return r;
+    std::vector<uint32_t> lr(n);
+    for (uint32_t i = 0; i < n; ++i) lr[i] = i;
+    r = forward_rows_host(c, n, seq, pos, tok, n, lr.data());
+    if (r) return r;
+    HIPCHK(c, hipStreamSynchronize(c->st), "rows sync");
+    if (logits_host)
+      HIPCHK(c, hipMemcpy(logits_host, c->rows.logits, (size_t)n * c->cfg.vocab * sizeof(float),
+                          hipMemcpyDeviceToHost),
+             "logits copy");
+    if (argmax_out)
+      HIPCHK(c, hipMemcpy(argmax_out, c->rows.arg, (size_t)n * 4, hipMemcpyDeviceToHost),
+             "argmax copy");
+    return check_err_flag(c);
+  }
   for (uint32_t i = 0; i < n; ++i) {
     if (seq[i] >= c->cfg.max_seqs) return fail(c, CIS2_E_ARG, "sequence index out of range");
     if (pos[i] >= c->cfg.max_pos) return fail(c, CIS2_E_RANGE, "position beyond max_pos");
@@ -810,10 +1007,26 @@ int cis2_decode_begin(cis2_ctx* c, uint32_t seq, const uint32_t* prompt, uint32_
   HIPCHK(c, hipMemcpy(c->d_prompt, prompt, (size_t)n_prompt * 4, hipMemcpyHostToDevice),
          "prompt upload");
   S.fast = use_fast(c);
-  for (uint32_t p = 0; p < n_prompt; ++p) {
-    r = S.fast ? forward_fast(c, seq, p, c->d_prompt + p, p + 1 == n_prompt)
-               : forward_one(c, seq, p, c->d_prompt + p, p + 1 == n_prompt);
+  if (n_prompt > 1 && !c->trace && !c->seq_prefill) {
+    // all prompt positions in one row-batched pass (bit-identical to the
+    // position-by-position prefill); the last row's logits and argmax go
+    // where the decode steps expect them
+    std::vector<uint32_t> sq(n_prompt, seq), ps(n_prompt);
+    for (uint32_t p = 0; p < n_prompt; ++p) ps[p] = p;
+    const uint32_t last = n_prompt - 1;
+    r = forward_rows_host(c, n_prompt, sq.data(), ps.data(), prompt, 1, &last);
     if (r) return r;
+    HIPCHK(c, hipMemcpyAsync(c->logits, c->rows.logits, (size_t)c->cfg.vocab * sizeof(float),
+                             hipMemcpyDeviceToDevice, c->st),
+           "prefill logits");
+    HIPCHK(c, hipMemcpyAsync(c->d_tok, c->rows.arg, 4, hipMemcpyDeviceToDevice, c->st),
+           "prefill argmax");
+  } else {
+    for (uint32_t p = 0; p < n_prompt; ++p) {
+      r = S.fast ? forward_fast(c, seq, p, c->d_prompt + p, p + 1 == n_prompt)
+                 : forward_one(c, seq, p, c->d_prompt + p, p + 1 == n_prompt);
+      if (r) return r;
+    }
   }
   HIPCHK(c, hipStreamSynchronize(c->st), "prefill sync");
   S.active = true;
@@ -887,21 +1100,229 @@ int cis2_decode(cis2_ctx* c, uint32_t seq, const uint32_t* prompt, uint32_t n_pr
   return r;
 }
 
+// Greedy decode of `G` sequences (cache slots 0..G-1) in row-batched
+// passes: one prefill over every prompt position of every sequence, then
+// one row per sequence per step.  Per sequence, the witness and argmax
+// digest are built exactly as cis2_decode builds them.
+static int decode_group(cis2_ctx* c, uint32_t G, const uint32_t* prompts, const uint32_t* lens,
+                        uint32_t gen, const uint8_t hdr[96], uint32_t* out_ids, uint8_t* witness,
+                        uint8_t* argmax_digest) {
+  const uint32_t V = c->cfg.vocab;
+  std::vector<uint32_t> seq, pos, tok, lrows(G), off(G + 1, 0);
+  for (uint32_t b = 0; b < G; ++b) {
+    if (lens[b] == 0) return fail(c, CIS2_E_ARG, "empty prompt");
+    if ((uint64_t)lens[b] + gen > c->cfg.max_pos)
+      return fail(c, CIS2_E_RANGE, "prompt + gen_toks exceeds max_pos");
+    off[b + 1] = off[b] + lens[b];
+    for (uint32_t p = 0; p < lens[b]; ++p) {
+      if (prompts[off[b] + p] >= V) return fail(c, CIS2_E_RANGE, "prompt token id >= vocab");
+      seq.push_back(b);
+      pos.push_back(p);
+      tok.push_back(prompts[off[b] + p]);
+    }
+    lrows[b] = off[b + 1] - 1;
+  }
+  for (uint32_t b = 0; b < G; ++b) {
+    int r = cis2_reset_seq(c, b);
+    if (r) return r;
+  }
+  std::vector<Sha256> w(G), a(G);
+  for (uint32_t b = 0; b < G; ++b) {
+    w[b].update(hdr, 96);
+    w[b].update(c->table_dig, 32);
+    w[b].update(c->invf_dig, 32);
+    for (uint32_t p = 0; p < lens[b]; ++p) {
+      w[b].update_u32le(prompts[off[b] + p]);
+      a[b].update_u32le(prompts[off[b] + p]);
+    }
+  }
+  // prefill: all prompt rows; logits of each sequence's last prompt row
+  int r = forward_rows_host(c, (uint32_t)seq.size(), seq.data(), pos.data(), tok.data(), G,
+                            lrows.data());
+  if (r) return r;
+  if (gen == 0) {
+    HIPCHK(c, hipStreamSynchronize(c->st), "prefill sync");
+  } else {
+    // decode rows: row b = sequence b at position lens[b] + step
+    RowsBuf& rb = c->rows;
+    std::vector<uint32_t> dseq(G), dpos(G), ident(G);
+    uint32_t max_len = 0;
+    for (uint32_t b = 0; b < G; ++b) {
+      dseq[b] = b;
+      ident[b] = b;
+    }
+    float* host = nullptr;
+    uint32_t* hid = nullptr;
+    HIPCHK(c, hipHostMalloc((void**)&host, 2 * (size_t)G * V * sizeof(float), 0), "pinned logits");
+    if (hipHostMalloc((void**)&hid, 2 * (size_t)G * 4, 0) != hipSuccess) {
+      (void)hipHostFree(host);
+      return fail(c, CIS2_E_OOM, "pinned ids");
+    }
+    hipEvent_t ev[2] = {nullptr, nullptr};
+    int rc = CIS2_OK;
+    for (int i = 0; i < 2 && rc == CIS2_OK; ++i)
+      if (hipEventCreateWithFlags(&ev[i], hipEventDisableTiming) != hipSuccess)
+        rc = fail(c, CIS2_E_DEVICE, "event create");
+    std::vector<uint32_t> ids(G);
+    for (uint32_t step = 0; step < gen && rc == CIS2_OK; ++step) {
+      const uint32_t slot = step & 1;
+      float* hl = host + (size_t)slot * G * V;
+      uint32_t* hi = hid + (size_t)slot * G;
+      if (hipMemcpyAsync(hl, rb.logits, (size_t)G * V * sizeof(float), hipMemcpyDeviceToHost,
+                         c->st) != hipSuccess ||
+          hipMemcpyAsync(hi, rb.arg, (size_t)G * 4, hipMemcpyDeviceToHost, c->st) != hipSuccess ||
+          hipEventRecord(ev[slot], c->st) != hipSuccess) {
+        rc = fail(c, CIS2_E_DEVICE, "logits copy");
+        break;
+      }
+      if (step + 1 < gen) {  // next rows: the argmax ids at the next positions
+        max_len = 0;
+        for (uint32_t b = 0; b < G; ++b) {
+          dpos[b] = lens[b] + step;
+          max_len = std::max(max_len, dpos[b] + 1);
+        }
+        if (step == 0) {
+          rc = rows_reserve(c, G, G);
+          if (rc) break;
+          if (hipMemcpyAsync(rb.seq, dseq.data(), (size_t)G * 4, hipMemcpyHostToDevice, c->st) !=
+                  hipSuccess ||
+              hipMemcpyAsync(rb.lrows, ident.data(), (size_t)G * 4, hipMemcpyHostToDevice,
+                             c->st) != hipSuccess) {
+            rc = fail(c, CIS2_E_DEVICE, "rows upload");
+            break;
+          }
+        }
+        if (hipMemcpyAsync(rb.pos, dpos.data(), (size_t)G * 4, hipMemcpyHostToDevice, c->st) !=
+            hipSuccess) {
+          rc = fail(c, CIS2_E_DEVICE, "rows upload");
+          break;
+        }
+        // the embed reads rb.arg before this pass's argmax overwrites it
+        rc = forward_rows(c, G, rb.arg, max_len, G);
+        if (rc) break;
+      }
+      if (hipEventSynchronize(ev[slot]) != hipSuccess) {
+        rc = fail(c, CIS2_E_DEVICE, "logits wait");
+        break;
+      }
+      fold_rows(w, hl, hi, G, V);
+      for (uint32_t b = 0; b < G; ++b) {
+        a[b].update_u32le(hi[b]);
+        out_ids[off[b] + (size_t)b * gen + lens[b] + step] = hi[b];
+      }
+    }
+    if (rc == CIS2_OK && hipStreamSynchronize(c->st) != hipSuccess)
+      rc = fail(c, CIS2_E_DEVICE, "decode sync");
+    for (int i = 0; i < 2; ++i)
+      if (ev[i]) (void)hipEventDestroy(ev[i]);
+    (void)hipHostFree(host);
+    (void)hipHostFree(hid);
+    if (rc) return rc;
+  }
+  for (uint32_t b = 0; b < G; ++b) {
+    memcpy(out_ids + off[b] + (size_t)b * gen, prompts + off[b], (size_t)lens[b] * 4);
+    w[b].finish(witness + 32 * (size_t)b);
+    a[b].finish(argmax_digest + 32 * (size_t)b);
+  }
+  return check_err_flag(c);
+}
+
 int cis2_decode_batch(cis2_ctx* c, uint32_t nseq, const uint32_t* prompts,
                       const uint32_t* prompt_lens, uint32_t gen_toks, const uint8_t hdr[96],
                       uint32_t* out_ids, uint8_t* witness, uint8_t* argmax_digest) {
   if (!c || !prompts || !prompt_lens || !hdr || !out_ids || !witness || !argmax_digest)
     return CIS2_E_ARG;
+  int r = cis2_check_ready(c);
+  if (r) return r;
   size_t in_off = 0, out_off = 0;
-  for (uint32_t b = 0; b < nseq; ++b) {
-    int r = cis2_decode(c, b % c->cfg.max_seqs, prompts + in_off, prompt_lens[b], gen_toks, hdr,
-                        out_ids + out_off, witness + 32 * (size_t)b,
-                        argmax_digest + 32 * (size_t)b, nullptr);
+  if (nseq == 1 || c->trace) {  // one sequence (or tracing): the single-row path
+    for (uint32_t b = 0; b < nseq; ++b) {
+      r = cis2_decode(c, b % c->cfg.max_seqs, prompts + in_off, prompt_lens[b], gen_toks, hdr,
+                      out_ids + out_off, witness + 32 * (size_t)b,
+                      argmax_digest + 32 * (size_t)b, nullptr);
+      if (r) return r;
+      in_off += prompt_lens[b];
+      out_off += (size_t)prompt_lens[b] + gen_toks;
+    }
+    return CIS2_OK;
+  }
+  // groups of up to max_seqs sequences, one KV-cache slot each
+  for (uint32_t b0 = 0; b0 < nseq; b0 += c->cfg.max_seqs) {
+    const uint32_t G = std::min(c->cfg.max_seqs, nseq - b0);
+    r = decode_group(c, G, prompts + in_off, prompt_lens + b0, gen_toks, hdr, out_ids + out_off,
+                     witness + 32 * (size_t)b0, argmax_digest + 32 * (size_t)b0);
     if (r) return r;
-    in_off += prompt_lens[b];
-    out_off += (size_t)prompt_lens[b] + gen_toks;
+    for (uint32_t b = 0; b < G; ++b) {
+      in_off += prompt_lens[b0 + b];
+      out_off += (size_t)prompt_lens[b0 + b] + gen_toks;
+    }
   }
   return CIS2_OK;
+}
+
+// Teacher-forced verification of a claimed continuation in one row-batched
+// pass (code/cis2-fp/verify3/model.c:923-1005): the rows are positions
+// 0 .. n_prompt + n_gen - 2 of sequence `seq` fed prompt ++ claimed; the
+// logits of position n_prompt - 1 + s predict claimed[s].  Witness and
+// argmax digest fold each step's logits and their argmax (not the claimed
+// id), as the reference does; first_mismatch is the first s whose argmax
+// differs from claimed[s], or -1.
+int cis2_verify_prefill(cis2_ctx* c, uint32_t seq, const uint32_t* prompt, uint32_t n_prompt,
+                        const uint32_t* claimed, uint32_t n_gen, const uint8_t hdr[96],
+                        uint32_t* generated, uint8_t witness[32], uint8_t argmax_digest[32],
+                        int64_t* first_mismatch, float* logits_host) {
+  if (!c || !prompt || (n_gen && !claimed) || !hdr || (n_gen && !generated) || !witness ||
+      !argmax_digest || !first_mismatch)
+    return CIS2_E_ARG;
+  if (n_prompt == 0 || seq >= c->cfg.max_seqs) return fail(c, CIS2_E_ARG, "bad prompt or seq");
+  if ((uint64_t)n_prompt + n_gen > (uint64_t)c->cfg.max_pos + 1)
+    return fail(c, CIS2_E_RANGE, "prompt + claimed tokens exceed max_pos");
+  const uint32_t V = c->cfg.vocab;
+  for (uint32_t i = 0; i < n_prompt; ++i)
+    if (prompt[i] >= V) return fail(c, CIS2_E_RANGE, "prompt token id >= vocab");
+  for (uint32_t i = 0; i < n_gen; ++i)
+    if (claimed[i] >= V) return fail(c, CIS2_E_RANGE, "claimed token id >= vocab");
+  int r = cis2_check_ready(c);
+  if (r) return r;
+  r = cis2_reset_seq(c, seq);
+  if (r) return r;
+  *first_mismatch = -1;
+  Sha256 w, a;
+  w.update(hdr, 96);
+  w.update(c->table_dig, 32);
+  w.update(c->invf_dig, 32);
+  for (uint32_t i = 0; i < n_prompt; ++i) {
+    w.update_u32le(prompt[i]);
+    a.update_u32le(prompt[i]);
+  }
+  if (n_gen) {
+    const uint32_t n = n_prompt + n_gen - 1;
+    std::vector<uint32_t> sq(n, seq), ps(n), tk(n), lr(n_gen);
+    for (uint32_t p = 0; p < n; ++p) {
+      ps[p] = p;
+      tk[p] = p < n_prompt ? prompt[p] : claimed[p - n_prompt];
+    }
+    for (uint32_t s = 0; s < n_gen; ++s) lr[s] = n_prompt - 1 + s;
+    r = forward_rows_host(c, n, sq.data(), ps.data(), tk.data(), n_gen, lr.data());
+    if (r) return r;
+    std::vector<float> lg((size_t)n_gen * V);
+    HIPCHK(c, hipStreamSynchronize(c->st), "prefill sync");
+    HIPCHK(c, hipMemcpy(lg.data(), c->rows.logits, lg.size() * sizeof(float),
+                        hipMemcpyDeviceToHost),
+           "logits copy");
+    HIPCHK(c, hipMemcpy(generated, c->rows.arg, (size_t)n_gen * 4, hipMemcpyDeviceToHost),
+           "argmax copy");
+    for (uint32_t s = 0; s < n_gen; ++s) {
+      w.update(lg.data() + (size_t)s * V, (size_t)V * sizeof(float));
+      w.update_u32le(generated[s]);
+      a.update_u32le(generated[s]);
+      if (*first_mismatch < 0 && generated[s] != claimed[s]) *first_mismatch = s;
+    }
+    if (logits_host) memcpy(logits_host, lg.data(), lg.size() * sizeof(float));
+  }
+  w.finish(witness);
+  a.finish(argmax_digest);
+  return check_err_flag(c);
 }
 
 // ---- standalone GEMV ------------------------------------------------------

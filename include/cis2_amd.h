@@ -106,11 +106,15 @@ int cis2_digests(cis2_ctx *ctx, uint8_t table[32], uint8_t inv_freq[32]);
 /* Clears a sequence's KV cache (a fresh prompt). */
 int cis2_reset_seq(cis2_ctx *ctx, uint32_t seq);
 
-/* One forward pass per listed sequence: sequence seq[i] at position pos[i]
- * with input token tok[i].  logits_host (n * vocab floats) and argmax_out
- * (n ids, strict-> first maximum) may each be NULL.  Replaces one call of
- * cis2_forward_token + cis2_download + cis2_argmax per sequence
- * (cis2_model.h:685-774). */
+/* One forward pass per listed row: sequence seq[i] at position pos[i] with
+ * input token tok[i].  logits_host (n * vocab floats) and argmax_out (n
+ * ids, strict-> first maximum) may each be NULL.  Replaces one call of
+ * cis2_forward_token + cis2_download + cis2_argmax per row
+ * (cis2_model.h:685-774).  With n > 1 the rows run as one row-batched
+ * pass: every row's K/V reach the caches before any row's attention, so
+ * rows of one sequence at different positions are causal among themselves
+ * (a teacher-forced prefill); no two rows may share a (seq, pos)
+ * (CIS2_E_ARG).  Each row's results equal its single-row call bit for bit. */
 int cis2_forward(cis2_ctx *ctx, uint32_t n, const uint32_t *seq, const uint32_t *pos,
                  const uint32_t *tok, float *logits_host, uint32_t *argmax_out);
 
@@ -140,7 +144,10 @@ int cis2_decode_end(cis2_ctx *ctx, uint32_t *out_ids, uint8_t witness[32],
                     uint8_t argmax_digest[32], uint8_t *step_digests);
 
 /* Batched greedy decode: nseq independent sequences with their own prompts
- * (ragged lengths allowed), each decoded for gen_toks steps.  Every row's
+ * (ragged lengths allowed), each decoded for gen_toks steps.  Groups of up
+ * to max_seqs sequences run together (KV-cache slots 0..max_seqs-1): one
+ * row-batched prefill of all their prompt positions, then one row per
+ * sequence per step, each at its own position.  Every row's
  * outputs equal its bs=1 cis2_decode outputs bit for bit (the reference's
  * per-row batch semantics: code/patches/cis2-fp__cm_gpu3-batched-full.patch
  * :443-458,687-763).  prompts = concatenated ids, prompt_lens[nseq];
@@ -149,6 +156,21 @@ int cis2_decode_end(cis2_ctx *ctx, uint32_t *out_ids, uint8_t witness[32],
 int cis2_decode_batch(cis2_ctx *ctx, uint32_t nseq, const uint32_t *prompts,
                       const uint32_t *prompt_lens, uint32_t gen_toks, const uint8_t hdr[96],
                       uint32_t *out_ids, uint8_t *witness, uint8_t *argmax_digest);
+
+/* Teacher-forced verification of a claimed continuation in one row-batched
+ * pass over prompt ++ claimed (cis2_verify_receipt_prefill,
+ * code/cis2-fp/verify3/model.c:923-1005; first_mismatch_pos as
+ * verify3/prefilltest.c:60-76).  The logits at position n_prompt-1+s
+ * predict claimed[s]; generated[s] receives their argmax.  witness and
+ * argmax_digest are built as cis2_decode builds them, from the logits and
+ * their argmax ids, so an honest claim reproduces the decode's digests.
+ * *first_mismatch = first s with generated[s] != claimed[s], else -1.
+ * logits_host (optional) receives n_gen * vocab floats.  Uses KV-cache slot
+ * `seq` (cleared first); n_prompt + n_gen - 1 <= max_pos. */
+int cis2_verify_prefill(cis2_ctx *ctx, uint32_t seq, const uint32_t *prompt, uint32_t n_prompt,
+                        const uint32_t *claimed, uint32_t n_gen, const uint8_t hdr[96],
+                        uint32_t *generated, uint8_t witness[32], uint8_t argmax_digest[32],
+                        int64_t *first_mismatch, float *logits_host);
 
 /* Per-op tracing (--trace); NULL disables.  Tracing synchronises after every
  * op, so it is a verification mode, not a fast path. */

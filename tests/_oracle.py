@@ -164,6 +164,15 @@ class OracleModel:
         lib().orc_model_digests(self.m, t, f)
         return bytes(t).hex(), bytes(f).hex()
 
+    def forward(self, pos, tok):
+        """One forward pass at `pos` (positions are filled in order by the
+        caller); returns the logits."""
+        logits = np.empty(self.spec.vocab, dtype=np.float32)
+        rc = lib().orc_forward(self.m, int(pos), int(tok), ptr(logits, c_fp), TRACE_FN(), None)
+        if rc != 0:
+            raise RuntimeError("oracle forward failed (%d)" % rc)
+        return logits
+
     def decode(self, prompt, gen_toks, trace=None):
         prompt = np.ascontiguousarray(prompt, dtype=np.uint32)
         ids = np.zeros(prompt.size + gen_toks, dtype=np.uint32)

@@ -1,0 +1,143 @@
+"""The row-batched forward pass on the device: many rows per launch (a batch
+of sequences, or every position of one sequence) must give each row the
+bits of its single-row run and of the reference.
+
+  - cis2_forward with n > 1 rows (causal prefill of one sequence through the
+    KV cache) against the single-row calls and the oracle;
+  - cis2_verify_prefill (teacher-forced, verify3/model.c:923-1005): an
+    honest claim reproduces the reference decode's witness and argmax
+    digest; a claim tampered at step k reports first_mismatch == k
+    (verify3/prefilltest.c:84-160);
+  - cis2_decode_batch with ragged prompts equals the bs=1 decodes.
+"""
+import os
+
+import numpy as np
+import pytest
+
+import _oracle as O
+from cis2amd import Cis2Error, Cis2Model, artifacts
+
+pytestmark = pytest.mark.gpu
+
+TINY = ["tiny-llama", "tiny-untied", "tiny-qwen3", "tiny-qwen2"]
+
+
+def model_for(rec, max_seqs=1, extra_pos=0):
+    spec = artifacts.SPECS[rec["spec"]]
+    w = artifacts.Weights(spec, rec["seed"])
+    mode = 1 if rec.get("reduction") == "tree" else 0
+    return Cis2Model(spec, w, max_pos=len(rec["prompt"]) + rec["gen_toks"] + extra_pos,
+                     max_seqs=max_seqs, reduction_mode=mode), w
+
+
+@pytest.mark.parametrize("name", TINY + [n + "-tree" for n in TINY])
+def test_rows_prefill_equals_single_rows_and_oracle(name, model_fixtures):
+    rec = model_fixtures[name]
+    m, w = model_for(rec)
+    spec = m.spec
+    seq = rec["prompt"] + rec["tokens"][len(rec["prompt"]):]  # prompt ++ generated
+    n = len(seq)
+    rows_logits, rows_arg = m.forward_rows(np.zeros(n), np.arange(n), seq)
+    m.reset(0)
+    for p in range(n):
+        lg, am = m.forward_token(p, seq[p])
+        assert np.array_equal(lg.view(np.uint32), rows_logits[p].view(np.uint32)), "row %d" % p
+        assert am == rows_arg[p]
+    o = O.OracleModel(spec, w, max_pos=n, reduction=m.reduction_mode)
+    for p in range(n):
+        ol = o.forward(p, seq[p])
+        assert np.array_equal(ol.view(np.uint32), rows_logits[p].view(np.uint32)), "oracle row %d" % p
+
+
+def test_rows_rows_of_two_sequences_in_any_order(model_fixtures):
+    """Rows of two sequences interleaved and out of position order in one
+    call: each sequence's rows equal its own prefill."""
+    rec = model_fixtures["tiny-llama"]
+    m, _ = model_for(rec, max_seqs=2, extra_pos=8)
+    a = rec["prompt"]
+    b = [int(t) for t in artifacts.prompt_ids(99, m.spec.vocab, 9)]
+    la, _ = m.forward_rows(np.zeros(len(a)), np.arange(len(a)), a)
+    lb, _ = m.forward_rows(np.zeros(len(b)), np.arange(len(b)), b)
+    rows = [(0, p, a[p]) for p in range(len(a))] + [(1, p, b[p]) for p in range(len(b))]
+    rng = np.random.default_rng(5)
+    order = rng.permutation(len(rows))
+    rs = np.array([rows[i] for i in order], dtype=np.uint32)
+    lm, _ = m.forward_rows(rs[:, 0], rs[:, 1], rs[:, 2])
+    for j, i in enumerate(order):
+        s, p, _ = rows[i]
+        ref = la[p] if s == 0 else lb[p]
+        assert np.array_equal(lm[j].view(np.uint32), ref.view(np.uint32))
+
+
+def test_rows_duplicate_row_is_refused(model_fixtures):
+    rec = model_fixtures["tiny-llama"]
+    m, _ = model_for(rec)
+    with pytest.raises(Cis2Error) as e:
+        m.forward_rows([0, 0], [1, 1], [3, 4])
+    assert e.value.code == -1
+
+
+@pytest.mark.parametrize("name", ["smollm2-135m", "llama-160m-p0", "tiny-qwen3", "tiny-wide-tree",
+                                  "smollm2-135m-tree"])
+def test_verify_prefill_honest_claim_reproduces_reference_witness(name, model_fixtures):
+    rec = model_fixtures[name]
+    m, _ = model_for(rec)
+    n = len(rec["prompt"])
+    claimed = rec["tokens"][n:]
+    r = m.verify_prefill(rec["prompt"], claimed)
+    assert r["first_mismatch"] == -1
+    assert list(r["generated"]) == claimed
+    assert r["witness"] == rec["witness"]
+    assert r["argmax_digest"] == rec["argmax_digest"]
+
+
+def test_verify_prefill_tampered_claim_reports_first_mismatch(model_fixtures):
+    rec = model_fixtures["smollm2-135m"]
+    m, _ = model_for(rec)
+    n = len(rec["prompt"])
+    claimed = list(rec["tokens"][n:])
+    for k in (0, 17, 200, len(claimed) - 1):
+        bad = list(claimed)
+        bad[k] = (bad[k] + 1) % m.spec.vocab
+        r = m.verify_prefill(rec["prompt"], bad)
+        assert r["first_mismatch"] == k
+        # positions before the tamper see the honest prefix
+        assert list(r["generated"][:k + 1]) == claimed[:k + 1]
+        assert r["witness"] != rec["witness"] or k == len(claimed) - 1
+
+
+def test_decode_prefill_paths_agree(model_fixtures):
+    """The decode's prefill runs as one row-batched pass; the position by
+    position prefill (CIS2_PREFILL=seq) gives the same witness."""
+    rec = model_fixtures["tiny-qwen3"]
+    spec = artifacts.SPECS[rec["spec"]]
+    w = artifacts.Weights(spec, rec["seed"])
+    os.environ["CIS2_PREFILL"] = "seq"
+    try:
+        ms = Cis2Model(spec, w, max_pos=len(rec["prompt"]) + rec["gen_toks"])
+    finally:
+        del os.environ["CIS2_PREFILL"]
+    mr = Cis2Model(spec, w, max_pos=len(rec["prompt"]) + rec["gen_toks"])
+    a = ms.decode(rec["prompt"], rec["gen_toks"])
+    b = mr.decode(rec["prompt"], rec["gen_toks"])
+    assert a["witness"] == b["witness"] == rec["witness"]
+    assert a["step_digests"] == b["step_digests"]
+
+
+@pytest.mark.parametrize("B", [2, 5])
+def test_decode_batch_ragged_equals_bs1(B):
+    """B sequences with ragged prompts through cis2_decode_batch (row-batched
+    prefill and steps) against each sequence's bs=1 decode."""
+    spec = artifacts.SPECS["tiny-untied"]
+    w = artifacts.Weights(spec, 2)
+    prompts = [artifacts.set_prompt(2, i, spec.vocab, 1, 40, 9) for i in range(B)]
+    gen = 24
+    m = Cis2Model(spec, w, max_pos=40 + gen, max_seqs=3)  # B=5: two groups
+    rows = m.decode_batch(prompts, gen)
+    solo = Cis2Model(spec, w, max_pos=40 + gen)
+    for i, p in enumerate(prompts):
+        s = solo.decode(p, gen, step_digests=False)
+        assert rows[i]["witness"] == s["witness"]
+        assert rows[i]["argmax_digest"] == s["argmax_digest"]
+        assert np.array_equal(rows[i]["ids"], s["ids"])
