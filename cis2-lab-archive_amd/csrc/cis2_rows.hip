@@ -11,6 +11,10 @@
 namespace cis2 {
 namespace {
 
+// 16-byte vector as a native vector type: local arrays of it stay in
+// registers (the struct-based float4 keeps them in scratch memory).
+typedef float v4 __attribute__((ext_vector_type(4)));
+
 constexpr uint32_t kT = 256;
 // LDS per batched-GEMM workgroup: two workgroups fit one CU.
 constexpr uint32_t kBgemmLds = 78 * 1024;
@@ -18,7 +22,7 @@ constexpr uint32_t kBgemmLds = 78 * 1024;
 // ---------------------------------------------------------------------------
 // Batched GEMM.  A workgroup owns one R-row block of W and TB = 256 / R batch
 // rows: thread t computes output (row b0 + t / R, column blk * R + t % R).
-// K runs in chunks of KC: the block's [KC/4][R] float4 slice (contiguous in
+// K runs in chunks of KC: the block's [KC/4][R] v4 slice (contiguous in
 // the blocked layout) and the TB input rows' KC floats are staged in LDS,
 // then each thread continues its own chain acc = acc + W[m][k] * X[b][k],
 // k ascending (code/cis2-fp/src/main.rs:228-243, math.rs:40-48); in tree
@@ -30,16 +34,16 @@ struct BgemmArgs {
 };
 
 __global__ __launch_bounds__(256) void k_bgemm(BgemmArgs a) {
-  extern __shared__ float4 sm[];
+  extern __shared__ v4 sm[];
   const BgemmSeg& g = a.s;
   const uint32_t R = g.R, TB = a.TB, KC = a.KC, K = g.K;
   const uint32_t blk = blockIdx.x, b0 = blockIdx.y * TB, t = threadIdx.x;
   const uint32_t r = t % R, bb = t / R;
   const bool live = t < R * TB;
   const uint32_t qmax = KC / 4, xs4 = qmax + 1;  // padded X rows: no bank aliasing
-  float4* Ws = sm;
-  float4* Xs = sm + (size_t)qmax * R;
-  const float4* Wg = reinterpret_cast<const float4*>(g.W + (size_t)blk * R * K);
+  v4* Ws = sm;
+  v4* Xs = sm + (size_t)qmax * R;
+  const v4* Wg = reinterpret_cast<const v4*>(g.W + (size_t)blk * R * K);
   float acc = 0.0f;
   for (uint32_t k0 = 0; k0 < K; k0 += KC) {
     const uint32_t q4 = std::min(KC, K - k0) / 4, g0 = k0 / 4;
@@ -47,18 +51,18 @@ __global__ __launch_bounds__(256) void k_bgemm(BgemmArgs a) {
     for (uint32_t i = t; i < TB * q4; i += kT) {
       const uint32_t bx = i / q4, q = i - bx * q4;
       const uint32_t row = std::min(b0 + bx, a.n - 1);
-      Xs[bx * xs4 + q] = reinterpret_cast<const float4*>(g.X + (size_t)row * g.ldx)[g0 + q];
+      Xs[bx * xs4 + q] = reinterpret_cast<const v4*>(g.X + (size_t)row * g.ldx)[g0 + q];
     }
     __syncthreads();
     if (live) {
-      const float4* wp = Ws + r;
-      const float4* xp = Xs + bb * xs4;
+      const v4* wp = Ws + r;
+      const v4* xp = Xs + bb * xs4;
       if (a.tree) {
         for (uint32_t q = 0; q < q4; q += 8) {
           float l[32];
 #pragma unroll
           for (uint32_t j = 0; j < 8; ++j) {
-            float4 w = make_float4(0.0f, 0.0f, 0.0f, 0.0f), x = w;
+            v4 w = v4{0.0f, 0.0f, 0.0f, 0.0f}, x = w;
             if (q + j < q4) {
               w = wp[(size_t)(q + j) * R];
               x = xp[q + j];
@@ -73,7 +77,7 @@ __global__ __launch_bounds__(256) void k_bgemm(BgemmArgs a) {
       } else {
 #pragma unroll 4
         for (uint32_t q = 0; q < q4; ++q) {
-          const float4 w = wp[(size_t)q * R], x = xp[q];
+          const v4 w = wp[(size_t)q * R], x = xp[q];
           float p;
           p = w.x * x.x; acc = acc + p;
           p = w.y * x.y; acc = acc + p;
@@ -171,7 +175,7 @@ __global__ __launch_bounds__(256) void k_rope_store_rows(float* q, float* k, con
     vc[sb + (size_t)idx * max_pos + pos] = vr[idx];
 }
 
-// One workgroup per (query head, row): scores_j = dot(q, k_j) * scale
+// One workgroup per (row, query head): scores_j = dot(q, k_j) * scale
 // (dot_seq, or dot_tree), softmax (first-wins max, pinned exp, strict or
 // tree denominator, true divide), then out_d = fold_j (p_j * v_j[d]) in
 // position order (code/cis2-fp/src/main.rs:429-467; math.rs:425-465).
@@ -185,7 +189,7 @@ __global__ __launch_bounds__(256) void k_attention_rows(const float* __restrict_
   extern __shared__ float sh[];
   __shared__ Pick red[4];
   __shared__ float s_den;
-  const uint32_t qh = blockIdx.x, r = blockIdx.y;
+  const uint32_t r = blockIdx.x, qh = blockIdx.y;  // rows on x: up to 2^31 of them
   const uint32_t group = nh / nkv, kvh = qh / group, pos = rows.pos[r], len = pos + 1;
   const size_t sb = (size_t)rows.seq[r] * seq_stride;
   float* sq = sh;
@@ -206,8 +210,20 @@ __global__ __launch_bounds__(256) void k_attention_rows(const float* __restrict_
         acc = acc + tree32(l);
       }
     } else {
-      for (uint32_t d = 0; d < hd; ++d) {
-        float p = sq[d] * kb[(size_t)d * max_pos + j];
+      // the column's loads go out 16 at a time, then their 16 chain steps
+      uint32_t d0 = 0;
+      for (; d0 + 16 <= hd; d0 += 16) {
+        float kv[16];
+#pragma unroll
+        for (uint32_t i = 0; i < 16; ++i) kv[i] = kb[(size_t)(d0 + i) * max_pos + j];
+#pragma unroll
+        for (uint32_t i = 0; i < 16; ++i) {
+          float p = sq[d0 + i] * kv[i];
+          acc = acc + p;
+        }
+      }
+      for (; d0 < hd; ++d0) {
+        float p = sq[d0] * kb[(size_t)d0 * max_pos + j];
         acc = acc + p;
       }
     }
@@ -255,9 +271,26 @@ __global__ __launch_bounds__(256) void k_attention_rows(const float* __restrict_
   const float* vb = vc + sb + (size_t)kvh * hd * max_pos;
   float* o = out + (size_t)r * nh * hd + (size_t)qh * hd;
   for (uint32_t d = threadIdx.x; d < hd; d += blockDim.x) {
-    const float* vr = vb + (size_t)d * max_pos;
+    // row d of V is contiguous: 16-byte loads, 8 of them (32 positions) in
+    // flight ahead of the chain
+    const v4* vr4 = reinterpret_cast<const v4*>(vb + (size_t)d * max_pos);
     float acc = 0.0f;
-    for (uint32_t j = 0; j < len; ++j) {
+    uint32_t j = 0;
+    for (; j + 32 <= len; j += 32) {
+      v4 v[8];
+#pragma unroll
+      for (uint32_t u = 0; u < 8; ++u) v[u] = vr4[j / 4 + u];
+#pragma unroll
+      for (uint32_t u = 0; u < 8; ++u) {
+        float p;
+        p = ss[j + 4 * u] * v[u].x; acc = acc + p;
+        p = ss[j + 4 * u + 1] * v[u].y; acc = acc + p;
+        p = ss[j + 4 * u + 2] * v[u].z; acc = acc + p;
+        p = ss[j + 4 * u + 3] * v[u].w; acc = acc + p;
+      }
+    }
+    const float* vr = vb + (size_t)d * max_pos;
+    for (; j < len; ++j) {
       float p = ss[j] * vr[j];
       acc = acc + p;
     }
@@ -351,11 +384,12 @@ hipError_t launch_attention_rows(const float* q, const float* kc, const float* v
                                  uint32_t hd, uint32_t max_pos, uint64_t seq_stride, float scale,
                                  float* out, bool tree, hipStream_t st) {
   if (rows.n == 0) return hipSuccess;
-  if (nkv == 0 || nh % nkv || max_len == 0 || max_len > max_pos) return hipErrorInvalidValue;
+  if (nkv == 0 || nh % nkv || max_len == 0 || max_len > max_pos || max_pos % 4)
+    return hipErrorInvalidValue;
   // q, scores, and the denominator's block partials
   const size_t shmem = ((size_t)hd + max_len + (max_len + 31) / 32) * sizeof(float);
   if (shmem > 60 * 1024) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_attention_rows, dim3(nh, rows.n), dim3(kT), shmem, st, q, kc, vc, rows,
+  hipLaunchKernelGGL(k_attention_rows, dim3(rows.n, nh), dim3(kT), shmem, st, q, kc, vc, rows,
                      nh, nkv, hd, max_pos, seq_stride, scale, out, tree ? 1u : 0u);
   return hipGetLastError();
 }
