@@ -17,6 +17,14 @@ divided by the launch's device time from HIP events on the library's own
 stream (cis2_profile), summed over the timed steps.  `traffic` is the HBM
 bytes per launch from the committed rocprofv3 counter summary, when present.
 
+Beside the headline line, the same JSON object carries the other
+measured workloads: the strict-order GEMV at 1536x576 (gemv_config1), the
+batched decode of the batch-stress sequences at B = 8, 32, 64
+(batch_decode), the Qwen3-0.6B-shape 4096-token prefill + 256-step decode
+(qwen3_4096), and the CPU baseline both single-thread (cpu_baseline, the
+reference protocol) and row-parallel over the host cores
+(cpu_baseline_parallel).
+
 Prints ONE JSON line on stdout.
 """
 import argparse
@@ -108,6 +116,95 @@ def cpu_baseline(spec, weights, prompt, seconds=15.0):
                       % (n, n - 1, dt)}
 
 
+def batch_decode(spec, weights, sizes=(8, 32, 64)):
+    """Config 4: batched greedy decode of the batch-stress sequences (prompts of
+    16..512 tokens, 256 generated each) through cis2_decode_batch: one
+    row-batched prefill, then one row per sequence per step.  tok/s counts
+    generated tokens over the decode steps (total time minus the prefill-only
+    run).  The B=64 digests are checked against the reference's."""
+    from cis2amd import Cis2Model, artifacts
+    pset = artifacts.BATCH_SET
+    prompts = artifacts.set_prompts(pset)
+    gen = pset["gen_toks"]
+    m = Cis2Model(spec, weights, max_pos=pset["hi"] + gen, max_seqs=max(sizes))
+    m.decode_batch(prompts[:2], 4)
+    out = {}
+    for B in sizes:
+        P = prompts[:B]
+        t = time.perf_counter()
+        m.decode_batch(P, 0)
+        tp = time.perf_counter() - t
+        t = time.perf_counter()
+        rows = m.decode_batch(P, gen)
+        tt = time.perf_counter() - t
+        rec = {"tok_s": round(B * gen / (tt - tp), 1), "prefill_rows": sum(len(p) for p in P),
+               "prefill_s": round(tp, 4), "total_s": round(tt, 4)}
+        fx = os.path.join(ROOT, "tests", "golden", "batch_set.json")
+        if os.path.exists(fx):
+            doc = json.load(open(fx))
+            if doc.get("set") == pset:
+                rec["digests_bit_exact"] = all(
+                    [r["witness"], r["argmax_digest"]] == doc["cases"][str(i)]
+                    for i, r in enumerate(rows))
+        out["B=%d" % B] = rec
+        log("batch decode B=%d:" % B, rec)
+    m.close()
+    return out
+
+
+def qwen3_long(gen=256, n_prompt=4096, seed=6):
+    """Config 5: Qwen3-0.6B shape, 4096-token prompt (one row-batched prefill
+    pass) then 256 greedy steps of the persistent kernel with streamed
+    attention (positions 4096..4351)."""
+    from cis2amd import Cis2Model, artifacts
+    spec = artifacts.SPECS["qwen3-0.6b"]
+    w = artifacts.Weights(spec, seed)
+    prompt = artifacts.prompt_ids(seed, spec.vocab, n_prompt)
+    m = Cis2Model(spec, w, max_pos=n_prompt + gen)
+    t = time.perf_counter()
+    m.begin(prompt, gen)
+    tp = time.perf_counter() - t
+    t = time.perf_counter()
+    m.steps(gen)
+    td = time.perf_counter() - t
+    r = m.end(gen)
+    m.close()
+    rec = {"prefill_s": round(tp, 4), "prefill_rows_s": round(n_prompt / tp, 1),
+           "decode_tok_s": round(gen / td, 2), "witness": r["witness"]}
+    fx = os.path.join(ROOT, "tests", "golden", "qwen3_fixture.json")
+    if os.path.exists(fx):
+        ref = json.load(open(fx)).get("qwen3-0.6b-4096")
+        if ref and ref["prompt"] == [int(v) for v in prompt]:
+            rec["witness_bit_exact"] = r["witness"] == ref["witness"]
+    log("qwen3 4096+256:", rec)
+    return rec
+
+
+def cpu_baseline_parallel(spec, weights, prompt, seconds=10.0):
+    """The oracle with its GEMV rows split over the host cores (same bits:
+    rows are independent), forward passes at consecutive positions."""
+    import numpy as np
+
+    import _oracle as O
+    threads = max(1, min(16, os.cpu_count() or 1))
+    m = O.OracleModel(spec, weights, max_pos=len(prompt) + 512, threads=threads)
+    logits = np.empty(spec.vocab, np.float32)
+    L = O.lib()
+    t0 = time.perf_counter()
+    n = 0
+    tok = int(prompt[0])
+    while True:
+        L.orc_forward(m.m, n, tok, O.ptr(logits, O.c_fp), O.TRACE_FN(), None)
+        n += 1
+        tok = int(prompt[n]) if n < len(prompt) else int(L.orc_argmax(O.ptr(logits, O.c_fp), spec.vocab))
+        if time.perf_counter() - t0 > seconds or n >= len(prompt) + 500:
+            break
+    dt = time.perf_counter() - t0
+    return {"value": round(n / dt, 3), "unit": "tok/s", "cores": threads, "kind": "port",
+            "sample": "%d forward passes (positions 0..%d), GEMV rows over %d threads, %.1f s"
+                      % (n, n - 1, threads, dt)}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -116,6 +213,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-roofline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--no-batch", action="store_true", help="skip the batched-decode sizes")
+    ap.add_argument("--no-qwen3", action="store_true", help="skip the Qwen3 4096+256 run")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 512 MiB device-to-device copy (counter calibration)")
     a = ap.parse_args()
@@ -192,9 +291,16 @@ def main():
     if not a.no_roofline:
         out["gemv_config1"] = gemv_roofline()
         log("standalone GEMV 1536x576:", out["gemv_config1"])
+    if not a.no_batch:
+        out["batch_decode"] = batch_decode(spec, weights)
+    if not a.no_qwen3:
+        out["qwen3_4096"] = qwen3_long()
     if not a.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(spec, weights, prompt, a.cpu_seconds)
         log("cpu baseline:", out["cpu_baseline"])
+        out["cpu_baseline_parallel"] = cpu_baseline_parallel(spec, weights, prompt,
+                                                             a.cpu_seconds * 2 / 3)
+        log("cpu baseline (row-parallel):", out["cpu_baseline_parallel"])
     print(json.dumps(out), flush=True)
 
 
