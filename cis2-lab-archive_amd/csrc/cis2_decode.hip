@@ -1187,9 +1187,40 @@ __device__ __forceinline__ void run_lm(const DecodeArgs& a, const Lds& s) {
 
 // One 256-thread workgroup per CU (the LDS footprint allows no second one),
 // so one wave per SIMD: the compiler may use the whole register file.
-template <bool TR>
+// Model shapes compiled with their dimensions and row-block heights as
+// constants (loop bounds, chunk sizes and GEMV dispatch then fold at compile
+// time: 35-55 % fewer cycles per GEMV than with run-time K).  Shape 0 takes
+// them from the arguments and serves every other configuration.
+struct KShape {
+  uint32_t H, I, qd, hd, Rq, Ro, Rg, Rd, Rl;
+};
+constexpr KShape kShapes[] = {
+    {0, 0, 0, 0, 0, 0, 0, 0, 0},
+    {576, 1536, 576, 64, 32, 32, 16, 24, 32},     // SmolLM2-135M
+    {768, 3072, 768, 64, 32, 32, 16, 12, 32},     // llama-160m
+    {1024, 3072, 2048, 128, 32, 18, 16, 12, 32},  // Qwen3-0.6B
+};
+
+__host__ __device__ inline bool shape_matches(const DecodeArgs& a, const KShape& k) {
+  return a.H == k.H && a.I == k.I && a.qd == k.qd && a.hd == k.hd && a.Rq == k.Rq &&
+         a.Ro == k.Ro && a.Rg == k.Rg && a.Rd == k.Rd && a.Rl == k.Rl;
+}
+
+template <bool TR, int SH>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void k_decode(DecodeArgs a) {
+  if constexpr (SH > 0) {  // the launch checked that the arguments equal these
+    constexpr KShape k = kShapes[SH];
+    a.H = k.H;
+    a.I = k.I;
+    a.qd = k.qd;
+    a.hd = k.hd;
+    a.Rq = k.Rq;
+    a.Ro = k.Ro;
+    a.Rg = k.Rg;
+    a.Rd = k.Rd;
+    a.Rl = k.Rl;
+  }
   // 16-byte element type: the dynamic region follows the static LDS variables
   // (s_last) at a 16-byte boundary, so every ds_read/write_b128 is aligned
   // (a misaligned b128 access is split and runs several times slower).
@@ -1320,22 +1351,26 @@ size_t decode_lds_bytes(const DecodeArgs& a) {
   return decode_wregion_bytes(a) + decode_vec_floats(a) * 4 + 64 * 16 + 256;
 }
 
-template <bool TR>
+template <bool TR, int SH>
 hipError_t launch_decode_t(const DecodeArgs& a, hipStream_t s) {
   const size_t lds = decode_lds_bytes(a);
   static size_t configured = 0;
   if (lds > configured) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_decode<TR>),
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_decode<TR, SH>),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
     configured = lds;
   }
-  hipLaunchKernelGGL(k_decode<TR>, dim3(a.nwg), dim3(kThreads), lds, s, a);
+  hipLaunchKernelGGL((k_decode<TR, SH>), dim3(a.nwg), dim3(kThreads), lds, s, a);
   return hipGetLastError();
 }
 
 hipError_t launch_decode(const DecodeArgs& a, hipStream_t s) {
-  return a.tree ? launch_decode_t<true>(a, s) : launch_decode_t<false>(a, s);
+  if (a.tree) return launch_decode_t<true, 0>(a, s);
+  if (shape_matches(a, kShapes[1])) return launch_decode_t<false, 1>(a, s);
+  if (shape_matches(a, kShapes[2])) return launch_decode_t<false, 2>(a, s);
+  if (shape_matches(a, kShapes[3])) return launch_decode_t<false, 3>(a, s);
+  return launch_decode_t<false, 0>(a, s);
 }
 
 }  // namespace cis2
