@@ -1276,10 +1276,12 @@ void k_decode(DecodeArgs a) {
 // runs the same pipelined product pass and strict chains as the decode
 // kernel.
 // ---------------------------------------------------------------------------
-template <uint32_t R>
+// KC != 0: K fixed at compile time (the kernel takes K == KC).
+template <uint32_t R, uint32_t KC>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void k_gemv_blk(const float* __restrict__ W, const float* __restrict__ x, float* y, uint32_t M,
-                uint32_t K) {
+                uint32_t Krt) {
+  const uint32_t K = KC ? KC : Krt;
   extern __shared__ f4 lds_dyn[];
   lf* w = (lf*)lds_dyn;
   lf* xs = w + (size_t)R * K;
@@ -1302,38 +1304,32 @@ size_t gemv_blk_lds_bytes(uint32_t K, uint32_t R) {
   return ((size_t)R * K + K) * 4 + 64 * 16;
 }
 
+template <uint32_t R, uint32_t KC>
+static hipError_t launch_gemv_blk_t(const float* W, const float* x, float* y, uint32_t M,
+                                    uint32_t K, size_t lds, hipStream_t s) {
+  static size_t configured = 0;
+  if (lds > configured) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemv_blk<R, KC>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
+    configured = lds;
+  }
+  hipLaunchKernelGGL((k_gemv_blk<R, KC>), dim3((M + R - 1) / R), dim3(kThreads), lds, s, W, x,
+                     y, M, K);
+  return hipGetLastError();
+}
+
 hipError_t launch_gemv_blk(const float* W, const float* x, float* y, uint32_t M, uint32_t K,
                            uint32_t R, hipStream_t s) {
   const size_t lds = gemv_blk_lds_bytes(K, R);
   if (K % 4 || lds > 160 * 1024 - 64) return hipErrorInvalidValue;
-  const dim3 grid((M + R - 1) / R);
-  switch (R) {
-    case 16: {
-      static size_t configured = 0;
-      if (lds > configured) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemv_blk<16>),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        if (e != hipSuccess) return e;
-        configured = lds;
-      }
-      hipLaunchKernelGGL(k_gemv_blk<16>, grid, dim3(kThreads), lds, s, W, x, y, M, K);
-      break;
-    }
-    case 32: {
-      static size_t configured = 0;
-      if (lds > configured) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemv_blk<32>),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        if (e != hipSuccess) return e;
-        configured = lds;
-      }
-      hipLaunchKernelGGL(k_gemv_blk<32>, grid, dim3(kThreads), lds, s, W, x, y, M, K);
-      break;
-    }
-    default:
-      return hipErrorInvalidValue;
-  }
-  return hipGetLastError();
+  // the hidden size of SmolLM2-135M (K = 576: the 1536x576 up-projection)
+  // compiled with K fixed; any other K at run time
+  if (R == 16) return K == 576 ? launch_gemv_blk_t<16, 576>(W, x, y, M, K, lds, s)
+                               : launch_gemv_blk_t<16, 0>(W, x, y, M, K, lds, s);
+  if (R == 32) return K == 576 ? launch_gemv_blk_t<32, 576>(W, x, y, M, K, lds, s)
+                               : launch_gemv_blk_t<32, 0>(W, x, y, M, K, lds, s);
+  return hipErrorInvalidValue;
 }
 
 size_t decode_act_floats(uint32_t H, uint32_t I, uint32_t qd, uint32_t kvd) {
