@@ -266,15 +266,48 @@ __device__ __forceinline__ void copy_cache_tile(lf* dst, const float* rows, uint
            });
 }
 
-// In place rows[d][q] *= scale(d, q) (16-byte groups q < nq of rows d < nrows,
-// row stride s4 groups): waves take rows wv, wv+4, ..., lanes the groups;
-// 8 rows' reads are issued before their writes.
-template <class F>
-__device__ __forceinline__ void scale_rows(lf4* rows, uint32_t s4, uint32_t nrows, uint32_t nq,
-                                           F scale) {
+// In place rows[d][q] *= factor (16-byte groups q < nq of rows d < nrows, row
+// stride s4 groups): waves take rows wv, wv+4, ..., lanes the groups; the
+// reads of 8 rows, and their factors, are issued before any product, so no
+// product waits on a round trip of its own.  scale_rows_by_row multiplies
+// row d by the scalar f[d] (scores: q[d] * k_j[d]); scale_rows_by_col
+// multiplies group q by the four values f4[q] (V mix: p_j * v_j[d]).  Each
+// product is f * v, one rounding.
+__device__ __forceinline__ void scale_rows_by_row(lf4* rows, uint32_t s4, uint32_t nrows,
+                                                  uint32_t nq, const lf* f) {
   const uint32_t wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
   constexpr uint32_t B = 8;
   for (uint32_t q = lane; q < nq; q += 64) {
+    for (uint32_t d0 = wv; d0 < nrows; d0 += 4 * B) {
+      f4 v[B];
+      float c[B];
+#pragma unroll
+      for (uint32_t u = 0; u < B; ++u) {
+        if (d0 + 4 * u < nrows) {
+          v[u] = rows[(size_t)(d0 + 4 * u) * s4 + q];
+          c[u] = f[d0 + 4 * u];
+        }
+      }
+#pragma unroll
+      for (uint32_t u = 0; u < B; ++u) {
+        if (d0 + 4 * u < nrows) {
+          f4 r;
+          r.x = c[u] * v[u].x;
+          r.y = c[u] * v[u].y;
+          r.z = c[u] * v[u].z;
+          r.w = c[u] * v[u].w;
+          rows[(size_t)(d0 + 4 * u) * s4 + q] = r;
+        }
+      }
+    }
+  }
+}
+__device__ __forceinline__ void scale_rows_by_col(lf4* rows, uint32_t s4, uint32_t nrows,
+                                                  uint32_t nq, const lf4* f4c) {
+  const uint32_t wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  constexpr uint32_t B = 8;
+  for (uint32_t q = lane; q < nq; q += 64) {
+    const f4 c = f4c[q];
     for (uint32_t d0 = wv; d0 < nrows; d0 += 4 * B) {
       f4 v[B];
 #pragma unroll
@@ -283,7 +316,12 @@ __device__ __forceinline__ void scale_rows(lf4* rows, uint32_t s4, uint32_t nrow
 #pragma unroll
       for (uint32_t u = 0; u < B; ++u) {
         if (d0 + 4 * u < nrows) {
-          rows[(size_t)(d0 + 4 * u) * s4 + q] = scale(d0 + 4 * u, q, v[u]);
+          f4 r;
+          r.x = c.x * v[u].x;
+          r.y = c.y * v[u].y;
+          r.z = c.z * v[u].z;
+          r.w = c.w * v[u].w;
+          rows[(size_t)(d0 + 4 * u) * s4 + q] = r;
         }
       }
     }
@@ -715,18 +753,56 @@ __device__ __forceinline__ Cand cand_pick(Cand a, Cand b) {
   if (a.v > b.v) return a;
   return b.i < a.i ? b : a;
 }
-__device__ __forceinline__ Cand cand_wave(Cand x) {
-  for (int off = 32; off > 0; off >>= 1) {
-    Cand o;
-    o.v = __shfl_xor(x.v, off, 64);
-    o.i = __shfl_xor(x.i, off, 64);
-    x = cand_pick(x, o);
-  }
-  return x;
+// Cross-lane moves within a wave64 (DPP): row_shr:n inside 16-lane rows and
+// the broadcasts of lane 15 / lane 31 into later rows; lanes without a
+// source keep `old`.  A max (min) scan with shifts 1, 2, 4, 8 leaves each
+// row's extreme in its lane 15, the two broadcasts carry them to lane 63.
+template <int CTRL, int ROWMASK>
+__device__ __forceinline__ uint32_t dpp_move(uint32_t old, uint32_t src) {
+  return (uint32_t)__builtin_amdgcn_update_dpp((int)old, (int)src, CTRL, ROWMASK, 0xF, false);
+}
+template <int CTRL, int ROWMASK>
+__device__ __forceinline__ float max_step(float x) {
+  const uint32_t u = __float_as_uint(x);
+  const float y = __uint_as_float(dpp_move<CTRL, ROWMASK>(u, u));
+  return y > x ? y : x;
+}
+template <int CTRL, int ROWMASK>
+__device__ __forceinline__ uint32_t min_step(uint32_t x) {
+  const uint32_t y = dpp_move<CTRL, ROWMASK>(x, x);
+  return y < x ? y : x;
+}
+// Largest value over the wave (inputs NaN-free), in every lane.
+__device__ __forceinline__ float wave_max(float x) {
+  x = max_step<0x111, 0xF>(x);
+  x = max_step<0x112, 0xF>(x);
+  x = max_step<0x114, 0xF>(x);
+  x = max_step<0x118, 0xF>(x);
+  x = max_step<0x142, 0xA>(x);
+  x = max_step<0x143, 0xC>(x);
+  return __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(x), 63));
+}
+__device__ __forceinline__ uint32_t wave_min(uint32_t x) {
+  x = min_step<0x111, 0xF>(x);
+  x = min_step<0x112, 0xF>(x);
+  x = min_step<0x114, 0xF>(x);
+  x = min_step<0x118, 0xF>(x);
+  x = min_step<0x142, 0xA>(x);
+  x = min_step<0x143, 0xC>(x);
+  return __builtin_amdgcn_readlane(x, 63);
+}
+// The wave's cand_pick winner in registers: the largest value, then the
+// lowest index holding a value equal to it (+0 == -0, as the strict-> scan
+// sees them).  The returned value may be either zero of a +-0 tie; callers
+// that need the winner's own bits re-read them at the index.
+__device__ __forceinline__ Cand cand_wave_dpp(Cand c) {
+  const float m = wave_max(c.i == UINT32_MAX ? -__builtin_inff() : c.v);
+  const uint32_t i = (c.i != UINT32_MAX && c.v == m) ? c.i : UINT32_MAX;
+  return Cand{m, wave_min(i)};
 }
 // Block-wide pick over the 4 waves' candidates (scratch: 8 words in LDS).
 __device__ __forceinline__ Cand cand_block(Cand c, AS_LDS uint32_t* red) {
-  c = cand_wave(c);
+  c = cand_wave_dpp(c);
   if ((threadIdx.x & 63) == 0) {
     red[2 * (threadIdx.x >> 6)] = __float_as_uint(c.v);
     red[2 * (threadIdx.x >> 6) + 1] = c.i;
@@ -896,14 +972,7 @@ __device__ __forceinline__ void run_att(const DecodeArgs& a, uint32_t l, uint32_
   if (in_lds) {
     // products q[d] * k_j[d] in place (row d scaled by q[d]); tmp = q * k_pos
     const uint32_t kq = (pos + 3) >> 2, s4 = S >> 2;
-    scale_rows((lf4*)kl, s4, hd, kq, [=](uint32_t d, uint32_t, f4 v) {
-      const float qd = qv[d];
-      v.x = qd * v.x;
-      v.y = qd * v.y;
-      v.z = qd * v.z;
-      v.w = qd * v.w;
-      return v;
-    });
+    scale_rows_by_row((lf4*)kl, s4, hd, kq, qv);
     for (uint32_t d = threadIdx.x; d < hd; d += kThreads) tmp[d] = qv[d] * kv[d];
     __syncthreads();
     for (uint32_t j = threadIdx.x; j < len; j += kThreads) {
@@ -923,14 +992,7 @@ __device__ __forceinline__ void run_att(const DecodeArgs& a, uint32_t l, uint32_
       const uint32_t n = min(TP, pos - j0);
       copy_cache_tile(kt, kb, a.max_pos, hd, j0, n, TS);
       __syncthreads();
-      scale_rows((lf4*)kt, TS >> 2, hd, (n + 3) >> 2, [=](uint32_t d, uint32_t, f4 v) {
-        const float qd = qv[d];
-        v.x = qd * v.x;
-        v.y = qd * v.y;
-        v.z = qd * v.z;
-        v.w = qd * v.w;
-        return v;
-      });
+      scale_rows_by_row((lf4*)kt, TS >> 2, hd, (n + 3) >> 2, qv);
       __syncthreads();
       for (uint32_t jj = threadIdx.x; jj < n; jj += kThreads)
         ss[j0 + jj] = (TR ? tree_col(kt + jj, hd, TS, 0.0f) : chain1(kt + jj, hd, TS, 0.0f)) *
@@ -951,7 +1013,8 @@ __device__ __forceinline__ void run_att(const DecodeArgs& a, uint32_t l, uint32_
     if (v == v) best = cand_pick(best, Cand{v, j});
   }
   const Cand b = cand_block(best, red);
-  const float mx = (ss[0] != ss[0]) ? ss[0] : b.v;
+  // the first maximum's own bits (a NaN at position 0 wins outright)
+  const float mx = (ss[0] != ss[0] || b.i == UINT32_MAX) ? ss[0] : ss[b.i];
   for (uint32_t j = threadIdx.x; j < len; j += kThreads) {
     float dlt = ss[j] - mx;
     ss[j] = exp_pinned(dlt);
@@ -986,14 +1049,7 @@ __device__ __forceinline__ void run_att(const DecodeArgs& a, uint32_t l, uint32_
     const uint32_t kq = (pos + 3) >> 2, s4 = S >> 2;
     lf4* v4 = (lf4*)vl;
     const lf4* p4 = (const lf4*)ss;
-    scale_rows(v4, s4, hd, kq, [=](uint32_t, uint32_t q, f4 v) {
-      const f4 p = p4[q];
-      v.x = p.x * v.x;
-      v.y = p.y * v.y;
-      v.z = p.z * v.z;
-      v.w = p.w * v.w;
-      return v;
-    });
+    scale_rows_by_col(v4, s4, hd, kq, p4);
     __syncthreads();
     for (uint32_t d = threadIdx.x; d < hd; d += kThreads) {
       float acc = chain_vec(vl + (size_t)d * S, pos, 0.0f);
@@ -1013,14 +1069,7 @@ __device__ __forceinline__ void run_att(const DecodeArgs& a, uint32_t l, uint32_
       copy_cache_tile(vt, vb, a.max_pos, hd, j0, n, TS);
       __syncthreads();
       const lf4* p4 = (const lf4*)(ss + j0);
-      scale_rows((lf4*)vt, TS >> 2, hd, (n + 3) >> 2, [=](uint32_t, uint32_t q, f4 v) {
-        const f4 p = p4[q];
-        v.x = p.x * v.x;
-        v.y = p.y * v.y;
-        v.z = p.z * v.z;
-        v.w = p.w * v.w;
-        return v;
-      });
+      scale_rows_by_col((lf4*)vt, TS >> 2, hd, (n + 3) >> 2, p4);
       __syncthreads();
       if (threadIdx.x < hd) acc = chain_vec(vt + (size_t)threadIdx.x * TS, n, acc);
       __syncthreads();
@@ -1149,7 +1198,7 @@ __device__ __forceinline__ void run_lm(const DecodeArgs& a, const Lds& s) {
         logits[row] = acc;
         if (acc == acc) c = Cand{acc, row};
       }
-      c = cand_wave(c);
+      c = cand_wave_dpp(c);
       if (lane == 0) {
         st_ag(a.cand + 2 * b, __float_as_uint(c.v));
         st_ag(a.cand + 2 * b + 1, c.i);
