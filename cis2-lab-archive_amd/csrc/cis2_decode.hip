@@ -266,66 +266,92 @@ __device__ __forceinline__ void copy_cache_tile(lf* dst, const float* rows, uint
            });
 }
 
-// In place rows[d][q] *= factor (16-byte groups q < nq of rows d < nrows, row
-// stride s4 groups): waves take rows wv, wv+4, ..., lanes the groups; the
-// reads of 8 rows, and their factors, are issued before any product, so no
-// product waits on a round trip of its own.  scale_rows_by_row multiplies
-// row d by the scalar f[d] (scores: q[d] * k_j[d]); scale_rows_by_col
-// multiplies group q by the four values f4[q] (V mix: p_j * v_j[d]).  Each
-// product is f * v, one rounding.
-__device__ __forceinline__ void scale_rows_by_row(lf4* rows, uint32_t s4, uint32_t nrows,
-                                                  uint32_t nq, const lf* f) {
-  const uint32_t wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  constexpr uint32_t B = 8;
-  for (uint32_t q = lane; q < nq; q += 64) {
-    for (uint32_t d0 = wv; d0 < nrows; d0 += 4 * B) {
-      f4 v[B];
-      float c[B];
+// In place rows[d][q] *= factor for the 16-byte groups q < nq of rows
+// d < nrows (row stride s4 groups).  Short rows: items i = d*nq + q are
+// spread over all threads, four per thread; long rows: lanes take a row's
+// groups.  Either way the loads (row groups and factors) are issued before
+// any product.  scale_rows_by_row multiplies row d by the scalar f[d]
+// (scores: q[d] * k_j[d]); scale_rows_by_col multiplies group q by the four
+// values f4[q] (V mix: p_j * v_j[d]).  Each product is f * v, one rounding.
+template <bool BY_ROW>
+__device__ __forceinline__ void scale_rows(lf4* rows, uint32_t s4, uint32_t nrows, uint32_t nq,
+                                           const lf* f, const lf4* f4c) {
+  if (nq >= 48) {
+    // long rows: lanes take the groups of a row (most lanes busy), waves take
+    // rows wv, wv + 4, ...; 8 rows' groups and factors are read first
+    const uint32_t wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    constexpr uint32_t RB = 8;
+    for (uint32_t q = lane; q < nq; q += 64) {
+      f4 cq = {0.0f, 0.0f, 0.0f, 0.0f};
+      if constexpr (!BY_ROW) cq = f4c[q];
+      for (uint32_t d0 = wv; d0 < nrows; d0 += 4 * RB) {
+        f4 v[RB], c[RB];
 #pragma unroll
-      for (uint32_t u = 0; u < B; ++u) {
-        if (d0 + 4 * u < nrows) {
-          v[u] = rows[(size_t)(d0 + 4 * u) * s4 + q];
-          c[u] = f[d0 + 4 * u];
+        for (uint32_t u = 0; u < RB; ++u) {
+          if (d0 + 4 * u < nrows) {
+            v[u] = rows[(size_t)(d0 + 4 * u) * s4 + q];
+            if constexpr (BY_ROW) {
+              const float fd = f[d0 + 4 * u];
+              c[u] = f4{fd, fd, fd, fd};
+            } else {
+              c[u] = cq;
+            }
+          }
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < RB; ++u) {
+          if (d0 + 4 * u < nrows) {
+            f4 r;
+            r.x = c[u].x * v[u].x;
+            r.y = c[u].y * v[u].y;
+            r.z = c[u].z * v[u].z;
+            r.w = c[u].w * v[u].w;
+            rows[(size_t)(d0 + 4 * u) * s4 + q] = r;
+          }
         }
       }
+    }
+    return;
+  }
+  // short rows: items over all threads
+  const uint32_t total = nrows * nq;
+  constexpr uint32_t B = 4;
+  for (uint32_t i0 = threadIdx.x; i0 < total; i0 += B * kThreads) {
+    f4 v[B], c[B];
+    uint32_t off[B];
 #pragma unroll
-      for (uint32_t u = 0; u < B; ++u) {
-        if (d0 + 4 * u < nrows) {
-          f4 r;
-          r.x = c[u] * v[u].x;
-          r.y = c[u] * v[u].y;
-          r.z = c[u] * v[u].z;
-          r.w = c[u] * v[u].w;
-          rows[(size_t)(d0 + 4 * u) * s4 + q] = r;
-        }
+    for (uint32_t u = 0; u < B; ++u) {
+      const uint32_t i = min(i0 + u * kThreads, total - 1);  // past the end: re-read the last
+      const uint32_t d = i / nq, q = i - d * nq;
+      off[u] = d * s4 + q;
+      v[u] = rows[off[u]];
+      if constexpr (BY_ROW) {
+        const float fd = f[d];
+        c[u] = f4{fd, fd, fd, fd};
+      } else {
+        c[u] = f4c[q];
+      }
+    }
+#pragma unroll
+    for (uint32_t u = 0; u < B; ++u) {
+      if (i0 + u * kThreads < total) {
+        f4 r;
+        r.x = c[u].x * v[u].x;
+        r.y = c[u].y * v[u].y;
+        r.z = c[u].z * v[u].z;
+        r.w = c[u].w * v[u].w;
+        rows[off[u]] = r;
       }
     }
   }
 }
+__device__ __forceinline__ void scale_rows_by_row(lf4* rows, uint32_t s4, uint32_t nrows,
+                                                  uint32_t nq, const lf* f) {
+  scale_rows<true>(rows, s4, nrows, nq, f, nullptr);
+}
 __device__ __forceinline__ void scale_rows_by_col(lf4* rows, uint32_t s4, uint32_t nrows,
                                                   uint32_t nq, const lf4* f4c) {
-  const uint32_t wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  constexpr uint32_t B = 8;
-  for (uint32_t q = lane; q < nq; q += 64) {
-    const f4 c = f4c[q];
-    for (uint32_t d0 = wv; d0 < nrows; d0 += 4 * B) {
-      f4 v[B];
-#pragma unroll
-      for (uint32_t u = 0; u < B; ++u)
-        if (d0 + 4 * u < nrows) v[u] = rows[(size_t)(d0 + 4 * u) * s4 + q];
-#pragma unroll
-      for (uint32_t u = 0; u < B; ++u) {
-        if (d0 + 4 * u < nrows) {
-          f4 r;
-          r.x = c.x * v[u].x;
-          r.y = c.y * v[u].y;
-          r.z = c.z * v[u].z;
-          r.w = c.w * v[u].w;
-          rows[(size_t)(d0 + 4 * u) * s4 + q] = r;
-        }
-      }
-    }
-  }
+  scale_rows<false>(rows, s4, nrows, nq, nullptr, f4c);
 }
 
 // Row block blk ([K/4][R][4] floats) of a blocked matrix into LDS.
