@@ -362,6 +362,24 @@ __device__ __forceinline__ void prefetch_rows(const float* W, uint32_t R, uint32
   copy_to_lds((lf4*)dst, (uint32_t)(blkf / 4), [=](uint32_t i) { return src + i; });
 }
 
+// Row block blk into LDS without holding the waves: 16-byte global->LDS
+// loads (global_load_lds_dwordx4); each wave instruction fills 64
+// consecutive 16-byte slots.  The data is in LDS once vmcnt reaches 0, and
+// readable by other waves after a barrier.
+__device__ __forceinline__ void prefetch_rows_async(const float* W, uint32_t R, uint32_t K,
+                                                    uint32_t blk, lf* dst) {
+  const uint32_t n4 = R * K / 4;
+  const uint32_t wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  gf4* src = G4(W + (size_t)blk * R * K);
+  for (uint32_t i0 = wv * 64; i0 < n4; i0 += kThreads) {  // i0: wave-uniform
+    if (i0 + lane < n4)
+      __builtin_amdgcn_global_load_lds((const AS_GLB void*)(src + i0 + lane),
+                                       (AS_LDS void*)((lf4*)dst + i0), 16, 0, 0);
+  }
+}
+// s_waitcnt vmcnt(0) (expcnt, lgkmcnt fields at their maxima: no wait).
+__device__ __forceinline__ void wait_vm0() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
 // Row block blk of two matrices of the same shape, back to back in LDS.
 __device__ __forceinline__ void prefetch_rows2(const float* A, const float* B, uint32_t R,
                                                uint32_t K, uint32_t blk, lf* dst) {
@@ -1211,12 +1229,8 @@ __device__ __forceinline__ void run_lm(const DecodeArgs& a, const Lds& s) {
   rmsnorm_lds<TR>(x, nw, a.eps, a.H, hn, hn, misc);
   AS_GLB float* logits = GW(a.logits);
   uint32_t done = 0;
-  for (uint32_t b = wg; b < a.nl; b += a.nwg) {
-    if (b != wg) {
-      prefetch_rows(a.lm, a.Rl, a.H, b, s.w);
-      __syncthreads();
-    }
-    const float acc = gemv_sel<TR, 32>(a.Rl, s.w, hn, a.H, 1, s.pad);
+  // logits and argmax candidate of block b (wave 0)
+  auto publish = [&](uint32_t b, float acc) {
     if (wv == 0) {
       const uint32_t row = b * a.Rl + lane;
       Cand c = {0.0f, UINT32_MAX};
@@ -1231,8 +1245,40 @@ __device__ __forceinline__ void run_lm(const DecodeArgs& a, const Lds& s) {
       }
       if (b == 0 && lane == 0) st_ag(a.cand + 2 * a.nl, acc != acc ? 1u : 0u);
     }
-    ++done;
-    __syncthreads();
+  };
+  const size_t blkf = (size_t)a.Rl * a.H;
+  if (2 * blkf * 4 <= decode_wregion_bytes(a)) {
+    // two LDS buffers: block b + nwg streams in while block b is computed;
+    // block b's results are published after the wait, so the wait covers
+    // only loads and stores issued one GEMV earlier
+    lf* cur = s.w;
+    lf* nxt = s.w + blkf;
+    uint32_t prev = UINT32_MAX;
+    float prev_acc = 0.0f;
+    for (uint32_t b = wg; b < a.nl; b += a.nwg) {
+      if (prev != UINT32_MAX) publish(prev, prev_acc);
+      if (b + a.nwg < a.nl) prefetch_rows_async(a.lm, a.Rl, a.H, b + a.nwg, nxt);
+      prev_acc = gemv_sel<TR, 32>(a.Rl, cur, hn, a.H, 1, s.pad);
+      prev = b;
+      ++done;
+      wait_vm0();
+      __syncthreads();
+      lf* t = cur;
+      cur = nxt;
+      nxt = t;
+    }
+    if (prev != UINT32_MAX) publish(prev, prev_acc);
+  } else {
+    for (uint32_t b = wg; b < a.nl; b += a.nwg) {
+      if (b != wg) {
+        prefetch_rows(a.lm, a.Rl, a.H, b, s.w);
+        __syncthreads();
+      }
+      const float acc = gemv_sel<TR, 32>(a.Rl, s.w, hn, a.H, 1, s.pad);
+      publish(b, acc);
+      ++done;
+      __syncthreads();
+    }
   }
   stamp(a, L - 1, P_LM, wg, 2);
   if (done == 0) return;  // no blocks here (fewer blocks than workgroups)
