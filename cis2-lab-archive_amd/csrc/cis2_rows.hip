@@ -16,8 +16,10 @@ namespace {
 typedef float v4 __attribute__((ext_vector_type(4)));
 
 constexpr uint32_t kT = 256;
-// LDS per batched-GEMM workgroup: two workgroups fit one CU.
+// LDS per batched-GEMM workgroup: two workgroups fit one CU; small grids
+// may use one workgroup's worth of almost all of it.
 constexpr uint32_t kBgemmLds = 78 * 1024;
+constexpr uint32_t kBgemmLdsBig = 150 * 1024;
 
 // ---------------------------------------------------------------------------
 // Batched GEMM.  A workgroup owns one R-row block of W and TB = 256 / R batch
@@ -186,14 +188,15 @@ __global__ __launch_bounds__(256) void k_attention_rows(const float* __restrict_
                                                         uint32_t hd, uint32_t max_pos,
                                                         uint64_t seq_stride, float scale,
                                                         float* out, uint32_t tree) {
-  extern __shared__ float sh[];
+  extern __shared__ v4 sh4[];  // 16-byte aligned: the scores are read 16 bytes at a time
+  float* sh = reinterpret_cast<float*>(sh4);
   __shared__ Pick red[4];
   __shared__ float s_den;
   const uint32_t r = blockIdx.x, qh = blockIdx.y;  // rows on x: up to 2^31 of them
   const uint32_t group = nh / nkv, kvh = qh / group, pos = rows.pos[r], len = pos + 1;
   const size_t sb = (size_t)rows.seq[r] * seq_stride;
   float* sq = sh;
-  float* ss = sh + hd;
+  float* ss = sh + ((hd + 3) & ~3u);
   float* part = ss + len;
   const float* qv = q + (size_t)r * nh * hd + (size_t)qh * hd;
   for (uint32_t d = threadIdx.x; d < hd; d += blockDim.x) sq[d] = qv[d];
@@ -210,8 +213,18 @@ __global__ __launch_bounds__(256) void k_attention_rows(const float* __restrict_
         acc = acc + tree32(l);
       }
     } else {
-      // the column's loads go out 16 at a time, then their 16 chain steps
+      // the column's loads go out 64 at a time, then their 64 chain steps
       uint32_t d0 = 0;
+      for (; d0 + 64 <= hd; d0 += 64) {
+        float kv[64];
+#pragma unroll
+        for (uint32_t i = 0; i < 64; ++i) kv[i] = kb[(size_t)(d0 + i) * max_pos + j];
+#pragma unroll
+        for (uint32_t i = 0; i < 64; ++i) {
+          float p = sq[d0 + i] * kv[i];
+          acc = acc + p;
+        }
+      }
       for (; d0 + 16 <= hd; d0 += 16) {
         float kv[16];
 #pragma unroll
@@ -257,7 +270,22 @@ __global__ __launch_bounds__(256) void k_attention_rows(const float* __restrict_
     if (tree) {
       for (uint32_t t = 0; t < nb; ++t) acc = acc + part[t];
     } else {
-      for (uint32_t j = 0; j < len; ++j) acc = acc + ss[j];
+      // 16-byte reads (every lane the same address), 8 of them per batch
+      const v4* s4p = reinterpret_cast<const v4*>(ss);
+      uint32_t j = 0;
+      for (; j + 32 <= len; j += 32) {
+        v4 e[8];
+#pragma unroll
+        for (uint32_t u = 0; u < 8; ++u) e[u] = s4p[j / 4 + u];
+#pragma unroll
+        for (uint32_t u = 0; u < 8; ++u) {
+          acc = acc + e[u].x;
+          acc = acc + e[u].y;
+          acc = acc + e[u].z;
+          acc = acc + e[u].w;
+        }
+      }
+      for (; j < len; ++j) acc = acc + ss[j];
     }
     if (threadIdx.x == 0) s_den = acc;
   }
@@ -274,20 +302,32 @@ __global__ __launch_bounds__(256) void k_attention_rows(const float* __restrict_
     // row d of V is contiguous: 16-byte loads, 8 of them (32 positions) in
     // flight ahead of the chain
     const v4* vr4 = reinterpret_cast<const v4*>(vb + (size_t)d * max_pos);
+    const v4* p4 = reinterpret_cast<const v4*>(ss);
     float acc = 0.0f;
     uint32_t j = 0;
-    for (; j + 32 <= len; j += 32) {
-      v4 v[8];
+    constexpr uint32_t VB = 16;  // 64 positions per batch; the next batch loads meanwhile
+    v4 cur[VB], nxt[VB];
+    const uint32_t full = len / (4 * VB);
+    if (full > 0) {
 #pragma unroll
-      for (uint32_t u = 0; u < 8; ++u) v[u] = vr4[j / 4 + u];
+      for (uint32_t u = 0; u < VB; ++u) cur[u] = vr4[u];
+    }
+    for (uint32_t bt = 0; bt < full; ++bt, j += 4 * VB) {
+      if (bt + 1 < full) {
 #pragma unroll
-      for (uint32_t u = 0; u < 8; ++u) {
-        float p;
-        p = ss[j + 4 * u] * v[u].x; acc = acc + p;
-        p = ss[j + 4 * u + 1] * v[u].y; acc = acc + p;
-        p = ss[j + 4 * u + 2] * v[u].z; acc = acc + p;
-        p = ss[j + 4 * u + 3] * v[u].w; acc = acc + p;
+        for (uint32_t u = 0; u < VB; ++u) nxt[u] = vr4[(j + 4 * VB) / 4 + u];
       }
+#pragma unroll
+      for (uint32_t u = 0; u < VB; ++u) {
+        const v4 pp = p4[j / 4 + u];
+        float p;
+        p = pp.x * cur[u].x; acc = acc + p;
+        p = pp.y * cur[u].y; acc = acc + p;
+        p = pp.z * cur[u].z; acc = acc + p;
+        p = pp.w * cur[u].w; acc = acc + p;
+      }
+#pragma unroll
+      for (uint32_t u = 0; u < VB; ++u) cur[u] = nxt[u];
     }
     const float* vr = vb + (size_t)d * max_pos;
     for (; j < len; ++j) {
@@ -336,13 +376,26 @@ __global__ __launch_bounds__(1024) void k_argmax_rows(const float* __restrict__ 
 hipError_t launch_bgemm(const BgemmSeg& s, uint32_t n, bool tree, hipStream_t st) {
   if (n == 0) return hipSuccess;
   if (s.K % 4 || s.ldx % 4 || s.R == 0 || s.R > kT || s.M == 0) return hipErrorInvalidValue;
+  static int ncu = 0;
+  if (ncu == 0) {
+    int dev = 0;
+    (void)hipGetDevice(&dev);
+    if (hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        ncu <= 0)
+      ncu = 256;
+  }
   BgemmArgs a;
   a.s = s;
   a.n = n;
   a.TB = kT / s.R;
   a.tree = tree ? 1u : 0u;
-  // largest chunk (a multiple of 32 k) whose W slice and X rows fit the budget
-  const uint32_t q_fit = (kBgemmLds / 16 - a.TB) / (s.R + a.TB);
+  const uint64_t wgs = (uint64_t)((s.M + s.R - 1) / s.R) * ((n + a.TB - 1) / a.TB);
+  // a grid of at most two workgroups per CU may take most of a CU's LDS per
+  // workgroup (fewer K chunks, each a full round trip); larger grids keep
+  // two workgroups per CU
+  const uint32_t budget = wgs <= 2 * (uint64_t)ncu ? kBgemmLdsBig : kBgemmLds;
+  // largest chunk (a multiple of 32 k) whose W slice and X rows fit
+  const uint32_t q_fit = (budget / 16 - a.TB) / (s.R + a.TB);
   uint32_t KC = (q_fit * 4) & ~31u;
   if (KC == 0) return hipErrorInvalidValue;
   const uint32_t K32 = (s.K + 31) & ~31u;
@@ -352,7 +405,8 @@ hipError_t launch_bgemm(const BgemmSeg& s, uint32_t n, bool tree, hipStream_t st
   static bool configured = false;
   if (!configured) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_bgemm),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)kBgemmLds);
+                                       hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       (int)kBgemmLdsBig);
     if (e != hipSuccess) return e;
     configured = true;
   }
@@ -386,8 +440,8 @@ hipError_t launch_attention_rows(const float* q, const float* kc, const float* v
   if (rows.n == 0) return hipSuccess;
   if (nkv == 0 || nh % nkv || max_len == 0 || max_len > max_pos || max_pos % 4)
     return hipErrorInvalidValue;
-  // q, scores, and the denominator's block partials
-  const size_t shmem = ((size_t)hd + max_len + (max_len + 31) / 32) * sizeof(float);
+  // q (rounded to 16 bytes), scores, and the denominator's block partials
+  const size_t shmem = (((size_t)hd + 3) / 4 * 4 + max_len + (max_len + 31) / 32) * sizeof(float);
   if (shmem > 60 * 1024) return hipErrorInvalidValue;
   hipLaunchKernelGGL(k_attention_rows, dim3(rows.n, nh), dim3(kT), shmem, st, q, kc, vc, rows,
                      nh, nkv, hd, max_pos, seq_stride, scale, out, tree ? 1u : 0u);
