@@ -16,6 +16,19 @@ namespace {
 typedef float v4 __attribute__((ext_vector_type(4)));
 
 constexpr uint32_t kT = 256;
+
+#define AS_LDS __attribute__((address_space(3)))
+#define AS_GLB __attribute__((address_space(1)))
+
+// 16 bytes from global memory straight into LDS (global_load_lds_dwordx4).
+// The LDS address is dst_wave + 16 * lane, with dst_wave uniform across the
+// wave: lanes that take part fill consecutive slots.  The data is in LDS
+// once vmcnt reaches 0, and visible to other waves after a barrier.
+__device__ __forceinline__ void lds_load16(const v4* src, v4* dst_wave) {
+  __builtin_amdgcn_global_load_lds((const AS_GLB void*)src, (AS_LDS void*)dst_wave, 16, 0, 0);
+}
+// s_waitcnt vmcnt(0) (expcnt, lgkmcnt fields at their maxima: no wait).
+__device__ __forceinline__ void wait_vm0() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 // LDS per batched-GEMM workgroup: two workgroups fit one CU; small grids
 // may use one workgroup's worth of almost all of it.
 constexpr uint32_t kBgemmLds = 78 * 1024;
@@ -41,6 +54,7 @@ __global__ __launch_bounds__(256) void k_bgemm(BgemmArgs a) {
   const uint32_t R = g.R, TB = a.TB, KC = a.KC, K = g.K;
   const uint32_t blk = blockIdx.x, b0 = blockIdx.y * TB, t = threadIdx.x;
   const uint32_t r = t % R, bb = t / R;
+  const uint32_t wv = __builtin_amdgcn_readfirstlane(t >> 6), lane = t & 63;
   const bool live = t < R * TB;
   const uint32_t qmax = KC / 4, xs4 = qmax + 1;  // padded X rows: no bank aliasing
   v4* Ws = sm;
@@ -49,12 +63,19 @@ __global__ __launch_bounds__(256) void k_bgemm(BgemmArgs a) {
   float acc = 0.0f;
   for (uint32_t k0 = 0; k0 < K; k0 += KC) {
     const uint32_t q4 = std::min(KC, K - k0) / 4, g0 = k0 / 4;
-    for (uint32_t i = t; i < q4 * R; i += kT) Ws[i] = Wg[(size_t)g0 * R + i];
-    for (uint32_t i = t; i < TB * q4; i += kT) {
-      const uint32_t bx = i / q4, q = i - bx * q4;
+    // every load of the chunk in flight at once, straight into LDS; each
+    // wave instruction fills 64 consecutive 16-byte slots
+    const uint32_t nw4 = q4 * R;
+    for (uint32_t i0 = wv * 64; i0 < nw4; i0 += kT)
+      if (i0 + lane < nw4) lds_load16(Wg + (size_t)g0 * R + i0 + lane, Ws + i0);
+    const uint32_t pieces = (q4 + 63) / 64;
+    for (uint32_t j = wv; j < TB * pieces; j += kT / 64) {
+      const uint32_t bx = j / pieces, q0 = (j - bx * pieces) * 64;
       const uint32_t row = std::min(b0 + bx, a.n - 1);
-      Xs[bx * xs4 + q] = reinterpret_cast<const v4*>(g.X + (size_t)row * g.ldx)[g0 + q];
+      const v4* xr = reinterpret_cast<const v4*>(g.X + (size_t)row * g.ldx) + g0 + q0;
+      if (q0 + lane < q4) lds_load16(xr + lane, Xs + bx * xs4 + q0);
     }
+    wait_vm0();
     __syncthreads();
     if (live) {
       const v4* wp = Ws + r;
