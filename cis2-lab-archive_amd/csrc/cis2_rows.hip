@@ -42,25 +42,92 @@ constexpr uint32_t kBgemmLdsBig = 150 * 1024;
 // then each thread continues its own chain acc = acc + W[m][k] * X[b][k],
 // k ascending (code/cis2-fp/src/main.rs:228-243, math.rs:40-48); in tree
 // mode the chain adds one tree32 block result per 32 k (math.rs:60-125).
+//
+// One launch may cover up to three matrices that read the same X (q, k and
+// v): the grid's x blocks run over the segments in turn.  DUAL computes two
+// chains per thread over W and W2 (gate and up) and stores
+// silu(gate) * up (main.rs:484-487).  NORM applies the RMSNorm of each X row
+// first (main.rs:245-260): the row's squares are summed in one strict chain
+// (or tree32 blocks) from 0 while the first chunk's loads are in flight,
+// inv = 1/sqrt(sum/K + eps), and each staged element becomes (x*inv)*w[k].
 // ---------------------------------------------------------------------------
+constexpr uint32_t kMaxSegs = 3;
 struct BgemmArgs {
-  BgemmSeg s;
-  uint32_t n, TB, KC, tree;
+  BgemmSeg s[kMaxSegs];
+  uint32_t blk0[kMaxSegs + 1];  // first x block of each segment; blk0[nseg] = grid.x
+  uint32_t nseg, n, TB, KC, tree;
+  const float* W2;  // DUAL
+  const float* nw;  // NORM
+  float eps;
 };
 
+// RMSNorm factor of one row of K floats (K % 4 == 0), read from global
+// memory 16 loads ahead of the chain.
+__device__ float row_inv_rms(const float* x, uint32_t K, float eps, bool tree) {
+  const v4* x4 = reinterpret_cast<const v4*>(x);
+  const uint32_t K4 = K / 4;
+  float acc = 0.0f;
+  if (tree) {
+    for (uint32_t q0 = 0; q0 < K4; q0 += 8) {
+      float l[32];
+#pragma unroll
+      for (uint32_t i = 0; i < 8; ++i) {
+        const v4 v = q0 + i < K4 ? x4[q0 + i] : v4{0.0f, 0.0f, 0.0f, 0.0f};
+        l[4 * i] = v.x * v.x;
+        l[4 * i + 1] = v.y * v.y;
+        l[4 * i + 2] = v.z * v.z;
+        l[4 * i + 3] = v.w * v.w;
+      }
+      acc = acc + tree32(l);
+    }
+  } else {
+    constexpr uint32_t B = 16;
+    uint32_t q0 = 0;
+    for (; q0 + B <= K4; q0 += B) {
+      v4 v[B];
+#pragma unroll
+      for (uint32_t i = 0; i < B; ++i) v[i] = x4[q0 + i];
+#pragma unroll
+      for (uint32_t i = 0; i < B; ++i) {
+        float sq;
+        sq = v[i].x * v[i].x; acc = acc + sq;
+        sq = v[i].y * v[i].y; acc = acc + sq;
+        sq = v[i].z * v[i].z; acc = acc + sq;
+        sq = v[i].w * v[i].w; acc = acc + sq;
+      }
+    }
+    for (; q0 < K4; ++q0) {
+      const v4 v = x4[q0];
+      float sq;
+      sq = v.x * v.x; acc = acc + sq;
+      sq = v.y * v.y; acc = acc + sq;
+      sq = v.z * v.z; acc = acc + sq;
+      sq = v.w * v.w; acc = acc + sq;
+    }
+  }
+  const float mean = acc / (float)K;
+  const float arg = mean + eps;
+  return rsqrt_cr(arg);
+}
+
+template <bool DUAL, bool NORM>
 __global__ __launch_bounds__(256) void k_bgemm(BgemmArgs a) {
   extern __shared__ v4 sm[];
-  const BgemmSeg& g = a.s;
+  __shared__ float s_inv[kT];
+  uint32_t si = 0;
+  if (a.nseg > 1 && blockIdx.x >= a.blk0[1]) si = (a.nseg > 2 && blockIdx.x >= a.blk0[2]) ? 2 : 1;
+  const BgemmSeg g = si == 0 ? a.s[0] : (si == 1 ? a.s[1] : a.s[2]);
   const uint32_t R = g.R, TB = a.TB, KC = a.KC, K = g.K;
-  const uint32_t blk = blockIdx.x, b0 = blockIdx.y * TB, t = threadIdx.x;
+  const uint32_t blk = blockIdx.x - a.blk0[si], b0 = blockIdx.y * TB, t = threadIdx.x;
   const uint32_t r = t % R, bb = t / R;
   const uint32_t wv = __builtin_amdgcn_readfirstlane(t >> 6), lane = t & 63;
   const bool live = t < R * TB;
   const uint32_t qmax = KC / 4, xs4 = qmax + 1;  // padded X rows: no bank aliasing
-  v4* Ws = sm;
-  v4* Xs = sm + (size_t)qmax * R;
+  v4* Ws = sm;                                   // [q4][R] (DUAL: then W2's at Ws + qmax * R)
+  v4* Xs = sm + (size_t)(DUAL ? 2 : 1) * qmax * R;
   const v4* Wg = reinterpret_cast<const v4*>(g.W + (size_t)blk * R * K);
-  float acc = 0.0f;
+  const v4* Wg2 = DUAL ? reinterpret_cast<const v4*>(a.W2 + (size_t)blk * R * K) : nullptr;
+  float acc = 0.0f, acc2 = 0.0f;
   for (uint32_t k0 = 0; k0 < K; k0 += KC) {
     const uint32_t q4 = std::min(KC, K - k0) / 4, g0 = k0 / 4;
     // every load of the chunk in flight at once, straight into LDS; each
@@ -68,6 +135,10 @@ __global__ __launch_bounds__(256) void k_bgemm(BgemmArgs a) {
     const uint32_t nw4 = q4 * R;
     for (uint32_t i0 = wv * 64; i0 < nw4; i0 += kT)
       if (i0 + lane < nw4) lds_load16(Wg + (size_t)g0 * R + i0 + lane, Ws + i0);
+    if (DUAL) {
+      for (uint32_t i0 = wv * 64; i0 < nw4; i0 += kT)
+        if (i0 + lane < nw4) lds_load16(Wg2 + (size_t)g0 * R + i0 + lane, Ws + qmax * R + i0);
+    }
     const uint32_t pieces = (q4 + 63) / 64;
     for (uint32_t j = wv; j < TB * pieces; j += kT / 64) {
       const uint32_t bx = j / pieces, q0 = (j - bx * pieces) * 64;
@@ -75,27 +146,54 @@ __global__ __launch_bounds__(256) void k_bgemm(BgemmArgs a) {
       const v4* xr = reinterpret_cast<const v4*>(g.X + (size_t)row * g.ldx) + g0 + q0;
       if (q0 + lane < q4) lds_load16(xr + lane, Xs + bx * xs4 + q0);
     }
+    if (NORM && k0 == 0 && t < TB)
+      s_inv[t] = row_inv_rms(g.X + (size_t)std::min(b0 + t, a.n - 1) * g.ldx, K, a.eps, a.tree);
     wait_vm0();
     __syncthreads();
+    if (NORM) {
+      const v4* nw4p = reinterpret_cast<const v4*>(a.nw) + g0;
+      for (uint32_t i = t; i < TB * q4; i += kT) {
+        const uint32_t bx = i / q4, q = i - bx * q4;
+        const float inv = s_inv[bx];
+        const v4 x = Xs[bx * xs4 + q], w = nw4p[q];
+        v4 y;
+        float sx;
+        sx = x.x * inv; y.x = sx * w.x;
+        sx = x.y * inv; y.y = sx * w.y;
+        sx = x.z * inv; y.z = sx * w.z;
+        sx = x.w * inv; y.w = sx * w.w;
+        Xs[bx * xs4 + q] = y;
+      }
+      __syncthreads();
+    }
     if (live) {
       const v4* wp = Ws + r;
+      const v4* wp2 = Ws + qmax * R + r;
       const v4* xp = Xs + bb * xs4;
       if (a.tree) {
         for (uint32_t q = 0; q < q4; q += 8) {
-          float l[32];
+          float l[32], l2[32];
 #pragma unroll
           for (uint32_t j = 0; j < 8; ++j) {
-            v4 w = v4{0.0f, 0.0f, 0.0f, 0.0f}, x = w;
+            v4 w = v4{0.0f, 0.0f, 0.0f, 0.0f}, x = w, w2 = w;
             if (q + j < q4) {
               w = wp[(size_t)(q + j) * R];
               x = xp[q + j];
+              if (DUAL) w2 = wp2[(size_t)(q + j) * R];
             }
             l[4 * j] = w.x * x.x;
             l[4 * j + 1] = w.y * x.y;
             l[4 * j + 2] = w.z * x.z;
             l[4 * j + 3] = w.w * x.w;
+            if (DUAL) {
+              l2[4 * j] = w2.x * x.x;
+              l2[4 * j + 1] = w2.y * x.y;
+              l2[4 * j + 2] = w2.z * x.z;
+              l2[4 * j + 3] = w2.w * x.w;
+            }
           }
           acc = acc + tree32(l);
+          if (DUAL) acc2 = acc2 + tree32(l2);
         }
       } else {
 #pragma unroll 4
@@ -106,6 +204,13 @@ __global__ __launch_bounds__(256) void k_bgemm(BgemmArgs a) {
           p = w.y * x.y; acc = acc + p;
           p = w.z * x.z; acc = acc + p;
           p = w.w * x.w; acc = acc + p;
+          if (DUAL) {
+            const v4 w2 = wp2[(size_t)q * R];
+            p = w2.x * x.x; acc2 = acc2 + p;
+            p = w2.y * x.y; acc2 = acc2 + p;
+            p = w2.z * x.z; acc2 = acc2 + p;
+            p = w2.w * x.w; acc2 = acc2 + p;
+          }
         }
       }
     }
@@ -114,8 +219,14 @@ __global__ __launch_bounds__(256) void k_bgemm(BgemmArgs a) {
   const uint32_t row = b0 + bb, m = blk * R + r;
   if (live && row < a.n && m < g.M) {
     float y = acc;
-    if (g.epi == kEpiBias) y = acc + g.add[m];
-    else if (g.epi == kEpiResidual) y = g.add[(size_t)row * g.ldadd + m] + acc;
+    if (DUAL) {
+      const float sg = silu_pinned(acc);
+      y = sg * acc2;
+    } else if (g.epi == kEpiBias) {
+      y = acc + g.add[m];
+    } else if (g.epi == kEpiResidual) {
+      y = g.add[(size_t)row * g.ldadd + m] + acc;
+    }
     g.Y[(size_t)row * g.ldy + m] = y;
   }
 }
@@ -376,6 +487,11 @@ __global__ void k_gather_rows(const float* __restrict__ src, const uint32_t* __r
   for (uint32_t i = threadIdx.x; i < width; i += blockDim.x) dst[(size_t)r * width + i] = s[i];
 }
 
+__global__ void k_advance_rows(uint32_t* pos, uint32_t n) {
+  const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) pos[i] = pos[i] + 1u;
+}
+
 __global__ __launch_bounds__(1024) void k_argmax_rows(const float* __restrict__ v,
                                                       uint32_t width, uint32_t* out) {
   __shared__ Pick red[16];
@@ -394,9 +510,26 @@ __global__ __launch_bounds__(1024) void k_argmax_rows(const float* __restrict__ 
 
 }  // namespace
 
-hipError_t launch_bgemm(const BgemmSeg& s, uint32_t n, bool tree, hipStream_t st) {
+template <bool DUAL, bool NORM>
+hipError_t launch_bgemm_t(const BgemmArgs& a, dim3 grid, size_t lds, hipStream_t st) {
+  static bool configured = false;
+  if (!configured) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_bgemm<DUAL, NORM>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       (int)kBgemmLdsBig);
+    if (e != hipSuccess) return e;
+    configured = true;
+  }
+  hipLaunchKernelGGL((k_bgemm<DUAL, NORM>), grid, dim3(kT), lds, st, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_bgemm_multi(const BgemmSeg* segs, uint32_t nseg, uint32_t n,
+                              const BgemmOpts& o, hipStream_t st) {
   if (n == 0) return hipSuccess;
-  if (s.K % 4 || s.ldx % 4 || s.R == 0 || s.R > kT || s.M == 0) return hipErrorInvalidValue;
+  if (nseg == 0 || nseg > kMaxSegs || (o.W2 && nseg != 1)) return hipErrorInvalidValue;
+  const BgemmSeg& s0 = segs[0];
+  if (s0.K % 4 || s0.ldx % 4 || s0.R == 0 || s0.R > kT) return hipErrorInvalidValue;
   static int ncu = 0;
   if (ncu == 0) {
     int dev = 0;
@@ -405,35 +538,51 @@ hipError_t launch_bgemm(const BgemmSeg& s, uint32_t n, bool tree, hipStream_t st
         ncu <= 0)
       ncu = 256;
   }
-  BgemmArgs a;
-  a.s = s;
+  BgemmArgs a = {};
+  a.blk0[0] = 0;
+  for (uint32_t i = 0; i < nseg; ++i) {
+    const BgemmSeg& s = segs[i];
+    if (s.M == 0 || s.K != s0.K || s.R != s0.R || s.X != s0.X || s.ldx != s0.ldx)
+      return hipErrorInvalidValue;
+    a.s[i] = s;
+    a.blk0[i + 1] = a.blk0[i] + (s.M + s.R - 1) / s.R;
+  }
+  for (uint32_t i = nseg; i < kMaxSegs; ++i) {
+    a.s[i] = s0;
+    a.blk0[i + 1] = a.blk0[nseg];
+  }
+  a.nseg = nseg;
   a.n = n;
-  a.TB = kT / s.R;
-  a.tree = tree ? 1u : 0u;
-  const uint64_t wgs = (uint64_t)((s.M + s.R - 1) / s.R) * ((n + a.TB - 1) / a.TB);
+  a.TB = kT / s0.R;
+  a.tree = o.tree ? 1u : 0u;
+  a.W2 = o.W2;
+  a.nw = o.norm_w;
+  a.eps = o.eps;
+  const uint32_t S = o.W2 ? 2 : 1;
+  const uint64_t wgs = (uint64_t)a.blk0[nseg] * ((n + a.TB - 1) / a.TB);
   // a grid of at most two workgroups per CU may take most of a CU's LDS per
   // workgroup (fewer K chunks, each a full round trip); larger grids keep
   // two workgroups per CU
   const uint32_t budget = wgs <= 2 * (uint64_t)ncu ? kBgemmLdsBig : kBgemmLds;
-  // largest chunk (a multiple of 32 k) whose W slice and X rows fit
-  const uint32_t q_fit = (budget / 16 - a.TB) / (s.R + a.TB);
+  // largest chunk (a multiple of 32 k) whose W slices and X rows fit
+  const uint32_t q_fit = (budget / 16 - a.TB) / (S * s0.R + a.TB);
   uint32_t KC = (q_fit * 4) & ~31u;
   if (KC == 0) return hipErrorInvalidValue;
-  const uint32_t K32 = (s.K + 31) & ~31u;
+  const uint32_t K32 = (s0.K + 31) & ~31u;
   if (KC > K32) KC = K32;
   a.KC = KC;
-  const size_t lds = ((size_t)(KC / 4) * s.R + (size_t)a.TB * (KC / 4 + 1)) * 16;
-  static bool configured = false;
-  if (!configured) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_bgemm),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       (int)kBgemmLdsBig);
-    if (e != hipSuccess) return e;
-    configured = true;
-  }
-  const dim3 grid((s.M + s.R - 1) / s.R, (n + a.TB - 1) / a.TB);
-  hipLaunchKernelGGL(k_bgemm, grid, dim3(kT), lds, st, a);
-  return hipGetLastError();
+  const size_t lds = ((size_t)(KC / 4) * s0.R * S + (size_t)a.TB * (KC / 4 + 1)) * 16;
+  const dim3 grid(a.blk0[nseg], (n + a.TB - 1) / a.TB);
+  if (o.W2) return o.norm_w ? launch_bgemm_t<true, true>(a, grid, lds, st)
+                            : launch_bgemm_t<true, false>(a, grid, lds, st);
+  return o.norm_w ? launch_bgemm_t<false, true>(a, grid, lds, st)
+                  : launch_bgemm_t<false, false>(a, grid, lds, st);
+}
+
+hipError_t launch_bgemm(const BgemmSeg& s, uint32_t n, bool tree, hipStream_t st) {
+  BgemmOpts o;
+  o.tree = tree;
+  return launch_bgemm_multi(&s, 1, n, o, st);
 }
 
 hipError_t launch_embed_rows(const float* E, RowsDesc rows, uint32_t H, uint32_t vocab,
@@ -481,6 +630,12 @@ hipError_t launch_gather_rows(const float* src, const uint32_t* idx, uint32_t n,
                               float* dst, hipStream_t st) {
   if (n == 0) return hipSuccess;
   hipLaunchKernelGGL(k_gather_rows, dim3(n), dim3(kT), 0, st, src, idx, width, dst);
+  return hipGetLastError();
+}
+
+hipError_t launch_advance_rows(uint32_t* pos, uint32_t n, hipStream_t st) {
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(k_advance_rows, dim3((n + kT - 1) / kT), dim3(kT), 0, st, pos, n);
   return hipGetLastError();
 }
 

@@ -30,6 +30,22 @@ struct BgemmSeg {
 };
 hipError_t launch_bgemm(const BgemmSeg& s, uint32_t n, bool tree, hipStream_t st);
 
+// Options of a multi-matrix launch.
+struct BgemmOpts {
+  // RMSNorm weight (main.rs:245-260): each X row is normalised first,
+  // inv = 1/sqrt(sum of squares / K + eps), x' = (x*inv)*w[k]
+  const float* norm_w = nullptr;
+  float eps = 0.0f;
+  // second matrix of segs[0]'s shape and layout (one segment only):
+  // Y = silu(X.W) * (X.W2), the gated MLP's hidden row (main.rs:484-487)
+  const float* W2 = nullptr;
+  bool tree = false;
+};
+// Up to three matrices over the same X rows (same K, R, X, ldx) in one
+// launch, each with its own M, Y and epilogue.
+hipError_t launch_bgemm_multi(const BgemmSeg* segs, uint32_t nseg, uint32_t n,
+                              const BgemmOpts& o, hipStream_t st);
+
 // Per-row device descriptors: seq[r], pos[r], tok[r].
 struct RowsDesc {
   const uint32_t* seq;
@@ -61,6 +77,8 @@ hipError_t launch_silu_mul(const float* g, const float* u, float* hid, uint64_t 
 // dst[i] = src[idx[i]] rows of `width` floats, i < n.
 hipError_t launch_gather_rows(const float* src, const uint32_t* idx, uint32_t n, uint32_t width,
                               float* dst, hipStream_t st);
+// pos[i] += 1 for i < n (the next decode step's positions, on the device).
+hipError_t launch_advance_rows(uint32_t* pos, uint32_t n, hipStream_t st);
 // Greedy argmax of each of n rows of v (stride `width`): strict >, first
 // maximum wins, NaN at index 0 wins.
 hipError_t launch_argmax_rows(const float* v, uint32_t n, uint32_t width, uint32_t* out,

@@ -72,11 +72,15 @@ struct Session {
 struct RowsBuf {
   uint32_t cap = 0, lcap = 0;  // rows / logit rows allocated
   float *h = nullptr, *h2 = nullptr, *x = nullptr, *q = nullptr, *k = nullptr, *v = nullptr,
-        *att = nullptr, *g = nullptr, *u = nullptr, *hid = nullptr;  // [cap][width]
+        *att = nullptr, *hid = nullptr;  // [cap][width]
   float *lx = nullptr, *logits = nullptr;                            // [lcap][H], [lcap][V]
   uint32_t *seq = nullptr, *pos = nullptr, *tok = nullptr;           // [cap]
   uint32_t *lrows = nullptr, *arg = nullptr;                         // [lcap]
-  std::vector<void*> mem, lmem;
+  // the decode steps' second logit / argmax buffer, [cap2][V] and [cap2]
+  float* logits2 = nullptr;
+  uint32_t* arg2 = nullptr;
+  uint32_t cap2 = 0;
+  std::vector<void*> mem, lmem, mem2;
 };
 
 }  // namespace
@@ -86,6 +90,7 @@ struct cis2_ctx {
   uint32_t qd = 0, kvd = 0;
   float scale = 0.0f;
   hipStream_t st = nullptr;
+  hipStream_t cs = nullptr;  // device-to-host copies that overlap the next pass
   std::vector<Layer> L;
   float *embed = nullptr, *lm_head = nullptr, *final_norm = nullptr;
   float *inv_freq = nullptr, *rope_cs = nullptr;
@@ -417,8 +422,7 @@ int rows_reserve(cis2_ctx* c, uint32_t n, uint32_t nl) {
     bool ok = (b.h = rows_alloc<float>(b.mem, n * H)) && (b.h2 = rows_alloc<float>(b.mem, n * H)) &&
               (b.x = rows_alloc<float>(b.mem, n * H)) && (b.q = rows_alloc<float>(b.mem, n * QD)) &&
               (b.k = rows_alloc<float>(b.mem, n * KV)) && (b.v = rows_alloc<float>(b.mem, n * KV)) &&
-              (b.att = rows_alloc<float>(b.mem, n * QD)) && (b.g = rows_alloc<float>(b.mem, n * I)) &&
-              (b.u = rows_alloc<float>(b.mem, n * I)) && (b.hid = rows_alloc<float>(b.mem, n * I)) &&
+              (b.att = rows_alloc<float>(b.mem, n * QD)) && (b.hid = rows_alloc<float>(b.mem, n * I)) &&
               (b.seq = rows_alloc<uint32_t>(b.mem, n)) && (b.pos = rows_alloc<uint32_t>(b.mem, n)) &&
               (b.tok = rows_alloc<uint32_t>(b.mem, n));
     if (!ok) return fail(c, CIS2_E_OOM, "row buffers");
@@ -446,7 +450,14 @@ int rows_reserve(cis2_ctx* c, uint32_t n, uint32_t nl) {
 // each other causally.  max_len = 1 + the largest position.  The final
 // norm, LM head and argmax run for the nl rows listed in rows.lrows:
 // logits[i] and arg[i] belong to row lrows[i].
-int forward_rows(cis2_ctx* c, uint32_t n, const uint32_t* d_tok, uint32_t max_len, uint32_t nl) {
+// Row counts up to which forward_rows applies the layer norms inside the
+// projections that read them.
+constexpr uint32_t kFuseNormRows = 256;
+
+// The logits and argmax go to b.logits / b.arg unless `logits` / `arg` name
+// other buffers of at least nl rows.
+int forward_rows(cis2_ctx* c, uint32_t n, const uint32_t* d_tok, uint32_t max_len, uint32_t nl,
+                 float* logits = nullptr, uint32_t* arg = nullptr) {
   const cis2_config& f = c->cfg;
   RowsBuf& b = c->rows;
   const uint32_t H = f.hidden, I = f.inter, hd = f.head_dim, QD = c->qd, KV = c->kvd;
@@ -456,17 +467,32 @@ int forward_rows(cis2_ctx* c, uint32_t n, const uint32_t* d_tok, uint32_t max_le
   const size_t per = (size_t)KV * f.max_pos;           // one layer's K (or V) of one sequence
   const uint64_t seq_stride = (uint64_t)f.n_layers * 2 * per;
   LAUNCH(launch_embed_rows(c->embed, rd, H, f.vocab, b.h, c->d_err, s), "rows embed");
+  // for few rows (decode steps) the RMSNorms run inside the launches that
+  // consume them; each workgroup then repeats the norm chain of its rows,
+  // which is latency hidden by the launch it saves only while the grid is
+  // small
+  const bool fuse_norm = n <= kFuseNormRows;
   for (uint32_t l = 0; l < f.n_layers; ++l) {
     const Layer& Ly = c->L[l];
     float* kc = c->kv + (size_t)l * 2 * per;
     float* vc = kc + per;
-    LAUNCH(launch_rmsnorm(b.h, Ly.ln1, f.eps, H, n, b.x, s, tree), "rows norm1");
-    const BgemmSeg sq{Ly.wq, QD, H, c->Rq, b.x, H, b.q, QD, Ly.bq, 0, Ly.bq ? kEpiBias : kEpiNone};
-    const BgemmSeg sk{Ly.wk, KV, H, c->Rq, b.x, H, b.k, KV, Ly.bk, 0, Ly.bk ? kEpiBias : kEpiNone};
-    const BgemmSeg sv{Ly.wv, KV, H, c->Rq, b.x, H, b.v, KV, Ly.bv, 0, Ly.bv ? kEpiBias : kEpiNone};
-    LAUNCH(launch_bgemm(sq, n, tree, s), "rows q");
-    LAUNCH(launch_bgemm(sk, n, tree, s), "rows k");
-    LAUNCH(launch_bgemm(sv, n, tree, s), "rows v");
+    // q, k and v in one launch over norm1(h): the norm inside the launch
+    // for few rows, as its own pass for many
+    BgemmOpts o1;
+    o1.tree = tree;
+    const float* xin = b.h;
+    if (fuse_norm) {
+      o1.norm_w = Ly.ln1;
+      o1.eps = f.eps;
+    } else {
+      LAUNCH(launch_rmsnorm(b.h, Ly.ln1, f.eps, H, n, b.x, s, tree), "rows norm1");
+      xin = b.x;
+    }
+    const BgemmSeg qkv[3] = {
+        {Ly.wq, QD, H, c->Rq, xin, H, b.q, QD, Ly.bq, 0, Ly.bq ? kEpiBias : kEpiNone},
+        {Ly.wk, KV, H, c->Rq, xin, H, b.k, KV, Ly.bk, 0, Ly.bk ? kEpiBias : kEpiNone},
+        {Ly.wv, KV, H, c->Rq, xin, H, b.v, KV, Ly.bv, 0, Ly.bv ? kEpiBias : kEpiNone}};
+    LAUNCH(launch_bgemm_multi(qkv, 3, n, o1, s), "rows qkv");
     if (Ly.qn) LAUNCH(launch_rmsnorm(b.q, Ly.qn, f.eps, hd, n * f.n_heads, b.q, s, tree), "rows q_norm");
     if (Ly.kn) LAUNCH(launch_rmsnorm(b.k, Ly.kn, f.eps, hd, n * f.n_kv_heads, b.k, s, tree), "rows k_norm");
     LAUNCH(launch_rope_store_rows(b.q, b.k, b.v, c->rope_cs, rd, f.n_heads, f.n_kv_heads, hd,
@@ -478,12 +504,20 @@ int forward_rows(cis2_ctx* c, uint32_t n, const uint32_t* d_tok, uint32_t max_le
     const BgemmSeg so{Ly.wo, H, QD, c->Ro, b.att, QD, b.h2, H, b.h, H, kEpiResidual};
     LAUNCH(launch_bgemm(so, n, tree, s), "rows o_proj");
     std::swap(b.h, b.h2);
-    LAUNCH(launch_rmsnorm(b.h, Ly.ln2, f.eps, H, n, b.x, s, tree), "rows norm2");
-    const BgemmSeg sg{Ly.wg, I, H, c->Rg, b.x, H, b.g, I, nullptr, 0, kEpiNone};
-    const BgemmSeg su{Ly.wu, I, H, c->Rg, b.x, H, b.u, I, nullptr, 0, kEpiNone};
-    LAUNCH(launch_bgemm(sg, n, tree, s), "rows gate");
-    LAUNCH(launch_bgemm(su, n, tree, s), "rows up");
-    LAUNCH(launch_silu_mul(b.g, b.u, b.hid, (uint64_t)n * I, s), "rows silu");
+    // gate and up as two chains per thread, silu(gate) * up stored
+    BgemmOpts o2;
+    o2.tree = tree;
+    o2.W2 = Ly.wu;
+    const float* x2 = b.h;
+    if (fuse_norm) {
+      o2.norm_w = Ly.ln2;
+      o2.eps = f.eps;
+    } else {
+      LAUNCH(launch_rmsnorm(b.h, Ly.ln2, f.eps, H, n, b.x, s, tree), "rows norm2");
+      x2 = b.x;
+    }
+    const BgemmSeg sg{Ly.wg, I, H, c->Rg, x2, H, b.hid, I, nullptr, 0, kEpiNone};
+    LAUNCH(launch_bgemm_multi(&sg, 1, n, o2, s), "rows gate_up");
     const BgemmSeg sd{Ly.wd, H, I, c->Rd, b.hid, I, b.h2, H, b.h, H, kEpiResidual};
     LAUNCH(launch_bgemm(sd, n, tree, s), "rows down");
     std::swap(b.h, b.h2);
@@ -491,10 +525,12 @@ int forward_rows(cis2_ctx* c, uint32_t n, const uint32_t* d_tok, uint32_t max_le
   if (nl) {
     LAUNCH(launch_gather_rows(b.h, b.lrows, nl, H, b.lx, s), "rows gather");
     LAUNCH(launch_rmsnorm(b.lx, c->final_norm, f.eps, H, nl, b.lx, s, tree), "rows final_norm");
-    const BgemmSeg sl{c->lm_head, f.vocab, H, c->Rl, b.lx, H, b.logits, f.vocab, nullptr, 0,
+    if (!logits) logits = b.logits;
+    if (!arg) arg = b.arg;
+    const BgemmSeg sl{c->lm_head, f.vocab, H, c->Rl, b.lx, H, logits, f.vocab, nullptr, 0,
                       kEpiNone};
     LAUNCH(launch_bgemm(sl, nl, tree, s), "rows lm_head");
-    LAUNCH(launch_argmax_rows(b.logits, nl, f.vocab, b.arg, s), "rows argmax");
+    LAUNCH(launch_argmax_rows(logits, nl, f.vocab, arg, s), "rows argmax");
   }
   return CIS2_OK;
 }
@@ -613,6 +649,7 @@ void cis2_ctx_destroy(cis2_ctx* c) {
   for (void* p : c->allocs) (void)hipFree(p);
   for (void* p : c->rows.mem) (void)hipFree(p);
   for (void* p : c->rows.lmem) (void)hipFree(p);
+  for (void* p : c->rows.mem2) (void)hipFree(p);
   if (c->tline_file) fclose(c->tline_file);
   for (hipEvent_t e : c->prof_ev)
     if (e) (void)hipEventDestroy(e);
@@ -620,6 +657,10 @@ void cis2_ctx_destroy(cis2_ctx* c) {
   if (c->ring_tok) (void)hipHostFree(c->ring_tok);
   for (int i = 0; i < kRing; ++i)
     if (c->ring_ev[i]) (void)hipEventDestroy(c->ring_ev[i]);
+  if (c->cs) {
+    (void)hipStreamSynchronize(c->cs);
+    (void)hipStreamDestroy(c->cs);
+  }
   if (c->st) (void)hipStreamDestroy(c->st);
   delete c;
 }
@@ -1100,6 +1141,146 @@ int cis2_decode(cis2_ctx* c, uint32_t seq, const uint32_t* prompt, uint32_t n_pr
   return r;
 }
 
+// The generation steps of decode_group, after its prefill has left logit
+// set 0 (each sequence's last prompt row) in rb.logits / rb.arg.  Logit set
+// t (t >= 1) comes from a rows pass over row b = sequence b at position
+// lens[b] + t - 1 whose input tokens are set t-1's argmax ids.  Sets
+// alternate between two device buffers, so pass t runs while set t-1 is
+// copied to pinned host memory on a second stream and folded into the
+// witnesses on the host; pass t+1 waits only for the copy of set t-1 (the
+// buffer it overwrites).  Both passes are captured once as HIP graphs
+// (CIS2_GRAPH=0: launched op by op); the positions advance on the device
+// at the end of each pass.
+static int decode_steps(cis2_ctx* c, uint32_t G, const uint32_t* lens, const uint32_t* off,
+                        uint32_t gen, std::vector<Sha256>& w, std::vector<Sha256>& a,
+                        uint32_t* out_ids) {
+  const uint32_t V = c->cfg.vocab;
+  RowsBuf& rb = c->rows;
+  int rc = rows_reserve(c, G, G);
+  if (rc) return rc;
+  if (G > rb.cap2) {
+    HIPCHK(c, hipStreamSynchronize(c->st), "rows sync");
+    for (void* p : rb.mem2) (void)hipFree(p);
+    rb.mem2.clear();
+    rb.cap2 = 0;
+    if (!(rb.logits2 = rows_alloc<float>(rb.mem2, (size_t)G * V)) ||
+        !(rb.arg2 = rows_alloc<uint32_t>(rb.mem2, G)))
+      return fail(c, CIS2_E_OOM, "second logit buffer");
+    rb.cap2 = G;
+  }
+  if (!c->cs) HIPCHK(c, hipStreamCreateWithFlags(&c->cs, hipStreamNonBlocking), "copy stream");
+  // buffer of set t: (t + 1) & 1; set 0 is the prefill's
+  float* logb[2] = {rb.logits2, rb.logits};
+  uint32_t* argb[2] = {rb.arg2, rb.arg};
+  std::vector<uint32_t> dseq(G), dpos(G), ident(G);
+  uint32_t max_len = 0;
+  for (uint32_t b = 0; b < G; ++b) {
+    dseq[b] = b;
+    ident[b] = b;
+    dpos[b] = lens[b];
+    max_len = std::max(max_len, lens[b] + gen - 1);  // the last pass's largest pos + 1
+  }
+  HIPCHK(c, hipMemcpyAsync(rb.seq, dseq.data(), (size_t)G * 4, hipMemcpyHostToDevice, c->st),
+         "rows upload");
+  HIPCHK(c, hipMemcpyAsync(rb.lrows, ident.data(), (size_t)G * 4, hipMemcpyHostToDevice, c->st),
+         "rows upload");
+  HIPCHK(c, hipMemcpyAsync(rb.pos, dpos.data(), (size_t)G * 4, hipMemcpyHostToDevice, c->st),
+         "rows upload");
+  // one pass into buffer j: tokens from buffer 1 - j
+  auto pass = [&](uint32_t j) -> int {
+    int r = forward_rows(c, G, argb[1 - j], max_len, G, logb[j], argb[j]);
+    if (r) return r;
+    HIPCHK(c, launch_advance_rows(rb.pos, G, c->st), "rows advance");
+    return CIS2_OK;
+  };
+  hipGraphExec_t gx[2] = {nullptr, nullptr};
+  const char* ge = getenv("CIS2_GRAPH");
+  bool graphs = gen > 1 && !(ge && ge[0] == '0');
+  for (uint32_t j = 0; j < 2 && graphs; ++j) {
+    if (hipStreamBeginCapture(c->st, hipStreamCaptureModeThreadLocal) != hipSuccess) {
+      graphs = false;
+      break;
+    }
+    const int r = pass(j);
+    hipGraph_t g = nullptr;
+    const hipError_t e = hipStreamEndCapture(c->st, &g);
+    if (r == CIS2_OK && e == hipSuccess && g &&
+        hipGraphInstantiate(&gx[j], g, nullptr, nullptr, 0) != hipSuccess)
+      gx[j] = nullptr;
+    if (g) (void)hipGraphDestroy(g);
+    if (!gx[j]) {  // not capturable here: launch op by op
+      (void)hipGetLastError();
+      c->err.clear();
+      graphs = false;
+    }
+  }
+  float* host = nullptr;
+  uint32_t* hid = nullptr;
+  hipEvent_t evd[2] = {nullptr, nullptr}, evc[2] = {nullptr, nullptr};
+  if (hipHostMalloc((void**)&host, 2 * (size_t)G * V * sizeof(float), 0) != hipSuccess ||
+      hipHostMalloc((void**)&hid, 2 * (size_t)G * 4, 0) != hipSuccess)
+    rc = fail(c, CIS2_E_OOM, "pinned logits");
+  for (int i = 0; i < 2 && rc == CIS2_OK; ++i)
+    if (hipEventCreateWithFlags(&evd[i], hipEventDisableTiming) != hipSuccess ||
+        hipEventCreateWithFlags(&evc[i], hipEventDisableTiming) != hipSuccess)
+      rc = fail(c, CIS2_E_DEVICE, "event create");
+  // waits for set t's copy and folds it into the witnesses
+  auto consume = [&](uint32_t t) -> int {
+    const uint32_t j = (t + 1) & 1;
+    if (hipEventSynchronize(evc[j]) != hipSuccess) return fail(c, CIS2_E_DEVICE, "logits wait");
+    const float* hl = host + (size_t)j * G * V;
+    const uint32_t* hi = hid + (size_t)j * G;
+    fold_rows(w, hl, hi, G, V);
+    for (uint32_t b = 0; b < G; ++b) {
+      a[b].update_u32le(hi[b]);
+      out_ids[off[b] + (size_t)b * gen + lens[b] + t] = hi[b];
+    }
+    return CIS2_OK;
+  };
+  for (uint32_t t = 0; t < gen && rc == CIS2_OK; ++t) {
+    const uint32_t j = (t + 1) & 1;
+    if (t >= 1) {
+      if (t >= 2 && hipStreamWaitEvent(c->st, evc[j], 0) != hipSuccess) {
+        rc = fail(c, CIS2_E_DEVICE, "copy wait");
+        break;
+      }
+      if (graphs) {
+        if (hipGraphLaunch(gx[j], c->st) != hipSuccess) {
+          rc = fail(c, CIS2_E_DEVICE, "graph launch");
+          break;
+        }
+      } else if ((rc = pass(j)) != CIS2_OK) {
+        break;
+      }
+    }
+    if (hipEventRecord(evd[j], c->st) != hipSuccess ||
+        hipStreamWaitEvent(c->cs, evd[j], 0) != hipSuccess ||
+        hipMemcpyAsync(host + (size_t)j * G * V, logb[j], (size_t)G * V * sizeof(float),
+                       hipMemcpyDeviceToHost, c->cs) != hipSuccess ||
+        hipMemcpyAsync(hid + (size_t)j * G, argb[j], (size_t)G * 4, hipMemcpyDeviceToHost,
+                       c->cs) != hipSuccess ||
+        hipEventRecord(evc[j], c->cs) != hipSuccess) {
+      rc = fail(c, CIS2_E_DEVICE, "logits copy");
+      break;
+    }
+    if (t >= 1) rc = consume(t - 1);
+  }
+  if (rc == CIS2_OK) rc = consume(gen - 1);
+  // drain both streams before the pinned buffers go
+  if (hipStreamSynchronize(c->st) != hipSuccess && rc == CIS2_OK)
+    rc = fail(c, CIS2_E_DEVICE, "decode sync");
+  if (hipStreamSynchronize(c->cs) != hipSuccess && rc == CIS2_OK)
+    rc = fail(c, CIS2_E_DEVICE, "copy sync");
+  for (int i = 0; i < 2; ++i) {
+    if (evd[i]) (void)hipEventDestroy(evd[i]);
+    if (evc[i]) (void)hipEventDestroy(evc[i]);
+    if (gx[i]) (void)hipGraphExecDestroy(gx[i]);
+  }
+  if (host) (void)hipHostFree(host);
+  if (hid) (void)hipHostFree(hid);
+  return rc;
+}
+
 // Greedy decode of `G` sequences (cache slots 0..G-1) in row-batched
 // passes: one prefill over every prompt position of every sequence, then
 // one row per sequence per step.  Per sequence, the witness and argmax
@@ -1143,81 +1324,8 @@ static int decode_group(cis2_ctx* c, uint32_t G, const uint32_t* prompts, const 
   if (gen == 0) {
     HIPCHK(c, hipStreamSynchronize(c->st), "prefill sync");
   } else {
-    // decode rows: row b = sequence b at position lens[b] + step
-    RowsBuf& rb = c->rows;
-    std::vector<uint32_t> dseq(G), dpos(G), ident(G);
-    uint32_t max_len = 0;
-    for (uint32_t b = 0; b < G; ++b) {
-      dseq[b] = b;
-      ident[b] = b;
-    }
-    float* host = nullptr;
-    uint32_t* hid = nullptr;
-    HIPCHK(c, hipHostMalloc((void**)&host, 2 * (size_t)G * V * sizeof(float), 0), "pinned logits");
-    if (hipHostMalloc((void**)&hid, 2 * (size_t)G * 4, 0) != hipSuccess) {
-      (void)hipHostFree(host);
-      return fail(c, CIS2_E_OOM, "pinned ids");
-    }
-    hipEvent_t ev[2] = {nullptr, nullptr};
-    int rc = CIS2_OK;
-    for (int i = 0; i < 2 && rc == CIS2_OK; ++i)
-      if (hipEventCreateWithFlags(&ev[i], hipEventDisableTiming) != hipSuccess)
-        rc = fail(c, CIS2_E_DEVICE, "event create");
-    std::vector<uint32_t> ids(G);
-    for (uint32_t step = 0; step < gen && rc == CIS2_OK; ++step) {
-      const uint32_t slot = step & 1;
-      float* hl = host + (size_t)slot * G * V;
-      uint32_t* hi = hid + (size_t)slot * G;
-      if (hipMemcpyAsync(hl, rb.logits, (size_t)G * V * sizeof(float), hipMemcpyDeviceToHost,
-                         c->st) != hipSuccess ||
-          hipMemcpyAsync(hi, rb.arg, (size_t)G * 4, hipMemcpyDeviceToHost, c->st) != hipSuccess ||
-          hipEventRecord(ev[slot], c->st) != hipSuccess) {
-        rc = fail(c, CIS2_E_DEVICE, "logits copy");
-        break;
-      }
-      if (step + 1 < gen) {  // next rows: the argmax ids at the next positions
-        max_len = 0;
-        for (uint32_t b = 0; b < G; ++b) {
-          dpos[b] = lens[b] + step;
-          max_len = std::max(max_len, dpos[b] + 1);
-        }
-        if (step == 0) {
-          rc = rows_reserve(c, G, G);
-          if (rc) break;
-          if (hipMemcpyAsync(rb.seq, dseq.data(), (size_t)G * 4, hipMemcpyHostToDevice, c->st) !=
-                  hipSuccess ||
-              hipMemcpyAsync(rb.lrows, ident.data(), (size_t)G * 4, hipMemcpyHostToDevice,
-                             c->st) != hipSuccess) {
-            rc = fail(c, CIS2_E_DEVICE, "rows upload");
-            break;
-          }
-        }
-        if (hipMemcpyAsync(rb.pos, dpos.data(), (size_t)G * 4, hipMemcpyHostToDevice, c->st) !=
-            hipSuccess) {
-          rc = fail(c, CIS2_E_DEVICE, "rows upload");
-          break;
-        }
-        // the embed reads rb.arg before this pass's argmax overwrites it
-        rc = forward_rows(c, G, rb.arg, max_len, G);
-        if (rc) break;
-      }
-      if (hipEventSynchronize(ev[slot]) != hipSuccess) {
-        rc = fail(c, CIS2_E_DEVICE, "logits wait");
-        break;
-      }
-      fold_rows(w, hl, hi, G, V);
-      for (uint32_t b = 0; b < G; ++b) {
-        a[b].update_u32le(hi[b]);
-        out_ids[off[b] + (size_t)b * gen + lens[b] + step] = hi[b];
-      }
-    }
-    if (rc == CIS2_OK && hipStreamSynchronize(c->st) != hipSuccess)
-      rc = fail(c, CIS2_E_DEVICE, "decode sync");
-    for (int i = 0; i < 2; ++i)
-      if (ev[i]) (void)hipEventDestroy(ev[i]);
-    (void)hipHostFree(host);
-    (void)hipHostFree(hid);
-    if (rc) return rc;
+    r = decode_steps(c, G, lens, off.data(), gen, w, a, out_ids);
+    if (r) return r;
   }
   for (uint32_t b = 0; b < G; ++b) {
     memcpy(out_ids + off[b] + (size_t)b * gen, prompts + off[b], (size_t)lens[b] * 4);

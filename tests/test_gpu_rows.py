@@ -125,16 +125,23 @@ def test_decode_prefill_paths_agree(model_fixtures):
     assert a["step_digests"] == b["step_digests"]
 
 
+@pytest.mark.parametrize("graph", ["1", "0"])
 @pytest.mark.parametrize("B", [2, 5])
-def test_decode_batch_ragged_equals_bs1(B):
+def test_decode_batch_ragged_equals_bs1(B, graph):
     """B sequences with ragged prompts through cis2_decode_batch (row-batched
-    prefill and steps) against each sequence's bs=1 decode."""
+    prefill and steps) against each sequence's bs=1 decode.  The steps run
+    as two alternating captured graphs, replayed 23 times between host
+    folds (graph "1"), or op by op (CIS2_GRAPH=0)."""
     spec = artifacts.SPECS["tiny-untied"]
     w = artifacts.Weights(spec, 2)
     prompts = [artifacts.set_prompt(2, i, spec.vocab, 1, 40, 9) for i in range(B)]
     gen = 24
     m = Cis2Model(spec, w, max_pos=40 + gen, max_seqs=3)  # B=5: two groups
-    rows = m.decode_batch(prompts, gen)
+    os.environ["CIS2_GRAPH"] = graph
+    try:
+        rows = m.decode_batch(prompts, gen)
+    finally:
+        del os.environ["CIS2_GRAPH"]
     solo = Cis2Model(spec, w, max_pos=40 + gen)
     for i, p in enumerate(prompts):
         s = solo.decode(p, gen, step_digests=False)
