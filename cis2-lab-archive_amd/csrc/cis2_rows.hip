@@ -16,6 +16,10 @@ namespace {
 typedef float v4 __attribute__((ext_vector_type(4)));
 
 constexpr uint32_t kT = 256;
+// Query heads per attention workgroup at most (those of one KV head).
+constexpr uint32_t kMaxHeadsPerWg = 4;
+// Threads per attention workgroup.
+constexpr uint32_t kAttT = 256;
 
 #define AS_LDS __attribute__((address_space(3)))
 #define AS_GLB __attribute__((address_space(1)))
@@ -309,43 +313,62 @@ __global__ __launch_bounds__(256) void k_rope_store_rows(float* q, float* k, con
     vc[sb + (size_t)idx * max_pos + pos] = vr[idx];
 }
 
-// One workgroup per (row, query head): scores_j = dot(q, k_j) * scale
-// (dot_seq, or dot_tree), softmax (first-wins max, pinned exp, strict or
-// tree denominator, true divide), then out_d = fold_j (p_j * v_j[d]) in
-// position order (code/cis2-fp/src/main.rs:429-467; math.rs:425-465).
-__global__ __launch_bounds__(256) void k_attention_rows(const float* __restrict__ q,
+// One workgroup per (row, HPW query heads that share one KV head): per head
+// scores_j = dot(q, k_j) * scale (dot_seq, or dot_tree), softmax (first-wins
+// max, pinned exp, strict or tree denominator, true divide), then
+// out_d = fold_j (p_j * v_j[d]) in position order
+// (code/cis2-fp/src/main.rs:429-467; math.rs:425-465).  The heads of a
+// workgroup read each K and V element once: a column's K values are loaded
+// once for all HPW score chains, and the V rows of the HPW * hd output
+// chains come from the same addresses.
+// LDS: q [HPW][hd4], scores [HPW][ls], tree partials [HPW][nbs], with
+// hd4 = hd rounded up to 4 and ls = max_len rounded up to 4.
+template <uint32_t HPW>
+__global__ __launch_bounds__(kAttT) void k_attention_rows(const float* __restrict__ q,
                                                         const float* __restrict__ kc,
                                                         const float* __restrict__ vc,
                                                         RowsDesc rows, uint32_t nh, uint32_t nkv,
                                                         uint32_t hd, uint32_t max_pos,
                                                         uint64_t seq_stride, float scale,
-                                                        float* out, uint32_t tree) {
-  extern __shared__ v4 sh4[];  // 16-byte aligned: the scores are read 16 bytes at a time
+                                                        float* out, uint32_t tree, uint32_t ls) {
+  extern __shared__ v4 sh4[];  // 16-byte aligned: q and scores are read 16 bytes at a time
   float* sh = reinterpret_cast<float*>(sh4);
-  __shared__ Pick red[4];
-  __shared__ float s_den;
-  const uint32_t r = blockIdx.x, qh = blockIdx.y;  // rows on x: up to 2^31 of them
-  const uint32_t group = nh / nkv, kvh = qh / group, pos = rows.pos[r], len = pos + 1;
+  __shared__ Pick red[kAttT / 64];
+  __shared__ float s_den[HPW];
+  const uint32_t r = blockIdx.x, qh0 = blockIdx.y * HPW;  // rows on x: up to 2^31 of them
+  const uint32_t group = nh / nkv, kvh = qh0 / group, pos = rows.pos[r], len = pos + 1;
+  const uint32_t hd4 = (hd + 3) & ~3u, nbs = (ls + 31) / 32, t = threadIdx.x;
   const size_t sb = (size_t)rows.seq[r] * seq_stride;
   float* sq = sh;
-  float* ss = sh + ((hd + 3) & ~3u);
-  float* part = ss + len;
-  const float* qv = q + (size_t)r * nh * hd + (size_t)qh * hd;
-  for (uint32_t d = threadIdx.x; d < hd; d += blockDim.x) sq[d] = qv[d];
+  float* ssb = sh + HPW * hd4;
+  float* partb = ssb + HPW * ls;
+  const float* qv = q + (size_t)r * nh * hd + (size_t)qh0 * hd;
+  for (uint32_t i = t; i < HPW * hd; i += blockDim.x) {
+    const uint32_t h = i / hd, d = i - h * hd;
+    sq[h * hd4 + d] = qv[i];
+  }
   __syncthreads();
   const float* kb = kc + sb + (size_t)kvh * hd * max_pos;
-  for (uint32_t j = threadIdx.x; j < len; j += blockDim.x) {
-    float acc = 0.0f;
+  for (uint32_t j = t; j < len; j += blockDim.x) {
+    float acc[HPW];
+#pragma unroll
+    for (uint32_t h = 0; h < HPW; ++h) acc[h] = 0.0f;
     if (tree) {
       for (uint32_t d0 = 0; d0 < hd; d0 += 32) {
-        float l[32];
+        float kv[32];
 #pragma unroll
-        for (uint32_t i = 0; i < 32; ++i)
-          l[i] = d0 + i < hd ? sq[d0 + i] * kb[(size_t)(d0 + i) * max_pos + j] : 0.0f;
-        acc = acc + tree32(l);
+        for (uint32_t i = 0; i < 32; ++i) kv[i] = d0 + i < hd ? kb[(size_t)(d0 + i) * max_pos + j] : 0.0f;
+#pragma unroll
+        for (uint32_t h = 0; h < HPW; ++h) {
+          float l[32];
+#pragma unroll
+          for (uint32_t i = 0; i < 32; ++i) l[i] = d0 + i < hd ? sq[h * hd4 + d0 + i] * kv[i] : 0.0f;
+          acc[h] = acc[h] + tree32(l);
+        }
       }
     } else {
-      // the column's loads go out 64 at a time, then their 64 chain steps
+      // the column's loads go out 64 at a time, then the heads' chain steps
+      // over them, interleaved
       uint32_t d0 = 0;
       for (; d0 + 64 <= hd; d0 += 64) {
         float kv[64];
@@ -353,56 +376,63 @@ __global__ __launch_bounds__(256) void k_attention_rows(const float* __restrict_
         for (uint32_t i = 0; i < 64; ++i) kv[i] = kb[(size_t)(d0 + i) * max_pos + j];
 #pragma unroll
         for (uint32_t i = 0; i < 64; ++i) {
-          float p = sq[d0 + i] * kv[i];
-          acc = acc + p;
-        }
-      }
-      for (; d0 + 16 <= hd; d0 += 16) {
-        float kv[16];
 #pragma unroll
-        for (uint32_t i = 0; i < 16; ++i) kv[i] = kb[(size_t)(d0 + i) * max_pos + j];
-#pragma unroll
-        for (uint32_t i = 0; i < 16; ++i) {
-          float p = sq[d0 + i] * kv[i];
-          acc = acc + p;
+          for (uint32_t h = 0; h < HPW; ++h) {
+            const float p = sq[h * hd4 + d0 + i] * kv[i];
+            acc[h] = acc[h] + p;
+          }
         }
       }
       for (; d0 < hd; ++d0) {
-        float p = sq[d0] * kb[(size_t)d0 * max_pos + j];
-        acc = acc + p;
+        const float kv = kb[(size_t)d0 * max_pos + j];
+#pragma unroll
+        for (uint32_t h = 0; h < HPW; ++h) {
+          const float p = sq[h * hd4 + d0] * kv;
+          acc[h] = acc[h] + p;
+        }
       }
     }
-    ss[j] = acc * scale;
+#pragma unroll
+    for (uint32_t h = 0; h < HPW; ++h) ssb[h * ls + j] = acc[h] * scale;
   }
   __syncthreads();
-  Pick best = {0.0f, UINT32_MAX};
-  for (uint32_t j = threadIdx.x; j < len; j += blockDim.x) {
-    const float v = ss[j];
-    if (v == v) best = pick2(best, Pick{v, j});
-  }
-  best = pick_block(best, red);
-  const float mx = (ss[0] != ss[0]) ? ss[0] : best.v;
-  for (uint32_t j = threadIdx.x; j < len; j += blockDim.x) {
-    float dlt = ss[j] - mx;
-    ss[j] = exp_pinned(dlt);
+  // per head: first-wins maximum (NaN at 0 wins), then exp(s - max)
+  for (uint32_t h = 0; h < HPW; ++h) {
+    float* ss = ssb + h * ls;
+    Pick best = {0.0f, UINT32_MAX};
+    for (uint32_t j = t; j < len; j += blockDim.x) {
+      const float v = ss[j];
+      if (v == v) best = pick2(best, Pick{v, j});
+    }
+    best = pick_block(best, red);
+    const float mx = (ss[0] != ss[0]) ? ss[0] : best.v;
+    for (uint32_t j = t; j < len; j += blockDim.x) {
+      const float dlt = ss[j] - mx;
+      ss[j] = exp_pinned(dlt);
+    }
   }
   __syncthreads();
   const uint32_t nb = (len + 31) / 32;
   if (tree) {
-    for (uint32_t t = threadIdx.x; t < nb; t += blockDim.x) {
+    for (uint32_t i = t; i < HPW * nb; i += blockDim.x) {
+      const uint32_t h = i / nb, tb = i - h * nb;
+      const float* ss = ssb + h * ls;
       float l[32];
 #pragma unroll
-      for (uint32_t i = 0; i < 32; ++i) l[i] = 32 * t + i < len ? ss[32 * t + i] : 0.0f;
-      part[t] = tree32(l);
+      for (uint32_t k = 0; k < 32; ++k) l[k] = 32 * tb + k < len ? ss[32 * tb + k] : 0.0f;
+      partb[h * nbs + tb] = tree32(l);
     }
     __syncthreads();
   }
-  if (threadIdx.x < 64) {
+  // denominators: wave w sums heads w, w + 4, ...; every lane of the wave
+  // runs the same chain
+  for (uint32_t h = t >> 6; h < HPW; h += blockDim.x >> 6) {
     float acc = 0.0f;
     if (tree) {
-      for (uint32_t t = 0; t < nb; ++t) acc = acc + part[t];
+      for (uint32_t tb = 0; tb < nb; ++tb) acc = acc + partb[h * nbs + tb];
     } else {
       // 16-byte reads (every lane the same address), 8 of them per batch
+      const float* ss = ssb + h * ls;
       const v4* s4p = reinterpret_cast<const v4*>(ss);
       uint32_t j = 0;
       for (; j + 32 <= len; j += 32) {
@@ -419,25 +449,27 @@ __global__ __launch_bounds__(256) void k_attention_rows(const float* __restrict_
       }
       for (; j < len; ++j) acc = acc + ss[j];
     }
-    if (threadIdx.x == 0) s_den = acc;
+    if ((t & 63) == 0) s_den[h] = acc;
   }
   __syncthreads();
-  const float den = s_den;
-  for (uint32_t j = threadIdx.x; j < len; j += blockDim.x) {
-    float pj = ss[j] / den;
-    ss[j] = pj;
+  for (uint32_t i = t; i < HPW * len; i += blockDim.x) {
+    const uint32_t h = i / len, j = i - h * len;
+    const float pj = ssb[h * ls + j] / s_den[h];
+    ssb[h * ls + j] = pj;
   }
   __syncthreads();
   const float* vb = vc + sb + (size_t)kvh * hd * max_pos;
-  float* o = out + (size_t)r * nh * hd + (size_t)qh * hd;
-  for (uint32_t d = threadIdx.x; d < hd; d += blockDim.x) {
-    // row d of V is contiguous: 16-byte loads, 8 of them (32 positions) in
-    // flight ahead of the chain
+  for (uint32_t i = t; i < HPW * hd; i += blockDim.x) {
+    const uint32_t h = i / hd, d = i - h * hd;
+    float* o = out + (size_t)r * nh * hd + (size_t)(qh0 + h) * hd;
+    const float* ss = ssb + h * ls;
+    // row d of V is contiguous: 16-byte loads, a batch of 64 positions in
+    // flight while the previous batch's chain steps run
     const v4* vr4 = reinterpret_cast<const v4*>(vb + (size_t)d * max_pos);
     const v4* p4 = reinterpret_cast<const v4*>(ss);
     float acc = 0.0f;
     uint32_t j = 0;
-    constexpr uint32_t VB = 16;  // 64 positions per batch; the next batch loads meanwhile
+    constexpr uint32_t VB = 16;
     v4 cur[VB], nxt[VB];
     const uint32_t full = len / (4 * VB);
     if (full > 0) {
@@ -463,7 +495,7 @@ __global__ __launch_bounds__(256) void k_attention_rows(const float* __restrict_
     }
     const float* vr = vb + (size_t)d * max_pos;
     for (; j < len; ++j) {
-      float p = ss[j] * vr[j];
+      const float p = ss[j] * vr[j];
       acc = acc + p;
     }
     o[d] = acc;
@@ -610,11 +642,49 @@ hipError_t launch_attention_rows(const float* q, const float* kc, const float* v
   if (rows.n == 0) return hipSuccess;
   if (nkv == 0 || nh % nkv || max_len == 0 || max_len > max_pos || max_pos % 4)
     return hipErrorInvalidValue;
-  // q (rounded to 16 bytes), scores, and the denominator's block partials
-  const size_t shmem = (((size_t)hd + 3) / 4 * 4 + max_len + (max_len + 31) / 32) * sizeof(float);
+  const uint32_t group = nh / nkv;
+  const size_t hd4 = ((size_t)hd + 3) / 4 * 4, ls = ((size_t)max_len + 3) / 4 * 4;
+  auto lds_of = [&](uint32_t hpw) { return hpw * (hd4 + ls + (ls + 31) / 32) * sizeof(float); };
+  // Few rows (decode steps): one head per workgroup, for the most
+  // workgroups.  Many rows: the most heads of one KV head (a divisor of
+  // the group) whose LDS fits, so K and V are read once per group.
+  static int ncu = 0;
+  if (ncu == 0) {
+    int dev = 0;
+    (void)hipGetDevice(&dev);
+    if (hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        ncu <= 0)
+      ncu = 256;
+  }
+  uint32_t hpw = 1;
+  if ((uint64_t)rows.n * nkv >= 4 * (uint64_t)ncu) {
+    for (uint32_t h = std::min(group, kMaxHeadsPerWg); h > 1; --h)
+      if (group % h == 0 && lds_of(h) <= 60 * 1024) {
+        hpw = h;
+        break;
+      }
+  }
+  const size_t shmem = lds_of(hpw);
   if (shmem > 60 * 1024) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_attention_rows, dim3(rows.n, nh), dim3(kT), shmem, st, q, kc, vc, rows,
-                     nh, nkv, hd, max_pos, seq_stride, scale, out, tree ? 1u : 0u);
+  const dim3 grid(rows.n, nh / hpw);
+  const uint32_t tr = tree ? 1u : 0u, ls32 = (uint32_t)ls;
+  switch (hpw) {
+    case 4:
+      hipLaunchKernelGGL(k_attention_rows<4>, grid, dim3(kAttT), shmem, st, q, kc, vc, rows, nh,
+                         nkv, hd, max_pos, seq_stride, scale, out, tr, ls32);
+      break;
+    case 3:
+      hipLaunchKernelGGL(k_attention_rows<3>, grid, dim3(kAttT), shmem, st, q, kc, vc, rows, nh,
+                         nkv, hd, max_pos, seq_stride, scale, out, tr, ls32);
+      break;
+    case 2:
+      hipLaunchKernelGGL(k_attention_rows<2>, grid, dim3(kAttT), shmem, st, q, kc, vc, rows, nh,
+                         nkv, hd, max_pos, seq_stride, scale, out, tr, ls32);
+      break;
+    default:
+      hipLaunchKernelGGL(k_attention_rows<1>, grid, dim3(kAttT), shmem, st, q, kc, vc, rows, nh,
+                         nkv, hd, max_pos, seq_stride, scale, out, tr, ls32);
+  }
   return hipGetLastError();
 }
 

@@ -125,26 +125,48 @@ def test_decode_prefill_paths_agree(model_fixtures):
     assert a["step_digests"] == b["step_digests"]
 
 
-@pytest.mark.parametrize("graph", ["1", "0"])
+@pytest.mark.parametrize("graph,mode", [("1", 0), ("0", 0), ("1", 1)])
 @pytest.mark.parametrize("B", [2, 5])
-def test_decode_batch_ragged_equals_bs1(B, graph):
+def test_decode_batch_ragged_equals_bs1(B, graph, mode):
     """B sequences with ragged prompts through cis2_decode_batch (row-batched
     prefill and steps) against each sequence's bs=1 decode.  The steps run
     as two alternating captured graphs, replayed 23 times between host
-    folds (graph "1"), or op by op (CIS2_GRAPH=0)."""
+    folds (graph "1"), or op by op (CIS2_GRAPH=0); mode 1 is tree mode."""
     spec = artifacts.SPECS["tiny-untied"]
     w = artifacts.Weights(spec, 2)
     prompts = [artifacts.set_prompt(2, i, spec.vocab, 1, 40, 9) for i in range(B)]
     gen = 24
-    m = Cis2Model(spec, w, max_pos=40 + gen, max_seqs=3)  # B=5: two groups
+    m = Cis2Model(spec, w, max_pos=40 + gen, max_seqs=3, reduction_mode=mode)  # B=5: two groups
     os.environ["CIS2_GRAPH"] = graph
     try:
         rows = m.decode_batch(prompts, gen)
     finally:
         del os.environ["CIS2_GRAPH"]
-    solo = Cis2Model(spec, w, max_pos=40 + gen)
+    solo = Cis2Model(spec, w, max_pos=40 + gen, reduction_mode=mode)
     for i, p in enumerate(prompts):
         s = solo.decode(p, gen, step_digests=False)
         assert rows[i]["witness"] == s["witness"]
         assert rows[i]["argmax_digest"] == s["argmax_digest"]
         assert np.array_equal(rows[i]["ids"], s["ids"])
+
+
+@pytest.mark.parametrize("name", ["smollm2-135m", "smollm2-135m-tree"])
+def test_rows_many_rows_gqa_grouped_attention(name, model_fixtures):
+    """Enough rows that the attention groups the query heads of one KV head
+    in a workgroup and the norms run as their own pass: two sequences of
+    the fixture's 288 positions (576 rows, 3 KV heads) against the
+    single-row forward of every position."""
+    rec = model_fixtures[name]
+    m, w = model_for(rec, max_seqs=2)
+    seq = rec["prompt"] + rec["tokens"][len(rec["prompt"]):]
+    n = len(seq)
+    seqs = np.concatenate([np.zeros(n), np.ones(n)])
+    lg, am = m.forward_rows(seqs, np.concatenate([np.arange(n)] * 2), seq + seq)
+    m.reset(0)
+    for p in range(n):
+        sl, sa = m.forward_token(p, seq[p])
+        for base in (0, n):
+            assert np.array_equal(sl.view(np.uint32), lg[base + p].view(np.uint32)), "row %d" % p
+            assert sa == am[base + p]
+    # the argmax at the last prompt row is the fixture's first generated id
+    assert am[len(rec["prompt"]) - 1] == rec["tokens"][len(rec["prompt"])]
