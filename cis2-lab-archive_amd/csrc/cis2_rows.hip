@@ -200,20 +200,68 @@ __global__ __launch_bounds__(256) void k_bgemm(BgemmArgs a) {
           if (DUAL) acc2 = acc2 + tree32(l2);
         }
       } else {
-#pragma unroll 4
-        for (uint32_t q = 0; q < q4; ++q) {
+        // software pipelined over two register sets: the reads of the next
+        // 4 q go out before the current 4 q's products and chain steps
+        // (reads past the end are clamped to the last q and unused)
+        constexpr uint32_t U = 4;
+        v4 aw[U], ax[U], aw2[U], bw[U], bx[U], bw2[U];
+        auto load = [&](v4 (&w)[U], v4 (&x)[U], v4 (&w2)[U], uint32_t q0) {
+#pragma unroll
+          for (uint32_t u = 0; u < U; ++u) {
+            const uint32_t qq = std::min(q0 + u, q4 - 1);
+            w[u] = wp[(size_t)qq * R];
+            x[u] = xp[qq];
+            if (DUAL) w2[u] = wp2[(size_t)qq * R];
+          }
+        };
+        auto step = [&](const v4 (&w)[U], const v4 (&x)[U], const v4 (&w2)[U]) {
+          float p[4 * U], p2[4 * U];
+#pragma unroll
+          for (uint32_t u = 0; u < U; ++u) {
+            p[4 * u] = w[u].x * x[u].x;
+            p[4 * u + 1] = w[u].y * x[u].y;
+            p[4 * u + 2] = w[u].z * x[u].z;
+            p[4 * u + 3] = w[u].w * x[u].w;
+            if (DUAL) {
+              p2[4 * u] = w2[u].x * x[u].x;
+              p2[4 * u + 1] = w2[u].y * x[u].y;
+              p2[4 * u + 2] = w2[u].z * x[u].z;
+              p2[4 * u + 3] = w2[u].w * x[u].w;
+            }
+          }
+#pragma unroll
+          for (uint32_t i = 0; i < 4 * U; ++i) {
+            acc = acc + p[i];
+            if (DUAL) acc2 = acc2 + p2[i];
+          }
+        };
+        uint32_t q = 0;
+        if (q4 >= U) {
+          load(aw, ax, aw2, 0);
+          for (; q + 2 * U <= q4; q += 2 * U) {
+            load(bw, bx, bw2, q + U);
+            step(aw, ax, aw2);
+            load(aw, ax, aw2, q + 2 * U);
+            step(bw, bx, bw2);
+          }
+          if (q + U <= q4) {  // set a holds q .. q+U-1
+            step(aw, ax, aw2);
+            q += U;
+          }
+        }
+        for (; q < q4; ++q) {
           const v4 w = wp[(size_t)q * R], x = xp[q];
-          float p;
-          p = w.x * x.x; acc = acc + p;
-          p = w.y * x.y; acc = acc + p;
-          p = w.z * x.z; acc = acc + p;
-          p = w.w * x.w; acc = acc + p;
+          float pp;
+          pp = w.x * x.x; acc = acc + pp;
+          pp = w.y * x.y; acc = acc + pp;
+          pp = w.z * x.z; acc = acc + pp;
+          pp = w.w * x.w; acc = acc + pp;
           if (DUAL) {
             const v4 w2 = wp2[(size_t)q * R];
-            p = w2.x * x.x; acc2 = acc2 + p;
-            p = w2.y * x.y; acc2 = acc2 + p;
-            p = w2.z * x.z; acc2 = acc2 + p;
-            p = w2.w * x.w; acc2 = acc2 + p;
+            pp = w2.x * x.x; acc2 = acc2 + pp;
+            pp = w2.y * x.y; acc2 = acc2 + pp;
+            pp = w2.z * x.z; acc2 = acc2 + pp;
+            pp = w2.w * x.w; acc2 = acc2 + pp;
           }
         }
       }
@@ -592,10 +640,10 @@ hipError_t launch_bgemm_multi(const BgemmSeg* segs, uint32_t nseg, uint32_t n,
   a.eps = o.eps;
   const uint32_t S = o.W2 ? 2 : 1;
   const uint64_t wgs = (uint64_t)a.blk0[nseg] * ((n + a.TB - 1) / a.TB);
-  // a grid of at most two workgroups per CU may take most of a CU's LDS per
-  // workgroup (fewer K chunks, each a full round trip); larger grids keep
-  // two workgroups per CU
-  const uint32_t budget = wgs <= 2 * (uint64_t)ncu ? kBgemmLdsBig : kBgemmLds;
+  // a grid of at most one workgroup per CU may take most of a CU's LDS
+  // (fewer K chunks, each a full round trip); larger grids keep two
+  // workgroups per CU, so that up to two per CU all run at once
+  const uint32_t budget = wgs <= (uint64_t)ncu ? kBgemmLdsBig : kBgemmLds;
   // largest chunk (a multiple of 32 k) whose W slices and X rows fit
   const uint32_t q_fit = (budget / 16 - a.TB) / (S * s0.R + a.TB);
   uint32_t KC = (q_fit * 4) & ~31u;
