@@ -592,22 +592,36 @@ __global__ __launch_bounds__(1024) void k_argmax_rows(const float* __restrict__ 
 
 template <bool DUAL, bool NORM>
 hipError_t launch_bgemm_t(const BgemmArgs& a, dim3 grid, size_t lds, hipStream_t st) {
-  static bool configured = false;
-  if (!configured) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_bgemm<DUAL, NORM>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       (int)kBgemmLdsBig);
-    if (e != hipSuccess) return e;
-    configured = true;
-  }
   hipLaunchKernelGGL((k_bgemm<DUAL, NORM>), grid, dim3(kT), lds, st, a);
   return hipGetLastError();
+}
+
+// The LDS limit of every k_bgemm variant, set at the first launch of any
+// (so that no attribute call happens later, e.g. inside a graph capture).
+hipError_t bgemm_configure() {
+  static bool configured = false;
+  if (configured) return hipSuccess;
+  const void* fns[4] = {reinterpret_cast<const void*>(&k_bgemm<false, false>),
+                        reinterpret_cast<const void*>(&k_bgemm<false, true>),
+                        reinterpret_cast<const void*>(&k_bgemm<true, false>),
+                        reinterpret_cast<const void*>(&k_bgemm<true, true>)};
+  for (const void* f : fns) {
+    hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       (int)kBgemmLdsBig);
+    if (e != hipSuccess) return e;
+  }
+  configured = true;
+  return hipSuccess;
 }
 
 hipError_t launch_bgemm_multi(const BgemmSeg* segs, uint32_t nseg, uint32_t n,
                               const BgemmOpts& o, hipStream_t st) {
   if (n == 0) return hipSuccess;
   if (nseg == 0 || nseg > kMaxSegs || (o.W2 && nseg != 1)) return hipErrorInvalidValue;
+  {
+    hipError_t e = bgemm_configure();
+    if (e != hipSuccess) return e;
+  }
   const BgemmSeg& s0 = segs[0];
   if (s0.K % 4 || s0.ldx % 4 || s0.R == 0 || s0.R > kT) return hipErrorInvalidValue;
   static int ncu = 0;
