@@ -84,11 +84,19 @@ def gemv_roofline(M=1536, K=576, copies=128, iters=4096):
     ms = plan.time(iters)
     algo_bytes = 4 * M * K + 4 * K + 4 * M
     achieved = algo_bytes / (ms * 1e-3) / 1e9
+    # a stream of `copies` GEMVs per launch (each on its own replica and x)
+    plan.time_batch(copies, 4)
+    ms_b = plan.time_batch(copies, 32)
+    achieved_b = copies * algo_bytes / (ms_b * 1e-3) / 1e9
     plan.close()
     return {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
             "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
             "kernel": "k_gemv %dx%d strict order" % (M, K), "us_per_launch": round(ms * 1e3, 3),
-            "algorithmic_bytes": algo_bytes}
+            "algorithmic_bytes": algo_bytes,
+            "stream": {"gemvs_per_launch": copies, "us_per_launch": round(ms_b * 1e3, 2),
+                       "achieved": round(achieved_b, 2), "frac": round(achieved_b / HBM_PEAK_GBS, 4),
+                       "kernel": "k_gemv_many: %d independent %dx%d GEMVs per launch"
+                                 % (copies, M, K)}}
 
 
 def cpu_baseline(spec, weights, prompt, seconds=15.0):

@@ -72,6 +72,9 @@ SIGNATURES = {
                                              c_fp, ctypes.POINTER(ctypes.c_void_p)]),
     "cis2_gemv_plan_run": (ctypes.c_int, [ctypes.c_void_p, c_fp, c_fp]),
     "cis2_gemv_plan_time": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_uint32, c_fp]),
+    "cis2_gemv_plan_run_batch": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_uint32, c_fp, c_fp]),
+    "cis2_gemv_plan_time_batch": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_uint32,
+                                                 ctypes.c_uint32, c_fp]),
     "cis2_gemv_plan_destroy": (None, [ctypes.c_void_p]),
     "cis2_sha256": (None, [ctypes.c_void_p, ctypes.c_uint64, c_u8p]),
     "cis2_math_map": (ctypes.c_int, [ctypes.c_int, c_fp, c_fp, ctypes.c_uint64]),

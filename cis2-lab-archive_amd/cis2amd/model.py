@@ -230,6 +230,23 @@ class GemvPlan:
         check(_lib.lib().cis2_gemv_plan_time(self.plan, iters, ctypes.byref(ms)))
         return ms.value
 
+    def run_batch(self, X):
+        """n independent GEMVs in one launch: row i of the result is
+        W_(i mod copies) X[i]."""
+        X = np.ascontiguousarray(X, dtype=np.float32)
+        n = X.shape[0]
+        assert X.shape == (n, self.K)
+        Y = np.empty((n, self.M), dtype=np.float32)
+        check(_lib.lib().cis2_gemv_plan_run_batch(self.plan, n, _ptr(X, _lib.c_fp),
+                                                  _ptr(Y, _lib.c_fp)))
+        return Y
+
+    def time_batch(self, n, iters):
+        """Mean ms per launch of n GEMVs (device-resident inputs)."""
+        ms = ctypes.c_float()
+        check(_lib.lib().cis2_gemv_plan_time_batch(self.plan, n, iters, ctypes.byref(ms)))
+        return ms.value
+
     def close(self):
         if getattr(self, "plan", None):
             _lib.lib().cis2_gemv_plan_destroy(self.plan)

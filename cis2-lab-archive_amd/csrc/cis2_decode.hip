@@ -1419,6 +1419,33 @@ void k_gemv_blk(const float* __restrict__ W, const float* __restrict__ x, float*
   if (threadIdx.x < R && row < M) GW(y)[row] = acc;
 }
 
+// A batch of n independent GEMVs in one launch (gridDim.y = n): GEMV i is
+// y_i = W_c x_i with W_c the replica c = (first + i) % copies, x_i at
+// x + i*K, y_i at y + i*M.  The block's work is k_gemv_blk's; several
+// workgroups share a CU, so one block's copy overlaps another's chains and
+// the launch streams weights at HBM rate.
+template <uint32_t R, uint32_t KC>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 4)))
+void k_gemv_many(const float* __restrict__ W, uint64_t w_per, uint32_t copies, uint32_t first,
+                 const float* __restrict__ x, float* y, uint32_t M, uint32_t Krt) {
+  const uint32_t K = KC ? KC : Krt;
+  extern __shared__ f4 lds_dyn[];
+  lf* w = (lf*)lds_dyn;
+  lf* xs = w + (size_t)R * K;
+  lf4* pad = (lf4*)(xs + K);
+  const uint32_t b = blockIdx.x, i = blockIdx.y;
+  const uint32_t c = (first + i) % copies;
+  const size_t blkf = (size_t)R * K;
+  gf4* src = G4(W + c * w_per + b * blkf);
+  gf4* x4 = G4(x + (size_t)i * K);
+  const uint32_t n4 = (uint32_t)(blkf / 4), k4 = K >> 2;
+  copy_to_lds((lf4*)w, n4 + k4, [=](uint32_t j) { return j < n4 ? src + j : x4 + (j - n4); });
+  __syncthreads();
+  const float acc = gemv_lds_t<R>(w, xs, K, 1, pad);
+  const uint32_t row = b * R + threadIdx.x;
+  if (threadIdx.x < R && row < M) GW(y + (size_t)i * M)[row] = acc;
+}
+
 }  // namespace
 
 size_t gemv_blk_lds_bytes(uint32_t K, uint32_t R) {
@@ -1450,6 +1477,33 @@ hipError_t launch_gemv_blk(const float* W, const float* x, float* y, uint32_t M,
                                : launch_gemv_blk_t<16, 0>(W, x, y, M, K, lds, s);
   if (R == 32) return K == 576 ? launch_gemv_blk_t<32, 576>(W, x, y, M, K, lds, s)
                                : launch_gemv_blk_t<32, 0>(W, x, y, M, K, lds, s);
+  return hipErrorInvalidValue;
+}
+
+template <uint32_t R, uint32_t KC>
+static hipError_t launch_gemv_many_t(const float* W, uint64_t w_per, uint32_t copies,
+                                     uint32_t first, uint32_t n, const float* x, float* y,
+                                     uint32_t M, uint32_t K, size_t lds, hipStream_t s) {
+  static size_t configured = 0;
+  if (lds > configured) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemv_many<R, KC>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
+    configured = lds;
+  }
+  hipLaunchKernelGGL((k_gemv_many<R, KC>), dim3((M + R - 1) / R, n), dim3(kThreads), lds, s, W,
+                     w_per, copies, first, x, y, M, K);
+  return hipGetLastError();
+}
+
+hipError_t launch_gemv_many(const float* W, uint64_t w_per, uint32_t copies, uint32_t first,
+                            uint32_t n, const float* x, float* y, uint32_t M, uint32_t K,
+                            uint32_t R, hipStream_t s) {
+  const size_t lds = gemv_blk_lds_bytes(K, R);
+  if (n == 0) return hipSuccess;
+  if (K % 4 || lds > 160 * 1024 - 64 || copies == 0 || n > 65535) return hipErrorInvalidValue;
+  if (R == 16) return K == 576 ? launch_gemv_many_t<16, 576>(W, w_per, copies, first, n, x, y, M, K, lds, s)
+                               : launch_gemv_many_t<16, 0>(W, w_per, copies, first, n, x, y, M, K, lds, s);
   return hipErrorInvalidValue;
 }
 

@@ -75,5 +75,11 @@ hipError_t launch_decode(const DecodeArgs& a, hipStream_t s);
 size_t gemv_blk_lds_bytes(uint32_t K, uint32_t R);
 hipError_t launch_gemv_blk(const float* W, const float* x, float* y, uint32_t M, uint32_t K,
                            uint32_t R, hipStream_t s);
+// n independent GEMVs in one launch: y_i = W_c x_i, W_c the replica
+// c = (first + i) % copies at W + c * w_per (blocked layout), x_i = x + i*K,
+// y_i = y + i*M.
+hipError_t launch_gemv_many(const float* W, uint64_t w_per, uint32_t copies, uint32_t first,
+                            uint32_t n, const float* x, float* y, uint32_t M, uint32_t K,
+                            uint32_t R, hipStream_t s);
 
 }  // namespace cis2

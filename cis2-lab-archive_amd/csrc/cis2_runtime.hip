@@ -143,6 +143,8 @@ constexpr uint32_t kPlanR = 16;
 struct cis2_gemv_plan {
   uint32_t M, K, copies;
   float *W = nullptr, *x = nullptr, *y = nullptr;
+  float *xb = nullptr, *yb = nullptr;  // [ncap][K], [ncap][M]: batched launches
+  uint32_t ncap = 0;
   hipStream_t st = nullptr;
   hipEvent_t e0 = nullptr, e1 = nullptr;
 };
@@ -1490,9 +1492,64 @@ int cis2_gemv_plan_time(cis2_gemv_plan* p, uint32_t iters, float* ms) {
   return CIS2_OK;
 }
 
+// Device buffers for n GEMVs' inputs and outputs.
+static hipError_t plan_reserve(cis2_gemv_plan* p, uint32_t n) {
+  if (n <= p->ncap) return hipSuccess;
+  hipError_t e = hipStreamSynchronize(p->st);
+  if (p->xb) (void)hipFree(p->xb);
+  if (p->yb) (void)hipFree(p->yb);
+  p->xb = p->yb = nullptr;
+  p->ncap = 0;
+  if (e == hipSuccess) e = hipMalloc(&p->xb, (size_t)n * p->K * sizeof(float));
+  if (e == hipSuccess) e = hipMalloc(&p->yb, (size_t)n * p->M * sizeof(float) + 256);
+  if (e == hipSuccess) {
+    p->ncap = n;
+    // defined inputs for the timing runs
+    e = hipMemsetAsync(p->xb, 0, (size_t)n * p->K * sizeof(float), p->st);
+  }
+  return e;
+}
+
+int cis2_gemv_plan_run_batch(cis2_gemv_plan* p, uint32_t n, const float* x, float* y) {
+  if (!p || (n && (!x || !y)) || n > 65535) return CIS2_E_ARG;
+  if (n == 0) return CIS2_OK;
+  hipError_t e = plan_reserve(p, n);
+  if (e == hipSuccess)
+    e = hipMemcpyAsync(p->xb, x, (size_t)n * p->K * sizeof(float), hipMemcpyHostToDevice, p->st);
+  if (e == hipSuccess)
+    e = launch_gemv_many(p->W, blocked_floats(p->M, p->K, kPlanR), p->copies, 0, n, p->xb, p->yb,
+                         p->M, p->K, kPlanR, p->st);
+  if (e == hipSuccess)
+    e = hipMemcpyAsync(y, p->yb, (size_t)n * p->M * sizeof(float), hipMemcpyDeviceToHost, p->st);
+  if (e == hipSuccess) e = hipStreamSynchronize(p->st);
+  return e == hipSuccess ? CIS2_OK : (e == hipErrorOutOfMemory ? CIS2_E_OOM : CIS2_E_DEVICE);
+}
+
+int cis2_gemv_plan_time_batch(cis2_gemv_plan* p, uint32_t n, uint32_t iters, float* ms) {
+  if (!p || !ms || iters == 0 || n == 0 || n > 65535) return CIS2_E_ARG;
+  const uint64_t per = blocked_floats(p->M, p->K, kPlanR);
+  hipError_t e = plan_reserve(p, n);
+  auto launch = [&](uint32_t it) {
+    return launch_gemv_many(p->W, per, p->copies, (uint32_t)(((uint64_t)it * n) % p->copies), n,
+                            p->xb, p->yb, p->M, p->K, kPlanR, p->st);
+  };
+  if (e == hipSuccess) e = launch(0);  // warm-up
+  if (e == hipSuccess) e = hipEventRecord(p->e0, p->st);
+  for (uint32_t i = 0; e == hipSuccess && i < iters; ++i) e = launch(i + 1);
+  if (e == hipSuccess) e = hipEventRecord(p->e1, p->st);
+  if (e == hipSuccess) e = hipEventSynchronize(p->e1);
+  float t = 0.0f;
+  if (e == hipSuccess) e = hipEventElapsedTime(&t, p->e0, p->e1);
+  if (e != hipSuccess) return e == hipErrorOutOfMemory ? CIS2_E_OOM : CIS2_E_DEVICE;
+  *ms = t / (float)iters;
+  return CIS2_OK;
+}
+
 void cis2_gemv_plan_destroy(cis2_gemv_plan* p) {
   if (!p) return;
   if (p->st) (void)hipStreamSynchronize(p->st);
+  if (p->xb) (void)hipFree(p->xb);
+  if (p->yb) (void)hipFree(p->yb);
   if (p->W) (void)hipFree(p->W);
   if (p->x) (void)hipFree(p->x);
   if (p->y) (void)hipFree(p->y);

@@ -201,6 +201,16 @@ int cis2_gemv_plan_run(cis2_gemv_plan *p, const float *x, float *y);
 /* Times `iters` device-resident launches cycling through the replicas on one
  * stream (HIP events on that stream); returns the mean ms per launch. */
 int cis2_gemv_plan_time(cis2_gemv_plan *p, uint32_t iters, float *ms_per_launch);
+/* n independent GEMVs in one launch: y_i = W_(i mod copies) x_i with host
+ * x[n][K] and y[n][M], each bit-equal to cis2_gemv_plan_run on x_i (a
+ * GEMV stream, as the layers of a model issue them back to back; the
+ * reference runs one GEMV per call, rust-5 src/main.rs). n <= 65535. */
+int cis2_gemv_plan_run_batch(cis2_gemv_plan *p, uint32_t n, const float *x, float *y);
+/* Times `iters` launches of n GEMVs each over device-resident inputs,
+ * consecutive launches on consecutive replicas; returns the mean ms per
+ * launch. */
+int cis2_gemv_plan_time_batch(cis2_gemv_plan *p, uint32_t n, uint32_t iters,
+                              float *ms_per_launch);
 void cis2_gemv_plan_destroy(cis2_gemv_plan *p);
 
 /* SHA-256 of a host buffer (the witness header binds sha256 of

@@ -48,3 +48,17 @@ def test_subnormal_products_flush():
     y = GemvPlan(W)(x)
     assert np.array_equal(y.view(np.uint32), O.gemv(W, x).view(np.uint32))
     assert np.all(y == 0.0)
+
+
+@pytest.mark.parametrize("M,K,n", [(1536, 576, 7), (100, 576, 3), (65, 12, 5), (576, 1536, 2)])
+def test_batched_gemvs_equal_single_and_oracle(M, K, n):
+    """n GEMVs in one launch (replicas rotating) give each GEMV's own bits."""
+    rng = np.random.default_rng(M * 7 + K + n)
+    W = rng.standard_normal((M, K)).astype(np.float32)
+    X = rng.standard_normal((n, K)).astype(np.float32)
+    plan = GemvPlan(W, copies=3)
+    Y = plan.run_batch(X)
+    for i in range(n):
+        assert np.array_equal(Y[i].view(np.uint32), plan(X[i]).view(np.uint32)), i
+        assert np.array_equal(Y[i].view(np.uint32), O.gemv(W, X[i]).view(np.uint32)), i
+    plan.close()
