@@ -55,17 +55,18 @@ GEMV_WEIGHT_BYTES = 4 * (30 * 3538944 + 49152 * 576)
 NORM_BYTES = 4 * 61 * 576
 KV_BYTES_PER_POS = 4 * 2 * 192 * 30
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "k_decode_smollm2_pmc.txt")
+GEMV_STREAM_FILE = os.path.join(ROOT, "profiles", "k_gemv_many_1536x576_stream.txt")
 
 
 def decode_bytes(pos):
     return GEMV_WEIGHT_BYTES + NORM_BYTES + KV_BYTES_PER_POS * (int(pos) + 1)
 
 
-def measured_traffic():
-    """HBM bytes per decode launch (FETCH_SIZE + WRITE_SIZE, copy-calibrated)
-    from the committed counter summary, or None."""
+def measured_traffic(path=TRAFFIC_FILE):
+    """HBM bytes per launch (FETCH_SIZE + WRITE_SIZE, copy-calibrated) from a
+    committed counter summary, or None."""
     try:
-        for line in open(TRAFFIC_FILE):
+        for line in open(path):
             if line.startswith("traffic_bytes_per_launch="):
                 return int(line.split("=", 1)[1].split()[0])
     except OSError:
@@ -95,6 +96,7 @@ def gemv_roofline(M=1536, K=576, copies=128, iters=4096):
             "algorithmic_bytes": algo_bytes,
             "stream": {"gemvs_per_launch": copies, "us_per_launch": round(ms_b * 1e3, 2),
                        "achieved": round(achieved_b, 2), "frac": round(achieved_b / HBM_PEAK_GBS, 4),
+                       "traffic": measured_traffic(GEMV_STREAM_FILE) if copies == 128 else None,
                        "kernel": "k_gemv_many: %d independent %dx%d GEMVs per launch"
                                  % (copies, M, K)}}
 
