@@ -110,6 +110,24 @@ __host__ __device__ inline uint32_t att_tile_positions(uint32_t hd, uint32_t max
   return (uint32_t)tp;
 }
 
+// Split attention: output dims per mix task, and the floats of the tree
+// partials that follow the scores (one per 32 positions, rounded to 16 B).
+constexpr uint32_t kAttDV = 16;
+__host__ __device__ inline size_t att_part_floats(uint32_t max_pos) {
+  return ((size_t)max_pos / 32 + 1 + 3) & ~(size_t)3;
+}
+// Positions per V tile of a mix task: the largest multiple of 32 whose two
+// [kAttDV][TP+4] tiles fit beside the scores and partials; 0 if < 32.
+__host__ __device__ inline uint32_t att_mix_tile_positions(uint32_t max_pos, size_t wfloats) {
+  const size_t used = (size_t)max_pos + 64 + att_part_floats(max_pos);
+  const size_t room = wfloats > used ? wfloats - used : 0;
+  const size_t per = room / (2 * kAttDV);
+  if (per < 36) return 0;
+  size_t tp = (per - 4) & ~(size_t)31;
+  if (tp > 2048) tp = 2048;
+  return (uint32_t)tp;
+}
+
 // Floats of the vector region (input vectors and scratch of every role),
 // rounded up to 16 bytes.
 __host__ __device__ inline size_t decode_vec_floats(const DecodeArgs& a) {
@@ -946,6 +964,109 @@ __device__ __forceinline__ void prefetch_kv(const DecodeArgs& a, uint32_t l, uin
 }
 
 // Attention for query head h (code/cis2-fp/src/main.rs:415-467).
+// The inputs of query head h at this position, in LDS: q at qv[0..hd), the
+// head's k at qv[hd..2hd), v at qv[2hd..3hd) (gathered from the QKV tasks),
+// then Qwen3's per-head QK-norm (after bias, before RoPE;
+// labs/w1x-qwen3/scripts/qwen3-port.diff:66-80) and RoPE rotate-half of q
+// and k (main.rs:285-307): o1 = x1*c + (-x2)*s, o2 = x2*c + x1*s.  Ends with
+// a barrier.  tmp and misc: hd and 64 floats of scratch.
+template <bool TR>
+__device__ __forceinline__ void att_head_inputs(const DecodeArgs& a, uint32_t l, uint32_t h,
+                                                lf* qv, lf* tmp, lf* misc) {
+  const LayerW Lw = a.layers[l];
+  const Act ac = act_of(a, l);
+  const uint32_t hd = a.hd, kvh = h / (a.nh / a.nkv), pos = a.pos;
+  lf* kv = qv + hd;
+  NormW nq, nk;
+  if (Lw.qn) nq = load_normw(Lw.qn, hd);
+  if (Lw.kn) nk = load_normw(Lw.kn, hd);
+  // cos/sin of this position for the pair this thread rotates (hd <= 256)
+  const uint32_t half = hd / 2;
+  float rc = 0.0f, rsn = 0.0f;
+  if (threadIdx.x < 2 * half) {
+    const uint32_t i = threadIdx.x < half ? threadIdx.x : threadIdx.x - half;
+    gf* cs = G(a.rope_cs) + (size_t)pos * half * 2;
+    rc = cs[2 * i];
+    rsn = cs[2 * i + 1];
+  }
+  gather(qv, 3 * hd, a.epoch, a.err, [=](uint32_t i) {
+    const uint32_t seg = i >= hd ? (i >= 2 * hd ? 2u : 1u) : 0u, d = i - seg * hd;
+    return seg == 0 ? ac.q + (size_t)h * hd + d
+                    : (seg == 1 ? ac.k : ac.v) + (size_t)kvh * hd + d;
+  });
+  if (Lw.qn) rmsnorm_lds<TR>(qv, nq, a.eps, hd, tmp, qv, misc);
+  if (Lw.kn) rmsnorm_lds<TR>(kv, nk, a.eps, hd, tmp, kv, misc);
+  if (threadIdx.x < 2 * half) {
+    const uint32_t idx = threadIdx.x;
+    lf* hv = idx < half ? qv : kv;
+    uint32_t i = idx < half ? idx : idx - half;
+    float c = rc, sn = rsn;
+    float x1 = hv[i], x2 = hv[i + half];
+    float t1 = x1 * c;
+    float nx2 = -x2;
+    float t2 = nx2 * sn;
+    float t3 = x2 * c;
+    float t4 = x1 * sn;
+    hv[i] = t1 + t2;
+    hv[i + half] = t3 + t4;
+  }
+  __syncthreads();
+}
+
+// softmax over ss[0..len) in place: first-wins max, pinned exp, the
+// denominator as one strict chain (softmax_seq, math.rs:425-442) or tree32
+// block results folded from 0 (softmax_tree, math.rs:448-465; partials at
+// part[0..ceil(len/32))), then a true divide.  misc[1] and red: scratch.
+// Starts after and ends with a barrier.
+template <bool TR>
+__device__ __forceinline__ void softmax_lds(lf* ss, uint32_t len, lf* part, lf* misc,
+                                            AS_LDS uint32_t* red) {
+  Cand best = {0.0f, UINT32_MAX};
+  for (uint32_t j = threadIdx.x; j < len; j += kThreads) {
+    float v = ss[j];
+    if (v == v) best = cand_pick(best, Cand{v, j});
+  }
+  const Cand b = cand_block(best, red);
+  // the first maximum's own bits (a NaN at position 0 wins outright)
+  const float mx = (ss[0] != ss[0] || b.i == UINT32_MAX) ? ss[0] : ss[b.i];
+  for (uint32_t j = threadIdx.x; j < len; j += kThreads) {
+    float dlt = ss[j] - mx;
+    ss[j] = exp_pinned(dlt);
+  }
+  __syncthreads();
+  if constexpr (TR) {
+    const uint32_t nbk = (len + 31) / 32;
+    for (uint32_t t = threadIdx.x; t < nbk; t += kThreads)
+      part[t] = tree_part(ss + 32 * t, len - 32 * t, 1);
+    __syncthreads();
+    if (threadIdx.x < 64) {
+      const float acc = chain1(part, nbk, 1, 0.0f);
+      if (threadIdx.x == 0) misc[1] = acc;
+    }
+  } else if (threadIdx.x < 64) {
+    const float acc = chain_vec(ss, len, 0.0f);
+    if (threadIdx.x == 0) misc[1] = acc;
+  }
+  __syncthreads();
+  const float den = misc[1];
+  for (uint32_t j = threadIdx.x; j < len; j += kThreads) {
+    float pj = ss[j] / den;
+    ss[j] = pj;
+  }
+  __syncthreads();
+}
+
+// The rotated k and the raw v of this position into kv head kvh's caches.
+__device__ __forceinline__ void store_kv_pos(const DecodeArgs& a, uint32_t l, uint32_t kvh,
+                                             const lf* kv, const lf* vv) {
+  AS_GLB float* kc = GW(a.kc0 + (size_t)l * a.cache_stride);
+  AS_GLB float* vc = GW(a.vc0 + (size_t)l * a.cache_stride);
+  for (uint32_t d = threadIdx.x; d < a.hd; d += kThreads) {
+    kc[((size_t)kvh * a.hd + d) * a.max_pos + a.pos] = kv[d];
+    vc[((size_t)kvh * a.hd + d) * a.max_pos + a.pos] = vv[d];
+  }
+}
+
 template <bool TR>
 __device__ __forceinline__ void run_att(const DecodeArgs& a, uint32_t l, uint32_t h, const Lds& s,
                         size_t wfloats) {
@@ -966,52 +1087,9 @@ __device__ __forceinline__ void run_att(const DecodeArgs& a, uint32_t l, uint32_
   const bool in_lds = att_lds_floats(hd, pos, a.max_pos) <= wfloats;
   stamp(a, l, P_ATT, h, 0);
   if (in_lds) prefetch_kv(a, l, kvh, kl, S);
-  NormW nq, nk;
-  if (Lw.qn) nq = load_normw(Lw.qn, hd);
-  if (Lw.kn) nk = load_normw(Lw.kn, hd);
-  // cos/sin of this position for the pair this thread rotates (hd <= 256)
-  const uint32_t half = hd / 2;
-  float rc = 0.0f, rsn = 0.0f;
-  if (threadIdx.x < 2 * half) {
-    const uint32_t i = threadIdx.x < half ? threadIdx.x : threadIdx.x - half;
-    gf* cs = G(a.rope_cs) + (size_t)pos * half * 2;
-    rc = cs[2 * i];
-    rsn = cs[2 * i + 1];
-  }
-  gather(qv, 3 * hd, a.epoch, a.err, [=](uint32_t i) {
-    const uint32_t seg = i >= hd ? (i >= 2 * hd ? 2u : 1u) : 0u, d = i - seg * hd;
-    return seg == 0 ? ac.q + (size_t)h * hd + d
-                    : (seg == 1 ? ac.k : ac.v) + (size_t)kvh * hd + d;
-  });
+  att_head_inputs<TR>(a, l, h, qv, tmp, misc);
   stamp(a, l, P_ATT, h, 1);
-  // Qwen3 per-head QK-norm, after bias and before RoPE
-  // (labs/w1x-qwen3/scripts/qwen3-port.diff:66-80).
-  if (Lw.qn) rmsnorm_lds<TR>(qv, nq, a.eps, hd, tmp, qv, misc);
-  if (Lw.kn) rmsnorm_lds<TR>(kv, nk, a.eps, hd, tmp, kv, misc);
-  // RoPE rotate-half (main.rs:285-307): o1 = x1*c + (-x2)*s, o2 = x2*c + x1*s.
-  if (threadIdx.x < 2 * half) {
-    const uint32_t idx = threadIdx.x;
-    lf* hv = idx < half ? qv : kv;
-    uint32_t i = idx < half ? idx : idx - half;
-    float c = rc, sn = rsn;
-    float x1 = hv[i], x2 = hv[i + half];
-    float t1 = x1 * c;
-    float nx2 = -x2;
-    float t2 = nx2 * sn;
-    float t3 = x2 * c;
-    float t4 = x1 * sn;
-    hv[i] = t1 + t2;
-    hv[i + half] = t3 + t4;
-  }
-  __syncthreads();
-  AS_GLB float* kc = GW(a.kc0 + (size_t)l * a.cache_stride);
-  AS_GLB float* vc = GW(a.vc0 + (size_t)l * a.cache_stride);
-  if (h % group == 0) {  // one writer per kv head; the others use their own copy
-    for (uint32_t d = threadIdx.x; d < hd; d += kThreads) {
-      kc[((size_t)kvh * hd + d) * a.max_pos + pos] = kv[d];
-      vc[((size_t)kvh * hd + d) * a.max_pos + pos] = vv[d];
-    }
-  }
+  if (h % group == 0) store_kv_pos(a, l, kvh, kv, vv);  // one writer per kv head
   // scores_j = dot_seq(q, k_j) * scale (main.rs:440-445)
   if (in_lds) {
     // products q[d] * k_j[d] in place (row d scaled by q[d]); tmp = q * k_pos
@@ -1049,44 +1127,7 @@ __device__ __forceinline__ void run_att(const DecodeArgs& a, uint32_t l, uint32_
       ss[pos] = (TR ? tree_col(tmp, hd, 1, 0.0f) : chain1(tmp, hd, 1, 0.0f)) * a.scale;
   }
   __syncthreads();
-  // softmax_seq (math.rs:425-442): first-wins max, pinned exp, strict-chain
-  // denominator, true divide.
-  Cand best = {0.0f, UINT32_MAX};
-  for (uint32_t j = threadIdx.x; j < len; j += kThreads) {
-    float v = ss[j];
-    if (v == v) best = cand_pick(best, Cand{v, j});
-  }
-  const Cand b = cand_block(best, red);
-  // the first maximum's own bits (a NaN at position 0 wins outright)
-  const float mx = (ss[0] != ss[0] || b.i == UINT32_MAX) ? ss[0] : ss[b.i];
-  for (uint32_t j = threadIdx.x; j < len; j += kThreads) {
-    float dlt = ss[j] - mx;
-    ss[j] = exp_pinned(dlt);
-  }
-  __syncthreads();
-  if constexpr (TR) {
-    // softmax_tree (math.rs:448-465): block results of the exp values in
-    // the (now unused) K region, folded from 0
-    lf* part = ss + a.max_pos + 64;
-    const uint32_t nbk = (len + 31) / 32;
-    for (uint32_t t = threadIdx.x; t < nbk; t += kThreads)
-      part[t] = tree_part(ss + 32 * t, len - 32 * t, 1);
-    __syncthreads();
-    if (threadIdx.x < 64) {
-      const float acc = chain1(part, nbk, 1, 0.0f);
-      if (threadIdx.x == 0) misc[1] = acc;
-    }
-  } else if (threadIdx.x < 64) {
-    const float acc = chain_vec(ss, len, 0.0f);
-    if (threadIdx.x == 0) misc[1] = acc;
-  }
-  __syncthreads();
-  const float den = misc[1];
-  for (uint32_t j = threadIdx.x; j < len; j += kThreads) {
-    float pj = ss[j] / den;
-    ss[j] = pj;
-  }
-  __syncthreads();
+  softmax_lds<TR>(ss, len, ss + a.max_pos + 64, misc, red);  // tree partials in the K region
   stamp(a, l, P_ATT, h, 3);
   // V mix out_d = fold_j (p_j * v_j[d]) (main.rs:454-463)
   if (in_lds) {
@@ -1127,6 +1168,152 @@ __device__ __forceinline__ void run_att(const DecodeArgs& a, uint32_t l, uint32_
   }
   __syncthreads();
   stamp(a, l, P_ATT, h, 2);
+}
+
+// ---------------------------------------------------------------------------
+// Split attention, for contexts whose K/V rows do not fit one workgroup's
+// LDS.  The phase's tasks are natt_s score tasks and then natt_v mix tasks
+// (every workgroup runs its score tasks before its mix tasks, so waits stay
+// acyclic):
+//   score task (h, c): positions c*256 .. c*256+255 of query head h; thread
+//     j loads its column k_j[0..hd) straight from the cache, 64 loads in
+//     flight, and forms dot_seq(q, k_j) (or dot_tree) * scale, published as
+//     a tagged word; the chunk holding `pos` uses this position's own k and
+//     (for the first head of a kv group) stores k and v into the caches.
+//   mix task (h, dc): output dims d0 = dc*16 .. d0+15 of head h: gathers all
+//     of the head's scores, runs the softmax (the same order as one task),
+//     then lane d continues its one left-to-right V-mix chain over tiles of
+//     its V rows, each tile copied into LDS with global_load_lds while the
+//     previous tile is multiplied and chained (the first during the
+//     softmax).
+// Each head's K and V are read by many workgroups at once instead of
+// streaming through one.
+// ---------------------------------------------------------------------------
+template <bool TR>
+__device__ __forceinline__ void run_att_score(const DecodeArgs& a, uint32_t l, uint32_t t,
+                                              const Lds& s) {
+  const uint32_t C = a.att_chunks, h = t / C, c = t - h * C;
+  const uint32_t hd = a.hd, group = a.nh / a.nkv, kvh = h / group, pos = a.pos, len = pos + 1;
+  const uint32_t j0 = c * kThreads;
+  stamp(a, l, P_ATT, t, 0);
+  if (j0 >= len) {  // no positions in this chunk yet
+    stamp(a, l, P_ATT, t, 1);
+    stamp(a, l, P_ATT, t, 3);
+    stamp(a, l, P_ATT, t, 2);
+    return;
+  }
+  lf* qv = s.v;
+  lf* kv = qv + hd;
+  lf* vv = kv + hd;
+  lf* tmp = vv + hd;
+  lf* misc = tmp + hd;
+  att_head_inputs<TR>(a, l, h, qv, tmp, misc);
+  stamp(a, l, P_ATT, t, 1);
+  if (pos < j0 + kThreads && h % group == 0) store_kv_pos(a, l, kvh, kv, vv);
+  const uint32_t j = j0 + threadIdx.x;
+  if (j < len) {
+    const float* kb = a.kc0 + (size_t)l * a.cache_stride + (size_t)kvh * hd * a.max_pos + j;
+    const bool cached = j < pos;
+    float acc = 0.0f;
+    for (uint32_t d0 = 0; d0 < hd; d0 += 64) {
+      const uint32_t nd = min(64u, hd - d0);
+      float k[64];
+#pragma unroll
+      for (uint32_t i = 0; i < 64; ++i)
+        if (i < nd) k[i] = cached ? kb[(size_t)(d0 + i) * a.max_pos] : kv[d0 + i];
+      if (TR) {
+#pragma unroll
+        for (uint32_t b = 0; b < 64; b += 32) {
+          if (b < nd) {
+            float l32[32];
+#pragma unroll
+            for (uint32_t i = 0; i < 32; ++i) l32[i] = b + i < nd ? qv[d0 + b + i] * k[b + i] : 0.0f;
+            acc = acc + tree32(l32);
+          }
+        }
+      } else {
+#pragma unroll
+        for (uint32_t i = 0; i < 64; ++i) {
+          if (i < nd) {
+            const float p = qv[d0 + i] * k[i];
+            acc = acc + p;
+          }
+        }
+      }
+    }
+    put_word((gw*)a.scw + ((size_t)l * a.nh + h) * a.max_pos + j, acc * a.scale, a.epoch);
+  }
+  stamp(a, l, P_ATT, t, 3);
+  stamp(a, l, P_ATT, t, 2);
+}
+
+// Rows d0 .. d0+nd-1 of a kv head's V cache (row stride max_pos),
+// positions j0 .. j0+n-1 (rounded up to 4, inside max_pos), into LDS rows
+// of stride TS with global_load_lds_dwordx4: one wave instruction per 256
+// positions of a row, every one in flight.  Data is in LDS once vmcnt
+// reaches 0 and visible after a barrier.
+__device__ __forceinline__ void issue_v_tile(lf* dst, const float* vrows, uint32_t max_pos,
+                                             uint32_t nd, uint32_t j0, uint32_t n, uint32_t TS) {
+  const uint32_t n4 = (n + 3) >> 2, per_row = (n4 + 63) >> 6;
+  const uint32_t wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  for (uint32_t k = wv; k < nd * per_row; k += kThreads / 64) {
+    const uint32_t d = k / per_row, q0 = (k - d * per_row) * 64;
+    if (q0 + lane < n4)
+      __builtin_amdgcn_global_load_lds(
+          (const AS_GLB void*)(G4(vrows + (size_t)d * max_pos + j0) + q0 + lane),
+          (AS_LDS void*)((lf4*)(dst + (size_t)d * TS) + q0), 16, 0, 0);
+  }
+}
+
+template <bool TR>
+__device__ __forceinline__ void run_att_mix(const DecodeArgs& a, uint32_t l, uint32_t u,
+                                            const Lds& s) {
+  const Act ac = act_of(a, l);
+  const uint32_t DVc = a.att_dvc, h = u / DVc, dc = u - h * DVc;
+  const uint32_t hd = a.hd, kvh = h / (a.nh / a.nkv), pos = a.pos, len = pos + 1;
+  const uint32_t d0 = dc * kAttDV, nd = min(kAttDV, hd - d0);
+  const uint32_t t = a.natt_s + u;
+  lf* vv = s.v;        // v of this position, dims d0.. [kAttDV]
+  lf* misc = vv + 64;  // [1] den, [4..] reduction scratch
+  AS_LDS uint32_t* red = (AS_LDS uint32_t*)(misc + 4);
+  lf* ss = s.w;                                 // scores / probabilities [max_pos + 64]
+  lf* part = ss + a.max_pos + 64;               // tree partials
+  const uint32_t TP = a.att_tp, TS = TP + 4;
+  lf* vt0 = part + att_part_floats(a.max_pos);  // two V tiles [kAttDV][TS]
+  lf* vt1 = vt0 + (size_t)kAttDV * TS;
+  const float* vrows = a.vc0 + (size_t)l * a.cache_stride + ((size_t)kvh * hd + d0) * a.max_pos;
+  stamp(a, l, P_ATT, t, 0);
+  if (pos > 0) issue_v_tile(vt0, vrows, a.max_pos, nd, 0, min(TP, pos), TS);
+  gather(ss, len, a.epoch, a.err, [=](uint32_t i) {
+    return (const gw*)a.scw + ((size_t)l * a.nh + h) * a.max_pos + i;
+  });
+  gather(vv, nd, a.epoch, a.err, [=](uint32_t i) { return ac.v + (size_t)kvh * hd + d0 + i; });
+  stamp(a, l, P_ATT, t, 1);
+  __syncthreads();
+  softmax_lds<TR>(ss, len, part, misc, red);
+  stamp(a, l, P_ATT, t, 3);
+  // out_d = fold_j (p_j * v_j[d]) (main.rs:454-463), one chain per lane
+  float acc = 0.0f;
+  uint32_t it = 0;
+  for (uint32_t j0 = 0; j0 < pos; j0 += TP, ++it) {
+    const uint32_t n = min(TP, pos - j0);
+    lf* vt = (it & 1) ? vt1 : vt0;
+    wait_vm0();
+    __syncthreads();
+    if (j0 + TP < pos)
+      issue_v_tile((it & 1) ? vt0 : vt1, vrows, a.max_pos, nd, j0 + TP, min(TP, pos - j0 - TP),
+                   TS);
+    scale_rows_by_col((lf4*)vt, TS >> 2, nd, (n + 3) >> 2, (const lf4*)(ss + j0));
+    __syncthreads();
+    if (threadIdx.x < nd) acc = chain_vec(vt + (size_t)threadIdx.x * TS, n, acc);
+    __syncthreads();
+  }
+  if (threadIdx.x < nd) {
+    const float p = ss[pos] * vv[threadIdx.x];
+    acc = acc + p;
+    put_word(ac.att + (size_t)h * hd + d0 + threadIdx.x, acc, a.epoch);
+  }
+  stamp(a, l, P_ATT, t, 2);
 }
 
 // o_proj block + residual h1 = h + o (main.rs:470-472).
@@ -1378,7 +1565,11 @@ void k_decode(DecodeArgs a) {
       const uint32_t ph = task[i] >> 12, t = task[i] & 0xFFFu;
       switch (ph) {
         case P_QKV: run_qkv<TR>(a, l, t, s, tok); break;
-        case P_ATT: run_att<TR>(a, l, t, s, wbytes / 4); break;
+        case P_ATT:
+          if (!a.att_split) run_att<TR>(a, l, t, s, wbytes / 4);
+          else if (t < a.natt_s) run_att_score<TR>(a, l, t, s);
+          else run_att_mix<TR>(a, l, t - a.natt_s, s);
+          break;
         case P_O: run_o<TR>(a, l, t, s, tok); break;
         case P_GU: run_gu<TR>(a, l, t, s); break;
         case P_D: run_d<TR>(a, l, t, s); break;
@@ -1513,8 +1704,22 @@ size_t decode_act_floats(uint32_t H, uint32_t I, uint32_t qd, uint32_t kvd) {
 
 bool decode_att_ok(const DecodeArgs& a) {
   const size_t wfloats = decode_wregion_bytes(a) / 4;
+  if (a.att_split) return a.att_tp >= 32 && a.nh % a.nkv == 0;
   return att_lds_floats(a.hd, a.max_pos, a.max_pos) <= wfloats ||
          att_tile_positions(a.hd, a.max_pos, wfloats) >= 32;
+}
+
+bool decode_att_needs_split(const DecodeArgs& a) {
+  return att_lds_floats(a.hd, a.max_pos, a.max_pos) > decode_wregion_bytes(a) / 4;
+}
+
+void decode_att_plan(DecodeArgs& a, bool split) {
+  a.att_split = split ? 1u : 0u;
+  a.att_chunks = (a.max_pos + kThreads - 1) / kThreads;
+  a.natt_s = a.nh * a.att_chunks;
+  a.att_dvc = (a.hd + kAttDV - 1) / kAttDV;
+  a.natt_v = a.nh * a.att_dvc;
+  a.att_tp = att_mix_tile_positions(a.max_pos, decode_wregion_bytes(a) / 4);
 }
 
 size_t decode_lds_bytes(const DecodeArgs& a) {

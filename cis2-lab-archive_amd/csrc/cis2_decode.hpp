@@ -54,12 +54,19 @@ struct DecodeArgs {
   float eps, scale;
   uint32_t pos, epoch, lm_epoch, want_logits;
   uint32_t tree;  // 1: v0.4-candidate tree reduction order, 0: sequential
+  // Split attention (contexts whose K/V rows do not fit one workgroup's
+  // LDS): the ATT phase runs natt_s = nh * att_chunks score tasks (256
+  // positions each) and then natt_v = nh * att_dvc mix tasks (16 output
+  // dims each, V tiles of att_tp positions); scores pass through scw,
+  // tagged words [L][nh][max_pos] (zeroed at start).
+  uint32_t att_split, att_chunks, natt_s, att_dvc, natt_v, att_tp;
+  uint64_t* scw;
 };
 
 // Floats (4-byte units) of one layer's tagged activation storage.
 size_t decode_act_floats(uint32_t H, uint32_t I, uint32_t qd, uint32_t kvd);
 constexpr uint32_t kTimelineTasks = 64;
-constexpr uint32_t kMaxTasks = 4;       // tasks per workgroup per layer
+constexpr uint32_t kMaxTasks = 6;       // tasks per workgroup per layer
 constexpr uint16_t kNoTask = 0xFFFF;
 // Phases of a layer, in dependency order.
 enum { kPhaseQKV = 0, kPhaseATT = 1, kPhaseO = 2, kPhaseGU = 3, kPhaseD = 4, kPhases = 5 };
@@ -68,6 +75,11 @@ size_t decode_lds_bytes(const DecodeArgs& a);
 // True when attention fits the configuration: every cached position in LDS,
 // or tiles of at least 32 positions beside the scores.
 bool decode_att_ok(const DecodeArgs& a);
+// Fills the split-attention fields of a (split: on or off) from its shape
+// and LDS plan.
+void decode_att_plan(DecodeArgs& a, bool split);
+// True when one workgroup cannot hold a head's K/V rows at max_pos.
+bool decode_att_needs_split(const DecodeArgs& a);
 hipError_t launch_decode(const DecodeArgs& a, hipStream_t s);
 
 // Standalone strict-order GEMV y = W x on the blocked layout with R rows per

@@ -369,6 +369,11 @@ int forward_fast(cis2_ctx* c, uint32_t seq, uint32_t pos, uint32_t* tokp, bool w
                                                    c->kvd) * sizeof(float),
                              c->st),
            "tag reset");
+    if (a.scw)
+      HIPCHK(c, hipMemsetAsync(a.scw, 0,
+                               (size_t)c->cfg.n_layers * c->cfg.n_heads * c->cfg.max_pos * 8,
+                               c->st),
+             "score tag reset");
     c->epoch = 0;
   }
   a.epoch = ++c->epoch;
@@ -598,10 +603,14 @@ void fold_rows(std::vector<Sha256>& w, const float* logits, const uint32_t* ids,
 // workgroup with the fewest tasks so far, preferring one whose last task is
 // not in the phase just before (so its next weight copy has a phase of time
 // to land).  Every list is in phase order, which makes the waits acyclic: a
-// task only waits for tasks of earlier (layer, phase).  False when some
-// workgroup would need more than kMaxTasks or a task index exceeds 12 bits.
+// task only waits for tasks of earlier (layer, phase), or, for split
+// attention's mix tasks, for score tasks of the same phase, which come
+// first in every list (lower task indices are assigned first).  False when
+// some workgroup would need more than kMaxTasks or a task index exceeds 12
+// bits.
 static bool assign_tasks(const DecodeArgs& a, std::vector<uint16_t>& table) {
-  const uint32_t n[kPhases] = {a.nq, a.nh, a.no, a.ng, a.nd};
+  const uint32_t natt = a.att_split ? a.natt_s + a.natt_v : a.nh;
+  const uint32_t n[kPhases] = {a.nq, natt, a.no, a.ng, a.nd};
   const uint32_t W = a.nwg;
   table.assign((size_t)W * kMaxTasks, kNoTask);
   std::vector<uint32_t> cnt(W, 0);
@@ -611,7 +620,9 @@ static bool assign_tasks(const DecodeArgs& a, std::vector<uint16_t>& table) {
     for (uint32_t t = 0; t < n[p]; ++t) {
       uint32_t best = W;
       for (uint32_t w = 0; w < W; ++w) {
-        if (cnt[w] >= kMaxTasks || last[w] == (int)p) continue;
+        // one task of a phase per workgroup, unless the phase has more
+        // tasks than workgroups (split attention's score and mix tasks)
+        if (cnt[w] >= kMaxTasks || (last[w] == (int)p && n[p] <= W)) continue;
         if (best == W) { best = w; continue; }
         const bool adj_w = last[w] == (int)p - 1, adj_b = last[best] == (int)p - 1;
         if (cnt[w] < cnt[best] || (cnt[w] == cnt[best] && !adj_w && adj_b)) best = w;
@@ -799,6 +810,12 @@ int cis2_ctx_create(const cis2_config* cfg, cis2_ctx** out) {
       a.rope_cs = c->rope_cs;
       a.logits = c->logits;
       a.err = c->d_err;
+      // attention split over score and mix tasks when a head's K/V rows at
+      // max_pos do not fit one workgroup (CIS2_ATT=split / one: forced)
+      const char* pa = getenv("CIS2_ATT");
+      decode_att_plan(a, pa && !strcmp(pa, "split")  ? true
+                         : pa && !strcmp(pa, "one") ? false
+                                                    : decode_att_needs_split(a));
       // dynamic LDS plus the kernel's static LDS (a few words) within one CU
       const size_t need_lds = decode_lds_bytes(a) + 64;
       return assign_tasks(a, c->wg_tasks) && lds > 0 && need_lds <= (size_t)lds &&
@@ -841,6 +858,16 @@ int cis2_ctx_create(const cis2_config* cfg, cis2_ctx** out) {
     a.act = c->act;
     a.cnt = c->counters;
     a.cand = c->cand;
+    if (a.att_split) {
+      const size_t nw = (size_t)f.n_layers * f.n_heads * f.max_pos;
+      if (hipMalloc(&p, nw * 8) != hipSuccess) {
+        cis2_ctx_destroy(c);
+        return CIS2_E_OOM;
+      }
+      c->allocs.push_back(p);
+      (void)hipMemset(p, 0, nw * 8);  // tag 0: never a launch epoch
+      a.scw = static_cast<uint64_t*>(p);
+    }
     if (const char* tl = getenv("CIS2_TIMELINE")) {
       const size_t n = (size_t)f.n_layers * 6 * kTimelineTasks * 4;
       if (hipMalloc(&p, n * 8) == hipSuccess) {
