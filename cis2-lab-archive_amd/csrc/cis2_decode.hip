@@ -116,12 +116,12 @@ constexpr uint32_t kAttDV = 16;
 __host__ __device__ inline size_t att_part_floats(uint32_t max_pos) {
   return ((size_t)max_pos / 32 + 1 + 3) & ~(size_t)3;
 }
-// Positions per V tile of a mix task: the largest multiple of 32 whose two
-// [kAttDV][TP+4] tiles fit beside the scores and partials; 0 if < 32.
+// Positions per V tile of a mix task: the largest multiple of 32 whose
+// three [kAttDV][TP+4] tiles fit beside the scores and partials; 0 if < 32.
 __host__ __device__ inline uint32_t att_mix_tile_positions(uint32_t max_pos, size_t wfloats) {
   const size_t used = (size_t)max_pos + 64 + att_part_floats(max_pos);
   const size_t room = wfloats > used ? wfloats - used : 0;
-  const size_t per = room / (2 * kAttDV);
+  const size_t per = room / (3 * kAttDV);
   if (per < 36) return 0;
   size_t tp = (per - 4) & ~(size_t)31;
   if (tp > 2048) tp = 2048;
@@ -1182,10 +1182,10 @@ __device__ __forceinline__ void run_att(const DecodeArgs& a, uint32_t l, uint32_
 //     (for the first head of a kv group) stores k and v into the caches.
 //   mix task (h, dc): output dims d0 = dc*16 .. d0+15 of head h: gathers all
 //     of the head's scores, runs the softmax (the same order as one task),
-//     then lane d continues its one left-to-right V-mix chain over tiles of
-//     its V rows, each tile copied into LDS with global_load_lds while the
-//     previous tile is multiplied and chained (the first during the
-//     softmax).
+//     then lane d of wave 0 continues its one left-to-right V-mix chain over
+//     tiles of its V rows; waves 1..3 copy each tile into LDS with
+//     global_load_lds two tiles ahead and form its products one tile ahead
+//     (the first two tiles land during the softmax).
 // Each head's K and V are read by many workgroups at once instead of
 // streaming through one.
 // ---------------------------------------------------------------------------
@@ -1247,21 +1247,41 @@ __device__ __forceinline__ void run_att_score(const DecodeArgs& a, uint32_t l, u
   stamp(a, l, P_ATT, t, 2);
 }
 
-// Rows d0 .. d0+nd-1 of a kv head's V cache (row stride max_pos),
-// positions j0 .. j0+n-1 (rounded up to 4, inside max_pos), into LDS rows
-// of stride TS with global_load_lds_dwordx4: one wave instruction per 256
-// positions of a row, every one in flight.  Data is in LDS once vmcnt
-// reaches 0 and visible after a barrier.
-__device__ __forceinline__ void issue_v_tile(lf* dst, const float* vrows, uint32_t max_pos,
-                                             uint32_t nd, uint32_t j0, uint32_t n, uint32_t TS) {
-  const uint32_t n4 = (n + 3) >> 2, per_row = (n4 + 63) >> 6;
-  const uint32_t wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
-  for (uint32_t k = wv; k < nd * per_row; k += kThreads / 64) {
-    const uint32_t d = k / per_row, q0 = (k - d * per_row) * 64;
-    if (q0 + lane < n4)
-      __builtin_amdgcn_global_load_lds(
-          (const AS_GLB void*)(G4(vrows + (size_t)d * max_pos + j0) + q0 + lane),
-          (AS_LDS void*)((lf4*)(dst + (size_t)d * TS) + q0), 16, 0, 0);
+// The V-tile rows of loader wave w (1..3 of a workgroup): rows d < nd with
+// d % 3 == w - 1.  copy_v_rows copies positions j0 .. j0+n-1 (rounded up to
+// 4, inside max_pos) of those rows of a kv head's V cache (row stride
+// max_pos) into LDS rows of stride TS with global_load_lds_dwordx4, one wave
+// instruction per 256 positions, every one in flight; the data is in LDS
+// once this wave's vmcnt reaches 0.  scale_v_rows then forms the products
+// p_j * v_j[d] of the same rows in place (p at ss[j0..]): only the wave
+// that copied a row touches it until the next barrier.
+__device__ __forceinline__ void copy_v_rows(lf* dst, const float* vrows, uint32_t max_pos,
+                                            uint32_t nd, uint32_t j0, uint32_t n, uint32_t TS) {
+  const uint32_t n4 = (n + 3) >> 2, lane = threadIdx.x & 63;
+  const uint32_t w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  for (uint32_t d = w - 1; d < nd; d += 3)
+    for (uint32_t q0 = 0; q0 < n4; q0 += 64)
+      if (q0 + lane < n4)
+        __builtin_amdgcn_global_load_lds(
+            (const AS_GLB void*)(G4(vrows + (size_t)d * max_pos + j0) + q0 + lane),
+            (AS_LDS void*)((lf4*)(dst + (size_t)d * TS) + q0), 16, 0, 0);
+}
+__device__ __forceinline__ void scale_v_rows(lf* dst, const lf* ss, uint32_t nd, uint32_t j0,
+                                             uint32_t n, uint32_t TS) {
+  const uint32_t n4 = (n + 3) >> 2, lane = threadIdx.x & 63;
+  const uint32_t w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const lf4* p4 = (const lf4*)(ss + j0);
+  for (uint32_t d = w - 1; d < nd; d += 3) {
+    lf4* r4 = (lf4*)(dst + (size_t)d * TS);
+    for (uint32_t q = lane; q < n4; q += 64) {
+      const f4 f = p4[q], v = r4[q];
+      f4 y;
+      y.x = f.x * v.x;
+      y.y = f.y * v.y;
+      y.z = f.z * v.z;
+      y.w = f.w * v.w;
+      r4[q] = y;
+    }
   }
 }
 
@@ -1273,17 +1293,23 @@ __device__ __forceinline__ void run_att_mix(const DecodeArgs& a, uint32_t l, uin
   const uint32_t hd = a.hd, kvh = h / (a.nh / a.nkv), pos = a.pos, len = pos + 1;
   const uint32_t d0 = dc * kAttDV, nd = min(kAttDV, hd - d0);
   const uint32_t t = a.natt_s + u;
+  const bool loader = (threadIdx.x >> 6) != 0;  // waves 1..3 copy and scale V tiles
   lf* vv = s.v;        // v of this position, dims d0.. [kAttDV]
   lf* misc = vv + 64;  // [1] den, [4..] reduction scratch
   AS_LDS uint32_t* red = (AS_LDS uint32_t*)(misc + 4);
-  lf* ss = s.w;                                 // scores / probabilities [max_pos + 64]
-  lf* part = ss + a.max_pos + 64;               // tree partials
-  const uint32_t TP = a.att_tp, TS = TP + 4;
-  lf* vt0 = part + att_part_floats(a.max_pos);  // two V tiles [kAttDV][TS]
-  lf* vt1 = vt0 + (size_t)kAttDV * TS;
+  lf* ss = s.w;                    // scores / probabilities [max_pos + 64]
+  lf* part = ss + a.max_pos + 64;  // tree partials
+  const uint32_t TP = a.att_tp, TS = TP + 4, nt = (pos + TP - 1) / TP;
+  lf* vt0 = part + att_part_floats(a.max_pos);  // three V tiles [kAttDV][TS]
+  auto tile = [=](uint32_t i) { return vt0 + (size_t)(i % 3) * kAttDV * TS; };
+  auto tile_n = [=](uint32_t i) { return min(TP, pos - i * TP); };
   const float* vrows = a.vc0 + (size_t)l * a.cache_stride + ((size_t)kvh * hd + d0) * a.max_pos;
   stamp(a, l, P_ATT, t, 0);
-  if (pos > 0) issue_v_tile(vt0, vrows, a.max_pos, nd, 0, min(TP, pos), TS);
+  // the first two V tiles land during the gather and the softmax
+  if (loader) {
+    if (nt > 0) copy_v_rows(tile(0), vrows, a.max_pos, nd, 0, tile_n(0), TS);
+    if (nt > 1) copy_v_rows(tile(1), vrows, a.max_pos, nd, TP, tile_n(1), TS);
+  }
   gather(ss, len, a.epoch, a.err, [=](uint32_t i) {
     return (const gw*)a.scw + ((size_t)l * a.nh + h) * a.max_pos + i;
   });
@@ -1292,20 +1318,25 @@ __device__ __forceinline__ void run_att_mix(const DecodeArgs& a, uint32_t l, uin
   __syncthreads();
   softmax_lds<TR>(ss, len, part, misc, red);
   stamp(a, l, P_ATT, t, 3);
-  // out_d = fold_j (p_j * v_j[d]) (main.rs:454-463), one chain per lane
-  float acc = 0.0f;
-  uint32_t it = 0;
-  for (uint32_t j0 = 0; j0 < pos; j0 += TP, ++it) {
-    const uint32_t n = min(TP, pos - j0);
-    lf* vt = (it & 1) ? vt1 : vt0;
+  // out_d = fold_j (p_j * v_j[d]) (main.rs:454-463): lane d of wave 0
+  // continues one left-to-right chain over tile i while waves 1..3 form the
+  // products of tile i+1 and start copying tile i+2
+  if (loader && nt > 0) {
     wait_vm0();
-    __syncthreads();
-    if (j0 + TP < pos)
-      issue_v_tile((it & 1) ? vt0 : vt1, vrows, a.max_pos, nd, j0 + TP, min(TP, pos - j0 - TP),
-                   TS);
-    scale_rows_by_col((lf4*)vt, TS >> 2, nd, (n + 3) >> 2, (const lf4*)(ss + j0));
-    __syncthreads();
-    if (threadIdx.x < nd) acc = chain_vec(vt + (size_t)threadIdx.x * TS, n, acc);
+    scale_v_rows(tile(0), ss, nd, 0, tile_n(0), TS);
+  }
+  __syncthreads();
+  float acc = 0.0f;
+  for (uint32_t i = 0; i < nt; ++i) {
+    if (!loader) {
+      if (threadIdx.x < nd) acc = chain_vec(tile(i) + (size_t)threadIdx.x * TS, tile_n(i), acc);
+    } else {
+      if (i + 1 < nt) {
+        wait_vm0();
+        scale_v_rows(tile(i + 1), ss, nd, (i + 1) * TP, tile_n(i + 1), TS);
+      }
+      if (i + 2 < nt) copy_v_rows(tile(i + 2), vrows, a.max_pos, nd, (i + 2) * TP, tile_n(i + 2), TS);
+    }
     __syncthreads();
   }
   if (threadIdx.x < nd) {

@@ -170,3 +170,33 @@ def test_rows_many_rows_gqa_grouped_attention(name, model_fixtures):
             assert sa == am[base + p]
     # the argmax at the last prompt row is the fixture's first generated id
     assert am[len(rec["prompt"]) - 1] == rec["tokens"][len(rec["prompt"])]
+
+
+@pytest.mark.parametrize("gen", [1, 2, 3])
+def test_decode_batch_short_generations(gen):
+    """gen = 1 (the prefill's logits only), 2 (one captured step, replayed
+    once) and 3 (both alternating graphs): each row equals its bs=1 run."""
+    spec = artifacts.SPECS["tiny-qwen3"]
+    w = artifacts.Weights(spec, 3)
+    prompts = [artifacts.set_prompt(3, i, spec.vocab, 1, 12, 9) for i in range(3)]
+    m = Cis2Model(spec, w, max_pos=12 + gen, max_seqs=3)
+    rows = m.decode_batch(prompts, gen)
+    solo = Cis2Model(spec, w, max_pos=12 + gen)
+    for i, p in enumerate(prompts):
+        s = solo.decode(p, gen, step_digests=False)
+        assert rows[i]["witness"] == s["witness"], i
+        assert np.array_equal(rows[i]["ids"], s["ids"]), i
+
+
+def test_decode_batch_one_token_prompts():
+    """Prompts of a single token (the prefill is one row per sequence)."""
+    spec = artifacts.SPECS["tiny-llama"]
+    w = artifacts.Weights(spec, 1)
+    prompts = [[5], [17], [5]]
+    m = Cis2Model(spec, w, max_pos=1 + 16, max_seqs=3)
+    rows = m.decode_batch(prompts, 16)
+    solo = Cis2Model(spec, w, max_pos=1 + 16)
+    for i, p in enumerate(prompts):
+        s = solo.decode(p, 16, step_digests=False)
+        assert rows[i]["witness"] == s["witness"], i
+    assert rows[0]["witness"] == rows[2]["witness"]  # same prompt, same row
