@@ -550,16 +550,6 @@ __global__ __launch_bounds__(kAttT) void k_attention_rows(const float* __restric
   }
 }
 
-__global__ void k_silu_mul(const float* __restrict__ g, const float* __restrict__ u,
-                           float* hid, uint64_t n) {
-  uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
-  for (; i < n; i += stride) {
-    float sg = silu_pinned(g[i]);
-    hid[i] = sg * u[i];
-  }
-}
-
 __global__ void k_gather_rows(const float* __restrict__ src, const uint32_t* __restrict__ idx,
                               uint32_t width, float* dst) {
   const uint32_t r = blockIdx.x;
@@ -747,14 +737,6 @@ hipError_t launch_attention_rows(const float* q, const float* kc, const float* v
       hipLaunchKernelGGL(k_attention_rows<1>, grid, dim3(kAttT), shmem, st, q, kc, vc, rows, nh,
                          nkv, hd, max_pos, seq_stride, scale, out, tr, ls32);
   }
-  return hipGetLastError();
-}
-
-hipError_t launch_silu_mul(const float* g, const float* u, float* hid, uint64_t n,
-                           hipStream_t st) {
-  if (n == 0) return hipSuccess;
-  const uint64_t blocks = std::min<uint64_t>((n + kT - 1) / kT, 4096);
-  hipLaunchKernelGGL(k_silu_mul, dim3((uint32_t)blocks), dim3(kT), 0, st, g, u, hid, n);
   return hipGetLastError();
 }
 

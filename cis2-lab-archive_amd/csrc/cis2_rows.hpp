@@ -71,9 +71,6 @@ hipError_t launch_attention_rows(const float* q, const float* kc, const float* v
                                  RowsDesc rows, uint32_t max_len, uint32_t nh, uint32_t nkv,
                                  uint32_t hd, uint32_t max_pos, uint64_t seq_stride, float scale,
                                  float* out, bool tree, hipStream_t st);
-// hid = silu(gate) * up over n elements (main.rs:484-487).
-hipError_t launch_silu_mul(const float* g, const float* u, float* hid, uint64_t n,
-                           hipStream_t st);
 // dst[i] = src[idx[i]] rows of `width` floats, i < n.
 hipError_t launch_gather_rows(const float* src, const uint32_t* idx, uint32_t n, uint32_t width,
                               float* dst, hipStream_t st);
