@@ -39,7 +39,9 @@ sys.path.insert(0, os.path.join(ROOT, "tests"))
 
 METRIC = "bit-exact fp32 decode tok/s (SmolLM2-135M shape, bs=1); GEMV HBM GB/s % peak"
 HBM_PEAK_GBS = 8000.0
-CPU_REF_TOKS = 5.189  # C reference decode, SmolLM2-135M, 1 thread (rust-1 RESULT.md:26)
+# the reference's published C decode rate, SmolLM2-135M, 1 thread
+# (labs/rust-1/reports/rust-1/RESULT.md:26)
+CPU_REF_TOKS = 5.189
 SEED = 20261201
 
 

@@ -1,6 +1,6 @@
 /* oracle/cis2_oracle.c — CPU restatement of the CIS-2 pinned-order fp32
- * forward pass.  TEST INFRASTRUCTURE ONLY (the checker; never shipped,
- * never called by the product path).
+ * forward pass.  TEST INFRASTRUCTURE ONLY (it produces the expected bits
+ * for the tests; never shipped, never called by the product path).
  *
  * Build contract (oracle/Makefile): C11, -O2 -ffp-contract=off
  * -fno-fast-math -msse2 -mfpmath=sse -fexcess-precision=standard, no

@@ -1,9 +1,9 @@
 /* oracle/cis2_oracle.h — CPU restatement of the CIS-2 v0.3b pinned-order
  * fp32 decoder forward pass (and the v0.4-candidate tree order).
  *
- * TEST INFRASTRUCTURE ONLY.  This library is the checker: tests/, the
- * smoke() entry point and bench.py's cpu_baseline leg load it to produce the
- * expected bits.  The product path (the HIP library) never links, loads or
+ * TEST INFRASTRUCTURE ONLY.  tests/, the smoke() entry point and
+ * bench.py's cpu_baseline leg load this library to produce the expected
+ * bits.  The product path (the HIP library) never links, loads or
  * calls it.
  *
  * Every function cites the reference file:line whose semantics it restates.

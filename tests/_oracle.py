@@ -1,7 +1,7 @@
 """ctypes wrapper of the CPU oracle (oracle/liboracle.so).
 
-TEST INFRASTRUCTURE: the oracle is the checker.  Only tests/, the smoke()
-entry point and bench.py's cpu_baseline leg load it.
+TEST INFRASTRUCTURE: the oracle produces the expected bits.  Only tests/,
+the smoke() entry point and bench.py's cpu_baseline leg load it.
 """
 import ctypes
 import os
