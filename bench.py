@@ -243,8 +243,8 @@ def main():
         print(json.dumps({"copy_bytes": 4 * n, "copies": 3}), flush=True)
         return
     if a.gpus != 1:
-        print("bench.py: this build runs on one GPU only (the pinned-order decode does not shard "
-              "across GPUs here); use --gpus 1", file=sys.stderr)
+        print("bench.py: one GPU only (the pinned-order decode is not sharded across GPUs); "
+              "use --gpus 1", file=sys.stderr)
         sys.exit(2)
     from cis2amd import Cis2Model, artifacts
     spec = artifacts.SPECS["smollm2-135m"]
