@@ -18,12 +18,13 @@ stream (cis2_profile), summed over the timed steps.  `traffic` is the HBM
 bytes per launch from the committed rocprofv3 counter summary, when present.
 
 Beside the headline line, the same JSON object carries the other
-measured workloads: the strict-order GEMV at 1536x576 (gemv_config1), the
-batched decode of the batch-stress sequences at B = 8, 32, 64
-(batch_decode), the Qwen3-0.6B-shape 4096-token prefill + 256-step decode
-(qwen3_4096), and the CPU baseline both single-thread (cpu_baseline, the
-reference protocol) and row-parallel over the host cores
-(cpu_baseline_parallel).
+measured workloads: the strict-order GEMV at 1536x576, one per launch and
+128 per launch (gemv_config1), the batched decode of the batch-stress
+sequences at B = 1, 8, 32, 64 (batch_decode), the llama-160m set of 300
+prompts decoded as one batch (llama160m_set), the Qwen3-0.6B-shape
+4096-token prefill + 256-step decode (qwen3_4096), and the CPU baseline
+both single-thread (cpu_baseline, the reference protocol) and row-parallel
+over the host cores (cpu_baseline_parallel).
 
 Prints ONE JSON line on stdout.
 """
@@ -128,7 +129,7 @@ def cpu_baseline(spec, weights, prompt, seconds=15.0):
                       % (n, n - 1, dt)}
 
 
-def batch_decode(spec, weights, sizes=(8, 32, 64)):
+def batch_decode(spec, weights, sizes=(1, 8, 32, 64)):
     """Config 4: batched greedy decode of the batch-stress sequences (prompts of
     16..512 tokens, 256 generated each) through cis2_decode_batch: one
     row-batched prefill, then one row per sequence per step.  tok/s counts
@@ -162,6 +163,36 @@ def batch_decode(spec, weights, sizes=(8, 32, 64)):
         log("batch decode B=%d:" % B, rec)
     m.close()
     return out
+
+
+def llama_set():
+    """Config 3: llama-160m shape, the 300 seeded prompts of 8..64 tokens with
+    128 greedy tokens each, all through one cis2_decode_batch call (300
+    KV-cache slots): tok/s over the whole call, and whether every
+    sequence's digests equal the reference's."""
+    from cis2amd import Cis2Model, artifacts
+    pset = artifacts.LLAMA_SET
+    spec = artifacts.SPECS[pset["spec"]]
+    w = artifacts.Weights(spec, pset["seed"])
+    prompts = artifacts.set_prompts(pset)
+    gen = pset["gen_toks"]
+    m = Cis2Model(spec, w, max_pos=pset["hi"] + gen, max_seqs=len(prompts))
+    m.decode_batch(prompts[:2], 4)
+    t = time.perf_counter()
+    rows = m.decode_batch(prompts, gen)
+    tt = time.perf_counter() - t
+    rec = {"sequences": len(prompts), "gen_toks": gen, "total_s": round(tt, 4),
+           "tok_s": round(len(prompts) * gen / tt, 1)}
+    fx = os.path.join(ROOT, "tests", "golden", "llama160m_set.json")
+    if os.path.exists(fx):
+        doc = json.load(open(fx))
+        if doc.get("set") == pset and len(doc["cases"]) >= len(prompts):
+            rec["digests_bit_exact"] = all(
+                [r["witness"], r["argmax_digest"]] == doc["cases"][str(i)]
+                for i, r in enumerate(rows))
+    m.close()
+    log("llama-160m set:", rec)
+    return rec
 
 
 def qwen3_long(gen=256, n_prompt=4096, seed=6):
@@ -305,6 +336,7 @@ def main():
         log("standalone GEMV 1536x576:", out["gemv_config1"])
     if not a.no_batch:
         out["batch_decode"] = batch_decode(spec, weights)
+        out["llama160m_set"] = llama_set()
     if not a.no_qwen3:
         out["qwen3_4096"] = qwen3_long()
     if not a.no_cpu_baseline:
