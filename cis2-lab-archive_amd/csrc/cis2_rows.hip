@@ -550,6 +550,346 @@ __global__ __launch_bounds__(kAttT) void k_attention_rows(const float* __restric
   }
 }
 
+// ---------------------------------------------------------------------------
+// Attention of prefill rows in tiles.  A tile is up to kAttQT rows of one
+// sequence at consecutive positions p0 .. p0+nr-1 (built on the host); a
+// workgroup takes one tile and the HPW = nh/nkv query heads of one KV head,
+// P = kAttQT * HPW (row, head) pairs (pair a = row i * HPW + head h), and
+// reads each K and V element of the kv head once for all of them, where the
+// per-row kernel reads them once per row.  Each pair's arithmetic is the
+// per-row kernel's, in the same order (sequential reduction order only):
+//   scores  s_j = dot_seq(q, k_j) * scale, d ascending: K tiles of TK
+//           positions in LDS, a thread carries PB pairs x 4 positions; the
+//           scores go to a global scratch row per pair, the first-wins
+//           maximum (NaN at position 0 wins) is kept on the way;
+//   softmax the denominator as one strict chain per pair: waves 1..3 copy
+//           stages of TE scores into LDS one stage ahead and turn them into
+//           exp(s - max) in place (written back for the V-mix) while lanes
+//           a < P of wave 0 continue their chains;
+//   V-mix   out_d = fold_j (p_j * v_j[d]), j ascending, p_j = e_j / den:
+//           V tiles and e tiles of TK positions in LDS (the next pair copied
+//           while the current one is used), a thread carries PB3 pairs x 4
+//           dims.
+// LDS (floats): q [P][HD+4], then the phase regions (K tiles 2 x [HD][TK];
+// e stages 2 x [P][TE+4]; V tiles 2 x [HD][TK+4] + e tiles 2 x [P][TK+4]),
+// plus the per-pair maximum and denominator.
+// ---------------------------------------------------------------------------
+constexpr uint32_t kAttQT = kAttTileRows;  // rows per attention tile
+constexpr uint32_t kAttTE = 128; // positions per softmax stage
+
+template <uint32_t HPW, uint32_t HD, uint32_t TK>
+struct AttTileCfg {
+  static constexpr uint32_t P = kAttQT * HPW;
+  static constexpr uint32_t QS = HD + 4;                 // q row stride
+  static constexpr uint32_t PB = P * TK / 1024;          // pairs per thread, scores
+  static constexpr uint32_t PB3 = P * HD / 1024;         // pairs per thread, V-mix
+  static constexpr uint32_t ES = kAttTE + 4;             // e stage row stride
+  static constexpr uint32_t VS = TK + 4;                 // V / e tile row stride
+  static constexpr size_t region1 = 2 * (size_t)HD * TK;
+  static constexpr size_t region2 = 2 * (size_t)P * ES;
+  static constexpr size_t region3 = 2 * (size_t)HD * VS + 2 * (size_t)P * VS;
+  static constexpr size_t region = region1 > region2 ? (region1 > region3 ? region1 : region3)
+                                                     : (region2 > region3 ? region2 : region3);
+  static constexpr size_t floats = (size_t)P * QS + region + 2 * P;
+  static_assert(P * TK % 1024 == 0 && P * HD % 1024 == 0, "thread blocking");
+  static_assert(P <= 64, "one denominator lane per pair in wave 0");
+};
+
+// acc + p[0] + ... + p[n-1], strictly left to right (16-byte LDS reads,
+// eight of them per batch).
+__device__ __forceinline__ float chain_lds(const float* p, uint32_t n, float acc) {
+  const v4* p4 = reinterpret_cast<const v4*>(p);
+  uint32_t j = 0;
+  for (; j + 32 <= n; j += 32) {
+    v4 e[8];
+#pragma unroll
+    for (uint32_t u = 0; u < 8; ++u) e[u] = p4[j / 4 + u];
+#pragma unroll
+    for (uint32_t u = 0; u < 8; ++u) {
+      acc = acc + e[u].x;
+      acc = acc + e[u].y;
+      acc = acc + e[u].z;
+      acc = acc + e[u].w;
+    }
+  }
+  for (; j < n; ++j) acc = acc + p[j];
+  return acc;
+}
+
+// n positions of `rows` rows (row stride `gstride` floats in global memory,
+// starting at src) into LDS rows of stride `lstride` at dst, 16 bytes per
+// lane with global_load_lds_dwordx4, one wave instruction per 256 positions
+// of a row; waves [w0, w0 + nw) issue the rows w0-relative round-robin.
+__device__ __forceinline__ void copy_rows_lds(float* dst, uint32_t lstride, const float* src,
+                                              size_t gstride, uint32_t rows, uint32_t n,
+                                              uint32_t w0, uint32_t nw) {
+  const uint32_t n4 = (n + 3) >> 2, lane = threadIdx.x & 63;
+  const uint32_t w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  if (w < w0 || w >= w0 + nw) return;
+  for (uint32_t r = w - w0; r < rows; r += nw)
+    for (uint32_t q0 = 0; q0 < n4; q0 += 64)
+      if (q0 + lane < n4)
+        lds_load16(reinterpret_cast<const v4*>(src + r * gstride) + q0 + lane,
+                   reinterpret_cast<v4*>(dst + (size_t)r * lstride) + q0);
+}
+
+template <uint32_t HPW, uint32_t HD, uint32_t TK>
+__global__ __launch_bounds__(256) void k_attention_tiles(
+    const float* __restrict__ q, const float* __restrict__ kc, const float* __restrict__ vc,
+    const AttTile* __restrict__ tiles, uint32_t nh, uint32_t max_pos, uint64_t seq_stride,
+    float scale, float* out, float* scratch, uint32_t ls) {
+  using C = AttTileCfg<HPW, HD, TK>;
+  constexpr uint32_t P = C::P, QS = C::QS, PB = C::PB, PB3 = C::PB3, ES = C::ES, VS = C::VS;
+  extern __shared__ v4 sh4[];
+  float* sh = reinterpret_cast<float*>(sh4);
+  float* qs = sh;                                  // [P][QS]
+  float* reg = qs + (size_t)P * QS;                // phase region
+  float* smx = reg + C::region;                    // [P] maxima
+  float* sden = smx + P;                           // [P] denominators
+  const AttTile tl = tiles[blockIdx.x];
+  const uint32_t g = blockIdx.y, qh0 = g * HPW, nkv = nh / HPW, kvh = g;
+  const uint32_t t = threadIdx.x, wv = t >> 6, lane = t & 63;
+  const uint32_t npair = tl.nr * HPW, len_max = tl.p0 + tl.nr;
+  float* S = scratch + ((size_t)blockIdx.x * nkv + g) * P * ls;  // [P][ls] scores, then exps
+  const size_t sb = (size_t)tl.seq * seq_stride + (size_t)kvh * HD * max_pos;
+  const float* kb = kc + sb;
+  const float* vb = vc + sb;
+  auto pair_len = [=](uint32_t a) { return tl.p0 + a / HPW + 1; };
+  // q of every pair (rows past nr: zero, never stored)
+  for (uint32_t i = t; i < P * HD; i += 256) {
+    const uint32_t a = i / HD, d = i - a * HD, ri = a / HPW, h = a - ri * HPW;
+    qs[a * QS + d] = a < npair ? q[(size_t)(tl.row0 + ri) * nh * HD + (size_t)(qh0 + h) * HD + d]
+                               : 0.0f;
+  }
+  // ---- scores ------------------------------------------------------------
+  constexpr uint32_t TPR = TK / 4;  // threads per pair group (4 positions each)
+  const uint32_t pg = t / TPR, jg = t - pg * TPR;
+  Pick best[PB];
+  bool nan0[PB];
+#pragma unroll
+  for (uint32_t u = 0; u < PB; ++u) {
+    best[u] = Pick{0.0f, UINT32_MAX};
+    nan0[u] = false;
+  }
+  const uint32_t nkt = (len_max + TK - 1) / TK;
+  float* kt0 = reg;
+  auto kt = [=](uint32_t i) { return kt0 + (size_t)(i & 1) * HD * TK; };
+  auto copy_k = [=](uint32_t i) {
+    const uint32_t j0 = i * TK, n = min(TK, len_max - j0);
+    // rows of TK floats back to back: a wave instruction covers 64 / (TK/4) rows
+    const uint32_t n4 = (n + 3) >> 2, rows_per = 64 / (TK / 4);
+    float* dst = kt(i);
+    for (uint32_t r0 = wv * rows_per; r0 < HD; r0 += 4 * rows_per) {
+      const uint32_t r = r0 + lane / (TK / 4), qq = lane % (TK / 4);
+      if (r < HD && qq < n4)
+        lds_load16(reinterpret_cast<const v4*>(kb + (size_t)r * max_pos + j0) + qq,
+                   reinterpret_cast<v4*>(dst + (size_t)r0 * TK));
+    }
+  };
+  copy_k(0);
+  for (uint32_t i = 0; i < nkt; ++i) {
+    wait_vm0();
+    __syncthreads();
+    if (i + 1 < nkt) copy_k(i + 1);
+    const float* k = kt(i);
+    float acc[PB][4];
+#pragma unroll
+    for (uint32_t u = 0; u < PB; ++u)
+#pragma unroll
+      for (uint32_t v = 0; v < 4; ++v) acc[u][v] = 0.0f;
+#pragma unroll 2
+    for (uint32_t d4 = 0; d4 < HD; d4 += 4) {
+      v4 qv[PB], kk[4];
+#pragma unroll
+      for (uint32_t u = 0; u < PB; ++u)
+        qv[u] = *reinterpret_cast<const v4*>(qs + (size_t)(pg * PB + u) * QS + d4);
+#pragma unroll
+      for (uint32_t e = 0; e < 4; ++e)
+        kk[e] = *reinterpret_cast<const v4*>(k + (size_t)(d4 + e) * TK + 4 * jg);
+#pragma unroll
+      for (uint32_t e = 0; e < 4; ++e)
+#pragma unroll
+        for (uint32_t u = 0; u < PB; ++u) {
+          float p;
+          p = qv[u][e] * kk[e].x; acc[u][0] = acc[u][0] + p;
+          p = qv[u][e] * kk[e].y; acc[u][1] = acc[u][1] + p;
+          p = qv[u][e] * kk[e].z; acc[u][2] = acc[u][2] + p;
+          p = qv[u][e] * kk[e].w; acc[u][3] = acc[u][3] + p;
+        }
+    }
+#pragma unroll
+    for (uint32_t u = 0; u < PB; ++u) {
+      const uint32_t a = pg * PB + u;
+      if (a < npair) {
+        const uint32_t len = pair_len(a);
+#pragma unroll
+        for (uint32_t v = 0; v < 4; ++v) {
+          const uint32_t j = i * TK + 4 * jg + v;
+          if (j < len) {
+            const float s = acc[u][v] * scale;
+            S[(size_t)a * ls + j] = s;
+            if (s == s) best[u] = pick2(best[u], Pick{s, j});
+            else if (j == 0) nan0[u] = true;
+          }
+        }
+      }
+    }
+  }
+  // maxima: the TPR threads of a pair group are consecutive lanes of one wave
+#pragma unroll
+  for (uint32_t u = 0; u < PB; ++u) {
+    Pick b = best[u];
+    uint32_t n0 = nan0[u] ? 1u : 0u;
+    for (uint32_t off = TPR / 2; off > 0; off >>= 1) {
+      Pick o;
+      o.v = __shfl_xor(b.v, off, 64);
+      o.i = __shfl_xor(b.i, off, 64);
+      b = pick2(b, o);
+      n0 |= __shfl_xor(n0, off, 64);
+    }
+    const uint32_t a = pg * PB + u;
+    if (jg == 0 && a < P) smx[a] = n0 ? __builtin_nanf("") : b.v;
+  }
+  // ---- softmax denominators ---------------------------------------------
+  // the scores reach global memory, and no stale copy stays in this CU's
+  // cache, before they are read back (agent-scope fence: release + acquire)
+  __threadfence();
+  __syncthreads();
+  // a NaN at position 0 wins with its own bits: re-read the score
+  if (t < npair && smx[t] != smx[t]) smx[t] = S[(size_t)t * ls];
+  const uint32_t nst = (len_max + kAttTE - 1) / kAttTE;
+  float* es0 = reg;
+  auto es = [=](uint32_t i) { return es0 + (size_t)(i & 1) * P * ES; };
+  // waves 1..3: copy stage i of every pair's scores and exponentiate it in
+  // place, each wave on the pair rows it copied
+  auto load_stage = [=](uint32_t i) {
+    const uint32_t j0 = i * kAttTE, n = min(kAttTE, len_max - j0);
+    copy_rows_lds(es(i), ES, S + j0, ls, npair, n, 1, 3);
+  };
+  auto exp_stage = [=](uint32_t i) {
+    const uint32_t j0 = i * kAttTE;
+    float* st = es(i);
+    for (uint32_t a = wv - 1; a < npair; a += 3) {
+      const uint32_t len = pair_len(a);
+      if (j0 >= len) continue;
+      const uint32_t n = min(kAttTE, len - j0);
+      const float mx = smx[a];
+      for (uint32_t j = lane; j < n; j += 64) {
+        const float dlt = st[(size_t)a * ES + j] - mx;
+        const float e = exp_pinned(dlt);
+        st[(size_t)a * ES + j] = e;
+        S[(size_t)a * ls + j0 + j] = e;
+      }
+    }
+  };
+  __syncthreads();
+  if (wv >= 1) {
+    load_stage(0);
+    wait_vm0();
+    exp_stage(0);
+  }
+  __syncthreads();
+  float den = 0.0f;
+  for (uint32_t i = 0; i < nst; ++i) {
+    // lanes a < npair of wave 0 chain stage i; waves 1..3 prepare stage i+1
+    // in the other buffer (its stage i-1 was chained before this barrier)
+    if (wv == 0) {
+      if (lane < npair) {
+        const uint32_t j0 = i * kAttTE, len = pair_len(lane);
+        if (j0 < len) den = chain_lds(es(i) + (size_t)lane * ES, min(kAttTE, len - j0), den);
+      }
+    } else if (i + 1 < nst) {
+      load_stage(i + 1);
+      wait_vm0();
+      exp_stage(i + 1);
+    }
+    __syncthreads();
+  }
+  if (wv == 0 && lane < npair) sden[lane] = den;
+  // the exps written by waves 1..3 reach global memory before the V-mix
+  // reads them back through the async copies
+  __threadfence();
+  __syncthreads();
+  // ---- V-mix --------------------------------------------------------------
+  const uint32_t dg = t % (HD / 4), pg3 = t / (HD / 4);
+  float* vt0 = reg;                                // 2 x [HD][VS]
+  float* et0 = reg + 2 * (size_t)HD * VS;          // 2 x [P][VS]
+  auto vt = [=](uint32_t i) { return vt0 + (size_t)(i & 1) * HD * VS; };
+  auto et = [=](uint32_t i) { return et0 + (size_t)(i & 1) * P * VS; };
+  auto copy_ve = [=](uint32_t i) {
+    const uint32_t j0 = i * TK, n = min(TK, len_max - j0);
+    copy_rows_lds(vt(i), VS, vb + j0, max_pos, HD, n, 0, 4);
+    copy_rows_lds(et(i), VS, S + j0, ls, npair, n, 0, 4);
+  };
+  float acc3[PB3][4];
+#pragma unroll
+  for (uint32_t u = 0; u < PB3; ++u)
+#pragma unroll
+    for (uint32_t v = 0; v < 4; ++v) acc3[u][v] = 0.0f;
+  copy_ve(0);
+  for (uint32_t i = 0; i < nkt; ++i) {
+    wait_vm0();
+    __syncthreads();
+    // p_j = e_j / den in place (main.rs softmax: true divide)
+    {
+      const uint32_t j0 = i * TK;
+      float* e = et(i);
+      for (uint32_t x = t; x < npair * TK; x += 256) {
+        const uint32_t a = x / TK, j = x - a * TK;
+        if (j0 + j < pair_len(a)) {
+          const float pj = e[(size_t)a * VS + j] / sden[a];
+          e[(size_t)a * VS + j] = pj;
+        }
+      }
+    }
+    __syncthreads();
+    if (i + 1 < nkt) copy_ve(i + 1);
+    const float* v = vt(i);
+    const float* e = et(i);
+    const uint32_t j0 = i * TK, n = min(TK, len_max - j0);
+#pragma unroll
+    for (uint32_t u = 0; u < PB3; ++u) {
+      const uint32_t a = pg3 * PB3 + u;
+      if (a >= npair) continue;
+      const uint32_t len = pair_len(a);
+      if (j0 >= len) continue;
+      const uint32_t m = min(n, len - j0);  // positions of this tile the pair sees
+      const float* pr = e + (size_t)a * VS;
+      uint32_t j = 0;
+#pragma unroll 2
+      for (; j + 4 <= m; j += 4) {
+        const v4 pp = *reinterpret_cast<const v4*>(pr + j);
+#pragma unroll
+        for (uint32_t dd = 0; dd < 4; ++dd) {
+          const v4 vv = *reinterpret_cast<const v4*>(v + (size_t)(4 * dg + dd) * VS + j);
+          float p;
+          p = pp.x * vv.x; acc3[u][dd] = acc3[u][dd] + p;
+          p = pp.y * vv.y; acc3[u][dd] = acc3[u][dd] + p;
+          p = pp.z * vv.z; acc3[u][dd] = acc3[u][dd] + p;
+          p = pp.w * vv.w; acc3[u][dd] = acc3[u][dd] + p;
+        }
+      }
+      for (; j < m; ++j) {
+#pragma unroll
+        for (uint32_t dd = 0; dd < 4; ++dd) {
+          const float p = pr[j] * v[(size_t)(4 * dg + dd) * VS + j];
+          acc3[u][dd] = acc3[u][dd] + p;
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (uint32_t u = 0; u < PB3; ++u) {
+    const uint32_t a = pg3 * PB3 + u;
+    if (a < npair) {
+      const uint32_t ri = a / HPW, h = a - ri * HPW;
+      float* o = out + (size_t)(tl.row0 + ri) * nh * HD + (size_t)(qh0 + h) * HD + 4 * dg;
+#pragma unroll
+      for (uint32_t dd = 0; dd < 4; ++dd) o[dd] = acc3[u][dd];
+    }
+  }
+}
+
 __global__ void k_gather_rows(const float* __restrict__ src, const uint32_t* __restrict__ idx,
                               uint32_t width, float* dst) {
   const uint32_t r = blockIdx.x;
@@ -759,6 +1099,62 @@ hipError_t launch_argmax_rows(const float* v, uint32_t n, uint32_t width, uint32
   if (width == 0) return hipErrorInvalidValue;
   hipLaunchKernelGGL(k_argmax_rows, dim3(n), dim3(1024), 0, st, v, width, out);
   return hipGetLastError();
+}
+
+
+template <uint32_t HPW, uint32_t HD, uint32_t TK>
+static hipError_t launch_att_tiles_t(const float* q, const float* kc, const float* vc,
+                                     const AttTile* tiles, uint32_t ntiles, uint32_t nh,
+                                     uint32_t max_pos, uint64_t seq_stride, float scale, float* out,
+                                     float* scratch, uint32_t ls, hipStream_t st) {
+  using C = AttTileCfg<HPW, HD, TK>;
+  const size_t lds = C::floats * sizeof(float);
+  static bool configured = false;
+  if (!configured) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_attention_tiles<HPW, HD, TK>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
+    configured = true;
+  }
+  hipLaunchKernelGGL((k_attention_tiles<HPW, HD, TK>), dim3(ntiles, nh / HPW), dim3(256), lds, st,
+                     q, kc, vc, tiles, nh, max_pos, seq_stride, scale, out, scratch, ls);
+  return hipGetLastError();
+}
+
+bool attention_tiles_supported(uint32_t nh, uint32_t nkv, uint32_t hd) {
+  if (nkv == 0 || nh % nkv) return false;
+  const uint32_t g = nh / nkv;
+  if (hd == 64) return g >= 1 && g <= 4;
+  if (hd == 128) return g == 2 || g == 4;
+  return false;
+}
+
+size_t attention_tiles_scratch_floats(uint32_t ntiles, uint32_t nh, uint32_t nkv,
+                                      uint32_t max_len) {
+  const size_t ls = ((size_t)max_len + 3) / 4 * 4;
+  return (size_t)ntiles * nkv * kAttQT * (nh / nkv) * ls;
+}
+
+hipError_t launch_attention_tiles(const float* q, const float* kc, const float* vc,
+                                  const AttTile* tiles, uint32_t ntiles, uint32_t max_len,
+                                  uint32_t nh, uint32_t nkv, uint32_t hd, uint32_t max_pos,
+                                  uint64_t seq_stride, float scale, float* out, float* scratch,
+                                  hipStream_t st) {
+  if (ntiles == 0) return hipSuccess;
+  if (!attention_tiles_supported(nh, nkv, hd) || max_len == 0 || max_len > max_pos ||
+      max_pos % 4)
+    return hipErrorInvalidValue;
+  const uint32_t g = nh / nkv, ls = (max_len + 3) / 4 * 4;
+  if (hd == 64) {
+    switch (g) {
+      case 1: return launch_att_tiles_t<1, 64, 64>(q, kc, vc, tiles, ntiles, nh, max_pos, seq_stride, scale, out, scratch, ls, st);
+      case 2: return launch_att_tiles_t<2, 64, 64>(q, kc, vc, tiles, ntiles, nh, max_pos, seq_stride, scale, out, scratch, ls, st);
+      case 3: return launch_att_tiles_t<3, 64, 64>(q, kc, vc, tiles, ntiles, nh, max_pos, seq_stride, scale, out, scratch, ls, st);
+      default: return launch_att_tiles_t<4, 64, 64>(q, kc, vc, tiles, ntiles, nh, max_pos, seq_stride, scale, out, scratch, ls, st);
+    }
+  }
+  if (g == 2) return launch_att_tiles_t<2, 128, 32>(q, kc, vc, tiles, ntiles, nh, max_pos, seq_stride, scale, out, scratch, ls, st);
+  return launch_att_tiles_t<4, 128, 32>(q, kc, vc, tiles, ntiles, nh, max_pos, seq_stride, scale, out, scratch, ls, st);
 }
 
 }  // namespace cis2

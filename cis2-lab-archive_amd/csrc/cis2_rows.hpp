@@ -71,6 +71,24 @@ hipError_t launch_attention_rows(const float* q, const float* kc, const float* v
                                  RowsDesc rows, uint32_t max_len, uint32_t nh, uint32_t nkv,
                                  uint32_t hd, uint32_t max_pos, uint64_t seq_stride, float scale,
                                  float* out, bool tree, hipStream_t st);
+// Prefill attention in tiles: rows row0 .. row0+nr-1 (nr <= 16) are rows of
+// sequence seq at positions p0 .. p0+nr-1; each tile's rows get the same
+// bits as launch_attention_rows gives them (sequential order only), with
+// each K and V element read once per tile and KV head.  Shapes: head_dim
+// 64 with 1..4 query heads per KV head, head_dim 128 with 2 or 4.
+// scratch: attention_tiles_scratch_floats(ntiles, nh, nkv, max_len) floats.
+struct AttTile {
+  uint32_t row0, nr, seq, p0;
+};
+constexpr uint32_t kAttTileRows = 16;
+bool attention_tiles_supported(uint32_t nh, uint32_t nkv, uint32_t hd);
+size_t attention_tiles_scratch_floats(uint32_t ntiles, uint32_t nh, uint32_t nkv,
+                                      uint32_t max_len);
+hipError_t launch_attention_tiles(const float* q, const float* kc, const float* vc,
+                                  const AttTile* tiles, uint32_t ntiles, uint32_t max_len,
+                                  uint32_t nh, uint32_t nkv, uint32_t hd, uint32_t max_pos,
+                                  uint64_t seq_stride, float scale, float* out, float* scratch,
+                                  hipStream_t st);
 // dst[i] = src[idx[i]] rows of `width` floats, i < n.
 hipError_t launch_gather_rows(const float* src, const uint32_t* idx, uint32_t n, uint32_t width,
                               float* dst, hipStream_t st);

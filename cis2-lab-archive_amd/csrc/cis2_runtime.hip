@@ -80,7 +80,13 @@ struct RowsBuf {
   float* logits2 = nullptr;
   uint32_t* arg2 = nullptr;
   uint32_t cap2 = 0;
-  std::vector<void*> mem, lmem, mem2;
+  // prefill attention tiles (device copy of htiles) and their scratch
+  std::vector<AttTile> htiles;
+  AttTile* tiles = nullptr;
+  uint32_t tcap = 0;
+  float* ascr = nullptr;
+  size_t acap = 0;
+  std::vector<void*> mem, lmem, mem2, tmem;
 };
 
 }  // namespace
@@ -463,8 +469,10 @@ constexpr uint32_t kFuseNormRows = 256;
 
 // The logits and argmax go to b.logits / b.arg unless `logits` / `arg` name
 // other buffers of at least nl rows.
+// ntiles > 0: the attention runs over the ntiles tiles in c->rows.tiles
+// (runs of rows of one sequence at consecutive positions).
 int forward_rows(cis2_ctx* c, uint32_t n, const uint32_t* d_tok, uint32_t max_len, uint32_t nl,
-                 float* logits = nullptr, uint32_t* arg = nullptr) {
+                 float* logits = nullptr, uint32_t* arg = nullptr, uint32_t ntiles = 0) {
   const cis2_config& f = c->cfg;
   RowsBuf& b = c->rows;
   const uint32_t H = f.hidden, I = f.inter, hd = f.head_dim, QD = c->qd, KV = c->kvd;
@@ -505,9 +513,15 @@ int forward_rows(cis2_ctx* c, uint32_t n, const uint32_t* d_tok, uint32_t max_le
     LAUNCH(launch_rope_store_rows(b.q, b.k, b.v, c->rope_cs, rd, f.n_heads, f.n_kv_heads, hd,
                                   f.max_pos, kc, vc, seq_stride, s),
            "rows rope");
-    LAUNCH(launch_attention_rows(b.q, kc, vc, rd, max_len, f.n_heads, f.n_kv_heads, hd,
-                                 f.max_pos, seq_stride, c->scale, b.att, tree, s),
-           "rows attention");
+    if (ntiles)
+      LAUNCH(launch_attention_tiles(b.q, kc, vc, b.tiles, ntiles, max_len, f.n_heads,
+                                    f.n_kv_heads, hd, f.max_pos, seq_stride, c->scale, b.att,
+                                    b.ascr, s),
+             "rows attention tiles");
+    else
+      LAUNCH(launch_attention_rows(b.q, kc, vc, rd, max_len, f.n_heads, f.n_kv_heads, hd,
+                                   f.max_pos, seq_stride, c->scale, b.att, tree, s),
+             "rows attention");
     const BgemmSeg so{Ly.wo, H, QD, c->Ro, b.att, QD, b.h2, H, b.h, H, kEpiResidual};
     LAUNCH(launch_bgemm(so, n, tree, s), "rows o_proj");
     std::swap(b.h, b.h2);
@@ -543,6 +557,56 @@ int forward_rows(cis2_ctx* c, uint32_t n, const uint32_t* d_tok, uint32_t max_le
 }
 
 // Uploads row descriptors (and the logit-row list) and runs forward_rows.
+// Rows that attend in tiles: the prefill of many rows (runs of one sequence
+// at consecutive positions, up to kAttTileRows per tile) in the sequential
+// order, for the shapes the tiled kernel has; *ntiles = 0 otherwise.
+// CIS2_ATT_TILES=1 / 0 forces the tiles on / off (the bits are the same).
+int plan_tiles(cis2_ctx* c, uint32_t n, const uint32_t* seq, const uint32_t* pos,
+               uint32_t max_len, uint32_t* ntiles) {
+  const cis2_config& f = c->cfg;
+  RowsBuf& b = c->rows;
+  *ntiles = 0;
+  const char* pe = getenv("CIS2_ATT_TILES");
+  const bool force = pe && pe[0] == '1', off = pe && pe[0] == '0';
+  if (off || f.reduction_mode != 0 ||
+      !attention_tiles_supported(f.n_heads, f.n_kv_heads, f.head_dim))
+    return CIS2_OK;
+  if (!force && (uint64_t)n * f.n_kv_heads < 4 * (uint64_t)c->ncu) return CIS2_OK;
+  b.htiles.clear();
+  for (uint32_t i = 0; i < n;) {
+    uint32_t k = 1;
+    while (i + k < n && k < kAttTileRows && seq[i + k] == seq[i] && pos[i + k] == pos[i] + k) ++k;
+    b.htiles.push_back(AttTile{i, k, seq[i], pos[i]});
+    i += k;
+  }
+  const uint32_t nt = (uint32_t)b.htiles.size();
+  if (!force && (uint64_t)nt * 8 > n) return CIS2_OK;  // short runs: per-row attention
+  const size_t scr = attention_tiles_scratch_floats(nt, f.n_heads, f.n_kv_heads, max_len);
+  if (nt > b.tcap || scr > b.acap) {
+    HIPCHK(c, hipStreamSynchronize(c->st), "tiles sync");
+    for (void* p : b.tmem) (void)hipFree(p);
+    b.tmem.clear();
+    b.tcap = 0;
+    b.acap = 0;
+    void* p = nullptr;
+    if (hipMalloc(&p, (size_t)nt * sizeof(AttTile)) != hipSuccess)
+      return fail(c, CIS2_E_OOM, "attention tiles");
+    b.tmem.push_back(p);
+    b.tiles = static_cast<AttTile*>(p);
+    if (hipMalloc(&p, scr * sizeof(float)) != hipSuccess)
+      return fail(c, CIS2_E_OOM, "attention tile scratch");
+    b.tmem.push_back(p);
+    b.ascr = static_cast<float*>(p);
+    b.tcap = nt;
+    b.acap = scr;
+  }
+  HIPCHK(c, hipMemcpyAsync(b.tiles, b.htiles.data(), (size_t)nt * sizeof(AttTile),
+                           hipMemcpyHostToDevice, c->st),
+         "tiles upload");
+  *ntiles = nt;
+  return CIS2_OK;
+}
+
 int forward_rows_host(cis2_ctx* c, uint32_t n, const uint32_t* seq, const uint32_t* pos,
                       const uint32_t* tok, uint32_t nl, const uint32_t* lrows) {
   int r = rows_reserve(c, n, nl);
@@ -556,7 +620,10 @@ int forward_rows_host(cis2_ctx* c, uint32_t n, const uint32_t* seq, const uint32
   if (nl)
     HIPCHK(c, hipMemcpyAsync(b.lrows, lrows, (size_t)nl * 4, hipMemcpyHostToDevice, c->st),
            "rows lrows");
-  return forward_rows(c, n, b.tok, max_len, nl);
+  uint32_t ntiles = 0;
+  r = plan_tiles(c, n, seq, pos, max_len, &ntiles);
+  if (r) return r;
+  return forward_rows(c, n, b.tok, max_len, nl, nullptr, nullptr, ntiles);
 }
 
 // Checks a row set: sequence and position ranges, token ranges, and no two
@@ -663,6 +730,7 @@ void cis2_ctx_destroy(cis2_ctx* c) {
   for (void* p : c->rows.mem) (void)hipFree(p);
   for (void* p : c->rows.lmem) (void)hipFree(p);
   for (void* p : c->rows.mem2) (void)hipFree(p);
+  for (void* p : c->rows.tmem) (void)hipFree(p);
   if (c->tline_file) fclose(c->tline_file);
   for (hipEvent_t e : c->prof_ev)
     if (e) (void)hipEventDestroy(e);

@@ -200,3 +200,59 @@ def test_decode_batch_one_token_prompts():
         s = solo.decode(p, 16, step_digests=False)
         assert rows[i]["witness"] == s["witness"], i
     assert rows[0]["witness"] == rows[2]["witness"]  # same prompt, same row
+
+
+def _with_env(key, val, fn):
+    old = os.environ.get(key)
+    os.environ[key] = val
+    try:
+        return fn()
+    finally:
+        if old is None:
+            del os.environ[key]
+        else:
+            os.environ[key] = old
+
+
+@pytest.mark.parametrize("name", ["smollm2-135m", "llama-160m-p0"])
+def test_verify_prefill_tiled_attention(name, model_fixtures):
+    """The prefill's attention in tiles of up to 16 consecutive rows (forced
+    on for these row counts): the reference's witness, and logits bitwise
+    equal to the per-row attention's."""
+    rec = model_fixtures[name]
+    m, _ = model_for(rec)
+    n = len(rec["prompt"])
+    claimed = rec["tokens"][n:]
+    rt = _with_env("CIS2_ATT_TILES", "1", lambda: m.verify_prefill(rec["prompt"], claimed,
+                                                                   want_logits=True))
+    rr = _with_env("CIS2_ATT_TILES", "0", lambda: m.verify_prefill(rec["prompt"], claimed,
+                                                                   want_logits=True))
+    assert rt["first_mismatch"] == -1
+    assert rt["witness"] == rec["witness"]
+    assert np.array_equal(rt["logits"].view(np.uint32), rr["logits"].view(np.uint32))
+
+
+@pytest.mark.parametrize("shuffle", [False, True])
+def test_rows_tiled_attention_two_sequences(shuffle, model_fixtures):
+    """Rows of two sequences (runs of consecutive positions, or shuffled
+    into runs of one) through the tiled attention equal the per-row
+    attention's logits bit for bit."""
+    rec = model_fixtures["smollm2-135m"]
+    m, _ = model_for(rec, max_seqs=2, extra_pos=0)
+    a = rec["prompt"] + rec["tokens"][len(rec["prompt"]):len(rec["prompt"]) + 40]
+    b = [int(t) for t in artifacts.prompt_ids(7, m.spec.vocab, 53)]
+    rows = [(0, p, a[p]) for p in range(len(a))] + [(1, p, b[p]) for p in range(len(b))]
+    if shuffle:
+        order = np.random.default_rng(11).permutation(len(rows))
+        rows = [rows[i] for i in order]
+    rs = np.array(rows, dtype=np.uint32)
+
+    def run():
+        m.reset(0)
+        m.reset(1)
+        return m.forward_rows(rs[:, 0], rs[:, 1], rs[:, 2])
+
+    lt, at = _with_env("CIS2_ATT_TILES", "1", run)
+    lr, ar = _with_env("CIS2_ATT_TILES", "0", run)
+    assert np.array_equal(lt.view(np.uint32), lr.view(np.uint32))
+    assert np.array_equal(at, ar)
