@@ -580,7 +580,8 @@ int plan_tiles(cis2_ctx* c, uint32_t n, const uint32_t* seq, const uint32_t* pos
     i += k;
   }
   const uint32_t nt = (uint32_t)b.htiles.size();
-  if (!force && (uint64_t)nt * 8 > n) return CIS2_OK;  // short runs: per-row attention
+  // short runs, or too few tile workgroups to fill the GPU: per-row attention
+  if (!force && ((uint64_t)nt * 8 > n || (uint64_t)nt * f.n_kv_heads < c->ncu)) return CIS2_OK;
   const size_t scr = attention_tiles_scratch_floats(nt, f.n_heads, f.n_kv_heads, max_len);
   if (nt > b.tcap || scr > b.acap) {
     HIPCHK(c, hipStreamSynchronize(c->st), "tiles sync");
