@@ -847,29 +847,40 @@ __global__ __launch_bounds__(256) void k_attention_tiles(
     const float* v = vt(i);
     const float* e = et(i);
     const uint32_t j0 = i * TK, n = min(TK, len_max - j0);
+    // positions of this tile each of the thread's pairs sees; the common
+    // 4-aligned part reads each V group once for all the pairs
+    uint32_t m[PB3], mall = n;
 #pragma unroll
     for (uint32_t u = 0; u < PB3; ++u) {
       const uint32_t a = pg3 * PB3 + u;
-      if (a >= npair) continue;
-      const uint32_t len = pair_len(a);
-      if (j0 >= len) continue;
-      const uint32_t m = min(n, len - j0);  // positions of this tile the pair sees
-      const float* pr = e + (size_t)a * VS;
-      uint32_t j = 0;
+      const uint32_t len = a < npair ? pair_len(a) : 0;
+      m[u] = len > j0 ? min(n, len - j0) : 0;
+      mall = min(mall, m[u]);
+    }
+    const uint32_t m4 = mall & ~3u;
 #pragma unroll 2
-      for (; j + 4 <= m; j += 4) {
-        const v4 pp = *reinterpret_cast<const v4*>(pr + j);
+    for (uint32_t j = 0; j < m4; j += 4) {
+      v4 vv[4];
+#pragma unroll
+      for (uint32_t dd = 0; dd < 4; ++dd)
+        vv[dd] = *reinterpret_cast<const v4*>(v + (size_t)(4 * dg + dd) * VS + j);
+#pragma unroll
+      for (uint32_t u = 0; u < PB3; ++u) {
+        const v4 pp = *reinterpret_cast<const v4*>(e + (size_t)(pg3 * PB3 + u) * VS + j);
 #pragma unroll
         for (uint32_t dd = 0; dd < 4; ++dd) {
-          const v4 vv = *reinterpret_cast<const v4*>(v + (size_t)(4 * dg + dd) * VS + j);
           float p;
-          p = pp.x * vv.x; acc3[u][dd] = acc3[u][dd] + p;
-          p = pp.y * vv.y; acc3[u][dd] = acc3[u][dd] + p;
-          p = pp.z * vv.z; acc3[u][dd] = acc3[u][dd] + p;
-          p = pp.w * vv.w; acc3[u][dd] = acc3[u][dd] + p;
+          p = pp.x * vv[dd].x; acc3[u][dd] = acc3[u][dd] + p;
+          p = pp.y * vv[dd].y; acc3[u][dd] = acc3[u][dd] + p;
+          p = pp.z * vv[dd].z; acc3[u][dd] = acc3[u][dd] + p;
+          p = pp.w * vv[dd].w; acc3[u][dd] = acc3[u][dd] + p;
         }
       }
-      for (; j < m; ++j) {
+    }
+#pragma unroll
+    for (uint32_t u = 0; u < PB3; ++u) {
+      const float* pr = e + (size_t)(pg3 * PB3 + u) * VS;
+      for (uint32_t j = m4; j < m[u]; ++j) {
 #pragma unroll
         for (uint32_t dd = 0; dd < 4; ++dd) {
           const float p = pr[j] * v[(size_t)(4 * dg + dd) * VS + j];
