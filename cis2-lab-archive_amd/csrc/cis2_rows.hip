@@ -7,6 +7,7 @@
 #include "cis2_rows.hpp"
 
 #include <algorithm>
+#include <cstdlib>
 
 namespace cis2 {
 namespace {
@@ -114,16 +115,16 @@ __device__ float row_inv_rms(const float* x, uint32_t K, float eps, bool tree) {
   return rsqrt_cr(arg);
 }
 
-template <bool DUAL, bool NORM>
+template <bool DUAL, bool NORM, uint32_t CB>
 __global__ __launch_bounds__(256) void k_bgemm(BgemmArgs a) {
   extern __shared__ v4 sm[];
   __shared__ float s_inv[kT];
   uint32_t si = 0;
   if (a.nseg > 1 && blockIdx.x >= a.blk0[1]) si = (a.nseg > 2 && blockIdx.x >= a.blk0[2]) ? 2 : 1;
   const BgemmSeg g = si == 0 ? a.s[0] : (si == 1 ? a.s[1] : a.s[2]);
-  const uint32_t R = g.R, TB = a.TB, KC = a.KC, K = g.K;
-  const uint32_t blk = blockIdx.x - a.blk0[si], b0 = blockIdx.y * TB, t = threadIdx.x;
-  const uint32_t r = t % R, bb = t / R;
+  const uint32_t R = g.R, TB = a.TB, KC = a.KC, K = g.K, NB = TB * CB;  // NB batch rows staged
+  const uint32_t blk = blockIdx.x - a.blk0[si], b0 = blockIdx.y * NB, t = threadIdx.x;
+  const uint32_t r = t % R, bb = t / R;  // the thread's rows: b0 + bb + c * TB, c < CB
   const uint32_t wv = __builtin_amdgcn_readfirstlane(t >> 6), lane = t & 63;
   const bool live = t < R * TB;
   const uint32_t qmax = KC / 4, xs4 = qmax + 1;  // padded X rows: no bank aliasing
@@ -131,7 +132,9 @@ __global__ __launch_bounds__(256) void k_bgemm(BgemmArgs a) {
   v4* Xs = sm + (size_t)(DUAL ? 2 : 1) * qmax * R;
   const v4* Wg = reinterpret_cast<const v4*>(g.W + (size_t)blk * R * K);
   const v4* Wg2 = DUAL ? reinterpret_cast<const v4*>(a.W2 + (size_t)blk * R * K) : nullptr;
-  float acc = 0.0f, acc2 = 0.0f;
+  float acc[CB], acc2[CB];
+#pragma unroll
+  for (uint32_t c = 0; c < CB; ++c) acc[c] = acc2[c] = 0.0f;
   for (uint32_t k0 = 0; k0 < K; k0 += KC) {
     const uint32_t q4 = std::min(KC, K - k0) / 4, g0 = k0 / 4;
     // every load of the chunk in flight at once, straight into LDS; each
@@ -144,19 +147,19 @@ __global__ __launch_bounds__(256) void k_bgemm(BgemmArgs a) {
         if (i0 + lane < nw4) lds_load16(Wg2 + (size_t)g0 * R + i0 + lane, Ws + qmax * R + i0);
     }
     const uint32_t pieces = (q4 + 63) / 64;
-    for (uint32_t j = wv; j < TB * pieces; j += kT / 64) {
+    for (uint32_t j = wv; j < NB * pieces; j += kT / 64) {
       const uint32_t bx = j / pieces, q0 = (j - bx * pieces) * 64;
       const uint32_t row = std::min(b0 + bx, a.n - 1);
       const v4* xr = reinterpret_cast<const v4*>(g.X + (size_t)row * g.ldx) + g0 + q0;
       if (q0 + lane < q4) lds_load16(xr + lane, Xs + bx * xs4 + q0);
     }
-    if (NORM && k0 == 0 && t < TB)
+    if (NORM && k0 == 0 && t < NB)
       s_inv[t] = row_inv_rms(g.X + (size_t)std::min(b0 + t, a.n - 1) * g.ldx, K, a.eps, a.tree);
     wait_vm0();
     __syncthreads();
     if (NORM) {
       const v4* nw4p = reinterpret_cast<const v4*>(a.nw) + g0;
-      for (uint32_t i = t; i < TB * q4; i += kT) {
+      for (uint32_t i = t; i < NB * q4; i += kT) {
         const uint32_t bx = i / q4, q = i - bx * q4;
         const float inv = s_inv[bx];
         const v4 x = Xs[bx * xs4 + q], w = nw4p[q];
@@ -173,66 +176,76 @@ __global__ __launch_bounds__(256) void k_bgemm(BgemmArgs a) {
     if (live) {
       const v4* wp = Ws + r;
       const v4* wp2 = Ws + qmax * R + r;
-      const v4* xp = Xs + bb * xs4;
+      const v4* xp[CB];
+#pragma unroll
+      for (uint32_t c = 0; c < CB; ++c) xp[c] = Xs + (bb + c * TB) * xs4;
       if (a.tree) {
         for (uint32_t q = 0; q < q4; q += 8) {
-          float l[32], l2[32];
 #pragma unroll
-          for (uint32_t j = 0; j < 8; ++j) {
-            v4 w = v4{0.0f, 0.0f, 0.0f, 0.0f}, x = w, w2 = w;
-            if (q + j < q4) {
-              w = wp[(size_t)(q + j) * R];
-              x = xp[q + j];
-              if (DUAL) w2 = wp2[(size_t)(q + j) * R];
+          for (uint32_t c = 0; c < CB; ++c) {
+            float l[32], l2[32];
+#pragma unroll
+            for (uint32_t j = 0; j < 8; ++j) {
+              v4 w = v4{0.0f, 0.0f, 0.0f, 0.0f}, x = w, w2 = w;
+              if (q + j < q4) {
+                w = wp[(size_t)(q + j) * R];
+                x = xp[c][q + j];
+                if (DUAL) w2 = wp2[(size_t)(q + j) * R];
+              }
+              l[4 * j] = w.x * x.x;
+              l[4 * j + 1] = w.y * x.y;
+              l[4 * j + 2] = w.z * x.z;
+              l[4 * j + 3] = w.w * x.w;
+              if (DUAL) {
+                l2[4 * j] = w2.x * x.x;
+                l2[4 * j + 1] = w2.y * x.y;
+                l2[4 * j + 2] = w2.z * x.z;
+                l2[4 * j + 3] = w2.w * x.w;
+              }
             }
-            l[4 * j] = w.x * x.x;
-            l[4 * j + 1] = w.y * x.y;
-            l[4 * j + 2] = w.z * x.z;
-            l[4 * j + 3] = w.w * x.w;
-            if (DUAL) {
-              l2[4 * j] = w2.x * x.x;
-              l2[4 * j + 1] = w2.y * x.y;
-              l2[4 * j + 2] = w2.z * x.z;
-              l2[4 * j + 3] = w2.w * x.w;
-            }
+            acc[c] = acc[c] + tree32(l);
+            if (DUAL) acc2[c] = acc2[c] + tree32(l2);
           }
-          acc = acc + tree32(l);
-          if (DUAL) acc2 = acc2 + tree32(l2);
         }
       } else {
         // software pipelined over two register sets: the reads of the next
         // 4 q go out before the current 4 q's products and chain steps
-        // (reads past the end are clamped to the last q and unused)
+        // (reads past the end are clamped to the last q and unused); a W
+        // group read serves the CB rows' chains
         constexpr uint32_t U = 4;
-        v4 aw[U], ax[U], aw2[U], bw[U], bx[U], bw2[U];
-        auto load = [&](v4 (&w)[U], v4 (&x)[U], v4 (&w2)[U], uint32_t q0) {
+        v4 aw[U], ax[CB][U], aw2[U], bw[U], bx[CB][U], bw2[U];
+        auto load = [&](v4 (&w)[U], v4 (&x)[CB][U], v4 (&w2)[U], uint32_t q0) {
 #pragma unroll
           for (uint32_t u = 0; u < U; ++u) {
             const uint32_t qq = std::min(q0 + u, q4 - 1);
             w[u] = wp[(size_t)qq * R];
-            x[u] = xp[qq];
+#pragma unroll
+            for (uint32_t c = 0; c < CB; ++c) x[c][u] = xp[c][qq];
             if (DUAL) w2[u] = wp2[(size_t)qq * R];
           }
         };
-        auto step = [&](const v4 (&w)[U], const v4 (&x)[U], const v4 (&w2)[U]) {
-          float p[4 * U], p2[4 * U];
+        auto step = [&](const v4 (&w)[U], const v4 (&x)[CB][U], const v4 (&w2)[U]) {
 #pragma unroll
-          for (uint32_t u = 0; u < U; ++u) {
-            p[4 * u] = w[u].x * x[u].x;
-            p[4 * u + 1] = w[u].y * x[u].y;
-            p[4 * u + 2] = w[u].z * x[u].z;
-            p[4 * u + 3] = w[u].w * x[u].w;
-            if (DUAL) {
-              p2[4 * u] = w2[u].x * x[u].x;
-              p2[4 * u + 1] = w2[u].y * x[u].y;
-              p2[4 * u + 2] = w2[u].z * x[u].z;
-              p2[4 * u + 3] = w2[u].w * x[u].w;
+          for (uint32_t c = 0; c < CB; ++c) {
+            float p[4 * U], p2[4 * U];
+#pragma unroll
+            for (uint32_t u = 0; u < U; ++u) {
+              p[4 * u] = w[u].x * x[c][u].x;
+              p[4 * u + 1] = w[u].y * x[c][u].y;
+              p[4 * u + 2] = w[u].z * x[c][u].z;
+              p[4 * u + 3] = w[u].w * x[c][u].w;
+              if (DUAL) {
+                p2[4 * u] = w2[u].x * x[c][u].x;
+                p2[4 * u + 1] = w2[u].y * x[c][u].y;
+                p2[4 * u + 2] = w2[u].z * x[c][u].z;
+                p2[4 * u + 3] = w2[u].w * x[c][u].w;
+              }
             }
-          }
 #pragma unroll
-          for (uint32_t i = 0; i < 4 * U; ++i) {
-            acc = acc + p[i];
-            if (DUAL) acc2 = acc2 + p2[i];
+            for (uint32_t i = 0; i < 4 * U; ++i) {
+              acc[c] = acc[c] + p[i];
+              if (DUAL) acc2[c] = acc2[c] + p2[i];
+            }
           }
         };
         uint32_t q = 0;
@@ -250,36 +263,44 @@ __global__ __launch_bounds__(256) void k_bgemm(BgemmArgs a) {
           }
         }
         for (; q < q4; ++q) {
-          const v4 w = wp[(size_t)q * R], x = xp[q];
-          float pp;
-          pp = w.x * x.x; acc = acc + pp;
-          pp = w.y * x.y; acc = acc + pp;
-          pp = w.z * x.z; acc = acc + pp;
-          pp = w.w * x.w; acc = acc + pp;
-          if (DUAL) {
-            const v4 w2 = wp2[(size_t)q * R];
-            pp = w2.x * x.x; acc2 = acc2 + pp;
-            pp = w2.y * x.y; acc2 = acc2 + pp;
-            pp = w2.z * x.z; acc2 = acc2 + pp;
-            pp = w2.w * x.w; acc2 = acc2 + pp;
+          const v4 w = wp[(size_t)q * R];
+          const v4 w2 = DUAL ? wp2[(size_t)q * R] : w;
+#pragma unroll
+          for (uint32_t c = 0; c < CB; ++c) {
+            const v4 x = xp[c][q];
+            float pp;
+            pp = w.x * x.x; acc[c] = acc[c] + pp;
+            pp = w.y * x.y; acc[c] = acc[c] + pp;
+            pp = w.z * x.z; acc[c] = acc[c] + pp;
+            pp = w.w * x.w; acc[c] = acc[c] + pp;
+            if (DUAL) {
+              pp = w2.x * x.x; acc2[c] = acc2[c] + pp;
+              pp = w2.y * x.y; acc2[c] = acc2[c] + pp;
+              pp = w2.z * x.z; acc2[c] = acc2[c] + pp;
+              pp = w2.w * x.w; acc2[c] = acc2[c] + pp;
+            }
           }
         }
       }
     }
     __syncthreads();
   }
-  const uint32_t row = b0 + bb, m = blk * R + r;
-  if (live && row < a.n && m < g.M) {
-    float y = acc;
-    if (DUAL) {
-      const float sg = silu_pinned(acc);
-      y = sg * acc2;
-    } else if (g.epi == kEpiBias) {
-      y = acc + g.add[m];
-    } else if (g.epi == kEpiResidual) {
-      y = g.add[(size_t)row * g.ldadd + m] + acc;
+  const uint32_t m = blk * R + r;
+#pragma unroll
+  for (uint32_t c = 0; c < CB; ++c) {
+    const uint32_t row = b0 + bb + c * TB;
+    if (live && row < a.n && m < g.M) {
+      float y = acc[c];
+      if (DUAL) {
+        const float sg = silu_pinned(acc[c]);
+        y = sg * acc2[c];
+      } else if (g.epi == kEpiBias) {
+        y = acc[c] + g.add[m];
+      } else if (g.epi == kEpiResidual) {
+        y = g.add[(size_t)row * g.ldadd + m] + acc[c];
+      }
+      g.Y[(size_t)row * g.ldy + m] = y;
     }
-    g.Y[(size_t)row * g.ldy + m] = y;
   }
 }
 
@@ -931,9 +952,9 @@ __global__ __launch_bounds__(1024) void k_argmax_rows(const float* __restrict__ 
 
 }  // namespace
 
-template <bool DUAL, bool NORM>
+template <bool DUAL, bool NORM, uint32_t CB>
 hipError_t launch_bgemm_t(const BgemmArgs& a, dim3 grid, size_t lds, hipStream_t st) {
-  hipLaunchKernelGGL((k_bgemm<DUAL, NORM>), grid, dim3(kT), lds, st, a);
+  hipLaunchKernelGGL((k_bgemm<DUAL, NORM, CB>), grid, dim3(kT), lds, st, a);
   return hipGetLastError();
 }
 
@@ -942,10 +963,12 @@ hipError_t launch_bgemm_t(const BgemmArgs& a, dim3 grid, size_t lds, hipStream_t
 hipError_t bgemm_configure() {
   static bool configured = false;
   if (configured) return hipSuccess;
-  const void* fns[4] = {reinterpret_cast<const void*>(&k_bgemm<false, false>),
-                        reinterpret_cast<const void*>(&k_bgemm<false, true>),
-                        reinterpret_cast<const void*>(&k_bgemm<true, false>),
-                        reinterpret_cast<const void*>(&k_bgemm<true, true>)};
+  const void* fns[6] = {reinterpret_cast<const void*>(&k_bgemm<false, false, 1>),
+                        reinterpret_cast<const void*>(&k_bgemm<false, true, 1>),
+                        reinterpret_cast<const void*>(&k_bgemm<true, false, 1>),
+                        reinterpret_cast<const void*>(&k_bgemm<true, true, 1>),
+                        reinterpret_cast<const void*>(&k_bgemm<false, false, 2>),
+                        reinterpret_cast<const void*>(&k_bgemm<true, false, 2>)};
   for (const void* f : fns) {
     hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize,
                                        (int)kBgemmLdsBig);
@@ -953,6 +976,17 @@ hipError_t bgemm_configure() {
   }
   configured = true;
   return hipSuccess;
+}
+
+// CIS2_BGEMM_CB=1 keeps one batch row per thread on every grid (for A/B
+// timing of the two-row form; the results are the same bits either way).
+static bool bgemm_cb_allowed() {
+  static int allowed = -1;
+  if (allowed < 0) {
+    const char* e = std::getenv("CIS2_BGEMM_CB");
+    allowed = (e && e[0] == '1' && e[1] == 0) ? 0 : 1;
+  }
+  return allowed == 1;
 }
 
 hipError_t launch_bgemm_multi(const BgemmSeg* segs, uint32_t nseg, uint32_t n,
@@ -995,23 +1029,29 @@ hipError_t launch_bgemm_multi(const BgemmSeg* segs, uint32_t nseg, uint32_t n,
   a.eps = o.eps;
   const uint32_t S = o.W2 ? 2 : 1;
   const uint64_t wgs = (uint64_t)a.blk0[nseg] * ((n + a.TB - 1) / a.TB);
+  // grids of many workgroups per CU (prefill) give each thread two batch
+  // rows, so that one W read from LDS feeds two chains
+  const uint32_t CB = (!o.norm_w && !o.tree && wgs >= 8ull * ncu && bgemm_cb_allowed()) ? 2 : 1;
+  const uint32_t NB = a.TB * CB;
   // a grid of at most one workgroup per CU may take most of a CU's LDS
   // (fewer K chunks, each a full round trip); larger grids keep two
   // workgroups per CU, so that up to two per CU all run at once
   const uint32_t budget = wgs <= (uint64_t)ncu ? kBgemmLdsBig : kBgemmLds;
   // largest chunk (a multiple of 32 k) whose W slices and X rows fit
-  const uint32_t q_fit = (budget / 16 - a.TB) / (S * s0.R + a.TB);
+  const uint32_t q_fit = (budget / 16 - NB) / (S * s0.R + NB);
   uint32_t KC = (q_fit * 4) & ~31u;
   if (KC == 0) return hipErrorInvalidValue;
   const uint32_t K32 = (s0.K + 31) & ~31u;
   if (KC > K32) KC = K32;
   a.KC = KC;
-  const size_t lds = ((size_t)(KC / 4) * s0.R * S + (size_t)a.TB * (KC / 4 + 1)) * 16;
-  const dim3 grid(a.blk0[nseg], (n + a.TB - 1) / a.TB);
-  if (o.W2) return o.norm_w ? launch_bgemm_t<true, true>(a, grid, lds, st)
-                            : launch_bgemm_t<true, false>(a, grid, lds, st);
-  return o.norm_w ? launch_bgemm_t<false, true>(a, grid, lds, st)
-                  : launch_bgemm_t<false, false>(a, grid, lds, st);
+  const size_t lds = ((size_t)(KC / 4) * s0.R * S + (size_t)NB * (KC / 4 + 1)) * 16;
+  const dim3 grid(a.blk0[nseg], (n + NB - 1) / NB);
+  if (CB == 2) return o.W2 ? launch_bgemm_t<true, false, 2>(a, grid, lds, st)
+                           : launch_bgemm_t<false, false, 2>(a, grid, lds, st);
+  if (o.W2) return o.norm_w ? launch_bgemm_t<true, true, 1>(a, grid, lds, st)
+                            : launch_bgemm_t<true, false, 1>(a, grid, lds, st);
+  return o.norm_w ? launch_bgemm_t<false, true, 1>(a, grid, lds, st)
+                  : launch_bgemm_t<false, false, 1>(a, grid, lds, st);
 }
 
 hipError_t launch_bgemm(const BgemmSeg& s, uint32_t n, bool tree, hipStream_t st) {
