@@ -22,7 +22,7 @@ CIS2_OK = 0
 ERRORS = {
     -1: "CIS2_E_ARG", -2: "CIS2_E_UNSUPPORTED", -3: "CIS2_E_MISSING_TENSOR",
     -4: "CIS2_E_SHAPE", -5: "CIS2_E_NAME", -6: "CIS2_E_FPENV", -7: "CIS2_E_DEVICE",
-    -8: "CIS2_E_OOM", -9: "CIS2_E_RANGE",
+    -8: "CIS2_E_OOM", -9: "CIS2_E_RANGE", -10: "CIS2_E_NUMERIC",
 }
 
 
@@ -35,6 +35,13 @@ class Cis2Config(ctypes.Structure):
         ("max_pos", ctypes.c_uint32), ("max_seqs", ctypes.c_uint32),
         ("reduction_mode", ctypes.c_uint32), ("eps", ctypes.c_float),
         ("rope_theta", ctypes.c_double),
+    ]
+
+
+class Cis2Sampling(ctypes.Structure):
+    _fields_ = [
+        ("mode", ctypes.c_uint32), ("top_k", ctypes.c_uint32), ("seed", ctypes.c_uint64),
+        ("temperature", ctypes.c_float), ("top_p", ctypes.c_float),
     ]
 
 
@@ -64,6 +71,9 @@ SIGNATURES = {
     "cis2_verify_prefill": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_uint32, c_u32p, ctypes.c_uint32,
                                            c_u32p, ctypes.c_uint32, c_u8p, c_u32p, c_u8p, c_u8p,
                                            ctypes.POINTER(ctypes.c_int64), c_fp]),
+    "cis2_set_sampling": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(Cis2Sampling)]),
+    "cis2_sample_logits": (ctypes.c_int, [ctypes.c_void_p, c_fp, ctypes.c_uint32, c_u32p, c_u32p,
+                                          c_u32p]),
     "cis2_trace_enable": (ctypes.c_int, [ctypes.c_void_p, TRACE_FN, ctypes.c_void_p]),
     "cis2_profile": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int]),
     "cis2_profile_read": (ctypes.c_int, [ctypes.c_void_p, c_u64p, ctypes.POINTER(ctypes.c_double),

@@ -7,6 +7,9 @@ code/cis2-fp/gpu/cis2_host.cpp:61-249):
                                                 -> Cis2Model.forward_token(pos, tok)
   the cis2_host greedy/witness loop              -> Cis2Model.decode(prompt, gen_toks)
   Cis2Trace (--trace)                            -> Cis2Model.trace(prompt, gen_toks)
+  the seeded-sampling driver (--sample seed,T,K,P; v0.4 draft section 14,
+  code/patches/cis2-spec__seeded-sampling.patch:57-196)
+                                                -> Cis2Model.set_sampling(...), then decode
 Errors surface as Cis2Error (the reference exits with status 2 instead).
 """
 import ctypes
@@ -93,9 +96,36 @@ class Cis2Model:
                                       _ptr(am, _lib.c_u32p)), self.ctx)
         return logits, int(am[0])
 
+    def set_sampling(self, seed=None, temperature=1.0, top_k=0, top_p=1.0):
+        """Seeded sampling for the following decodes (seed None: greedy).
+        temperature and top_p are narrowed to f32 as given (pass the f32
+        value, e.g. np.float32(0.8)); invalid values raise Cis2Error."""
+        if seed is None:
+            sp = _lib.Cis2Sampling(mode=0)
+        else:
+            sp = _lib.Cis2Sampling(mode=1, top_k=int(top_k), seed=int(seed),
+                                   temperature=float(np.float32(temperature)),
+                                   top_p=float(np.float32(top_p)))
+        check(_lib.lib().cis2_set_sampling(self.ctx, ctypes.byref(sp)), self.ctx)
+
+    def sample_logits(self, logits, steps):
+        """Draws with the current sampling parameters from host logit rows
+        (float32 [n, vocab]) at the given generation steps; returns (ids,
+        kept-set sizes)."""
+        lg = np.ascontiguousarray(logits, dtype=np.float32).reshape(-1, self.spec.vocab)
+        n = lg.shape[0]
+        st = np.ascontiguousarray(steps, dtype=np.uint32).reshape(n)
+        ids = np.zeros(n, dtype=np.uint32)
+        nk = np.zeros(n, dtype=np.uint32)
+        check(_lib.lib().cis2_sample_logits(self.ctx, _ptr(lg, _lib.c_fp), n, _ptr(st, _lib.c_u32p),
+                                            _ptr(ids, _lib.c_u32p), _ptr(nk, _lib.c_u32p)),
+              self.ctx)
+        return ids, nk
+
     def decode(self, prompt, gen_toks, seq=0, step_digests=True):
-        """Greedy decode with the witness fold; returns a dict with ids,
-        witness, argmax_digest and the per-step logit digests."""
+        """Greedy (or, after set_sampling, sampled) decode with the witness
+        fold; returns a dict with ids, witness, argmax_digest and the
+        per-step logit digests."""
         prompt = np.ascontiguousarray(prompt, dtype=np.uint32)
         n = prompt.size
         ids = np.zeros(n + gen_toks, dtype=np.uint32)

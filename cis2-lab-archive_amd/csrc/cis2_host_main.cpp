@@ -10,7 +10,10 @@
 #include "cis2_artifacts.hpp"
 #include "cis2_sha256.hpp"
 
+#include <errno.h>
+#include <math.h>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include <string>
@@ -58,12 +61,48 @@ uint32_t num_key(const JValue& cfg, const char* k) {
   return (uint32_t)v->num;
 }
 
+// "SEED,T,K,P": seed u64 (decimal or 0x hex), T and P by strtof (correctly
+// rounded decimal to f32, draft 14.1), K u32.  False when malformed or out
+// of range.
+bool parse_sample(const char* txt, cis2_sampling* out) {
+  std::string t(txt);
+  std::vector<std::string> f;
+  size_t b = 0;
+  for (size_t e; (e = t.find(',', b)) != std::string::npos; b = e + 1) f.push_back(t.substr(b, e - b));
+  f.push_back(t.substr(b));
+  if (f.size() != 4) return false;
+  for (const std::string& x : f)
+    if (x.empty()) return false;
+  char* end = nullptr;
+  errno = 0;
+  const unsigned long long seed = strtoull(f[0].c_str(), &end, 0);
+  if (*end || errno || f[0][0] == '-') return false;
+  const float T = strtof(f[1].c_str(), &end);
+  if (*end) return false;
+  errno = 0;
+  const unsigned long k = strtoul(f[2].c_str(), &end, 10);
+  if (*end || errno || k > 0xFFFFFFFFul || f[2][0] == '-') return false;
+  const float P = strtof(f[3].c_str(), &end);
+  if (*end) return false;
+  if (!(T > 0.0f) || T == HUGE_VALF || !(P > 0.0f) || !(P <= 1.0f)) return false;
+  out->mode = 1;
+  out->seed = seed;
+  out->temperature = T;
+  out->top_k = (uint32_t)k;
+  out->top_p = P;
+  return true;
+}
+
 }  // namespace
 
 int main(int argc, char** argv) {
   std::string weights_dir = "weights", ids_path, trace_path;
   int gen_toks = 16, prompt_idx = 0;
   uint32_t reduction = 0;  // --reduction sequential|tree (code/cis2-fp/src/main.rs:775-782)
+  // --sample SEED,T,K,P: seeded sampling (v0.4 draft section 14; the lab
+  // driver's flag, labs/w1x-sample/feed/cm-hq__cis2-sample-hq-r2/job.sh:22-28)
+  cis2_sampling samp;
+  memset(&samp, 0, sizeof samp);
   for (int i = 1; i < argc; ++i) {
     std::string a = argv[i];
     if (a == "--weights-dir" && i + 1 < argc) weights_dir = argv[++i];
@@ -78,6 +117,13 @@ int main(int argc, char** argv) {
       else {
         fprintf(stderr, "FATAL: --reduction: expected 'sequential' or 'tree', got %s\n",
                 r.c_str());
+        return 2;
+      }
+    }
+    else if (a == "--sample" && i + 1 < argc) {
+      if (!parse_sample(argv[++i], &samp)) {
+        fprintf(stderr, "FATAL: --sample: expected SEED,T,K,P with T finite > 0 and P in (0,1], "
+                        "got %s\n", argv[i]);
         return 2;
       }
     }
@@ -122,6 +168,10 @@ int main(int argc, char** argv) {
   cis2_ctx* ctx = nullptr;
   int rc = cis2_ctx_create(&cfg, &ctx);
   if (rc) fatal(std::string("cis2_ctx_create: ") + cis2_strerror(rc));
+  if (samp.mode) {
+    rc = cis2_set_sampling(ctx, &samp);
+    if (rc) fatal(std::string("--sample: ") + cis2_last_error(ctx));
+  }
 
   fprintf(stderr, "loading + widening weights (bf16 -> fp32, exact bit-shift)...\n");
   SafeTensors st;
@@ -183,6 +233,8 @@ int main(int argc, char** argv) {
   if (sink.fp) fclose(sink.fp);
   for (int s = 0; s < gen_toks; ++s)
     fprintf(stderr, "[run1] step %d: token_id=%u\n", s, ids[prompt.size() + s]);
+  if (samp.mode)  // the sampled ids, one line per step (what the lab's ids16 hash reads)
+    for (int s = 0; s < gen_toks; ++s) printf("step %d next_id=%u\n", s, ids[prompt.size() + s]);
 
   uint8_t table[32], invf[32];
   cis2_digests(ctx, table, invf);
@@ -195,6 +247,13 @@ int main(int argc, char** argv) {
   printf("prompt_idx=%d run1_tokens=%s\n", prompt_idx, ids_list(ids).c_str());
   printf("prompt_idx=%d run1_witness_digest=%s\n", prompt_idx, hex(wit, 32).c_str());
   printf("prompt_idx=%d run1_argmax_digest=%s\n", prompt_idx, hex(adig, 32).c_str());
+  if (samp.mode) {
+    uint32_t tb, pb;
+    memcpy(&tb, &samp.temperature, 4);
+    memcpy(&pb, &samp.top_p, 4);
+    printf("prompt_idx=%d sample_mode=1 seed=%llu temperature=%08x top_k=%u top_p=%08x\n",
+           prompt_idx, (unsigned long long)samp.seed, tb, samp.top_k, pb);
+  }
   const char* mode = reduction ? "tree" : "sequential";
   printf("prompt_idx=%d reduction_mode=%s\n", prompt_idx, mode);
   printf("CIS2_REF digest=%s prompt_idx=%d prompt_toks=%zu gen_toks=%d dtype=fp32 "

@@ -5,6 +5,7 @@
 #include "cis2_decode.hpp"
 #include "cis2_kernels.hpp"
 #include "cis2_rows.hpp"
+#include "cis2_sample.hpp"
 #include "cis2_sha256.hpp"
 
 #include <hip/hip_runtime.h>
@@ -138,6 +139,10 @@ struct cis2_ctx {
   bool prof_on = false;
   std::vector<hipEvent_t> prof_ev;  // [2 * kProfMax], created on first use
   std::vector<uint32_t> prof_pos;
+  // seeded sampling (cis2_set_sampling): parameters and device scratch
+  bool samp_on = false;
+  SampleParams samp{};
+  SampleBufs sbuf;
   RowsBuf rows;
   std::vector<void*> allocs;
 };
@@ -330,6 +335,7 @@ int check_err_flag(cis2_ctx* c) {
       return fail(c, CIS2_E_DEVICE,
                   "persistent decode kernel: a phase wait hit its spin cap "
                   "(workgroups not co-resident)");
+    if (e & 0x100u) return fail(c, CIS2_E_NUMERIC, "NaN among logits / temperature in a sampled draw");
     return fail(c, CIS2_E_RANGE, "token id out of range on the device");
   }
   return CIS2_OK;
@@ -718,6 +724,7 @@ const char* cis2_strerror(int code) {
     case CIS2_E_DEVICE: return "HIP device error";
     case CIS2_E_OOM: return "out of memory";
     case CIS2_E_RANGE: return "position or token out of range";
+    case CIS2_E_NUMERIC: return "NaN logit in a sampled draw";
     default: return "unknown error";
   }
 }
@@ -1098,6 +1105,80 @@ int cis2_forward(cis2_ctx* c, uint32_t n, const uint32_t* seq, const uint32_t* p
   return check_err_flag(c);
 }
 
+// Receipt header of a sampled decode (draft 14.5): "CIS2-SAMPLE-1", seed
+// (u64 LE), temperature bits, top_k, top_p bits (u32 LE).
+static void fold_sample_header(Sha256& w, const SampleParams& p) {
+  w.update("CIS2-SAMPLE-1", 13);
+  w.update_u32le((uint32_t)p.seed);
+  w.update_u32le((uint32_t)(p.seed >> 32));
+  uint32_t tb, pb;
+  memcpy(&tb, &p.temperature, 4);
+  memcpy(&pb, &p.top_p, 4);
+  w.update_u32le(tb);
+  w.update_u32le(p.top_k);
+  w.update_u32le(pb);
+}
+
+int cis2_set_sampling(cis2_ctx* c, const cis2_sampling* sp) {
+  if (!c) return CIS2_E_ARG;
+  if (c->sess.active) return fail(c, CIS2_E_ARG, "sampling cannot change during a decode session");
+  if (!sp || sp->mode == 0) {
+    c->samp_on = false;
+    return CIS2_OK;
+  }
+  const float T = sp->temperature, P = sp->top_p;
+  if (sp->mode != 1 || !(T > 0.0f) || T == __builtin_inff() || !(P > 0.0f) || !(P <= 1.0f))
+    return fail(c, CIS2_E_ARG, "invalid sampling parameters (mode 1, T finite > 0, top_p in (0,1])");
+  const uint32_t V = c->cfg.vocab;
+  SampleBufs& b = c->sbuf;
+  if (b.V != V) {
+    const uint32_t Vp = sample_sort_len(V);
+    void *k = nullptr, *e = nullptr, *cd = nullptr, *nk = nullptr;
+    if (hipMalloc(&k, (size_t)Vp * 8) != hipSuccess || hipMalloc(&e, (size_t)V * 4) != hipSuccess ||
+        hipMalloc(&cd, (size_t)kSampleBlocks * 8) != hipSuccess || hipMalloc(&nk, 64) != hipSuccess) {
+      for (void* q : {k, e, cd, nk})
+        if (q) (void)hipFree(q);
+      return fail(c, CIS2_E_OOM, "sampling scratch");
+    }
+    for (void* q : {k, e, cd, nk}) c->allocs.push_back(q);
+    b.V = V;
+    b.Vp = Vp;
+    b.key = static_cast<uint64_t*>(k);
+    b.e = static_cast<float*>(e);
+    b.cand = static_cast<uint64_t*>(cd);
+    b.nkeep = static_cast<uint32_t*>(nk);
+  }
+  c->samp = SampleParams{sp->seed, T, sp->top_k, P};
+  c->samp_on = true;
+  return CIS2_OK;
+}
+
+int cis2_sample_logits(cis2_ctx* c, const float* logits_host, uint32_t n, const uint32_t* steps,
+                       uint32_t* ids_out, uint32_t* nkeep_out) {
+  if (!c || !logits_host || !steps || !ids_out) return CIS2_E_ARG;
+  if (!c->samp_on) return fail(c, CIS2_E_ARG, "sampling is not enabled (cis2_set_sampling)");
+  if (c->sess.active) return fail(c, CIS2_E_ARG, "a decode session holds the logit buffer");
+  const uint32_t V = c->cfg.vocab;
+  for (uint32_t i = 0; i < n; ++i) {
+    HIPCHK(c, hipMemcpyAsync(c->logits, logits_host + (size_t)i * V, (size_t)V * 4,
+                             hipMemcpyHostToDevice, c->st),
+           "logits upload");
+    LAUNCH(launch_sample(c->logits, V, c->samp, steps[i], c->sbuf, c->d_tok + 1, c->d_err, c->st),
+           "sample");
+    HIPCHK(c, hipMemcpyAsync(&ids_out[i], c->d_tok + 1, 4, hipMemcpyDeviceToHost, c->st), "id copy");
+    if (nkeep_out) {
+      const uint32_t K = (c->samp.top_k > 0 && c->samp.top_k < V) ? c->samp.top_k : V;
+      if (K == V && !(c->samp.top_p < 1.0f))
+        nkeep_out[i] = V;
+      else
+        HIPCHK(c, hipMemcpyAsync(&nkeep_out[i], c->sbuf.nkeep, 4, hipMemcpyDeviceToHost, c->st),
+               "nkeep copy");
+    }
+    HIPCHK(c, hipStreamSynchronize(c->st), "sample sync");
+  }
+  return check_err_flag(c);
+}
+
 // Greedy decode + witness (code/cis2-fp/gpu/cis2_host.cpp:176-218).  The
 // host enqueues step s, then folds step s - (kRing-1) while the GPU runs:
 // argmax and the next token stay on the device, the logits stream to a
@@ -1142,6 +1223,7 @@ int cis2_decode_begin(cis2_ctx* c, uint32_t seq, const uint32_t* prompt, uint32_
   S.w.update(c->table_dig, 32);
   S.w.update(c->invf_dig, 32);
   for (uint32_t i = 0; i < n_prompt; ++i) S.w.update_u32le(prompt[i]);
+  if (c->samp_on) fold_sample_header(S.w, c->samp);
   // Prefill: every prompt position; only the last needs its logits.
   HIPCHK(c, hipMemcpy(c->d_prompt, prompt, (size_t)n_prompt * 4, hipMemcpyHostToDevice),
          "prompt upload");
@@ -1187,8 +1269,12 @@ int cis2_decode_steps(cis2_ctx* c, uint32_t n) {
       r = fold_step(c);
       if (r) return r;
     }
-    // the persistent kernel already left the argmax of these logits in d_tok
-    if (!S.fast) LAUNCH(launch_argmax(c->logits, V, c->d_tok, s), "argmax");
+    // the persistent kernel already left the argmax of these logits in d_tok;
+    // a sampled draw replaces it (generation step = this step's index)
+    if (c->samp_on)
+      LAUNCH(launch_sample(c->logits, V, c->samp, step, c->sbuf, c->d_tok, c->d_err, s), "sample");
+    else if (!S.fast)
+      LAUNCH(launch_argmax(c->logits, V, c->d_tok, s), "argmax");
     HIPCHK(c, hipMemcpyAsync(c->ring + (size_t)slot * V, c->logits, (size_t)V * sizeof(float),
                              hipMemcpyDeviceToHost, s),
            "logits d2h");
@@ -1438,6 +1524,7 @@ int cis2_decode_batch(cis2_ctx* c, uint32_t nseq, const uint32_t* prompts,
                       uint32_t* out_ids, uint8_t* witness, uint8_t* argmax_digest) {
   if (!c || !prompts || !prompt_lens || !hdr || !out_ids || !witness || !argmax_digest)
     return CIS2_E_ARG;
+  if (c->samp_on) return fail(c, CIS2_E_UNSUPPORTED, "the batched decode is greedy only");
   int r = cis2_check_ready(c);
   if (r) return r;
   size_t in_off = 0, out_off = 0;
@@ -1480,6 +1567,7 @@ int cis2_verify_prefill(cis2_ctx* c, uint32_t seq, const uint32_t* prompt, uint3
   if (!c || !prompt || (n_gen && !claimed) || !hdr || (n_gen && !generated) || !witness ||
       !argmax_digest || !first_mismatch)
     return CIS2_E_ARG;
+  if (c->samp_on) return fail(c, CIS2_E_UNSUPPORTED, "the teacher-forced verifier is greedy only");
   if (n_prompt == 0 || seq >= c->cfg.max_seqs) return fail(c, CIS2_E_ARG, "bad prompt or seq");
   if ((uint64_t)n_prompt + n_gen > (uint64_t)c->cfg.max_pos + 1)
     return fail(c, CIS2_E_RANGE, "prompt + claimed tokens exceed max_pos");

@@ -49,7 +49,8 @@ enum {
   CIS2_E_FPENV = -6,           /* device FTZ/DAZ self-test failed            */
   CIS2_E_DEVICE = -7,          /* HIP runtime error                          */
   CIS2_E_OOM = -8,             /* device or pinned host allocation failed    */
-  CIS2_E_RANGE = -9            /* position beyond max_pos / token >= vocab   */
+  CIS2_E_RANGE = -9,           /* position beyond max_pos / token >= vocab   */
+  CIS2_E_NUMERIC = -10         /* NaN logit in a sampled draw                */
 };
 
 typedef struct cis2_ctx cis2_ctx;
@@ -142,6 +143,35 @@ int cis2_decode_begin(cis2_ctx *ctx, uint32_t seq, const uint32_t *prompt, uint3
 int cis2_decode_steps(cis2_ctx *ctx, uint32_t n);
 int cis2_decode_end(cis2_ctx *ctx, uint32_t *out_ids, uint8_t witness[32],
                     uint8_t argmax_digest[32], uint8_t *step_digests);
+
+/* Seeded sampling (CIS-2 v0.4 draft section 14,
+ * code/patches/cis2-spec__seeded-sampling.patch:57-196; the reference
+ * driver's `--sample seed,T,K,P`, labs/w1x-sample/feed/cm-hq__cis2-sample-hq-r2/
+ * job.sh:22-28).  mode 1 replaces the greedy argmax of cis2_decode /
+ * cis2_decode_begin..end by a stateless Gumbel-max draw: s = l / T,
+ * rank-order top-k and top-p, z = s + g(seed, step, index) with
+ * MurmurHash3_x86_32 noise and the pinned ln, first index of max z.  The
+ * witness absorbs "CIS2-SAMPLE-1", seed (u64 LE), T, top_k, top_p (bit
+ * patterns, u32 LE) after the prompt ids; the argmax digest is fed the
+ * drawn ids.  mode 0 (or s == NULL) restores greedy decoding, whose
+ * receipts are unchanged.  Invalid parameters (T not finite or <= 0,
+ * top_p outside (0, 1]) give CIS2_E_ARG.  The batched decode and the
+ * teacher-forced verifier stay greedy (CIS2_E_UNSUPPORTED in mode 1). */
+typedef struct {
+  uint32_t mode;      /* 0 greedy, 1 seeded sampling                   */
+  uint32_t top_k;     /* 0 or >= vocab: disabled                       */
+  uint64_t seed;
+  float temperature;  /* finite, > 0                                   */
+  float top_p;        /* (0, 1]; 1.0: disabled                         */
+} cis2_sampling;
+int cis2_set_sampling(cis2_ctx *ctx, const cis2_sampling *s);
+
+/* The same draw on n host logit rows (vocab floats each) with the
+ * context's sampling parameters, row i at generation step steps[i]:
+ * ids_out[i] = drawn id, nkeep_out[i] (optional) = size of the kept set.
+ * For hosts that hold logits themselves, and for tests. */
+int cis2_sample_logits(cis2_ctx *ctx, const float *logits_host, uint32_t n,
+                       const uint32_t *steps, uint32_t *ids_out, uint32_t *nkeep_out);
 
 /* Batched greedy decode: nseq independent sequences with their own prompts
  * (ragged lengths allowed), each decoded for gen_toks steps.  Groups of up

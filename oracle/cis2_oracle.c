@@ -14,6 +14,7 @@
 #include "cis2_oracle.h"
 
 #include <emmintrin.h>
+#include <math.h>
 #include <pthread.h>
 #include <stdatomic.h>
 #include <stdio.h>
@@ -1074,6 +1075,203 @@ int orc_decode(orc_model *m, const uint32_t *prompt, int n_prompt, int gen_toks,
     if (step_digests) sha_floats(lg, (size_t)c->vocab, step_digests + 32 * (size_t)s);
     out_ids[n_prompt + s] = nid;
     int rc = orc_forward(m, n_prompt + s, nid, lg, cb, user);
+    if (rc) return rc;
+  }
+  sha_final(&w, witness);
+  sha_t a;
+  sha_init(&a);
+  for (int i = 0; i < n_prompt + gen_toks; ++i) sha_u32le(&a, out_ids[i]);
+  sha_final(&a, argmax_digest);
+  return 0;
+}
+
+/* ======================================================================
+ * Seeded sampling, CIS-2 v0.4 draft section 14
+ * (code/patches/cis2-spec__seeded-sampling.patch:57-196).
+ * ====================================================================== */
+
+static uint32_t rotl32(uint32_t x, int r) { return (x << r) | (x >> (32 - r)); }
+
+/* MurmurHash3_x86_32: 4-byte little-endian blocks mixed into h, the tail,
+ * the length, then the fmix32 finaliser (draft 14.2: the public-domain
+ * reference function of that name). */
+uint32_t orc_murmur3_32(const void *key, size_t len, uint32_t seed) {
+  const uint8_t *d = (const uint8_t *)key;
+  const uint32_t c1 = 0xcc9e2d51u, c2 = 0x1b873593u;
+  uint32_t h = seed;
+  const size_t nb = len / 4;
+  for (size_t i = 0; i < nb; ++i) {
+    uint32_t k = (uint32_t)d[4 * i] | ((uint32_t)d[4 * i + 1] << 8) |
+                 ((uint32_t)d[4 * i + 2] << 16) | ((uint32_t)d[4 * i + 3] << 24);
+    k *= c1;
+    k = rotl32(k, 15);
+    k *= c2;
+    h ^= k;
+    h = rotl32(h, 13);
+    h = h * 5u + 0xe6546b64u;
+  }
+  const uint8_t *t = d + 4 * nb;
+  uint32_t k = 0;
+  switch (len & 3) {
+    case 3: k ^= (uint32_t)t[2] << 16; /* fall through */
+    case 2: k ^= (uint32_t)t[1] << 8;  /* fall through */
+    case 1:
+      k ^= t[0];
+      k *= c1;
+      k = rotl32(k, 15);
+      k *= c2;
+      h ^= k;
+  }
+  h ^= (uint32_t)len;
+  h ^= h >> 16;
+  h *= 0x85ebca6bu;
+  h ^= h >> 13;
+  h *= 0xc2b2ae35u;
+  h ^= h >> 16;
+  return h;
+}
+
+/* Draft 14.2: key = seed (u64 LE) || step (u32 LE) || index (u32 LE),
+ * hash seed 0x43495332 ("CIS2"); m = (h >> 9) * 2 + 1 (odd, < 2^24),
+ * u = f32(m) * 2^-24 (both exact); g = 0 - ln(0 - ln(u)) with the pinned
+ * logarithm of section 6.5. */
+void orc_sample_noise(uint64_t seed, uint32_t step, uint32_t index, uint32_t *h,
+                      float *u, float *g) {
+  uint8_t key[16];
+  for (int i = 0; i < 8; ++i) key[i] = (uint8_t)(seed >> (8 * i));
+  for (int i = 0; i < 4; ++i) key[8 + i] = (uint8_t)(step >> (8 * i));
+  for (int i = 0; i < 4; ++i) key[12 + i] = (uint8_t)(index >> (8 * i));
+  const uint32_t hv = orc_murmur3_32(key, 16, 0x43495332u);
+  const uint32_t m = (hv >> 9) * 2u + 1u;
+  const float two_m24 = 5.9604644775390625e-08f; /* 2^-24 */
+  const float uv = (float)m * two_m24;
+  const float inner = 0.0f - orc_ln(uv);
+  const float gv = 0.0f - orc_ln(inner);
+  if (h) *h = hv;
+  if (u) *u = uv;
+  if (g) *g = gv;
+}
+
+/* Draft 14.1: temperature finite and > 0; top_p in (0, 1]. */
+int orc_sample_params_ok(float temperature, uint32_t top_k, float top_p) {
+  (void)top_k;
+  if (!(temperature > 0.0f) || temperature == INFINITY) return -1;
+  if (!(top_p > 0.0f) || !(top_p <= 1.0f)) return -1;
+  return 0;
+}
+
+/* rank order of 14.3 step 2: i precedes j iff s_i > s_j, or s_i == s_j and
+ * i < j (so -0 and +0 tie and fall back to the index) */
+static const float *g_rank_s;
+static int rank_cmp(const void *a, const void *b) {
+  const uint32_t i = *(const uint32_t *)a, j = *(const uint32_t *)b;
+  const float si = g_rank_s[i], sj = g_rank_s[j];
+  if (si > sj) return -1;
+  if (si < sj) return 1;
+  return i < j ? -1 : (i > j ? 1 : 0);
+}
+
+/* Draft 14.3-14.4.  s_i = l_i / T; rank order; top-k keeps ranks < k;
+ * top-p over the kept ranks: m = s of rank 0, e_r = exp(s_r - m),
+ * denom = sum_seq(e) in rank order, p_r = e_r / denom, running c_r =
+ * c_{r-1} + p_r from 0; rank r is kept iff r == 0 or c_{r-1} < top_p.
+ * z_i = s_i + g_i for kept i, -inf otherwise; the first index of the
+ * maximum z (strict > scan from index 0, section 11.2) is drawn. */
+uint32_t orc_sample(const float *logits, int V, uint64_t seed, uint32_t step,
+                    float temperature, uint32_t top_k, float top_p, float *z,
+                    uint32_t *nkeep) {
+  if (V <= 0 || orc_sample_params_ok(temperature, top_k, top_p)) return UINT32_MAX;
+  float *s = (float *)malloc((size_t)V * sizeof(float));
+  uint32_t *ord = (uint32_t *)malloc((size_t)V * sizeof(uint32_t));
+  float *zz = z ? z : (float *)malloc((size_t)V * sizeof(float));
+  uint32_t res = UINT32_MAX;
+  if (!s || !ord || !zz) goto done;
+  for (int i = 0; i < V; ++i) {
+    s[i] = logits[i] / temperature;
+    if (s[i] != s[i]) goto done;
+    ord[i] = (uint32_t)i;
+  }
+  g_rank_s = s;
+  qsort(ord, (size_t)V, sizeof(uint32_t), rank_cmp);
+  uint32_t K = (top_k > 0 && top_k < (uint32_t)V) ? top_k : (uint32_t)V;
+  uint32_t keep = K;
+  if (top_p < 1.0f) {
+    float *e = (float *)malloc((size_t)K * sizeof(float));
+    if (!e) goto done;
+    const float m = s[ord[0]];
+    for (uint32_t r = 0; r < K; ++r) e[r] = orc_exp(s[ord[r]] - m);
+    float den = 0.0f;
+    for (uint32_t r = 0; r < K; ++r) den = den + e[r];
+    float c = 0.0f;
+    for (uint32_t r = 0; r < K; ++r) {
+      if (r > 0 && !(c < top_p)) {
+        keep = r;
+        break;
+      }
+      const float p = e[r] / den;
+      c = c + p;
+    }
+    free(e);
+  }
+  for (int i = 0; i < V; ++i) zz[i] = -INFINITY;
+  for (uint32_t r = 0; r < keep; ++r) {
+    const uint32_t i = ord[r];
+    float g;
+    orc_sample_noise(seed, step, i, NULL, NULL, &g);
+    zz[i] = s[i] + g;
+  }
+  res = orc_argmax(zz, V);
+  if (nkeep) *nkeep = keep;
+done:
+  free(s);
+  free(ord);
+  if (!z) free(zz);
+  return res;
+}
+
+/* Draft 14.5: greedy receipt with, after the prompt ids, "CIS2-SAMPLE-1"
+ * (13 bytes), seed (u64 LE), temperature bits, top_k, top_p bits (u32
+ * LE); per step the logits then the drawn id; the argmax digest is fed the
+ * drawn ids. */
+int orc_decode_sampled(orc_model *m, const uint32_t *prompt, int n_prompt, int gen_toks,
+                       const uint8_t hdr[96], uint64_t seed, float temperature,
+                       uint32_t top_k, float top_p, uint32_t *out_ids, uint8_t witness[32],
+                       uint8_t argmax_digest[32], uint8_t *step_digests) {
+  const orc_config *c = &m->c;
+  if (n_prompt <= 0) return -6;
+  if (n_prompt + gen_toks > c->max_pos) return -3;
+  if (orc_sample_params_ok(temperature, top_k, top_p)) return -1;
+  orc_model_reset(m);
+  sha_t w;
+  sha_init(&w);
+  sha_update(&w, hdr, 96);
+  sha_update(&w, m->table_dig, 32);
+  sha_update(&w, m->invf_dig, 32);
+  for (int i = 0; i < n_prompt; ++i) sha_u32le(&w, prompt[i]);
+  sha_update(&w, "CIS2-SAMPLE-1", 13);
+  sha_u32le(&w, (uint32_t)seed);
+  sha_u32le(&w, (uint32_t)(seed >> 32));
+  uint32_t tb, pb;
+  memcpy(&tb, &temperature, 4);
+  memcpy(&pb, &top_p, 4);
+  sha_u32le(&w, tb);
+  sha_u32le(&w, top_k);
+  sha_u32le(&w, pb);
+  float *lg = m->logits;
+  for (int p = 0; p < n_prompt; ++p) {
+    int rc = orc_forward(m, p, prompt[p], lg, NULL, NULL);
+    if (rc) return rc;
+  }
+  for (int i = 0; i < n_prompt; ++i) out_ids[i] = prompt[i];
+  for (int s = 0; s < gen_toks; ++s) {
+    const uint32_t nid = orc_sample(lg, c->vocab, seed, (uint32_t)s, temperature, top_k, top_p,
+                                    NULL, NULL);
+    if (nid == UINT32_MAX) return -10;
+    sha_update(&w, lg, (size_t)c->vocab * sizeof(float));
+    sha_u32le(&w, nid);
+    if (step_digests) sha_floats(lg, (size_t)c->vocab, step_digests + 32 * (size_t)s);
+    out_ids[n_prompt + s] = nid;
+    int rc = orc_forward(m, n_prompt + s, nid, lg, NULL, NULL);
     if (rc) return rc;
   }
   sha_final(&w, witness);

@@ -120,6 +120,34 @@ int orc_decode(orc_model *m, const uint32_t *prompt, int n_prompt, int gen_toks,
                uint8_t argmax_digest[32], uint8_t *step_digests,
                orc_trace_fn cb, void *user);
 
+/* ---- seeded sampling (CIS-2 v0.4 draft section 14) ------------------
+ * code/patches/cis2-spec__seeded-sampling.patch:57-196
+ * (docs/CIS2_SPEC_v0.4-draft-seeded-sampling.md).  Pinned by the draft's
+ * known answers: MurmurHash3 of the empty key (seeds 0 and 1), the four
+ * (seed, step, index) -> hash, u, g rows of 14.6 and the 14.6 toy vector
+ * (kept set, z bit patterns, next_id); the rank and top-p rules by a
+ * brute-force restatement on small vocabularies (tests/). */
+/* MurmurHash3_x86_32 (Appleby, public domain) of len bytes. */
+uint32_t orc_murmur3_32(const void *key, size_t len, uint32_t seed);
+/* hash, uniform and Gumbel noise of (seed, step, vocab index), 14.2. */
+void orc_sample_noise(uint64_t seed, uint32_t step, uint32_t index, uint32_t *h,
+                      float *u, float *g);
+/* 0 when (temperature, top_k, top_p) are valid (14.1), else -1. */
+int orc_sample_params_ok(float temperature, uint32_t top_k, float top_p);
+/* Next id drawn from V logits at generation step `step` (14.3-14.4).
+ * z (optional, V floats) receives the z values (masked: -inf), nkeep
+ * (optional) the size of the kept set.  Returns UINT32_MAX for invalid
+ * parameters or a NaN among l / temperature. */
+uint32_t orc_sample(const float *logits, int V, uint64_t seed, uint32_t step,
+                    float temperature, uint32_t top_k, float top_p, float *z,
+                    uint32_t *nkeep);
+/* orc_decode with the draw of orc_sample in place of the argmax, and the
+ * section 14.5 receipt header after the prompt ids. */
+int orc_decode_sampled(orc_model *m, const uint32_t *prompt, int n_prompt, int gen_toks,
+                       const uint8_t hdr[96], uint64_t seed, float temperature,
+                       uint32_t top_k, float top_p, uint32_t *out_ids, uint8_t witness[32],
+                       uint8_t argmax_digest[32], uint8_t *step_digests);
+
 #ifdef __cplusplus
 }
 #endif

@@ -69,6 +69,17 @@ def lib():
         L.orc_model_digests.argtypes = [ctypes.c_void_p, c_u8p, c_u8p]
         L.orc_forward.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_uint32, c_fp,
                                   TRACE_FN, ctypes.c_void_p]
+        L.orc_murmur3_32.restype = ctypes.c_uint32
+        L.orc_murmur3_32.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_uint32]
+        L.orc_sample_noise.argtypes = [ctypes.c_uint64, ctypes.c_uint32, ctypes.c_uint32, c_u32p,
+                                       c_fp, c_fp]
+        L.orc_sample_params_ok.argtypes = [ctypes.c_float, ctypes.c_uint32, ctypes.c_float]
+        L.orc_sample.restype = ctypes.c_uint32
+        L.orc_sample.argtypes = [c_fp, ctypes.c_int, ctypes.c_uint64, ctypes.c_uint32,
+                                 ctypes.c_float, ctypes.c_uint32, ctypes.c_float, c_fp, c_u32p]
+        L.orc_decode_sampled.argtypes = [ctypes.c_void_p, c_u32p, ctypes.c_int, ctypes.c_int, c_u8p,
+                                         ctypes.c_uint64, ctypes.c_float, ctypes.c_uint32,
+                                         ctypes.c_float, c_u32p, c_u8p, c_u8p, c_u8p]
         L.orc_decode.argtypes = [ctypes.c_void_p, c_u32p, ctypes.c_int, ctypes.c_int, c_u8p,
                                  c_u32p, c_u8p, c_u8p, c_u8p, TRACE_FN, ctypes.c_void_p]
         L.orc_fpenv_pin.restype = ctypes.c_int
@@ -173,6 +184,22 @@ class OracleModel:
             raise RuntimeError("oracle forward failed (%d)" % rc)
         return logits
 
+    def decode_sampled(self, prompt, gen_toks, seed, temperature, top_k, top_p):
+        """The sampled decode of draft section 14 (orc_decode_sampled)."""
+        prompt = np.ascontiguousarray(prompt, dtype=np.uint32)
+        ids = np.zeros(prompt.size + gen_toks, dtype=np.uint32)
+        wit, adg = (ctypes.c_uint8 * 32)(), (ctypes.c_uint8 * 32)()
+        steps = (ctypes.c_uint8 * (32 * max(gen_toks, 1)))()
+        hdr = (ctypes.c_uint8 * 96).from_buffer_copy(self.hdr)
+        rc = lib().orc_decode_sampled(self.m, ptr(prompt, c_u32p), prompt.size, gen_toks, hdr,
+                                      int(seed), float(np.float32(temperature)), int(top_k),
+                                      float(np.float32(top_p)), ptr(ids, c_u32p), wit, adg, steps)
+        if rc != 0:
+            raise RuntimeError("oracle sampled decode failed (%d)" % rc)
+        sb = bytes(steps)
+        return {"ids": ids, "witness": bytes(wit).hex(), "argmax_digest": bytes(adg).hex(),
+                "step_digests": [sb[32 * i:32 * i + 32].hex() for i in range(gen_toks)]}
+
     def decode(self, prompt, gen_toks, trace=None):
         prompt = np.ascontiguousarray(prompt, dtype=np.uint32)
         ids = np.zeros(prompt.size + gen_toks, dtype=np.uint32)
@@ -192,3 +219,24 @@ class OracleModel:
         sb = bytes(steps)
         return {"ids": ids, "witness": bytes(wit).hex(), "argmax_digest": bytes(adg).hex(),
                 "step_digests": [sb[32 * i:32 * i + 32].hex() for i in range(gen_toks)]}
+
+
+def sample_noise(seed, step, index):
+    """(hash, u, g) of draft 14.2 from the oracle."""
+    h = (ctypes.c_uint32 * 1)()
+    u = (ctypes.c_float * 1)()
+    g = (ctypes.c_float * 1)()
+    lib().orc_sample_noise(int(seed), int(step), int(index), h, u, g)
+    return int(h[0]), float(u[0]), float(g[0])
+
+
+def sample(logits, seed, step, temperature, top_k, top_p):
+    """(next_id, z[V], kept-set size) of draft 14.3-14.4 from the oracle;
+    next_id is None for invalid parameters or NaN scaled logits."""
+    lg = np.ascontiguousarray(logits, dtype=np.float32)
+    z = np.empty(lg.size, dtype=np.float32)
+    nk = (ctypes.c_uint32 * 1)()
+    r = lib().orc_sample(ptr(lg, c_fp), lg.size, int(seed), int(step),
+                         float(np.float32(temperature)), int(top_k), float(np.float32(top_p)),
+                         ptr(z, c_fp), nk)
+    return (None if r == 0xFFFFFFFF else int(r)), z, int(nk[0])
