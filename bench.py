@@ -18,7 +18,8 @@ stream (cis2_profile), summed over the timed steps.  `traffic` is the HBM
 bytes per launch from the committed rocprofv3 counter summary, when present.
 
 Beside the headline line, the same JSON object carries the other
-measured workloads: the strict-order GEMV at 1536x576, one per launch and
+measured workloads: the same decode with seeded sampling in place of the
+argmax (sampled_decode), the strict-order GEMV at 1536x576, one per launch and
 128 per launch (gemv_config1), the batched decode of the batch-stress
 sequences at B = 1, 8, 32, 64 (batch_decode), the llama-160m set of 300
 prompts decoded as one batch (llama160m_set), the Qwen3-0.6B-shape
@@ -223,6 +224,41 @@ def qwen3_long(gen=256, n_prompt=4096, seed=6):
     return rec
 
 
+def sampled_decode(spec, weights, prompt):
+    """Seeded sampling (v0.4 draft section 14) in place of the argmax: the
+    same 32 + 256 workload under the fixture's two parameter sets (the
+    draft's T 0.8 / top-k 40 / top-p 0.95, and top-p 0.95 over the whole
+    vocabulary, which sorts all 49,152 logits and runs two rank-order chains
+    over most of them per step).  tok/s over the 256 steps (prefill
+    excluded); witness and ids against the oracle's fixture."""
+    import struct
+    from cis2amd import Cis2Model
+    fx = os.path.join(ROOT, "tests", "golden", "sample_fixture.json")
+    if not os.path.exists(fx):
+        return None
+    doc = json.load(open(fx))
+    if doc["prompt"] != [int(v) for v in prompt]:
+        return None
+    gen = doc["gen_toks"]
+    m = Cis2Model(spec, weights, max_pos=len(prompt) + gen)
+    out = {}
+    for name, c in doc["cases"].items():
+        T = struct.unpack("<f", struct.pack("<I", c["temperature_bits"]))[0]
+        P = struct.unpack("<f", struct.pack("<I", c["top_p_bits"]))[0]
+        m.set_sampling(c["seed"], T, c["top_k"], P)
+        m.begin(prompt, gen)
+        t = time.perf_counter()
+        m.steps(gen)
+        dt = time.perf_counter() - t
+        r = m.end(gen)
+        out[name] = {"tok_s": round(gen / dt, 1), "top_k": c["top_k"], "top_p": round(P, 6),
+                     "witness_bit_exact": r["witness"] == c["witness"] and
+                     [int(v) for v in r["ids"][len(prompt):]] == c["ids"]}
+        log("sampled decode %s:" % name, out[name])
+    m.close()
+    return out
+
+
 def cpu_baseline_parallel(spec, weights, prompt, seconds=10.0):
     """The oracle with its GEMV rows split over the host cores (same bits:
     rows are independent), forward passes at consecutive positions."""
@@ -331,6 +367,9 @@ def main():
     }
     if roof is not None:
         out["roofline"] = roof
+    sd = sampled_decode(spec, weights, prompt)
+    if sd is not None:
+        out["sampled_decode"] = sd
     if not a.no_roofline:
         out["gemv_config1"] = gemv_roofline()
         log("standalone GEMV 1536x576:", out["gemv_config1"])

@@ -133,72 +133,108 @@ __global__ __launch_bounds__(256) void k_bitonic_pass(uint64_t* key, uint32_t Vp
 // cut; with top_p < 1, m = s of rank 0, e_r = exp(s_r - m), denom =
 // sum_seq(e) in rank order, p_r = e_r / denom, c_r = c_{r-1} + p_r from 0,
 // and the kept ranks end at the first r > 0 with !(c_{r-1} < top_p).
-// The sums are one lane's strict chains; c never decreases (p_r >= 0), so
-// a group of four needs a per-rank test only when its third sum fails.
+// The ranks pass through LDS in tiles of kKeepTile: all threads form a
+// tile's terms, then lane 0 runs the strict chain over it (16 LDS reads in
+// flight).  c never decreases (p_r >= 0), so a group of four needs a
+// per-rank test only when its third sum fails.
+constexpr uint32_t kKeepTile = 8192;
+
 __global__ __launch_bounds__(1024) void k_keep(const uint64_t* __restrict__ key,
                                                const float* __restrict__ l, float T, uint32_t K,
                                                float top_p, float* e, uint32_t* nkeep) {
+  __shared__ __attribute__((aligned(16))) float t[kKeepTile];
   __shared__ float s_den;
+  __shared__ uint32_t s_keep;
   if (!(top_p < 1.0f)) {
     if (threadIdx.x == 0) *nkeep = K;
     return;
   }
   const float m = l[(uint32_t)key[0]] / T;
-  for (uint32_t r = threadIdx.x; r < K; r += blockDim.x) {
-    const float s = l[(uint32_t)key[r]] / T;
-    const float d = s - m;
-    e[r] = exp_pinned(d);
-  }
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    float den = 0.0f;
-    uint32_t r = 0;
-    for (; r + 4 <= K; r += 4) {
-      const float4 v = *reinterpret_cast<const float4*>(e + r);
-      den = den + v.x;
-      den = den + v.y;
-      den = den + v.z;
-      den = den + v.w;
+  const float4* t4 = reinterpret_cast<const float4*>(t);
+  // the denominator
+  float den = 0.0f;
+  for (uint32_t base = 0; base < K; base += kKeepTile) {
+    const uint32_t n = min(kKeepTile, K - base);
+    for (uint32_t j = threadIdx.x; j < n; j += blockDim.x) {
+      const float s = l[(uint32_t)key[base + j]] / T;
+      const float d = s - m;
+      const float ev = exp_pinned(d);
+      t[j] = ev;
+      e[base + j] = ev;
     }
-    for (; r < K; ++r) den = den + e[r];
-    s_den = den;
-  }
-  __syncthreads();
-  const float den = s_den;
-  for (uint32_t r = threadIdx.x; r < K; r += blockDim.x) {
-    const float p = e[r] / den;
-    e[r] = p;
-  }
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    float c = 0.0f;
-    uint32_t keep = K, r = 0;
-    for (; r + 4 <= K; r += 4) {
-      const float4 p = *reinterpret_cast<const float4*>(e + r);
-      const float c0 = c + p.x;
-      const float c1 = c0 + p.y;
-      const float c2 = c1 + p.z;
-      const float c3 = c2 + p.w;
-      if (!(c2 < top_p)) {  // the prefix ends inside ranks r..r+3
-        if (r > 0 && !(c < top_p)) keep = r;
-        else if (!(c0 < top_p)) keep = r + 1;
-        else if (!(c1 < top_p)) keep = r + 2;
-        else keep = r + 3;
-        break;
-      }
-      c = c3;
-    }
-    if (keep == K) {
-      for (; r < K; ++r) {
-        if (r > 0 && !(c < top_p)) {
-          keep = r;
-          break;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      const uint32_t n4 = n / 4;
+      uint32_t g = 0;
+      for (; g + 16 <= n4; g += 16) {
+        float4 v[16];
+#pragma unroll
+        for (uint32_t u = 0; u < 16; ++u) v[u] = t4[g + u];
+#pragma unroll
+        for (uint32_t u = 0; u < 16; ++u) {
+          den = den + v[u].x;
+          den = den + v[u].y;
+          den = den + v[u].z;
+          den = den + v[u].w;
         }
-        c = c + e[r];
       }
+      for (uint32_t r = 4 * g; r < n; ++r) den = den + t[r];
     }
-    *nkeep = keep;
+    __syncthreads();
   }
+  if (threadIdx.x == 0) {
+    s_den = den;
+    s_keep = 0xFFFFFFFFu;
+  }
+  __syncthreads();
+  den = s_den;
+  // the running sum up to the first failing rank
+  float c = 0.0f;
+  for (uint32_t base = 0; base < K; base += kKeepTile) {
+    const uint32_t n = min(kKeepTile, K - base);
+    for (uint32_t j = threadIdx.x; j < n; j += blockDim.x) {
+      const float p = e[base + j] / den;
+      t[j] = p;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      uint32_t keep = 0xFFFFFFFFu;
+      const uint32_t n4 = n / 4;
+      uint32_t g = 0;
+      for (; g < n4 && keep == 0xFFFFFFFFu; g += 16) {
+        float4 v[16];
+#pragma unroll
+        for (uint32_t u = 0; u < 16; ++u)
+          if (g + u < n4) v[u] = t4[g + u];
+#pragma unroll
+        for (uint32_t u = 0; u < 16; ++u) {
+          if (g + u < n4 && keep == 0xFFFFFFFFu) {
+            const uint32_t r = base + 4 * (g + u);
+            const float c0 = c + v[u].x;
+            const float c1 = c0 + v[u].y;
+            const float c2 = c1 + v[u].z;
+            const float c3 = c2 + v[u].w;
+            if (!(c2 < top_p)) {  // the prefix ends inside ranks r..r+3
+              if (r > 0 && !(c < top_p)) keep = r;
+              else if (!(c0 < top_p)) keep = r + 1;
+              else if (!(c1 < top_p)) keep = r + 2;
+              else keep = r + 3;
+            }
+            c = c3;
+          }
+        }
+      }
+      for (uint32_t j = 4 * n4; j < n && keep == 0xFFFFFFFFu; ++j) {
+        const uint32_t r = base + j;
+        if (r > 0 && !(c < top_p)) keep = r;
+        else c = c + t[j];
+      }
+      s_keep = keep;
+    }
+    __syncthreads();
+    if (s_keep != 0xFFFFFFFFu) break;
+  }
+  if (threadIdx.x == 0) *nkeep = s_keep == 0xFFFFFFFFu ? K : s_keep;
 }
 
 // (z, index) candidate packed so that a larger value is the better one:

@@ -192,3 +192,23 @@ def test_cli_sample_flag(tmp_path):
         r = subprocess.run([cli, "--weights-dir", str(tmp_path), "--ids", str(ids), "--sample", bad],
                            capture_output=True, text=True, timeout=60)
         assert r.returncode == 2 and "FATAL: --sample" in r.stderr, bad
+
+
+def test_smollm2_256_sampled_tokens_match_fixture():
+    """The bench workload (SmolLM2-135M shape, 32-token prompt, 256 drawn
+    tokens) under both fixture parameter sets, against the oracle's
+    witnesses (tests/golden/sample_fixture.json)."""
+    import json
+    import os
+    doc = json.load(open(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden",
+                                      "sample_fixture.json")))
+    spec = artifacts.SPECS[doc["spec"]]
+    w = artifacts.Weights(spec, doc["weights_seed"])
+    prompt = np.array(doc["prompt"], dtype=np.uint32)
+    m = Cis2Model(spec, w, max_pos=prompt.size + doc["gen_toks"])
+    for name, c in doc["cases"].items():
+        m.set_sampling(c["seed"], f32(c["temperature_bits"]), c["top_k"], f32(c["top_p_bits"]))
+        r = m.decode(prompt, doc["gen_toks"])
+        assert r["witness"] == c["witness"], name
+        assert [int(v) for v in r["ids"][prompt.size:]] == c["ids"], name
+    m.close()
