@@ -202,6 +202,92 @@ struct SafeTensors {
   }
 };
 
+// ---- architecture gate on config.json alone (code/cis2-fp/src/main.rs:545-644) ----
+// Refuses by name every configuration outside the specified subset, so that
+// no digest is ever printed for arithmetic this build does not implement.
+// Returns the refusal reason, or "" to accept.  Same checks, order and
+// messages as the reference's gate, with one extension: model_type "qwen3"
+// (the archived Qwen3 port, labs/w1x-qwen3/scripts/qwen3-port.diff, which
+// reads head_dim from the config and applies the per-head QK-norm) is in
+// the subset, and for it an explicit head_dim is honoured instead of
+// refused.
+inline std::string json_debug_str(const std::string& v) {  // Rust {:?} of a &str
+  std::string o = "\"";
+  for (char ch : v) {
+    if (ch == '"' || ch == '\\') o.push_back('\\');
+    o.push_back(ch);
+  }
+  return o + "\"";
+}
+inline bool json_u64(const JValue* v, uint64_t* out) {  // serde as_u64
+  if (!v || v->kind != JValue::NUM || !(v->num >= 0.0) || v->num > 18446744073709549568.0 ||
+      v->num != (double)(uint64_t)v->num)
+    return false;
+  *out = (uint64_t)v->num;
+  return true;
+}
+inline std::string json_f64_display(double x) {  // Rust Display of an f64 (shortest round trip)
+  char b[64];
+  for (int prec = 1; prec <= 17; ++prec) {
+    snprintf(b, sizeof b, "%.*g", prec, x);
+    if (strtod(b, nullptr) == x) break;
+  }
+  return b;
+}
+inline std::string gate_architecture(const JValue& c) {
+  auto present = [&](const char* k) {
+    const JValue* v = c.find(k);
+    return v && v->kind != JValue::NUL;
+  };
+  std::string mt;
+  if (const JValue* v = c.find("model_type"); v && v->kind == JValue::STR) {
+    mt = v->str;
+    if (mt != "llama" && mt != "qwen2" && mt != "qwen3")
+      return "model_type=" + json_debug_str(mt) +
+             " is not in the CIS-2 specified subset [\"llama\", \"qwen2\", \"qwen3\"]";
+  }
+  if (const JValue* v = c.find("torch_dtype"); v && v->kind == JValue::STR && v->str != "bfloat16")
+    return "torch_dtype=" + json_debug_str(v->str) +
+           "; CIS-2 pins bf16-on-disk weights (\xc2\xa7" "3.5)";
+  uint64_t h = 0, nh = 0;
+  if (json_u64(c.find("hidden_size"), &h) && json_u64(c.find("num_attention_heads"), &nh)) {
+    if (nh == 0) return "num_attention_heads=0";
+    const uint64_t derived = h / nh;
+    uint64_t used = derived, explicit_hd = 0;
+    if (json_u64(c.find("head_dim"), &explicit_hd)) {
+      if (mt == "qwen3") {
+        used = explicit_hd;
+      } else if (explicit_hd != derived) {
+        return "config declares head_dim=" + std::to_string(explicit_hd) +
+               " but this implementation derives hidden_size/num_attention_heads=" +
+               std::to_string(derived) +
+               "; the decode path uses the derived value, so the explicit one would be "
+               "silently ignored";
+      }
+    }
+    if (used % 2 != 0)
+      return (used == derived ? "derived head_dim=" : "head_dim=") + std::to_string(used) +
+             " is odd; RoPE pairs require even";
+  }
+  if (const JValue* v = c.find("partial_rotary_factor"); v && v->kind == JValue::NUM && v->num != 1.0)
+    return "partial_rotary_factor=" + json_f64_display(v->num) + "; only full rotary is specified";
+  if (present("rope_scaling")) return "rope_scaling is set; only unscaled RoPE is specified";
+  if (const JValue* v = c.find("use_sliding_window"); v && v->kind == JValue::BOOL && v->b)
+    return "use_sliding_window=true; only full causal attention is specified";
+  if (present("quantization_config"))
+    return "quantization_config is present; CIS-2 reads unquantized bf16 weights";
+  for (const char* k : {"attention_multiplier", "embedding_multiplier", "residual_multiplier",
+                        "logits_scaling", "attn_logit_softcapping", "final_logit_softcapping",
+                        "query_pre_attn_scalar"})
+    if (present(k))
+      return std::string(k) +
+             " is set; this implementation hardcodes rsqrt(head_dim) attention scaling and no "
+             "logit scaling, so the result would be silently wrong";
+  for (const char* k : {"num_local_experts", "num_experts", "n_routed_experts", "moe_intermediate_size"})
+    if (present(k)) return std::string(k) + " is set; MoE routing is not specified";
+  return "";
+}
+
 // ---- --ids file: decimal ids separated by whitespace or commas ------------------
 inline std::vector<uint32_t> read_ids(const std::string& path) {
   std::string t = read_file(path);

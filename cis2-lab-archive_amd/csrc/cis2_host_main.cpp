@@ -134,12 +134,20 @@ int main(int argc, char** argv) {
   const std::string wpath = weights_dir + "/model.safetensors";
   const std::string tpath = weights_dir + "/tokenizer.json";
   const std::string cpath = weights_dir + "/config.json";
+  JValue cfgj = parse_json(read_file(cpath));
+  // scope gate on config.json alone, before any weights are opened or hashed
+  // (code/cis2-fp/src/main.rs:817-823)
+  const std::string reason = gate_architecture(cfgj);
+  if (!reason.empty()) {
+    fprintf(stderr, "CIS2_REF_UNSUPPORTED reason=%s\n", reason.c_str());
+    fprintf(stderr, "This checkpoint is outside the CIS-2 specified subset; no digest emitted.\n");
+    return 2;
+  }
   uint8_t hdr[96];
   file_sha(wpath, hdr);
   file_sha(tpath, hdr + 32);
   file_sha(cpath, hdr + 64);
 
-  JValue cfgj = parse_json(read_file(cpath));
   cis2_config cfg;
   memset(&cfg, 0, sizeof cfg);
   cfg.hidden = num_key(cfgj, "hidden_size");
