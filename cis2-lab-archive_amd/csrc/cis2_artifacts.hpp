@@ -9,6 +9,8 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <algorithm>
+#include <set>
 #include <string>
 #include <utility>
 #include <vector>
@@ -39,9 +41,13 @@ struct JValue {
 class JParser {
  public:
   JParser(const char* b, const char* e) : p_(b), e_(e) {}
-  JValue value() {
+  // Nesting deeper than this is refused (a header is two levels deep; an
+  // unbounded recursion would let a crafted file overflow the stack).
+  static constexpr int kMaxDepth = 64;
+  JValue value(int depth = 0) {
     skip();
     if (p_ >= e_) fatal("JSON parse error: unexpected end");
+    if (depth > kMaxDepth) fatal("JSON parse error: nesting too deep");
     JValue v;
     char ch = *p_;
     if (ch == '{') {
@@ -49,13 +55,15 @@ class JParser {
       ++p_;
       skip();
       if (p_ < e_ && *p_ == '}') { ++p_; return v; }
+      std::set<std::string> seen;
       while (true) {
         skip();
         std::string k = string();
+        if (!seen.insert(k).second) fatal("JSON parse error: duplicate key " + k);
         skip();
         if (p_ >= e_ || *p_ != ':') fatal("JSON parse error: expected ':'");
         ++p_;
-        v.obj.emplace_back(std::move(k), value());
+        v.obj.emplace_back(std::move(k), value(depth + 1));
         skip();
         if (p_ < e_ && *p_ == ',') { ++p_; continue; }
         if (p_ < e_ && *p_ == '}') { ++p_; return v; }
@@ -68,7 +76,7 @@ class JParser {
       skip();
       if (p_ < e_ && *p_ == ']') { ++p_; return v; }
       while (true) {
-        v.arr.push_back(value());
+        v.arr.push_back(value(depth + 1));
         skip();
         if (p_ < e_ && *p_ == ',') { ++p_; continue; }
         if (p_ < e_ && *p_ == ']') { ++p_; return v; }
@@ -80,7 +88,7 @@ class JParser {
     if (lit("false")) { v.kind = JValue::BOOL; v.b = false; return v; }
     if (lit("null")) return v;
     std::string num;
-    while (p_ < e_ && strchr("+-0123456789.eE", *p_)) num.push_back(*p_++);
+    while (p_ < e_ && *p_ && strchr("+-0123456789.eE", *p_)) num.push_back(*p_++);
     if (num.empty()) fatal("JSON parse error: expected a value");
     char* stop = nullptr;
     v.kind = JValue::NUM;
@@ -159,6 +167,30 @@ struct SafeTensors {
   uint64_t data_off = 0;
   std::vector<TensorView> tensors;
 
+  // Element size of a safetensors dtype, 0 when unknown.
+  static uint64_t dtype_size(const std::string& d) {
+    if (d == "BOOL" || d == "U8" || d == "I8" || d == "F8_E5M2" || d == "F8_E4M3") return 1;
+    if (d == "I16" || d == "U16" || d == "F16" || d == "BF16") return 2;
+    if (d == "I32" || d == "U32" || d == "F32") return 4;
+    if (d == "I64" || d == "U64" || d == "F64") return 8;
+    return 0;
+  }
+  // A JSON number that is an exact non-negative integer below 2^53.
+  static bool as_index(const JValue& v, uint64_t* out) {
+    if (v.kind != JValue::NUM || !(v.num >= 0.0) || v.num >= 9007199254740992.0 ||
+        v.num != (double)(uint64_t)v.num)
+      return false;
+    *out = (uint64_t)v.num;
+    return true;
+  }
+
+  // Reads the file and checks the whole header before any tensor is used:
+  // header length within the file, a JSON object without duplicate keys,
+  // every entry with a known dtype, integer shape and offsets, shape
+  // product (no overflow) x element size == end - begin, every range inside
+  // the data section and no two ranges overlapping.  Any violation is
+  // fatal: a file whose declared sizes disagree with its length is never
+  // accepted.
   void open(const std::string& path) {
     blob = read_file(path);
     if (blob.size() < 8) fatal("safetensors too short");
@@ -168,19 +200,44 @@ struct SafeTensors {
     JValue j = parse_json(blob.substr(8, hlen));
     if (j.kind != JValue::OBJ) fatal("safetensors header not an object");
     data_off = 8 + hlen;
+    const uint64_t data_len = blob.size() - data_off;
     for (auto& kv : j.obj) {
-      if (kv.first == "__metadata__") continue;
+      if (kv.first == "__metadata__") {
+        if (kv.second.kind != JValue::OBJ) fatal("safetensors __metadata__ not an object");
+        continue;
+      }
+      const std::string& n = kv.first;
       const JValue *dt = kv.second.find("dtype"), *sh = kv.second.find("shape"),
                    *of = kv.second.find("data_offsets");
-      if (!dt || !sh || !of || of->arr.size() != 2) continue;
+      if (kv.second.kind != JValue::OBJ || !dt || dt->kind != JValue::STR || !sh ||
+          sh->kind != JValue::ARR || !of || of->kind != JValue::ARR || of->arr.size() != 2)
+        fatal("tensor " + n + " entry malformed");
       TensorView t;
-      t.name = kv.first;
+      t.name = n;
       t.dtype = dt->str;
-      for (auto& d : sh->arr) t.shape.push_back((uint64_t)d.num);
-      t.begin = (uint64_t)of->arr[0].num;
-      t.end = (uint64_t)of->arr[1].num;
+      const uint64_t esz = dtype_size(t.dtype);
+      if (!esz) fatal("tensor " + n + " unknown dtype " + t.dtype);
+      uint64_t count = 1;
+      for (auto& d : sh->arr) {
+        uint64_t v = 0;
+        if (!as_index(d, &v)) fatal("tensor " + n + " shape not a list of integers");
+        if (v && count > UINT64_MAX / v) fatal("tensor " + n + " shape product overflows");
+        count *= v;
+        t.shape.push_back(v);
+      }
+      if (!as_index(of->arr[0], &t.begin) || !as_index(of->arr[1], &t.end) || t.end < t.begin ||
+          t.end > data_len)
+        fatal("tensor " + n + " byte range invalid");
+      if (count > UINT64_MAX / esz || count * esz != t.end - t.begin)
+        fatal("tensor " + n + " element count mismatch");
       tensors.push_back(t);
     }
+    std::vector<std::pair<uint64_t, uint64_t>> r;
+    for (auto& t : tensors)
+      if (t.end > t.begin) r.emplace_back(t.begin, t.end);
+    std::sort(r.begin(), r.end());
+    for (size_t i = 1; i < r.size(); ++i)
+      if (r[i].first < r[i - 1].second) fatal("safetensors tensor byte ranges overlap");
   }
   const TensorView* find(const std::string& n) const {
     for (auto& t : tensors)
@@ -294,7 +351,7 @@ inline std::vector<uint32_t> read_ids(const std::string& path) {
   std::vector<uint32_t> ids;
   size_t i = 0;
   while (i < t.size()) {
-    while (i < t.size() && strchr("\n\r \t,", t[i])) ++i;
+    while (i < t.size() && t[i] && strchr("\n\r \t,", t[i])) ++i;
     if (i >= t.size()) break;
     size_t j = i;
     while (j < t.size() && t[j] >= '0' && t[j] <= '9') ++j;

@@ -173,21 +173,21 @@ int main(int argc, char** argv) {
   cfg.max_seqs = 1;
   cfg.reduction_mode = reduction;
 
-  cis2_ctx* ctx = nullptr;
-  int rc = cis2_ctx_create(&cfg, &ctx);
-  if (rc) fatal(std::string("cis2_ctx_create: ") + cis2_strerror(rc));
-  if (samp.mode) {
-    rc = cis2_set_sampling(ctx, &samp);
-    if (rc) fatal(std::string("--sample: ") + cis2_last_error(ctx));
-  }
-
+  // Every tensor is checked (presence, dtype, shape, byte range) before the
+  // device is touched, so a bad file fails fast and identically everywhere.
   fprintf(stderr, "loading + widening weights (bf16 -> fp32, exact bit-shift)...\n");
   SafeTensors st;
   st.open(wpath);
   const uint64_t H = cfg.hidden, I = cfg.inter, V = cfg.vocab;
   const uint64_t QD = (uint64_t)cfg.n_heads * cfg.head_dim,
                  KV = (uint64_t)cfg.n_kv_heads * cfg.head_dim, HD = cfg.head_dim;
-  auto load = [&](const std::string& name, std::vector<uint64_t> shape, bool optional) {
+  struct Up {
+    std::string name;
+    const uint16_t* p;
+    uint64_t n;
+  };
+  std::vector<Up> ups;
+  auto need = [&](const std::string& name, std::vector<uint64_t> shape, bool optional) {
     const TensorView* t = st.find(name);
     if (!t) {
       if (optional) return;
@@ -196,29 +196,40 @@ int main(int argc, char** argv) {
     const uint16_t* p = st.bf16(*t, shape);
     uint64_t n = 1;
     for (auto d : shape) n *= d;
-    int r = cis2_upload_bf16(ctx, name.c_str(), p, n);
-    if (r) fatal("upload " + name + ": " + cis2_last_error(ctx));
+    ups.push_back(Up{name, p, n});
   };
-  load("model.embed_tokens.weight", {V, H}, false);
+  need("model.embed_tokens.weight", {V, H}, false);
   for (uint32_t l = 0; l < cfg.n_layers; ++l) {
     std::string p = "model.layers." + std::to_string(l) + ".";
-    load(p + "input_layernorm.weight", {H}, false);
-    load(p + "post_attention_layernorm.weight", {H}, false);
-    load(p + "self_attn.q_proj.weight", {QD, H}, false);
-    load(p + "self_attn.k_proj.weight", {KV, H}, false);
-    load(p + "self_attn.v_proj.weight", {KV, H}, false);
-    load(p + "self_attn.o_proj.weight", {H, QD}, false);
-    load(p + "mlp.gate_proj.weight", {I, H}, false);
-    load(p + "mlp.up_proj.weight", {I, H}, false);
-    load(p + "mlp.down_proj.weight", {H, I}, false);
-    load(p + "self_attn.q_proj.bias", {QD}, true);
-    load(p + "self_attn.k_proj.bias", {KV}, true);
-    load(p + "self_attn.v_proj.bias", {KV}, true);
-    load(p + "self_attn.q_norm.weight", {HD}, true);
-    load(p + "self_attn.k_norm.weight", {HD}, true);
+    need(p + "input_layernorm.weight", {H}, false);
+    need(p + "post_attention_layernorm.weight", {H}, false);
+    need(p + "self_attn.q_proj.weight", {QD, H}, false);
+    need(p + "self_attn.k_proj.weight", {KV, H}, false);
+    need(p + "self_attn.v_proj.weight", {KV, H}, false);
+    need(p + "self_attn.o_proj.weight", {H, QD}, false);
+    need(p + "mlp.gate_proj.weight", {I, H}, false);
+    need(p + "mlp.up_proj.weight", {I, H}, false);
+    need(p + "mlp.down_proj.weight", {H, I}, false);
+    need(p + "self_attn.q_proj.bias", {QD}, true);
+    need(p + "self_attn.k_proj.bias", {KV}, true);
+    need(p + "self_attn.v_proj.bias", {KV}, true);
+    need(p + "self_attn.q_norm.weight", {HD}, true);
+    need(p + "self_attn.k_norm.weight", {HD}, true);
   }
-  load("model.norm.weight", {H}, false);
-  if (!cfg.tied) load("lm_head.weight", {V, H}, false);
+  need("model.norm.weight", {H}, false);
+  if (!cfg.tied) need("lm_head.weight", {V, H}, false);
+
+  cis2_ctx* ctx = nullptr;
+  int rc = cis2_ctx_create(&cfg, &ctx);
+  if (rc) fatal(std::string("cis2_ctx_create: ") + cis2_strerror(rc));
+  if (samp.mode) {
+    rc = cis2_set_sampling(ctx, &samp);
+    if (rc) fatal(std::string("--sample: ") + cis2_last_error(ctx));
+  }
+  for (const Up& u : ups) {
+    rc = cis2_upload_bf16(ctx, u.name.c_str(), u.p, u.n);
+    if (rc) fatal("upload " + u.name + ": " + cis2_last_error(ctx));
+  }
   st.blob.clear();
   st.blob.shrink_to_fit();
   rc = cis2_check_ready(ctx);
