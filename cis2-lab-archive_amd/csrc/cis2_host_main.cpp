@@ -103,6 +103,15 @@ int main(int argc, char** argv) {
   // driver's flag, labs/w1x-sample/feed/cm-hq__cis2-sample-hq-r2/job.sh:22-28)
   cis2_sampling samp;
   memset(&samp, 0, sizeof samp);
+  // cis2-verify2 line protocol (code/cis2-fp/verify2/src/main.rs:353-500, parsed
+  // by code/cis2-llm/server/app/runner.py:25-31): --verify2, or this binary
+  // invoked under the name cis2-verify2
+  bool verify2 = false;
+  {
+    std::string a0 = argv[0];
+    const size_t sl = a0.rfind('/');
+    verify2 = (sl == std::string::npos ? a0 : a0.substr(sl + 1)) == "cis2-verify2";
+  }
   for (int i = 1; i < argc; ++i) {
     std::string a = argv[i];
     if (a == "--weights-dir" && i + 1 < argc) weights_dir = argv[++i];
@@ -120,6 +129,7 @@ int main(int argc, char** argv) {
         return 2;
       }
     }
+    else if (a == "--verify2") verify2 = true;
     else if (a == "--sample" && i + 1 < argc) {
       if (!parse_sample(argv[++i], &samp)) {
         fprintf(stderr, "FATAL: --sample: expected SEED,T,K,P with T finite > 0 and P in (0,1], "
@@ -129,7 +139,7 @@ int main(int argc, char** argv) {
     }
     else { fprintf(stderr, "FATAL: unknown CLI argument: %s\n", a.c_str()); return 2; }
   }
-  if (ids_path.empty()) fatal("--ids FILE is required");
+  if (ids_path.empty() && !verify2) fatal("--ids FILE is required");
   if (gen_toks < 0) fatal("--gen-toks must be >= 0");
   const std::string wpath = weights_dir + "/model.safetensors";
   const std::string tpath = weights_dir + "/tokenizer.json";
@@ -168,7 +178,10 @@ int main(int argc, char** argv) {
   cfg.tied = 1;
   if (const JValue* t = cfgj.find("tie_word_embeddings"))
     cfg.tied = (t->kind == JValue::BOOL) ? (t->b ? 1 : 0) : 1;
-  std::vector<uint32_t> prompt = read_ids(ids_path);
+  // verify2 without --ids: the section 13.1 prompt, "Once upon a time" under
+  // the SmolLM2 tokenizer (verify2/src/main.rs:436-444)
+  std::vector<uint32_t> prompt =
+      ids_path.empty() ? std::vector<uint32_t>{6403, 1980, 253, 655} : read_ids(ids_path);
   cfg.max_pos = (uint32_t)(prompt.size() + gen_toks);
   cfg.max_seqs = 1;
   cfg.reduction_mode = reduction;
@@ -250,6 +263,29 @@ int main(int argc, char** argv) {
                    ids.data(), wit, adig, nullptr);
   if (rc) fatal(std::string("decode: ") + cis2_last_error(ctx));
   if (sink.fp) fclose(sink.fp);
+  if (verify2) {
+    // section 12.4: the whole decode twice in one process, identical results
+    // (verify2/src/main.rs:446-477), then the verifier's five lines
+    std::vector<uint32_t> ids2(ids.size());
+    uint8_t wit2[32], adig2[32];
+    rc = cis2_decode(ctx, 0, prompt.data(), (uint32_t)prompt.size(), (uint32_t)gen_toks, hdr,
+                     ids2.data(), wit2, adig2, nullptr);
+    if (rc) fatal(std::string("decode: ") + cis2_last_error(ctx));
+    if (memcmp(wit, wit2, 32)) fatal("section 12.4: witness digest differs across same-process runs");
+    if (memcmp(adig, adig2, 32)) fatal("section 12.4: argmax digest differs across same-process runs");
+    if (ids != ids2) fatal("section 12.4: generated token ids differ across same-process runs");
+    uint8_t table[32], invf[32];
+    cis2_digests(ctx, table, invf);
+    printf("CIS2_VERIFY2 digest=%s prompt_toks=%zu gen_toks=%d dtype=fp32\n", hex(wit, 32).c_str(),
+           prompt.size(), gen_toks);
+    printf("argmax_digest=%s\n", hex(adig, 32).c_str());
+    printf("table_digest=%s\n", hex(table, 32).c_str());
+    printf("inv_freq table_digest=%s\n", hex(invf, 32).c_str());
+    std::vector<uint32_t> gen(ids.begin() + prompt.size(), ids.end());
+    printf("generated_token_ids=%s\n", ids_list(gen).c_str());
+    cis2_ctx_destroy(ctx);
+    return 0;
+  }
   for (int s = 0; s < gen_toks; ++s)
     fprintf(stderr, "[run1] step %d: token_id=%u\n", s, ids[prompt.size() + s]);
   if (samp.mode)  // the sampled ids, one line per step (what the lab's ids16 hash reads)

@@ -51,3 +51,43 @@ def test_cli_missing_tensor_exits_2(model_fixtures, tmp_path):
     r = subprocess.run([CLI, "--weights-dir", str(tmp_path), "--ids", str(ids)],
                        capture_output=True, text=True, timeout=120)
     assert r.returncode == 2 and "FATAL: tensor model.norm.weight missing" in r.stderr
+
+
+def test_verify2_line_protocol(tmp_path):
+    """`cis2-verify2` (the same driver under the verifier's name, no
+    arguments, weights/ in the working directory) runs the section 13.1
+    prompt (6403, 1980, 253, 655) for 16 tokens twice and prints the five
+    lines the service's runner parses (code/cis2-llm/server/app/runner.py:
+    25-31; verify2/src/main.rs:479-500), with the oracle's digests."""
+    import _oracle as O
+    spec = artifacts.SPECS["smollm2-135m"]
+    w = artifacts.Weights(spec, 20261201)
+    (tmp_path / "weights").mkdir()
+    w.write_dir(str(tmp_path / "weights"))
+    v2 = os.path.join(ROOT, "cis2-lab-archive_amd", "bin", "cis2-verify2")
+    r = subprocess.run([v2], cwd=str(tmp_path), capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stderr[-2000:]
+    pats = {
+        "witness_digest": re.compile(r"^CIS2_VERIFY2 digest=([0-9a-f]+)"),
+        "argmax_digest": re.compile(r"^argmax_digest=([0-9a-f]+)"),
+        "table_digest": re.compile(r"^table_digest=([0-9a-f]+)"),
+        "inv_freq_table_digest": re.compile(r"^inv_freq table_digest=([0-9a-f]+)"),
+        "generated_token_ids": re.compile(r"^generated_token_ids=\[([0-9, ]+)\]"),
+    }
+    got = {}
+    for line in r.stdout.splitlines():
+        for k, p in pats.items():
+            m = p.match(line)
+            if m:
+                got[k] = m.group(1)
+    assert set(got) == set(pats), r.stdout
+    assert len(r.stdout.splitlines()) == 5
+    prompt = [6403, 1980, 253, 655]
+    o = O.OracleModel(spec, w, max_pos=4 + 16)
+    want = o.decode(prompt, 16)
+    t, f = o.digests()
+    assert got["witness_digest"] == want["witness"]
+    assert got["argmax_digest"] == want["argmax_digest"]
+    assert got["table_digest"] == t and got["inv_freq_table_digest"] == f
+    assert [int(x) for x in got["generated_token_ids"].split(",")] == [int(v) for v in want["ids"][4:]]
+    assert r.stdout.splitlines()[0].endswith(" prompt_toks=4 gen_toks=16 dtype=fp32")
