@@ -19,7 +19,8 @@ bytes per launch from the committed rocprofv3 counter summary, when present.
 
 Beside the headline line, the same JSON object carries the other
 measured workloads: the same decode with seeded sampling in place of the
-argmax (sampled_decode), the strict-order GEMV at 1536x576, one per launch and
+argmax (sampled_decode) and in the v0.4-candidate tree order (tree_decode),
+the strict-order GEMV at 1536x576, one per launch and
 128 per launch (gemv_config1), the batched decode of the batch-stress
 sequences at B = 1, 8, 32, 64 (batch_decode), the llama-160m set of 300
 prompts decoded as one batch (llama160m_set), the Qwen3-0.6B-shape
@@ -259,6 +260,30 @@ def sampled_decode(spec, weights, prompt):
     return out
 
 
+def tree_decode(spec, weights, prompt, gen=256):
+    """The same greedy workload in the v0.4-candidate tree reduction order
+    (reduction_mode 1, the reference's -DCIS2_REDUCTION_TREE build): tok/s
+    over steps 17..256 and the witness against the reference driver's
+    tree-order fixture."""
+    from cis2amd import Cis2Model
+    m = Cis2Model(spec, weights, max_pos=len(prompt) + gen, reduction_mode=1)
+    m.begin(prompt, gen)
+    m.steps(16)
+    t = time.perf_counter()
+    m.steps(gen - 16)
+    dt = time.perf_counter() - t
+    r = m.end(gen)
+    m.close()
+    rec = {"tok_s": round((gen - 16) / dt, 1), "witness": r["witness"]}
+    fx = os.path.join(ROOT, "tests", "golden", "model_fixtures.json")
+    if os.path.exists(fx):
+        ref = json.load(open(fx)).get("smollm2-135m-tree")
+        if ref and list(ref["prompt"]) == [int(v) for v in prompt] and ref["gen_toks"] == gen:
+            rec["witness_bit_exact"] = r["witness"] == ref["witness"]
+    log("tree-order decode:", rec)
+    return rec
+
+
 def cpu_baseline_parallel(spec, weights, prompt, seconds=10.0):
     """The oracle with its GEMV rows split over the host cores (same bits:
     rows are independent), forward passes at consecutive positions."""
@@ -370,6 +395,7 @@ def main():
     sd = sampled_decode(spec, weights, prompt)
     if sd is not None:
         out["sampled_decode"] = sd
+    out["tree_decode"] = tree_decode(spec, weights, prompt)
     if not a.no_roofline:
         out["gemv_config1"] = gemv_roofline()
         log("standalone GEMV 1536x576:", out["gemv_config1"])

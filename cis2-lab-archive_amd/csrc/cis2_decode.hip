@@ -1773,7 +1773,12 @@ hipError_t launch_decode_t(const DecodeArgs& a, hipStream_t s) {
 }
 
 hipError_t launch_decode(const DecodeArgs& a, hipStream_t s) {
-  if (a.tree) return launch_decode_t<true, 0>(a, s);
+  if (a.tree) {  // the v0.4-candidate order, with the same compile-time shapes
+    if (shape_matches(a, kShapes[1])) return launch_decode_t<true, 1>(a, s);
+    if (shape_matches(a, kShapes[2])) return launch_decode_t<true, 2>(a, s);
+    if (shape_matches(a, kShapes[3])) return launch_decode_t<true, 3>(a, s);
+    return launch_decode_t<true, 0>(a, s);
+  }
   if (shape_matches(a, kShapes[1])) return launch_decode_t<false, 1>(a, s);
   if (shape_matches(a, kShapes[2])) return launch_decode_t<false, 2>(a, s);
   if (shape_matches(a, kShapes[3])) return launch_decode_t<false, 3>(a, s);
