@@ -106,6 +106,11 @@ struct cis2_ctx {
         *att = nullptr, *o = nullptr, *g = nullptr, *u = nullptr, *hid = nullptr,
         *dn = nullptr, *logits = nullptr, *scores = nullptr, *probs = nullptr;
   uint32_t* d_tok = nullptr;     // [2]: input token of the current step, argmax out
+  // second token slot and logit buffer of the decode session's alternating
+  // steps (step s reads logits / token set s % 2 while the next pass writes
+  // the other set)
+  uint32_t* d_tok2 = nullptr;
+  float* logits2 = nullptr;
   uint32_t* d_err = nullptr;
   uint32_t* d_prompt = nullptr;  // [max_pos]: prompt ids of the sequence being prefilled
   std::map<std::string, Slot> slots;
@@ -118,6 +123,7 @@ struct cis2_ctx {
   float* ring = nullptr;
   uint32_t* ring_tok = nullptr;
   hipEvent_t ring_ev[kRing];
+  hipEvent_t ring_ready[kRing];  // main stream: step's logits and token final
   Session sess;
   // persistent decode kernel state
   uint32_t Rq = 0, Ro = 0, Rg = 0, Rd = 0, Rl = 0;
@@ -364,7 +370,8 @@ int prepare_fast(cis2_ctx* c) {
 
 // One position through the persistent kernel; the token is read from
 // *tokp on the device and the argmax is written to c->d_tok[0].
-int forward_fast(cis2_ctx* c, uint32_t seq, uint32_t pos, uint32_t* tokp, bool want_logits) {
+int forward_fast(cis2_ctx* c, uint32_t seq, uint32_t pos, uint32_t* tokp, bool want_logits,
+                 float* logits_out = nullptr, uint32_t* tok_out = nullptr) {
   int r = prepare_fast(c);
   if (r) return r;
   DecodeArgs& a = c->dargs;
@@ -372,7 +379,8 @@ int forward_fast(cis2_ctx* c, uint32_t seq, uint32_t pos, uint32_t* tokp, bool w
   a.kc0 = c->kv + (size_t)seq * c->cfg.n_layers * per_layer;
   a.vc0 = a.kc0 + (size_t)c->kvd * c->cfg.max_pos;
   a.tok_in = tokp;
-  a.tok_out = c->d_tok;
+  a.tok_out = tok_out ? tok_out : c->d_tok;
+  a.logits = logits_out ? logits_out : c->logits;
   a.pos = pos;
   if (c->epoch == UINT32_MAX) {  // tags would repeat: clear them and restart at 1
     HIPCHK(c, hipMemsetAsync(c->act, 0,
@@ -744,8 +752,10 @@ void cis2_ctx_destroy(cis2_ctx* c) {
     if (e) (void)hipEventDestroy(e);
   if (c->ring) (void)hipHostFree(c->ring);
   if (c->ring_tok) (void)hipHostFree(c->ring_tok);
-  for (int i = 0; i < kRing; ++i)
+  for (int i = 0; i < kRing; ++i) {
     if (c->ring_ev[i]) (void)hipEventDestroy(c->ring_ev[i]);
+    if (c->ring_ready[i]) (void)hipEventDestroy(c->ring_ready[i]);
+  }
   if (c->cs) {
     (void)hipStreamSynchronize(c->cs);
     (void)hipStreamDestroy(c->cs);
@@ -810,6 +820,11 @@ int cis2_ctx_create(const cis2_config* cfg, cis2_ctx** out) {
   c->d_tok = static_cast<uint32_t*>(tp);
   c->d_err = c->d_tok + 2;
   (void)hipMemset(tp, 0, 16);
+  if (hipMalloc(&tp, 16) != hipSuccess) { cis2_ctx_destroy(c); return CIS2_E_OOM; }
+  c->allocs.push_back(tp);
+  c->d_tok2 = static_cast<uint32_t*>(tp);
+  (void)hipMemset(tp, 0, 16);
+  if (!(c->logits2 = dalloc(c, V))) { cis2_ctx_destroy(c); return CIS2_E_OOM; }
   if (hipMalloc(&tp, (size_t)f.max_pos * sizeof(uint32_t)) != hipSuccess) {
     cis2_ctx_destroy(c);
     return CIS2_E_OOM;
@@ -844,7 +859,8 @@ int cis2_ctx_create(const cis2_config* cfg, cis2_ctx** out) {
     return CIS2_E_OOM;
   }
   for (int i = 0; i < kRing; ++i)
-    if (hipEventCreateWithFlags(&c->ring_ev[i], hipEventDisableTiming) != hipSuccess) {
+    if (hipEventCreateWithFlags(&c->ring_ev[i], hipEventDisableTiming) != hipSuccess ||
+        hipEventCreateWithFlags(&c->ring_ready[i], hipEventDisableTiming) != hipSuccess) {
       cis2_ctx_destroy(c);
       return CIS2_E_DEVICE;
     }
@@ -1262,6 +1278,14 @@ int cis2_decode_steps(cis2_ctx* c, uint32_t n) {
   const uint32_t V = c->cfg.vocab;
   hipStream_t s = c->st;
   int r;
+  // Persistent-kernel steps alternate between two logit buffers and two
+  // token slots: step t's logits and token (set t % 2) are copied to the
+  // host ring on the copy stream while pass t (which writes set (t+1) % 2)
+  // runs; pass t waits only for the copy of step t-1, whose set it
+  // overwrites.  The per-op path keeps one set and copies in stream order.
+  const bool alt = S.fast && !c->trace;
+  if (alt && !c->cs)
+    HIPCHK(c, hipStreamCreateWithFlags(&c->cs, hipStreamNonBlocking), "copy stream");
   for (uint32_t i = 0; i < n; ++i) {
     const uint32_t step = S.enqueued;
     const int slot = step % kRing;
@@ -1269,19 +1293,31 @@ int cis2_decode_steps(cis2_ctx* c, uint32_t n) {
       r = fold_step(c);
       if (r) return r;
     }
-    // the persistent kernel already left the argmax of these logits in d_tok;
-    // a sampled draw replaces it (generation step = this step's index)
+    const bool odd = alt && (step & 1);
+    float* lcur = odd ? c->logits2 : c->logits;
+    float* lnext = alt ? (odd ? c->logits : c->logits2) : c->logits;
+    uint32_t* tcur = odd ? c->d_tok2 : c->d_tok;
+    uint32_t* tnext = alt ? (odd ? c->d_tok : c->d_tok2) : c->d_tok;
+    // the persistent kernel already left the argmax of these logits in the
+    // token slot; a sampled draw replaces it (generation step = this step)
     if (c->samp_on)
-      LAUNCH(launch_sample(c->logits, V, c->samp, step, c->sbuf, c->d_tok, c->d_err, s), "sample");
+      LAUNCH(launch_sample(lcur, V, c->samp, step, c->sbuf, tcur, c->d_err, s), "sample");
     else if (!S.fast)
       LAUNCH(launch_argmax(c->logits, V, c->d_tok, s), "argmax");
-    HIPCHK(c, hipMemcpyAsync(c->ring + (size_t)slot * V, c->logits, (size_t)V * sizeof(float),
-                             hipMemcpyDeviceToHost, s),
+    hipStream_t cp = alt ? c->cs : s;
+    if (alt) {
+      HIPCHK(c, hipEventRecord(c->ring_ready[slot], s), "step event");
+      HIPCHK(c, hipStreamWaitEvent(cp, c->ring_ready[slot], 0), "copy wait");
+    }
+    HIPCHK(c, hipMemcpyAsync(c->ring + (size_t)slot * V, lcur, (size_t)V * sizeof(float),
+                             hipMemcpyDeviceToHost, cp),
            "logits d2h");
-    HIPCHK(c, hipMemcpyAsync(c->ring_tok + slot * 2, c->d_tok, 4, hipMemcpyDeviceToHost, s),
+    HIPCHK(c, hipMemcpyAsync(c->ring_tok + slot * 2, tcur, 4, hipMemcpyDeviceToHost, cp),
            "token d2h");
-    HIPCHK(c, hipEventRecord(c->ring_ev[slot], s), "ring event");
-    r = S.fast ? forward_fast(c, S.seq, S.n_prompt + step, c->d_tok, true)
+    HIPCHK(c, hipEventRecord(c->ring_ev[slot], cp), "ring event");
+    if (alt && step > 0)  // set (step+1) % 2 held step-1's results: copied by now
+      HIPCHK(c, hipStreamWaitEvent(s, c->ring_ev[(step - 1) % kRing], 0), "set reuse wait");
+    r = S.fast ? forward_fast(c, S.seq, S.n_prompt + step, tcur, true, lnext, tnext)
                : forward_one(c, S.seq, S.n_prompt + step, c->d_tok, true);
     if (r) return r;
     S.enqueued++;
