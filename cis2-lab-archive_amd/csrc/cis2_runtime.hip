@@ -1149,17 +1149,19 @@ int cis2_set_sampling(cis2_ctx* c, const cis2_sampling* sp) {
   SampleBufs& b = c->sbuf;
   if (b.V != V) {
     const uint32_t Vp = sample_sort_len(V);
-    void *k = nullptr, *e = nullptr, *cd = nullptr, *nk = nullptr;
-    if (hipMalloc(&k, (size_t)Vp * 8) != hipSuccess || hipMalloc(&e, (size_t)V * 4) != hipSuccess ||
+    void *k = nullptr, *k2 = nullptr, *e = nullptr, *cd = nullptr, *nk = nullptr;
+    if (hipMalloc(&k, (size_t)Vp * 8) != hipSuccess || hipMalloc(&k2, (size_t)Vp * 8) != hipSuccess ||
+        hipMalloc(&e, (size_t)V * 4) != hipSuccess ||
         hipMalloc(&cd, (size_t)kSampleBlocks * 8) != hipSuccess || hipMalloc(&nk, 64) != hipSuccess) {
-      for (void* q : {k, e, cd, nk})
+      for (void* q : {k, k2, e, cd, nk})
         if (q) (void)hipFree(q);
       return fail(c, CIS2_E_OOM, "sampling scratch");
     }
-    for (void* q : {k, e, cd, nk}) c->allocs.push_back(q);
+    for (void* q : {k, k2, e, cd, nk}) c->allocs.push_back(q);
     b.V = V;
     b.Vp = Vp;
     b.key = static_cast<uint64_t*>(k);
+    b.key2 = static_cast<uint64_t*>(k2);
     b.e = static_cast<float*>(e);
     b.cand = static_cast<uint64_t*>(cd);
     b.nkeep = static_cast<uint32_t*>(nk);

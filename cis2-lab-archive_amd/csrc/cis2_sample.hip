@@ -10,6 +10,8 @@
 //      active (every index is kept, no order is needed).
 //   2. bitonic sort of the keys: tiles of 4096 keys sorted and merged in
 //      LDS, strides of a tile or more as grid-wide compare-exchange passes.
+//      With top-k <= 4096 only the candidates are sorted: every tile is
+//      sorted, its first K keys gathered, and those sorted.
 //   3. k_keep: one workgroup; top-k cuts the ranks, then top-p runs its two
 //      strict rank-order chains (the denominator, then the running sum,
 //      stopping at the first rank whose predecessor sum reaches top_p).
@@ -94,7 +96,10 @@ __device__ __forceinline__ void cmpx(uint64_t& a, uint64_t& b, bool asc) {
 
 // One tile of kTile keys in LDS: k_level 0 sorts it completely (levels
 // 2..kTile); otherwise it runs the strides kTile/2..1 of level k_level.
-__global__ __launch_bounds__(1024) void k_bitonic_tile(uint64_t* key, uint32_t k_level) {
+// asc_all: every tile ascending (for the top-k selection), instead of the
+// alternating directions a following merge level needs.
+__global__ __launch_bounds__(1024) void k_bitonic_tile(uint64_t* key, uint32_t k_level,
+                                                       uint32_t asc_all) {
   __shared__ uint64_t t[kTile];
   const uint32_t base = blockIdx.x * kTile;
   for (uint32_t j = threadIdx.x; j < kTile; j += 1024) t[j] = key[base + j];
@@ -102,7 +107,7 @@ __global__ __launch_bounds__(1024) void k_bitonic_tile(uint64_t* key, uint32_t k
   auto pass = [&](uint32_t k, uint32_t j) {
     for (uint32_t x = threadIdx.x; x < kTile / 2; x += 1024) {
       const uint32_t i = 2 * x - (x & (j - 1));
-      cmpx(t[i], t[i + j], ((base + i) & k) == 0);
+      cmpx(t[i], t[i + j], (((asc_all ? 0u : base) + i) & k) == 0);
     }
     __syncthreads();
   };
@@ -127,6 +132,16 @@ __global__ __launch_bounds__(256) void k_bitonic_pass(uint64_t* key, uint32_t Vp
     key[i] = b;
     key[i + j] = a;
   }
+}
+
+// Top-k selection: the first K keys of every ascending-sorted tile (they
+// hold every key of the global top K) into cand[0 .. ntiles*K), the rest of
+// cand[0 .. Cp) padded to sort last.
+__global__ __launch_bounds__(256) void k_gather_top(const uint64_t* __restrict__ key, uint32_t K,
+                                                    uint32_t ntiles, uint32_t Cp, uint64_t* cand) {
+  const uint32_t x = blockIdx.x * blockDim.x + threadIdx.x;
+  if (x >= Cp) return;
+  cand[x] = x < ntiles * K ? key[(x / K) * kTile + x % K] : ~0ull;
 }
 
 // Draft 14.3 steps 3-4 over the sorted keys (one workgroup): K = top-k
@@ -314,20 +329,34 @@ hipError_t launch_sample(const float* logits, uint32_t V, const SampleParams& p,
   if (V == 0 || b.V != V || b.Vp < sample_sort_len(V)) return hipErrorInvalidValue;
   const uint32_t K = (p.top_k > 0 && p.top_k < V) ? p.top_k : V;
   const bool all = K == V && !(p.top_p < 1.0f);
+  const uint64_t* order = b.key;  // ascending rank keys, at least the first K sorted
   if (!all) {
-    const uint32_t Vp = b.Vp;
+    const uint32_t Vp = b.Vp, ntiles = Vp / kTile;
     hipLaunchKernelGGL(k_rank_keys, dim3((Vp + 255) / 256), dim3(256), 0, s, logits, V, Vp,
                        p.temperature, b.key, err);
-    hipLaunchKernelGGL(k_bitonic_tile, dim3(Vp / kTile), dim3(1024), 0, s, b.key, 0u);
-    for (uint32_t k = 2 * kTile; k <= Vp; k <<= 1) {
-      for (uint32_t j = k >> 1; j >= kTile; j >>= 1)
-        hipLaunchKernelGGL(k_bitonic_pass, dim3(Vp / 2 / 256), dim3(256), 0, s, b.key, Vp, k, j);
-      hipLaunchKernelGGL(k_bitonic_tile, dim3(Vp / kTile), dim3(1024), 0, s, b.key, k);
+    auto sort = [&](uint64_t* keys, uint32_t n) {  // n: a power of two >= kTile
+      hipLaunchKernelGGL(k_bitonic_tile, dim3(n / kTile), dim3(1024), 0, s, keys, 0u, 0u);
+      for (uint32_t k = 2 * kTile; k <= n; k <<= 1) {
+        for (uint32_t j = k >> 1; j >= kTile; j >>= 1)
+          hipLaunchKernelGGL(k_bitonic_pass, dim3(n / 2 / 256), dim3(256), 0, s, keys, n, k, j);
+        hipLaunchKernelGGL(k_bitonic_tile, dim3(n / kTile), dim3(1024), 0, s, keys, k, 0u);
+      }
+    };
+    if (K < V && K <= kTile && ntiles > 1) {
+      // top-k: sort the tiles, keep each tile's first K, sort those
+      hipLaunchKernelGGL(k_bitonic_tile, dim3(ntiles), dim3(1024), 0, s, b.key, 0u, 1u);
+      const uint32_t Cp = sample_sort_len(ntiles * K);
+      hipLaunchKernelGGL(k_gather_top, dim3((Cp + 255) / 256), dim3(256), 0, s, b.key, K, ntiles,
+                         Cp, b.key2);
+      sort(b.key2, Cp);
+      order = b.key2;
+    } else {
+      sort(b.key, Vp);
     }
-    hipLaunchKernelGGL(k_keep, dim3(1), dim3(1024), 0, s, b.key, logits, p.temperature, K,
+    hipLaunchKernelGGL(k_keep, dim3(1), dim3(1024), 0, s, order, logits, p.temperature, K,
                        p.top_p, b.e, b.nkeep);
   }
-  hipLaunchKernelGGL(k_draw, dim3(kSampleBlocks), dim3(256), 0, s, b.key, logits,
+  hipLaunchKernelGGL(k_draw, dim3(kSampleBlocks), dim3(256), 0, s, order, logits,
                      p.temperature, V, b.nkeep, all ? 1u : 0u, p.seed, step, b.cand, err);
   hipLaunchKernelGGL(k_draw_final, dim3(1), dim3(256), 0, s, b.cand, kSampleBlocks, out);
   return hipGetLastError();

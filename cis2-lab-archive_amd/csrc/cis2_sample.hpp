@@ -18,6 +18,7 @@ struct SampleParams {
 struct SampleBufs {
   uint32_t V = 0, Vp = 0;      // vocabulary, sort length (power of two >= V, >= tile)
   uint64_t* key = nullptr;     // [Vp] rank keys, sorted in place
+  uint64_t* key2 = nullptr;    // [Vp] top-k candidates
   float* e = nullptr;          // [V] exp terms / probabilities in rank order
   uint64_t* cand = nullptr;    // [kSampleBlocks] per-workgroup (z, index) candidates
   uint32_t* nkeep = nullptr;   // [1] size of the kept set
