@@ -148,16 +148,17 @@ __global__ __launch_bounds__(256) void k_gather_top(const uint64_t* __restrict__
 // cut; with top_p < 1, m = s of rank 0, e_r = exp(s_r - m), denom =
 // sum_seq(e) in rank order, p_r = e_r / denom, c_r = c_{r-1} + p_r from 0,
 // and the kept ranks end at the first r > 0 with !(c_{r-1} < top_p).
-// The ranks pass through LDS in tiles of kKeepTile: all threads form a
-// tile's terms, then lane 0 runs the strict chain over it (16 LDS reads in
-// flight).  c never decreases (p_r >= 0), so a group of four needs a
+// The ranks pass through LDS in tiles of kKeepTile: lane 0 runs the strict
+// chain over one tile (16 LDS reads in flight) while waves 1.. form the
+// next tile's terms in the other buffer.  c never decreases (p_r >= 0), so a group of four needs a
 // per-rank test only when its third sum fails.
 constexpr uint32_t kKeepTile = 8192;
 
 __global__ __launch_bounds__(1024) void k_keep(const uint64_t* __restrict__ key,
                                                const float* __restrict__ l, float T, uint32_t K,
                                                float top_p, float* e, uint32_t* nkeep) {
-  __shared__ __attribute__((aligned(16))) float t[kKeepTile];
+  // two tile buffers: wave 0 chains one while waves 1.. form the next
+  __shared__ __attribute__((aligned(16))) float t[2][kKeepTile];
   __shared__ float s_den;
   __shared__ uint32_t s_keep;
   if (!(top_p < 1.0f)) {
@@ -165,35 +166,46 @@ __global__ __launch_bounds__(1024) void k_keep(const uint64_t* __restrict__ key,
     return;
   }
   const float m = l[(uint32_t)key[0]] / T;
-  const float4* t4 = reinterpret_cast<const float4*>(t);
-  // the denominator
-  float den = 0.0f;
-  for (uint32_t base = 0; base < K; base += kKeepTile) {
-    const uint32_t n = min(kKeepTile, K - base);
-    for (uint32_t j = threadIdx.x; j < n; j += blockDim.x) {
+  const uint32_t nt = (K + kKeepTile - 1) / kKeepTile, wv = threadIdx.x >> 6;
+  const uint32_t fid = threadIdx.x - 64, fn = blockDim.x - 64;  // formers: waves 1..
+  auto len = [&](uint32_t tile) { return min(kKeepTile, K - tile * kKeepTile); };
+  // e_r = exp(s_r - m) of one tile, into LDS and (for the second pass) HBM
+  auto form_e = [&](uint32_t tile, float* dst, uint32_t id, uint32_t nthr) {
+    const uint32_t base = tile * kKeepTile, n = len(tile);
+    for (uint32_t j = id; j < n; j += nthr) {
       const float s = l[(uint32_t)key[base + j]] / T;
       const float d = s - m;
       const float ev = exp_pinned(d);
-      t[j] = ev;
+      dst[j] = ev;
       e[base + j] = ev;
     }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      const uint32_t n4 = n / 4;
-      uint32_t g = 0;
-      for (; g + 16 <= n4; g += 16) {
-        float4 v[16];
+  };
+  // the denominator
+  float den = 0.0f;
+  form_e(0, t[0], threadIdx.x, blockDim.x);
+  __syncthreads();
+  for (uint32_t tile = 0; tile < nt; ++tile) {
+    if (wv == 0) {
+      if (threadIdx.x == 0) {
+        const float4* t4 = reinterpret_cast<const float4*>(t[tile & 1]);
+        const uint32_t n = len(tile), n4 = n / 4;
+        uint32_t g = 0;
+        for (; g + 16 <= n4; g += 16) {
+          float4 v[16];
 #pragma unroll
-        for (uint32_t u = 0; u < 16; ++u) v[u] = t4[g + u];
+          for (uint32_t u = 0; u < 16; ++u) v[u] = t4[g + u];
 #pragma unroll
-        for (uint32_t u = 0; u < 16; ++u) {
-          den = den + v[u].x;
-          den = den + v[u].y;
-          den = den + v[u].z;
-          den = den + v[u].w;
+          for (uint32_t u = 0; u < 16; ++u) {
+            den = den + v[u].x;
+            den = den + v[u].y;
+            den = den + v[u].z;
+            den = den + v[u].w;
+          }
         }
+        for (uint32_t r = 4 * g; r < n; ++r) den = den + t[tile & 1][r];
       }
-      for (uint32_t r = 4 * g; r < n; ++r) den = den + t[r];
+    } else if (tile + 1 < nt) {
+      form_e(tile + 1, t[(tile + 1) & 1], fid, fn);
     }
     __syncthreads();
   }
@@ -203,48 +215,57 @@ __global__ __launch_bounds__(1024) void k_keep(const uint64_t* __restrict__ key,
   }
   __syncthreads();
   den = s_den;
+  // p_r = e_r / den of one tile, into LDS
+  auto form_p = [&](uint32_t tile, float* dst, uint32_t id, uint32_t nthr) {
+    const uint32_t base = tile * kKeepTile, n = len(tile);
+    for (uint32_t j = id; j < n; j += nthr) {
+      const float p = e[base + j] / den;
+      dst[j] = p;
+    }
+  };
   // the running sum up to the first failing rank
   float c = 0.0f;
-  for (uint32_t base = 0; base < K; base += kKeepTile) {
-    const uint32_t n = min(kKeepTile, K - base);
-    for (uint32_t j = threadIdx.x; j < n; j += blockDim.x) {
-      const float p = e[base + j] / den;
-      t[j] = p;
-    }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      uint32_t keep = 0xFFFFFFFFu;
-      const uint32_t n4 = n / 4;
-      uint32_t g = 0;
-      for (; g < n4 && keep == 0xFFFFFFFFu; g += 16) {
-        float4 v[16];
+  form_p(0, t[0], threadIdx.x, blockDim.x);
+  __syncthreads();
+  for (uint32_t tile = 0; tile < nt; ++tile) {
+    if (wv == 0) {
+      if (threadIdx.x == 0) {
+        const float* tb = t[tile & 1];
+        const float4* t4 = reinterpret_cast<const float4*>(tb);
+        const uint32_t base = tile * kKeepTile, n = len(tile), n4 = n / 4;
+        uint32_t keep = 0xFFFFFFFFu, g = 0;
+        for (; g < n4 && keep == 0xFFFFFFFFu; g += 16) {
+          float4 v[16];
 #pragma unroll
-        for (uint32_t u = 0; u < 16; ++u)
-          if (g + u < n4) v[u] = t4[g + u];
+          for (uint32_t u = 0; u < 16; ++u)
+            if (g + u < n4) v[u] = t4[g + u];
 #pragma unroll
-        for (uint32_t u = 0; u < 16; ++u) {
-          if (g + u < n4 && keep == 0xFFFFFFFFu) {
-            const uint32_t r = base + 4 * (g + u);
-            const float c0 = c + v[u].x;
-            const float c1 = c0 + v[u].y;
-            const float c2 = c1 + v[u].z;
-            const float c3 = c2 + v[u].w;
-            if (!(c2 < top_p)) {  // the prefix ends inside ranks r..r+3
-              if (r > 0 && !(c < top_p)) keep = r;
-              else if (!(c0 < top_p)) keep = r + 1;
-              else if (!(c1 < top_p)) keep = r + 2;
-              else keep = r + 3;
+          for (uint32_t u = 0; u < 16; ++u) {
+            if (g + u < n4 && keep == 0xFFFFFFFFu) {
+              const uint32_t r = base + 4 * (g + u);
+              const float c0 = c + v[u].x;
+              const float c1 = c0 + v[u].y;
+              const float c2 = c1 + v[u].z;
+              const float c3 = c2 + v[u].w;
+              if (!(c2 < top_p)) {  // the prefix ends inside ranks r..r+3
+                if (r > 0 && !(c < top_p)) keep = r;
+                else if (!(c0 < top_p)) keep = r + 1;
+                else if (!(c1 < top_p)) keep = r + 2;
+                else keep = r + 3;
+              }
+              c = c3;
             }
-            c = c3;
           }
         }
+        for (uint32_t j = 4 * n4; j < n && keep == 0xFFFFFFFFu; ++j) {
+          const uint32_t r = base + j;
+          if (r > 0 && !(c < top_p)) keep = r;
+          else c = c + tb[j];
+        }
+        s_keep = keep;
       }
-      for (uint32_t j = 4 * n4; j < n && keep == 0xFFFFFFFFu; ++j) {
-        const uint32_t r = base + j;
-        if (r > 0 && !(c < top_p)) keep = r;
-        else c = c + t[j];
-      }
-      s_keep = keep;
+    } else if (tile + 1 < nt) {
+      form_p(tile + 1, t[(tile + 1) & 1], fid, fn);
     }
     __syncthreads();
     if (s_keep != 0xFFFFFFFFu) break;
