@@ -74,6 +74,8 @@ SIGNATURES = {
     "cis2_set_sampling": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(Cis2Sampling)]),
     "cis2_sample_logits": (ctypes.c_int, [ctypes.c_void_p, c_fp, ctypes.c_uint32, c_u32p, c_u32p,
                                           c_u32p]),
+    "cis2_sample_logits_noalloc": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint32,
+                                                  c_u32p, ctypes.c_void_p, ctypes.c_void_p]),
     "cis2_trace_enable": (ctypes.c_int, [ctypes.c_void_p, TRACE_FN, ctypes.c_void_p]),
     "cis2_profile": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int]),
     "cis2_profile_read": (ctypes.c_int, [ctypes.c_void_p, c_u64p, ctypes.POINTER(ctypes.c_double),

@@ -94,6 +94,7 @@ struct RowsBuf {
 
 struct cis2_ctx {
   cis2_config cfg;
+  int dev = 0;  // the HIP device current at creation
   uint32_t qd = 0, kvd = 0;
   float scale = 0.0f;
   hipStream_t st = nullptr;
@@ -783,7 +784,13 @@ int cis2_ctx_create(const cis2_config* cfg, cis2_ctx** out) {
   c->qd = f.n_heads * f.head_dim;
   c->kvd = f.n_kv_heads * f.head_dim;
   c->L.resize(f.n_layers);
-  if (hipStreamCreateWithFlags(&c->st, hipStreamNonBlocking) != hipSuccess) {
+  if (hipGetDevice(&c->dev) != hipSuccess ||
+      hipStreamCreateWithFlags(&c->st, hipStreamNonBlocking) != hipSuccess) {
+    cis2_ctx_destroy(c);
+    return CIS2_E_DEVICE;
+  }
+  // this GPU's preallocated sampler scratch (cis2_sample_logits_noalloc)
+  if (sample_scratch_init() != hipSuccess) {
     cis2_ctx_destroy(c);
     return CIS2_E_DEVICE;
   }
@@ -1195,6 +1202,33 @@ int cis2_sample_logits(cis2_ctx* c, const float* logits_host, uint32_t n, const 
     HIPCHK(c, hipStreamSynchronize(c->st), "sample sync");
   }
   return check_err_flag(c);
+}
+
+int cis2_sample_logits_noalloc(cis2_ctx* c, const float* logits_dev, uint32_t n,
+                               const uint32_t* steps, uint32_t* ids_dev, uint32_t* nkeep_dev) {
+  if (!c) return CIS2_E_ARG;
+  if (n == 0) return CIS2_OK;
+  if (!logits_dev || !steps || !ids_dev) return fail(c, CIS2_E_ARG, "null argument");
+  if (!c->samp_on) return fail(c, CIS2_E_ARG, "sampling is not enabled (cis2_set_sampling)");
+  const uint32_t V = c->cfg.vocab;
+  if (V > kNoAllocMaxVocab)
+    return fail(c, CIS2_E_ARG, "vocabulary exceeds the no-allocation scratch (262144 entries)");
+  SampleBufs b;
+  uint32_t* err = nullptr;
+  HIPCHK(c, sample_scratch_bufs(c->dev, V, &b, &err), "sampler scratch");
+  // the scratch keeps the previous call's contents: only the error flag must
+  // start at zero (every other word is written before it is read)
+  LAUNCH(launch_fill_u32(err, 1, 0u, c->st), "clear error flag");
+  for (uint32_t i = 0; i < n; ++i)
+    LAUNCH(launch_sample(logits_dev + (size_t)i * V, V, c->samp, steps[i], b, ids_dev + i, err,
+                         c->st, nkeep_dev ? nkeep_dev + i : nullptr),
+           "sample");
+  uint32_t flag = 0;
+  HIPCHK(c, hipMemcpyAsync(&flag, err, 4, hipMemcpyDeviceToHost, c->st), "error flag");
+  HIPCHK(c, hipStreamSynchronize(c->st), "sample sync");
+  if (flag & 0x100u)
+    return fail(c, CIS2_E_NUMERIC, "NaN among logits / temperature in a sampled draw");
+  return CIS2_OK;
 }
 
 // Greedy decode + witness (code/cis2-fp/gpu/cis2_host.cpp:176-218).  The

@@ -20,6 +20,9 @@
 // Every value is the one the draft's arithmetic gives: true divides, the
 // pinned ln and exp, sequential f32 sums in rank order.
 #include "cis2_sample.hpp"
+
+#include <mutex>
+
 #include "cis2_device_math.hpp"
 
 namespace cis2 {
@@ -324,8 +327,12 @@ __global__ __launch_bounds__(256) void k_draw(const uint64_t* __restrict__ key,
 
 // The first index of the maximum z: the scan of section 11.2 starts at
 // index 0 (z = -inf when masked), so the candidates reduce from (-inf, 0).
+// nkeep_out (optional): the size of the kept set (V when nothing is cut).
 __global__ __launch_bounds__(256) void k_draw_final(const uint64_t* __restrict__ cand,
-                                                    uint32_t n, uint32_t* out) {
+                                                    uint32_t n, uint32_t* out,
+                                                    const uint32_t* __restrict__ nkeep,
+                                                    uint32_t all, uint32_t V,
+                                                    uint32_t* nkeep_out) {
   __shared__ ZI red[4];
   ZI best{-__builtin_inff(), 0u};
   for (uint32_t b = threadIdx.x; b < n; b += blockDim.x) {
@@ -334,7 +341,15 @@ __global__ __launch_bounds__(256) void k_draw_final(const uint64_t* __restrict__
     if (o.i != UINT32_MAX) best = zi_pick(best, o);
   }
   best = zi_block(best, red);
-  if (threadIdx.x == 0) *out = best.i;
+  if (threadIdx.x == 0) {
+    *out = best.i;
+    if (nkeep_out) *nkeep_out = all ? V : *nkeep;
+  }
+}
+
+__global__ void k_fill_u32(uint32_t* p, uint32_t n, uint32_t v) {
+  const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = v;
 }
 
 }  // namespace
@@ -346,7 +361,8 @@ uint32_t sample_sort_len(uint32_t V) {
 }
 
 hipError_t launch_sample(const float* logits, uint32_t V, const SampleParams& p, uint32_t step,
-                         const SampleBufs& b, uint32_t* out, uint32_t* err, hipStream_t s) {
+                         const SampleBufs& b, uint32_t* out, uint32_t* err, hipStream_t s,
+                         uint32_t* nkeep_out) {
   if (V == 0 || b.V != V || b.Vp < sample_sort_len(V)) return hipErrorInvalidValue;
   const uint32_t K = (p.top_k > 0 && p.top_k < V) ? p.top_k : V;
   const bool all = K == V && !(p.top_p < 1.0f);
@@ -379,7 +395,74 @@ hipError_t launch_sample(const float* logits, uint32_t V, const SampleParams& p,
   }
   hipLaunchKernelGGL(k_draw, dim3(kSampleBlocks), dim3(256), 0, s, order, logits,
                      p.temperature, V, b.nkeep, all ? 1u : 0u, p.seed, step, b.cand, err);
-  hipLaunchKernelGGL(k_draw_final, dim3(1), dim3(256), 0, s, b.cand, kSampleBlocks, out);
+  hipLaunchKernelGGL(k_draw_final, dim3(1), dim3(256), 0, s, b.cand, kSampleBlocks, out,
+                     b.nkeep, all ? 1u : 0u, V, nkeep_out);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Scratch of the no-allocation draw (cis2_sample_logits_noalloc): one copy
+// of this array per GPU, held until the process ends, carved into the
+// sampler's buffers for vocabularies up to kNoAllocMaxVocab.  In host code
+// `scratch` names a host-side stand-in, never device memory: every host use
+// goes through the address hipGetSymbolAddress returns for the device.
+// ---------------------------------------------------------------------------
+namespace {
+constexpr size_t kScrKeyWords = kNoAllocMaxVocab;        // [Vp] rank keys (Vp <= max vocab)
+constexpr size_t kScrEWords = kNoAllocMaxVocab / 2;      // [V] f32 terms, two per word
+constexpr size_t kScrCandWords = kSampleBlocks;          // per-workgroup candidates
+constexpr size_t kScrFlagWords = 8;                      // nkeep (u32), error flag (u32)
+constexpr size_t kScratchWords = 2 * kScrKeyWords + kScrEWords + kScrCandWords + kScrFlagWords;
+static_assert(kNoAllocMaxVocab % kTile == 0, "the sort length of the largest vocabulary");
+static_assert(kScratchWords * 8 == kNoAllocScratchBytes, "scratch size as declared");
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_dev[kMaxDevices];  // this GPU's address of `scratch`, or null
+}  // namespace
+
+static __device__ __align__(256) uint64_t scratch[kScratchWords];
+
+hipError_t sample_scratch_init() {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> g(g_scratch_mu);
+  if (g_scratch_dev[dev]) return hipSuccess;
+  void* ptr = nullptr;
+  e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+  if (e != hipSuccess) return e;
+  if (!ptr) return hipErrorInvalidSymbol;
+  g_scratch_dev[dev] = ptr;
+  return hipSuccess;
+}
+
+hipError_t sample_scratch_bufs(int dev, uint32_t V, SampleBufs* b, uint32_t** err) {
+  if (V == 0 || V > kNoAllocMaxVocab) return hipErrorInvalidValue;
+  if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+  void* base = nullptr;
+  {
+    std::lock_guard<std::mutex> g(g_scratch_mu);
+    base = g_scratch_dev[dev];
+  }
+  if (!base) return hipErrorNotInitialized;
+  uint64_t* w = static_cast<uint64_t*>(base);
+  b->V = V;
+  b->Vp = sample_sort_len(V);
+  b->key = w;
+  b->key2 = w + kScrKeyWords;
+  b->e = reinterpret_cast<float*>(w + 2 * kScrKeyWords);
+  b->cand = w + 2 * kScrKeyWords + kScrEWords;
+  uint32_t* flags = reinterpret_cast<uint32_t*>(b->cand + kScrCandWords);
+  b->nkeep = flags;
+  *err = flags + 1;
+  return hipSuccess;
+}
+
+hipError_t launch_fill_u32(uint32_t* p, uint32_t n, uint32_t v, hipStream_t s) {
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(k_fill_u32, dim3((n + 255) / 256), dim3(256), 0, s, p, n, v);
   return hipGetLastError();
 }
 

@@ -30,9 +30,26 @@ uint32_t sample_sort_len(uint32_t V);
 
 // Draws the next id from logits[V] at generation step `step` into *out on
 // stream s (no host synchronisation).  A NaN among logits / temperature
-// sets bit 0x100 of *err.  nkeep_host (optional) is not written here: read
-// b.nkeep after the stream drains.
+// sets bit 0x100 of *err.  nkeep_out (optional, device) receives the size
+// of the kept set.
 hipError_t launch_sample(const float* logits, uint32_t V, const SampleParams& p, uint32_t step,
-                         const SampleBufs& b, uint32_t* out, uint32_t* err, hipStream_t s);
+                         const SampleBufs& b, uint32_t* out, uint32_t* err, hipStream_t s,
+                         uint32_t* nkeep_out = nullptr);
+
+// ---- Preallocated per-GPU scratch for the no-allocation draw ----------------
+// Largest vocabulary the static scratch serves (Qwen3's 151,936 fits), and
+// its size: two key arrays of the sort length, the f32 terms, the candidates
+// and two flag words.
+constexpr uint32_t kNoAllocMaxVocab = 262144;
+constexpr size_t kNoAllocScratchBytes =
+    (2 * (size_t)kNoAllocMaxVocab + kNoAllocMaxVocab / 2 + kSampleBlocks + 8) * 8;
+// Resolves the current GPU's copy of the scratch array (once per device,
+// with that device current).  Called at context creation.
+hipError_t sample_scratch_init();
+// The sampler buffers and the error-flag word carved out of GPU dev's
+// scratch for a vocabulary of V (<= kNoAllocMaxVocab).  No allocation.
+hipError_t sample_scratch_bufs(int dev, uint32_t V, SampleBufs* b, uint32_t** err);
+// p[0..n) = v on stream s (a kernel, not a memset node).
+hipError_t launch_fill_u32(uint32_t* p, uint32_t n, uint32_t v, hipStream_t s);
 
 }  // namespace cis2

@@ -173,6 +173,23 @@ int cis2_set_sampling(cis2_ctx *ctx, const cis2_sampling *s);
 int cis2_sample_logits(cis2_ctx *ctx, const float *logits_host, uint32_t n,
                        const uint32_t *steps, uint32_t *ids_out, uint32_t *nkeep_out);
 
+/* ---- No-allocation draw (no counterpart in the reference) ----------------
+ * For callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc): the draw of
+ * cis2_sample_logits on n DEVICE-resident logit rows (logits_dev: n * vocab
+ * floats), row i at step steps[i] (host array), with the context's sampling
+ * parameters.  ids_dev[i] (device) receives the drawn id and nkeep_dev[i]
+ * (device, optional) the size of the kept set; the results equal
+ * cis2_sample_logits on the same rows bit for bit.  The call allocates
+ * nothing: its scratch is one static array per GPU of 5,244,992 bytes
+ * (two sort-key arrays, the f32 terms, candidates, flags), which serves
+ * vocabularies up to 262,144 (larger: CIS2_E_ARG) and is held until the
+ * process ends.  Every call on a GPU shares that GPU's array, so calls that
+ * overlap on one GPU (two contexts on two host threads) race.  Blocks until
+ * the draws are done; a NaN logit gives CIS2_E_NUMERIC. */
+int cis2_sample_logits_noalloc(cis2_ctx *ctx, const float *logits_dev, uint32_t n,
+                               const uint32_t *steps, uint32_t *ids_dev, uint32_t *nkeep_dev);
+
 /* Batched greedy decode: nseq independent sequences with their own prompts
  * (ragged lengths allowed), each decoded for gen_toks steps.  Groups of up
  * to max_seqs sequences run together (KV-cache slots 0..max_seqs-1): one
