@@ -63,8 +63,17 @@ static inline float opaque(float x) {
   return x;
 }
 
+/* Planted mistakes (orc_set_mutation): tests turn them on to show that a
+ * fixture detects the mistake; 0 everywhere else. */
+static _Atomic int g_mutation;
+void orc_set_mutation(int m) { atomic_store(&g_mutation, m); }
+
 int orc_fpenv_pin(void) {
   unsigned csr = _mm_getcsr();
+  if (atomic_load(&g_mutation) & ORC_MUT_NO_FTZ) { /* planted: subnormals kept */
+    _mm_setcsr(csr & ~((1u << 15) | (1u << 6)));
+    return 0;
+  }
   _mm_setcsr(csr | (1u << 15) | (1u << 6));
   csr = _mm_getcsr();
   if (!(csr & (1u << 15)) || !(csr & (1u << 6))) return -1;
@@ -395,6 +404,11 @@ void orc_softmax(float *v, int n, int mode) {
 uint32_t orc_argmax(const float *v, int n) {
   int best = 0;
   float bv = v[0];
+  if (atomic_load(&g_mutation) & ORC_MUT_ARGMAX_GE) { /* planted: last maximum wins */
+    for (int i = 0; i < n; ++i)
+      if (v[i] >= bv) { bv = v[i]; best = i; }
+    return (uint32_t)best;
+  }
   for (int i = 0; i < n; ++i)
     if (v[i] > bv) { bv = v[i]; best = i; }
   return (uint32_t)best;
@@ -441,6 +455,7 @@ static void *worker_main(void *arg) {
     pthread_mutex_unlock(&p->mu);
     int lo, hi;
     chunk_bounds(n, p->nthreads, idx, &lo, &hi);
+    orc_fpenv_pin(); /* per task: follows orc_set_mutation */
     if (lo < hi) fn(ctx, lo, hi);
     pthread_mutex_lock(&p->mu);
     if (--p->pending == 0) pthread_cond_signal(&p->done);
@@ -1039,6 +1054,12 @@ int orc_forward(orc_model *m, int pos, uint32_t token, float *logits,
   const float *lm = c->tied ? m->embed : m->lm_head;
   matvec(m, lm, m->x, c->vocab, H, logits);
   trace_emit(cb, user, pos, -1, "logits", logits, c->vocab);
+  return 0;
+}
+
+int orc_model_hidden(const orc_model *m, float *out) {
+  if (!m || !out || !m->x) return -1;
+  memcpy(out, m->x, sizeof(float) * (size_t)m->c.hidden);
   return 0;
 }
 

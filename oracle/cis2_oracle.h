@@ -109,6 +109,18 @@ void orc_model_reset(orc_model *m);
 /* One forward pass at `pos` for `token`; writes vocab logits. */
 int orc_forward(orc_model *m, int pos, uint32_t token, float *logits,
                 orc_trace_fn cb, void *user);
+/* The final-norm output (hidden floats) of the last orc_forward: the
+ * vector the LM head multiplies.  Used to construct coverage rows. */
+int orc_model_hidden(const orc_model *m, float *out);
+
+/* Planted mistakes for tests that show a fixture detects them; 0 (the
+ * default) runs the oracle as specified.
+ *   ORC_MUT_ARGMAX_GE  greedy argmax with >= (the last maximum wins)
+ *   ORC_MUT_NO_FTZ     FTZ/DAZ left off (subnormal inputs and results kept) */
+#define ORC_MUT_ARGMAX_GE 1
+#define ORC_MUT_NO_FTZ 2
+void orc_set_mutation(int m);
+
 /* Greedy decode exactly as the reference driver: prefill every prompt
  * position, then gen_toks steps of argmax -> witness fold -> forward.
  * hdr = sha256 of model.safetensors, tokenizer.json, config.json.

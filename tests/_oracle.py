@@ -83,6 +83,8 @@ def lib():
         L.orc_decode.argtypes = [ctypes.c_void_p, c_u32p, ctypes.c_int, ctypes.c_int, c_u8p,
                                  c_u32p, c_u8p, c_u8p, c_u8p, TRACE_FN, ctypes.c_void_p]
         L.orc_fpenv_pin.restype = ctypes.c_int
+        L.orc_model_hidden.argtypes = [ctypes.c_void_p, c_fp]
+        L.orc_set_mutation.argtypes = [ctypes.c_int]
         _o = L
         if L.orc_fpenv_pin() != 0:
             raise RuntimeError("oracle FTZ/DAZ pin failed")
@@ -184,6 +186,13 @@ class OracleModel:
             raise RuntimeError("oracle forward failed (%d)" % rc)
         return logits
 
+    def hidden(self):
+        """The final-norm output of the last forward (the LM head's input)."""
+        out = np.empty(self.spec.hidden, dtype=np.float32)
+        if lib().orc_model_hidden(self.m, ptr(out, c_fp)) != 0:
+            raise RuntimeError("no forward has run")
+        return out
+
     def decode_sampled(self, prompt, gen_toks, seed, temperature, top_k, top_p):
         """The sampled decode of draft section 14 (orc_decode_sampled)."""
         prompt = np.ascontiguousarray(prompt, dtype=np.uint32)
@@ -219,6 +228,28 @@ class OracleModel:
         sb = bytes(steps)
         return {"ids": ids, "witness": bytes(wit).hex(), "argmax_digest": bytes(adg).hex(),
                 "step_digests": [sb[32 * i:32 * i + 32].hex() for i in range(gen_toks)]}
+
+
+MUT_ARGMAX_GE = 1  # greedy argmax with >= (the last maximum wins)
+MUT_NO_FTZ = 2     # FTZ/DAZ left off
+
+
+class mutation:
+    """Context manager: runs the oracle with a planted mistake (a test that
+    shows a fixture detects it), and restores the specified oracle after."""
+
+    def __init__(self, m):
+        self.m = m
+
+    def __enter__(self):
+        lib().orc_set_mutation(self.m)
+        return self
+
+    def __exit__(self, *exc):
+        lib().orc_set_mutation(0)
+        if lib().orc_fpenv_pin() != 0:
+            raise RuntimeError("oracle FTZ/DAZ pin failed")
+        return False
 
 
 def sample_noise(seed, step, index):
