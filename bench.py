@@ -6,9 +6,11 @@ A step is one greedy decode step of the hot path: device argmax of the logits
 already computed, their witness fold on the host, and the forward pass of the
 chosen token (30 layers + LM head).  The workload is the 32-token prompt plus
 256 generated tokens of the SmolLM2-135M-shape synthetic model (seeded BF16
-weights ~N(0,0.02)); `--warmup` steps run first, then `--steps` are timed.
-When warmup + steps == 256 the run's witness digest is checked against the
-reference driver's digest for the same inputs (tests/golden).
+weights ~N(0,0.02)).  Every run decodes all 256 steps: `--warmup` steps run
+first, then `--steps` are timed, then the rest run untimed, and the run's
+witness digest and tokens are checked against the reference driver's for the
+same inputs (tests/golden).  vs_baseline is value / cpu_baseline.value, the
+same workload on the host CPU in the same run.
 
 The roofline object is the persistent decode kernel's (one launch computes one
 position: all layers, LM head, argmax): algorithmic bytes per launch are the
@@ -25,8 +27,9 @@ the strict-order GEMV at 1536x576, one per launch and
 sequences at B = 1, 8, 32, 64 (batch_decode), the llama-160m set of 300
 prompts decoded as one batch (llama160m_set), the Qwen3-0.6B-shape
 4096-token prefill + 256-step decode (qwen3_4096), and the CPU baseline
-both single-thread (cpu_baseline, the reference protocol) and row-parallel
-over the host cores (cpu_baseline_parallel).
+(the oracle decoding the same 256 steps after an untimed prefill, witness
+checked) both single-thread (cpu_baseline, the reference protocol) and
+row-parallel over up to 16 host threads (cpu_baseline_parallel).
 
 Prints ONE JSON line on stdout.
 """
@@ -46,6 +49,7 @@ HBM_PEAK_GBS = 8000.0
 # (labs/rust-1/reports/rust-1/RESULT.md:26)
 CPU_REF_TOKS = 5.189
 SEED = 20261201
+GEN = 256  # generated tokens of the workload (positions 32..287)
 
 
 def log(*a):
@@ -106,29 +110,72 @@ def gemv_roofline(M=1536, K=576, copies=128, iters=4096):
                                  % (copies, M, K)}}
 
 
-def cpu_baseline(spec, weights, prompt, seconds=15.0):
-    """The oracle (this repository's CPU restatement, bit-identical to the
-    reference) timed on the host: 1 thread, forward passes at consecutive
-    positions, stopping after about `seconds`."""
+def host_cpu():
+    """(model name, logical CPUs this process may use) of the host."""
+    name = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                name = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    return name, n
+
+
+def cpu_decode(spec, weights, prompt, gen, threads, fixture):
+    """The headline workload on the host CPU with the oracle (this
+    repository's CPU restatement, pinned bit-identical to the reference
+    driver): the 32-token prompt prefilled untimed, then `gen` greedy steps
+    timed as the reference protocol times them (argmax, witness fold of the
+    logits and the id, forward of the id; labs/rust-1/reports/rust-1/
+    RESULT.md:13).  The witness of the run is checked against the fixture."""
+    import hashlib
+    import struct
+
     import numpy as np
 
     import _oracle as O
-    m = O.OracleModel(spec, weights, max_pos=len(prompt) + 512, threads=1)
+    n = len(prompt)
+    m = O.OracleModel(spec, weights, max_pos=n + gen, threads=threads)
+    table, invf = (bytes.fromhex(h) for h in m.digests())
     logits = np.empty(spec.vocab, np.float32)
     L = O.lib()
+    for p, t in enumerate(prompt):
+        L.orc_forward(m.m, p, int(t), O.ptr(logits, O.c_fp), O.TRACE_FN(), None)
+    w = hashlib.sha256(weights.header_digests() + table + invf)
+    w.update(b"".join(struct.pack("<I", int(t)) for t in prompt))
+    ids = []
     t0 = time.perf_counter()
-    n = 0
-    tok = int(prompt[0])
-    while True:
-        L.orc_forward(m.m, n, tok, O.ptr(logits, O.c_fp), O.TRACE_FN(), None)
-        n += 1
-        tok = int(prompt[n]) if n < len(prompt) else int(L.orc_argmax(O.ptr(logits, O.c_fp), spec.vocab))
-        if time.perf_counter() - t0 > seconds or n >= len(prompt) + 500:
-            break
+    for s in range(gen):
+        nid = int(L.orc_argmax(O.ptr(logits, O.c_fp), spec.vocab))
+        w.update(logits.tobytes())
+        w.update(struct.pack("<I", nid))
+        ids.append(nid)
+        L.orc_forward(m.m, n + s, nid, O.ptr(logits, O.c_fp), O.TRACE_FN(), None)
     dt = time.perf_counter() - t0
-    return {"value": round(n / dt, 3), "unit": "tok/s", "cores": 1, "kind": "port",
-            "sample": "%d forward passes (positions 0..%d) of the same model, 1 thread, %.1f s"
-                      % (n, n - 1, dt)}
+    ok = None
+    if fixture is not None:
+        ok = (w.hexdigest() == fixture["witness"] and
+              [int(v) for v in prompt] + ids == fixture["tokens"])
+    return gen / dt, dt, ok
+
+
+def cpu_baseline(spec, weights, prompt, gen, fixture, threads=1):
+    """cpu_baseline: the whole 256-step decode (positions 32..287) on `threads`
+    host threads (1: the reference's single-thread protocol; more: the oracle's
+    GEMV rows split over threads, same bits since rows are independent)."""
+    tok_s, dt, ok = cpu_decode(spec, weights, prompt, gen, threads, fixture)
+    model, ncpu = host_cpu()
+    return {"value": round(tok_s, 3), "unit": "tok/s", "cores": threads, "kind": "port",
+            "sample": "the full workload: %d greedy steps (positions %d..%d) after an untimed "
+                      "%d-token prefill, %d thread(s), %.1f s" % (
+                          gen, len(prompt), len(prompt) + gen - 1, len(prompt), threads, dt),
+            "witness_bit_exact": ok, "cpu_model": model, "host_cpus": ncpu}
 
 
 def batch_decode(spec, weights, sizes=(1, 8, 32, 64)):
@@ -284,31 +331,6 @@ def tree_decode(spec, weights, prompt, gen=256):
     return rec
 
 
-def cpu_baseline_parallel(spec, weights, prompt, seconds=10.0):
-    """The oracle with its GEMV rows split over the host cores (same bits:
-    rows are independent), forward passes at consecutive positions."""
-    import numpy as np
-
-    import _oracle as O
-    threads = max(1, min(16, os.cpu_count() or 1))
-    m = O.OracleModel(spec, weights, max_pos=len(prompt) + 512, threads=threads)
-    logits = np.empty(spec.vocab, np.float32)
-    L = O.lib()
-    t0 = time.perf_counter()
-    n = 0
-    tok = int(prompt[0])
-    while True:
-        L.orc_forward(m.m, n, tok, O.ptr(logits, O.c_fp), O.TRACE_FN(), None)
-        n += 1
-        tok = int(prompt[n]) if n < len(prompt) else int(L.orc_argmax(O.ptr(logits, O.c_fp), spec.vocab))
-        if time.perf_counter() - t0 > seconds or n >= len(prompt) + 500:
-            break
-    dt = time.perf_counter() - t0
-    return {"value": round(n / dt, 3), "unit": "tok/s", "cores": threads, "kind": "port",
-            "sample": "%d forward passes (positions 0..%d), GEMV rows over %d threads, %.1f s"
-                      % (n, n - 1, threads, dt)}
-
-
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -316,7 +338,6 @@ def main():
     ap.add_argument("--warmup", type=int, default=16)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-roofline", action="store_true")
-    ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-batch", action="store_true", help="skip the batched-decode sizes")
     ap.add_argument("--no-qwen3", action="store_true", help="skip the Qwen3 4096+256 run")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -340,14 +361,25 @@ def main():
         sys.exit(2)
     from cis2amd import Cis2Model, artifacts
     spec = artifacts.SPECS["smollm2-135m"]
+    if a.warmup < 0 or a.steps < 1 or a.warmup + a.steps > GEN:
+        print("bench.py: --warmup + --steps must be within the workload's %d decode steps "
+              "(1 <= steps, warmup >= 0)" % GEN, file=sys.stderr)
+        sys.exit(2)
     t = time.perf_counter()
     weights = artifacts.Weights(spec, SEED)
     prompt = artifacts.prompt_ids(SEED, spec.vocab, 32)
     log("weights generated in %.1fs" % (time.perf_counter() - t))
-    total = a.warmup + a.steps
-    model = Cis2Model(spec, weights, max_pos=len(prompt) + total)
+    fixture = None
+    fx_path = os.path.join(ROOT, "tests", "golden", "model_fixtures.json")
+    if os.path.exists(fx_path):
+        rec = json.load(open(fx_path)).get("smollm2-135m")
+        if rec and list(rec["prompt"]) == [int(v) for v in prompt] and rec["gen_toks"] == GEN:
+            fixture = rec
+    # the whole workload every run: prefill, `warmup` steps, `steps` timed
+    # steps, the rest of the 256 untimed; the witness covers all 256
+    model = Cis2Model(spec, weights, max_pos=len(prompt) + GEN)
     t = time.perf_counter()
-    model.begin(prompt, total)
+    model.begin(prompt, GEN)
     prefill_s = time.perf_counter() - t
     model.steps(a.warmup)  # returns with the stream drained
     model.profile(True)
@@ -356,18 +388,19 @@ def main():
     t1 = time.perf_counter()
     model.profile(False)
     launches, kernel_ms, positions = model.profile_read()
-    res = model.end(total)
+    rest = GEN - a.warmup - a.steps
+    if rest:
+        model.steps(rest)
+    res = model.end(GEN)
     dt = t1 - t0
     value = a.steps / dt
     witness_ok = None
-    fx_path = os.path.join(ROOT, "tests", "golden", "model_fixtures.json")
-    if total == 256 and os.path.exists(fx_path):
-        rec = json.load(open(fx_path)).get("smollm2-135m")
-        if rec and list(rec["prompt"]) == [int(v) for v in prompt]:
-            witness_ok = (res["witness"] == rec["witness"] and
-                          [int(v) for v in res["ids"]] == rec["tokens"])
-    log("decode: %d steps in %.3fs -> %.1f tok/s; prefill 32 tokens %.3fs; witness_ok=%s"
-        % (a.steps, dt, value, prefill_s, witness_ok))
+    if fixture is not None:
+        witness_ok = (res["witness"] == fixture["witness"] and
+                      [int(v) for v in res["ids"]] == fixture["tokens"])
+    log("decode: %d timed steps (steps %d..%d of %d) in %.3fs -> %.1f tok/s; prefill 32 tokens "
+        "%.3fs; witness_ok=%s" % (a.steps, a.warmup, a.warmup + a.steps - 1, GEN, dt, value,
+                                  prefill_s, witness_ok))
     roof = None
     if launches:
         algo = sum(decode_bytes(p) for p in positions)
@@ -377,19 +410,29 @@ def main():
                 "traffic": measured_traffic(),
                 "kernel": "k_decode (persistent: 30 layers + LM head + argmax per launch)",
                 "launches": launches, "us_per_launch": round(kernel_ms * 1e3 / launches, 2),
-                "algorithmic_bytes_per_launch": int(round(algo / launches))}
+                "algorithmic_bytes_per_launch": int(round(algo / launches)),
+                "positions": [int(positions[0]), int(positions[-1])]}
         log("decode kernel roofline:", roof)
     model.close()
+    cpu = None
+    if not a.no_cpu_baseline:
+        cpu = cpu_baseline(spec, weights, prompt, GEN, fixture, threads=1)
+        log("cpu baseline:", cpu)
     out = {
         "metric": METRIC, "value": round(value, 3), "unit": "tok/s", "n_gpus": 1,
         "steps": a.steps, "warmup": a.warmup, "ms_per_step": round(dt * 1e3 / a.steps, 4),
         "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": round(value / CPU_REF_TOKS, 2), "dtype": "f32", "data": "synthetic",
+        "vs_baseline": round(value / cpu["value"], 2) if cpu else None,
+        "dtype": "f32", "data": "synthetic",
         "config": {"workload": "SmolLM2-135M-shape fp32 greedy decode, bs=1, 32-token prompt "
                                "+ 256 generated tokens, seeded BF16 weights ~N(0,0.02)",
-                   "global_batch": 1, "seq_len": len(prompt) + total, "parallelism": "none"},
+                   "global_batch": 1, "seq_len": len(prompt) + GEN, "parallelism": "none",
+                   "timed_steps": [a.warmup, a.warmup + a.steps - 1]},
         "witness_bit_exact": witness_ok, "witness": res["witness"],
+        "vs_published_cpu": round(value / CPU_REF_TOKS, 2),
     }
+    if cpu is not None:
+        out["cpu_baseline"] = cpu
     if roof is not None:
         out["roofline"] = roof
     sd = sampled_decode(spec, weights, prompt)
@@ -405,10 +448,9 @@ def main():
     if not a.no_qwen3:
         out["qwen3_4096"] = qwen3_long()
     if not a.no_cpu_baseline:
-        out["cpu_baseline"] = cpu_baseline(spec, weights, prompt, a.cpu_seconds)
-        log("cpu baseline:", out["cpu_baseline"])
-        out["cpu_baseline_parallel"] = cpu_baseline_parallel(spec, weights, prompt,
-                                                             a.cpu_seconds * 2 / 3)
+        _model, ncpu = host_cpu()
+        out["cpu_baseline_parallel"] = cpu_baseline(spec, weights, prompt, GEN, fixture,
+                                                    threads=max(1, min(16, ncpu)))
         log("cpu baseline (row-parallel):", out["cpu_baseline_parallel"])
     print(json.dumps(out), flush=True)
 

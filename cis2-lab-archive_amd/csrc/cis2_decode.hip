@@ -639,10 +639,13 @@ __device__ __forceinline__ float gemv_lds(uint32_t R, lf* W, const lf* x, uint32
 }
 
 // Tree order (v0.4 candidate, code/cis2-fp/src/math.rs:60-125) on LDS row
-// blocks: after the product pass, item (block b, k block kb, row r) reduces
-// its row's 32 products k in [32kb, 32kb + 32) by tree32 (+0 past K) and
-// leaves the result in the first product slot; lane r of wave b then folds
-// its row's block results from 0.  R = 0: height given at run time (Rr).
+// blocks: item (block b, k block kb, row r) forms its row's 32 products
+// W[r][k] * x[k], k in [32kb, 32kb + 32), in registers (+0 past K), reduces
+// them by tree32 and leaves the result in its first weight slot; lane r of
+// wave b then folds its row's block results from 0.  Each product is one
+// rounding, so forming them in the item gives the bits of a separate product
+// pass, with a quarter of its LDS traffic (the weights are read once, x by
+// broadcast, no products written back).  R = 0: height given at run time (Rr).
 template <uint32_t R>
 __device__ __forceinline__ float gemv_tree_t(uint32_t Rr, lf* W, const lf* x, uint32_t K,
                                              uint32_t nb, lf4* pad) {
@@ -653,34 +656,27 @@ __device__ __forceinline__ float gemv_tree_t(uint32_t Rr, lf* W, const lf* x, ui
   lf4* W4 = (lf4*)W;
   const lf4* x4 = (const lf4*)x;
   const uint32_t bf4 = KG * Rv;
-  if constexpr (R != 0) {
-    constexpr uint32_t GP = 64 / R;
-    prod_ins<R>(W4, x4, bf4, nb, KG, 0, (KG + GP - 1) / GP, wv, kThreads / 64, pad);
-  } else {
-    for (uint32_t i = threadIdx.x; i < nb * bf4; i += kThreads) {
-      const f4 xv = x4[(i % bf4) / Rv];
-      f4 w = W4[i];
-      w.x = w.x * xv.x;
-      w.y = w.y * xv.y;
-      w.z = w.z * xv.z;
-      w.w = w.w * xv.w;
-      W4[i] = w;
-    }
-  }
-  __syncthreads();
   const uint32_t KB = (KG + 7) / 8, items = nb * KB * Rv;
   for (uint32_t it = threadIdx.x; it < items; it += kThreads) {
     const uint32_t r = it % Rv, q = it / Rv, kb = q % KB, b = q / KB;
     lf4* p = W4 + (size_t)b * bf4 + (size_t)kb * 8 * Rv + r;
+    const lf4* xp = x4 + (size_t)kb * 8;
+    f4 wv4[8], xv4[8];
+#pragma unroll
+    for (uint32_t j = 0; j < 8; ++j) {
+      if (kb * 8 + j < KG) {
+        wv4[j] = p[(size_t)j * Rv];
+        xv4[j] = xp[j];
+      }
+    }
     float lv[32];
 #pragma unroll
     for (uint32_t j = 0; j < 8; ++j) {
-      f4 v = {0.0f, 0.0f, 0.0f, 0.0f};
-      if (kb * 8 + j < KG) v = p[(size_t)j * Rv];
-      lv[4 * j] = v.x;
-      lv[4 * j + 1] = v.y;
-      lv[4 * j + 2] = v.z;
-      lv[4 * j + 3] = v.w;
+      const bool in = kb * 8 + j < KG;
+      lv[4 * j] = in ? wv4[j].x * xv4[j].x : 0.0f;
+      lv[4 * j + 1] = in ? wv4[j].y * xv4[j].y : 0.0f;
+      lv[4 * j + 2] = in ? wv4[j].z * xv4[j].z : 0.0f;
+      lv[4 * j + 3] = in ? wv4[j].w * xv4[j].w : 0.0f;
     }
     ((lf*)p)[0] = tree32(lv);
   }

@@ -65,7 +65,7 @@ struct DecodeArgs {
 
 // Floats (4-byte units) of one layer's tagged activation storage.
 size_t decode_act_floats(uint32_t H, uint32_t I, uint32_t qd, uint32_t kvd);
-constexpr uint32_t kTimelineTasks = 64;
+constexpr uint32_t kTimelineTasks = 256;
 constexpr uint32_t kMaxTasks = 6;       // tasks per workgroup per layer
 constexpr uint16_t kNoTask = 0xFFFF;
 // Phases of a layer, in dependency order.
