@@ -5,9 +5,10 @@
 // and digest/trace gates (code/cis2-fp/gpu/Makefile:160-184) apply as is.
 //
 //   cis2_host --weights-dir DIR --ids FILE [--gen-toks N] [--trace FILE]
-//             [--prompt-idx I] [--device D]
+//             [--prompt-idx I] [--reduction sequential|tree] [--sample SEED,T,K,P]
+//             [--verify2]
 #include "cis2_amd.h"
-#include "cis2_artifacts.hpp"
+#include "cis2_checkpoint.hpp"
 #include "cis2_sha256.hpp"
 
 #include <errno.h>
@@ -42,11 +43,6 @@ std::string ids_list(const std::vector<uint32_t>& v) {
   return s + "]";
 }
 
-void file_sha(const std::string& path, uint8_t out[32]) {
-  std::string b = read_file(path);
-  sha256(b.data(), b.size(), out);
-}
-
 struct TraceSink {
   FILE* fp = nullptr;
 };
@@ -55,10 +51,14 @@ void trace_cb(int pos, int layer, const char* op, const uint8_t sha[32], void* u
   fprintf(t->fp, "pos=%d layer=%d op=%s sha256=%s\n", pos, layer, op, hex(sha, 32).c_str());
 }
 
-uint32_t num_key(const JValue& cfg, const char* k) {
-  const JValue* v = cfg.find(k);
-  if (!v) fatal(std::string("config.json missing ") + k);
-  return (uint32_t)v->num;
+// A config.json dimension: a whole number that fits 32 bits.
+uint32_t dim_key(const JsonDoc& cfg, const char* k) {
+  uint64_t v = 0;
+  const JsonNode* n = cfg.member(cfg.root(), k);
+  if (!n) fatal(std::string("config.json missing ") + k);
+  if (!config_u64(n, &v) || v > 0xFFFFFFFFull)
+    fatal(std::string("config.json ") + k + " is not a 32-bit whole number");
+  return (uint32_t)v;
 }
 
 // "SEED,T,K,P": seed u64 (decimal or 0x hex), T and P by strtof (correctly
@@ -93,58 +93,97 @@ bool parse_sample(const char* txt, cis2_sampling* out) {
   return true;
 }
 
-}  // namespace
-
-int main(int argc, char** argv) {
+// Command-line settings with the reference driver's defaults
+// (code/cis2-fp/gpu/cis2_host.cpp:61-85).
+struct Options {
   std::string weights_dir = "weights", ids_path, trace_path;
   int gen_toks = 16, prompt_idx = 0;
   uint32_t reduction = 0;  // --reduction sequential|tree (code/cis2-fp/src/main.rs:775-782)
   // --sample SEED,T,K,P: seeded sampling (v0.4 draft section 14; the lab
   // driver's flag, labs/w1x-sample/feed/cm-hq__cis2-sample-hq-r2/job.sh:22-28)
-  cis2_sampling samp;
-  memset(&samp, 0, sizeof samp);
+  cis2_sampling samp{};
   // cis2-verify2 line protocol (code/cis2-fp/verify2/src/main.rs:353-500, parsed
   // by code/cis2-llm/server/app/runner.py:25-31): --verify2, or this binary
   // invoked under the name cis2-verify2
   bool verify2 = false;
-  {
-    std::string a0 = argv[0];
-    const size_t sl = a0.rfind('/');
-    verify2 = (sl == std::string::npos ? a0 : a0.substr(sl + 1)) == "cis2-verify2";
-  }
+};
+
+bool whole_int(const char* t, int* out) {
+  char* end = nullptr;
+  errno = 0;
+  const long v = strtol(t, &end, 10);
+  if (!*t || *end || errno || v < INT32_MIN || v > INT32_MAX) return false;
+  *out = (int)v;
+  return true;
+}
+
+// Flags as a table: name, whether a value follows, and what the value sets.
+// Returns an error message, or "" when the command line is accepted.
+std::string parse_options(int argc, char** argv, Options& o) {
+  const std::string self = argv[0];
+  o.verify2 = self.substr(self.rfind('/') == std::string::npos ? 0 : self.rfind('/') + 1) ==
+              "cis2-verify2";
+  struct Flag {
+    const char* name;
+    bool value;
+    std::string (*apply)(Options&, const char*);
+  };
+  static const Flag flags[] = {
+      {"--weights-dir", true, [](Options& o, const char* v) { o.weights_dir = v; return std::string(); }},
+      {"--ids", true, [](Options& o, const char* v) { o.ids_path = v; return std::string(); }},
+      {"--trace", true, [](Options& o, const char* v) { o.trace_path = v; return std::string(); }},
+      {"--gen-toks", true, [](Options& o, const char* v) {
+         return whole_int(v, &o.gen_toks) ? std::string() : "--gen-toks: not an integer: " + std::string(v);
+       }},
+      {"--prompt-idx", true, [](Options& o, const char* v) {
+         return whole_int(v, &o.prompt_idx) ? std::string() : "--prompt-idx: not an integer: " + std::string(v);
+       }},
+      {"--reduction", true, [](Options& o, const char* v) {
+         const std::string r = v;
+         if (r != "sequential" && r != "tree")
+           return "--reduction: expected 'sequential' or 'tree', got " + r;
+         o.reduction = r == "tree" ? 1u : 0u;
+         return std::string();
+       }},
+      {"--sample", true, [](Options& o, const char* v) {
+         return parse_sample(v, &o.samp)
+                    ? std::string()
+                    : "--sample: expected SEED,T,K,P with T finite > 0 and P in (0,1], got " +
+                          std::string(v);
+       }},
+      {"--verify2", false, [](Options& o, const char*) { o.verify2 = true; return std::string(); }},
+  };
   for (int i = 1; i < argc; ++i) {
-    std::string a = argv[i];
-    if (a == "--weights-dir" && i + 1 < argc) weights_dir = argv[++i];
-    else if (a == "--ids" && i + 1 < argc) ids_path = argv[++i];
-    else if (a == "--gen-toks" && i + 1 < argc) gen_toks = atoi(argv[++i]);
-    else if (a == "--trace" && i + 1 < argc) trace_path = argv[++i];
-    else if (a == "--prompt-idx" && i + 1 < argc) prompt_idx = atoi(argv[++i]);
-    else if (a == "--reduction" && i + 1 < argc) {
-      std::string r = argv[++i];
-      if (r == "sequential") reduction = 0;
-      else if (r == "tree") reduction = 1;
-      else {
-        fprintf(stderr, "FATAL: --reduction: expected 'sequential' or 'tree', got %s\n",
-                r.c_str());
-        return 2;
-      }
-    }
-    else if (a == "--verify2") verify2 = true;
-    else if (a == "--sample" && i + 1 < argc) {
-      if (!parse_sample(argv[++i], &samp)) {
-        fprintf(stderr, "FATAL: --sample: expected SEED,T,K,P with T finite > 0 and P in (0,1], "
-                        "got %s\n", argv[i]);
-        return 2;
-      }
-    }
-    else { fprintf(stderr, "FATAL: unknown CLI argument: %s\n", a.c_str()); return 2; }
+    const Flag* f = nullptr;
+    for (const Flag& c : flags)
+      if (!strcmp(argv[i], c.name)) f = &c;
+    if (!f || (f->value && i + 1 >= argc)) return std::string("unknown CLI argument: ") + argv[i];
+    const std::string err = f->apply(o, f->value ? argv[++i] : nullptr);
+    if (!err.empty()) return err;
   }
+  return "";
+}
+
+}  // namespace
+
+int main(int argc, char** argv) {
+  Options opt;
+  if (const std::string err = parse_options(argc, argv, opt); !err.empty()) {
+    fprintf(stderr, "FATAL: %s\n", err.c_str());
+    return 2;
+  }
+  const std::string& ids_path = opt.ids_path;
+  const std::string& trace_path = opt.trace_path;
+  const int gen_toks = opt.gen_toks, prompt_idx = opt.prompt_idx;
+  const uint32_t reduction = opt.reduction;
+  const cis2_sampling& samp = opt.samp;
+  const bool verify2 = opt.verify2;
   if (ids_path.empty() && !verify2) fatal("--ids FILE is required");
   if (gen_toks < 0) fatal("--gen-toks must be >= 0");
-  const std::string wpath = weights_dir + "/model.safetensors";
-  const std::string tpath = weights_dir + "/tokenizer.json";
-  const std::string cpath = weights_dir + "/config.json";
-  JValue cfgj = parse_json(read_file(cpath));
+  const std::string wpath = opt.weights_dir + "/model.safetensors";
+  const std::string tpath = opt.weights_dir + "/tokenizer.json";
+  const std::string cpath = opt.weights_dir + "/config.json";
+  const JsonDoc cfgj = parse_json_text(slurp(cpath));
   // scope gate on config.json alone, before any weights are opened or hashed
   // (code/cis2-fp/src/main.rs:817-823)
   const std::string reason = gate_architecture(cfgj);
@@ -154,30 +193,42 @@ int main(int argc, char** argv) {
     return 2;
   }
   uint8_t hdr[96];
-  file_sha(wpath, hdr);
-  file_sha(tpath, hdr + 32);
-  file_sha(cpath, hdr + 64);
+  hash_file(wpath, hdr);
+  hash_file(tpath, hdr + 32);
+  hash_file(cpath, hdr + 64);
 
   cis2_config cfg;
   memset(&cfg, 0, sizeof cfg);
-  cfg.hidden = num_key(cfgj, "hidden_size");
-  cfg.inter = num_key(cfgj, "intermediate_size");
-  cfg.n_layers = num_key(cfgj, "num_hidden_layers");
-  cfg.n_heads = num_key(cfgj, "num_attention_heads");
-  cfg.n_kv_heads = num_key(cfgj, "num_key_value_heads");
-  cfg.vocab = num_key(cfgj, "vocab_size");
-  const JValue* eps = cfgj.find("rms_norm_eps");
-  const JValue* theta = cfgj.find("rope_theta");
-  if (!eps) fatal("config.json missing rms_norm_eps");
-  if (!theta) fatal("config.json missing rope_theta");
-  cfg.eps = (float)eps->num;  // one narrowing, as `as f32` does
-  cfg.rope_theta = theta->num;
+  cfg.hidden = dim_key(cfgj, "hidden_size");
+  cfg.inter = dim_key(cfgj, "intermediate_size");
+  cfg.n_layers = dim_key(cfgj, "num_hidden_layers");
+  cfg.n_heads = dim_key(cfgj, "num_attention_heads");
+  cfg.n_kv_heads = dim_key(cfgj, "num_key_value_heads");
+  cfg.vocab = dim_key(cfgj, "vocab_size");
+  const JsonNode* eps = cfgj.member(cfgj.root(), "rms_norm_eps");
+  const JsonNode* theta = cfgj.member(cfgj.root(), "rope_theta");
+  if (!eps || eps->type != JsonNode::Number) fatal("config.json missing rms_norm_eps");
+  if (!theta || theta->type != JsonNode::Number) fatal("config.json missing rope_theta");
+  cfg.eps = (float)eps->number;  // one narrowing, as `as f32` does
+  cfg.rope_theta = theta->number;
   if (cfg.n_heads == 0) fatal("num_attention_heads must be > 0");
+  // head_dim: hidden / heads, as the reference derives it
+  // (code/cis2-fp/gpu/cis2_host.cpp:114); an explicit value only for qwen3
+  // (labs/w1x-qwen3/scripts/qwen3-port.diff:104-110; the gate refuses any
+  // other explicit value that differs), absent or null = derived
   cfg.head_dim = cfg.hidden / cfg.n_heads;
-  if (const JValue* hd = cfgj.find("head_dim")) cfg.head_dim = (uint32_t)hd->num;
+  {
+    const JsonNode* mt = cfgj.member(cfgj.root(), "model_type");
+    uint64_t hd = 0;
+    if (mt && mt->type == JsonNode::String && mt->text == "qwen3" &&
+        config_u64(cfgj.member(cfgj.root(), "head_dim"), &hd)) {
+      if (hd == 0 || hd > 0xFFFFFFFFull) fatal("config.json head_dim out of range");
+      cfg.head_dim = (uint32_t)hd;
+    }
+  }
   cfg.tied = 1;
-  if (const JValue* t = cfgj.find("tie_word_embeddings"))
-    cfg.tied = (t->kind == JValue::BOOL) ? (t->b ? 1 : 0) : 1;
+  if (const JsonNode* t = cfgj.member(cfgj.root(), "tie_word_embeddings"))
+    cfg.tied = (t->type == JsonNode::Bool) ? (t->flag ? 1 : 0) : 1;
   // verify2 without --ids: the section 13.1 prompt, "Once upon a time" under
   // the SmolLM2 tokenizer (verify2/src/main.rs:436-444)
   std::vector<uint32_t> prompt =
@@ -186,30 +237,23 @@ int main(int argc, char** argv) {
   cfg.max_seqs = 1;
   cfg.reduction_mode = reduction;
 
-  // Every tensor is checked (presence, dtype, shape, byte range) before the
-  // device is touched, so a bad file fails fast and identically everywhere.
-  fprintf(stderr, "loading + widening weights (bf16 -> fp32, exact bit-shift)...\n");
-  SafeTensors st;
-  st.open(wpath);
+  // The header and every tensor's dtype and shape are checked before the
+  // device is touched, so a bad file fails fast and identically everywhere;
+  // the payloads are then read and uploaded one tensor at a time.
+  Checkpoint ck;
+  ck.open(wpath);
   const uint64_t H = cfg.hidden, I = cfg.inter, V = cfg.vocab;
   const uint64_t QD = (uint64_t)cfg.n_heads * cfg.head_dim,
                  KV = (uint64_t)cfg.n_kv_heads * cfg.head_dim, HD = cfg.head_dim;
-  struct Up {
-    std::string name;
-    const uint16_t* p;
-    uint64_t n;
-  };
-  std::vector<Up> ups;
+  std::vector<const Checkpoint::Tensor*> plan;
   auto need = [&](const std::string& name, std::vector<uint64_t> shape, bool optional) {
-    const TensorView* t = st.find(name);
+    const Checkpoint::Tensor* t = ck.find(name);
     if (!t) {
       if (optional) return;
       fatal("tensor " + name + " missing");
     }
-    const uint16_t* p = st.bf16(*t, shape);
-    uint64_t n = 1;
-    for (auto d : shape) n *= d;
-    ups.push_back(Up{name, p, n});
+    ck.require_bf16(*t, shape);
+    plan.push_back(t);
   };
   need("model.embed_tokens.weight", {V, H}, false);
   for (uint32_t l = 0; l < cfg.n_layers; ++l) {
@@ -239,15 +283,19 @@ int main(int argc, char** argv) {
     rc = cis2_set_sampling(ctx, &samp);
     if (rc) fatal(std::string("--sample: ") + cis2_last_error(ctx));
   }
-  for (const Up& u : ups) {
-    rc = cis2_upload_bf16(ctx, u.name.c_str(), u.p, u.n);
-    if (rc) fatal("upload " + u.name + ": " + cis2_last_error(ctx));
+  fprintf(stderr, "cis2_host: %zu tensors, read one at a time and widened on the device\n",
+          plan.size());
+  {
+    std::vector<uint16_t> buf;  // one tensor's payload at a time
+    for (const Checkpoint::Tensor* t : plan) {
+      ck.read_bf16(*t, buf);
+      rc = cis2_upload_bf16(ctx, t->name.c_str(), buf.data(), t->elements);
+      if (rc) fatal("upload " + t->name + ": " + cis2_last_error(ctx));
+    }
   }
-  st.blob.clear();
-  st.blob.shrink_to_fit();
+  ck.close();
   rc = cis2_check_ready(ctx);
   if (rc) fatal(cis2_last_error(ctx));
-  fprintf(stderr, "weights loaded.\n");
   fprintf(stderr, "[prompt %d] token ids (%zu toks): %s\n", prompt_idx, prompt.size(),
           ids_list(prompt).c_str());
 

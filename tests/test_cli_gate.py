@@ -99,6 +99,7 @@ def test_gate_checks(extra, reason, tmp_path):
 @pytest.mark.parametrize("extra", [
     {}, {"partial_rotary_factor": 1.0}, {"use_sliding_window": False}, {"head_dim": 64},
     {"model_type": "qwen3", "head_dim": 128}, {"model_type": "qwen2"},
+    {"head_dim": None}, {"model_type": "qwen3", "head_dim": None},
 ])
 def test_gate_accepts(extra, tmp_path):
     d = tmp_path / "w"

@@ -91,3 +91,26 @@ def test_verify2_line_protocol(tmp_path):
     assert got["table_digest"] == t and got["inv_freq_table_digest"] == f
     assert [int(x) for x in got["generated_token_ids"].split(",")] == [int(v) for v in want["ids"][4:]]
     assert r.stdout.splitlines()[0].endswith(" prompt_toks=4 gen_toks=16 dtype=fp32")
+
+
+def test_cli_head_dim_null_derives(model_fixtures, tmp_path):
+    """A llama config.json with "head_dim": null passes the gate and runs
+    with the derived head_dim (hidden / heads), as the reference driver
+    derives it (code/cis2-fp/gpu/cis2_host.cpp:114): the tokens and the
+    argmax digest equal the fixture's (the witness binds config.json's hash,
+    which the null key changes)."""
+    import json
+    rec = model_fixtures["tiny-llama"]
+    spec = artifacts.SPECS[rec["spec"]]
+    artifacts.Weights(spec, rec["seed"]).write_dir(str(tmp_path))
+    cfg = json.loads((tmp_path / "config.json").read_text())
+    cfg["head_dim"] = None
+    (tmp_path / "config.json").write_text(json.dumps(cfg))
+    ids = tmp_path / "ids.txt"
+    ids.write_text("\n".join(str(t) for t in rec["prompt"]) + "\n")
+    r = subprocess.run([CLI, "--weights-dir", str(tmp_path), "--ids", str(ids), "--gen-toks",
+                        str(rec["gen_toks"])], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stderr[-2000:]
+    assert "run1_argmax_digest=%s" % rec["argmax_digest"] in r.stdout
+    toks = re.search(r"run1_tokens=\[([0-9, ]*)\]", r.stdout).group(1)
+    assert [int(t) for t in toks.split(",")] == rec["tokens"]

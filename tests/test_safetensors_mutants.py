@@ -147,7 +147,8 @@ def test_reader_under_sanitizers(model_dir, tmp_path):
     src = os.path.join(ROOT, "tests", "st_harness.cpp")
     inc = os.path.join(ROOT, "cis2-lab-archive_amd", "csrc")
     b = subprocess.run([gxx, "-std=c++17", "-O1", "-g", "-fsanitize=address,undefined",
-                        "-fno-sanitize-recover=undefined", "-I" + inc, "-o", str(exe), src],
+                        "-fno-sanitize-recover=undefined", "-I" + inc, "-o", str(exe), src,
+                        os.path.join(inc, "cis2_sha256.cpp")],
                        capture_output=True, text=True, timeout=300)
     assert b.returncode == 0, b.stderr[-2000:]
     blob = (model_dir / "model.safetensors").read_bytes()
