@@ -35,6 +35,7 @@
 // access is a ds_* or global_* instruction, never flat_*.
 #include "cis2_decode.hpp"
 #include "cis2_device_math.hpp"
+#include "cis2_kernels.hpp"
 
 namespace cis2 {
 
@@ -1673,13 +1674,8 @@ size_t gemv_blk_lds_bytes(uint32_t K, uint32_t R) {
 template <uint32_t R, uint32_t KC>
 static hipError_t launch_gemv_blk_t(const float* W, const float* x, float* y, uint32_t M,
                                     uint32_t K, size_t lds, hipStream_t s) {
-  static size_t configured = 0;
-  if (lds > configured) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemv_blk<R, KC>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    if (e != hipSuccess) return e;
-    configured = lds;
-  }
+  hipError_t e = ensure_dynamic_lds(reinterpret_cast<const void*>(&k_gemv_blk<R, KC>), lds);
+  if (e != hipSuccess) return e;
   hipLaunchKernelGGL((k_gemv_blk<R, KC>), dim3((M + R - 1) / R), dim3(kThreads), lds, s, W, x,
                      y, M, K);
   return hipGetLastError();
@@ -1702,13 +1698,8 @@ template <uint32_t R, uint32_t KC>
 static hipError_t launch_gemv_many_t(const float* W, uint64_t w_per, uint32_t copies,
                                      uint32_t first, uint32_t n, const float* x, float* y,
                                      uint32_t M, uint32_t K, size_t lds, hipStream_t s) {
-  static size_t configured = 0;
-  if (lds > configured) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemv_many<R, KC>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    if (e != hipSuccess) return e;
-    configured = lds;
-  }
+  hipError_t e = ensure_dynamic_lds(reinterpret_cast<const void*>(&k_gemv_many<R, KC>), lds);
+  if (e != hipSuccess) return e;
   hipLaunchKernelGGL((k_gemv_many<R, KC>), dim3((M + R - 1) / R, n), dim3(kThreads), lds, s, W,
                      w_per, copies, first, x, y, M, K);
   return hipGetLastError();
@@ -1754,31 +1745,43 @@ size_t decode_lds_bytes(const DecodeArgs& a) {
   return decode_wregion_bytes(a) + decode_vec_floats(a) * 4 + 64 * 16 + 256;
 }
 
-template <bool TR, int SH>
-hipError_t launch_decode_t(const DecodeArgs& a, hipStream_t s) {
-  const size_t lds = decode_lds_bytes(a);
-  static size_t configured = 0;
-  if (lds > configured) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_decode<TR, SH>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    if (e != hipSuccess) return e;
-    configured = lds;
+// The k_decode instance for the arguments' order and shape.
+static const void* decode_kernel(const DecodeArgs& a) {
+  if (a.tree) {  // the v0.4-candidate order, with the same compile-time shapes
+    if (shape_matches(a, kShapes[1])) return reinterpret_cast<const void*>(&k_decode<true, 1>);
+    if (shape_matches(a, kShapes[2])) return reinterpret_cast<const void*>(&k_decode<true, 2>);
+    if (shape_matches(a, kShapes[3])) return reinterpret_cast<const void*>(&k_decode<true, 3>);
+    return reinterpret_cast<const void*>(&k_decode<true, 0>);
   }
-  hipLaunchKernelGGL((k_decode<TR, SH>), dim3(a.nwg), dim3(kThreads), lds, s, a);
-  return hipGetLastError();
+  if (shape_matches(a, kShapes[1])) return reinterpret_cast<const void*>(&k_decode<false, 1>);
+  if (shape_matches(a, kShapes[2])) return reinterpret_cast<const void*>(&k_decode<false, 2>);
+  if (shape_matches(a, kShapes[3])) return reinterpret_cast<const void*>(&k_decode<false, 3>);
+  return reinterpret_cast<const void*>(&k_decode<false, 0>);
 }
 
+hipError_t decode_coresident(const DecodeArgs& a, uint32_t ncu, bool* ok) {
+  *ok = false;
+  const void* fn = decode_kernel(a);
+  const size_t lds = decode_lds_bytes(a);
+  hipError_t e = ensure_dynamic_lds(fn, lds);
+  if (e != hipSuccess) return e;
+  int per_cu = 0;
+  e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, (int)kThreads, lds);
+  if (e != hipSuccess) return e;
+  *ok = per_cu > 0 && (uint64_t)per_cu * ncu >= a.nwg;
+  return hipSuccess;
+}
+
+// A cooperative launch: the runtime starts every workgroup at once or
+// refuses the launch, so the phase waits never depend on workgroups that
+// are not resident.
 hipError_t launch_decode(const DecodeArgs& a, hipStream_t s) {
-  if (a.tree) {  // the v0.4-candidate order, with the same compile-time shapes
-    if (shape_matches(a, kShapes[1])) return launch_decode_t<true, 1>(a, s);
-    if (shape_matches(a, kShapes[2])) return launch_decode_t<true, 2>(a, s);
-    if (shape_matches(a, kShapes[3])) return launch_decode_t<true, 3>(a, s);
-    return launch_decode_t<true, 0>(a, s);
-  }
-  if (shape_matches(a, kShapes[1])) return launch_decode_t<false, 1>(a, s);
-  if (shape_matches(a, kShapes[2])) return launch_decode_t<false, 2>(a, s);
-  if (shape_matches(a, kShapes[3])) return launch_decode_t<false, 3>(a, s);
-  return launch_decode_t<false, 0>(a, s);
+  const void* fn = decode_kernel(a);
+  const size_t lds = decode_lds_bytes(a);
+  hipError_t e = ensure_dynamic_lds(fn, lds);
+  if (e != hipSuccess) return e;
+  void* args[] = {const_cast<DecodeArgs*>(&a)};
+  return hipLaunchCooperativeKernel(fn, dim3(a.nwg), dim3(kThreads), args, (unsigned)lds, s);
 }
 
 }  // namespace cis2

@@ -81,6 +81,9 @@ void decode_att_plan(DecodeArgs& a, bool split);
 // True when one workgroup cannot hold a head's K/V rows at max_pos.
 bool decode_att_needs_split(const DecodeArgs& a);
 hipError_t launch_decode(const DecodeArgs& a, hipStream_t s);
+// *ok: every one of the a.nwg workgroups can be resident at once on the
+// current device (ncu CUs) with the kernel's LDS and registers.
+hipError_t decode_coresident(const DecodeArgs& a, uint32_t ncu, bool* ok);
 
 // Standalone strict-order GEMV y = W x on the blocked layout with R rows per
 // block (R = 16 or 32): one workgroup per block, block and x staged in LDS.

@@ -6,6 +6,10 @@
 #include "cis2_device_math.hpp"
 #include "cis2_kernels.hpp"
 
+#include <map>
+#include <mutex>
+#include <utility>
+
 #include <float.h>
 #include <string.h>
 
@@ -610,6 +614,20 @@ hipError_t launch_div_map(const float* a, const float* b, float* out, uint64_t n
                           hipStream_t s) {
   hipLaunchKernelGGL(k_div_map, dim3(1024), dim3(256), 0, s, a, b, out, n);
   return hipGetLastError();
+}
+
+hipError_t ensure_dynamic_lds(const void* fn, size_t bytes) {
+  static std::mutex mu;
+  static std::map<std::pair<int, const void*>, size_t> done;
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  std::lock_guard<std::mutex> g(mu);
+  size_t& have = done[{dev, fn}];
+  if (have >= bytes) return hipSuccess;
+  e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+  if (e == hipSuccess) have = bytes;
+  return e;
 }
 
 }  // namespace cis2

@@ -16,6 +16,12 @@ namespace cis2 {
 // Rows past M in the last block are zero.  K must be a multiple of 4.
 size_t blocked_floats(uint32_t M, uint32_t K, uint32_t R);
 
+// Raises kernel fn's dynamic-LDS limit to at least `bytes` on the current
+// device.  Each (device, kernel) is configured once per size: a process-wide
+// table under a lock, so contexts on different devices or host threads each
+// see their own device's setting.
+hipError_t ensure_dynamic_lds(const void* fn, size_t bytes);
+
 // One output segment of a multi-segment GEMV launch.
 struct GemvSeg {
   const float* W;      // blocked weights

@@ -5,6 +5,7 @@
 // which other rows share the launch (batch invariance).
 #include "cis2_device_math.hpp"
 #include "cis2_rows.hpp"
+#include "cis2_kernels.hpp"
 
 #include <algorithm>
 #include <cstdlib>
@@ -961,8 +962,6 @@ hipError_t launch_bgemm_t(const BgemmArgs& a, dim3 grid, size_t lds, hipStream_t
 // The LDS limit of every k_bgemm variant, set at the first launch of any
 // (so that no attribute call happens later, e.g. inside a graph capture).
 hipError_t bgemm_configure() {
-  static bool configured = false;
-  if (configured) return hipSuccess;
   const void* fns[6] = {reinterpret_cast<const void*>(&k_bgemm<false, false, 1>),
                         reinterpret_cast<const void*>(&k_bgemm<false, true, 1>),
                         reinterpret_cast<const void*>(&k_bgemm<true, false, 1>),
@@ -970,11 +969,9 @@ hipError_t bgemm_configure() {
                         reinterpret_cast<const void*>(&k_bgemm<false, false, 2>),
                         reinterpret_cast<const void*>(&k_bgemm<true, false, 2>)};
   for (const void* f : fns) {
-    hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       (int)kBgemmLdsBig);
+    hipError_t e = ensure_dynamic_lds(f, kBgemmLdsBig);
     if (e != hipSuccess) return e;
   }
-  configured = true;
   return hipSuccess;
 }
 
@@ -1160,13 +1157,8 @@ static hipError_t launch_att_tiles_t(const float* q, const float* kc, const floa
                                      float* scratch, uint32_t ls, hipStream_t st) {
   using C = AttTileCfg<HPW, HD, TK>;
   const size_t lds = C::floats * sizeof(float);
-  static bool configured = false;
-  if (!configured) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_attention_tiles<HPW, HD, TK>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    if (e != hipSuccess) return e;
-    configured = true;
-  }
+  hipError_t e = ensure_dynamic_lds(reinterpret_cast<const void*>(&k_attention_tiles<HPW, HD, TK>), lds);
+  if (e != hipSuccess) return e;
   hipLaunchKernelGGL((k_attention_tiles<HPW, HD, TK>), dim3(ntiles, nh / HPW), dim3(256), lds, st,
                      q, kc, vc, tiles, nh, max_pos, seq_stride, scale, out, scratch, ls);
   return hipGetLastError();

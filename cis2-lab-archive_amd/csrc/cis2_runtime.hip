@@ -922,6 +922,10 @@ int cis2_ctx_create(const cis2_config* cfg, cis2_ctx** out) {
              decode_att_ok(a);
     };
     c->fast_ok = plan(32) || plan(64);
+    if (c->fast_ok) {  // every workgroup resident at once, or the per-op path
+      bool res = false;
+      if (decode_coresident(a, c->ncu, &res) != hipSuccess || !res) c->fast_ok = false;
+    }
     c->Rq = a.Rq; c->Ro = a.Ro; c->Rg = a.Rg; c->Rd = a.Rd; c->Rl = a.Rl;
     void* p = nullptr;
     if (hipMalloc(&p, c->wg_tasks.size() * sizeof(uint16_t)) != hipSuccess) {
