@@ -1772,16 +1772,20 @@ hipError_t decode_coresident(const DecodeArgs& a, uint32_t ncu, bool* ok) {
   return hipSuccess;
 }
 
-// A cooperative launch: the runtime starts every workgroup at once or
-// refuses the launch, so the phase waits never depend on workgroups that
-// are not resident.
+// A plain launch of a grid the context checked at creation to fit the
+// device at once (decode_coresident).  Not a cooperative launch: once one
+// process has made a cooperative launch on a GPU, every other process's
+// cooperative launch there fails ("cannot be performed in the present
+// state", measured on MI355X), which would stop a second worker process.
+// Should other work hold CUs so that some workgroups start late, the phase
+// waits' spin cap ends the launch with an error instead of a hang.
 hipError_t launch_decode(const DecodeArgs& a, hipStream_t s) {
   const void* fn = decode_kernel(a);
   const size_t lds = decode_lds_bytes(a);
   hipError_t e = ensure_dynamic_lds(fn, lds);
   if (e != hipSuccess) return e;
   void* args[] = {const_cast<DecodeArgs*>(&a)};
-  return hipLaunchCooperativeKernel(fn, dim3(a.nwg), dim3(kThreads), args, (unsigned)lds, s);
+  return hipLaunchKernel(fn, dim3(a.nwg), dim3(kThreads), args, lds, s);
 }
 
 }  // namespace cis2

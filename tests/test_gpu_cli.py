@@ -114,3 +114,27 @@ def test_cli_head_dim_null_derives(model_fixtures, tmp_path):
     assert "run1_argmax_digest=%s" % rec["argmax_digest"] in r.stdout
     toks = re.search(r"run1_tokens=\[([0-9, ]*)\]", r.stdout).group(1)
     assert [int(t) for t in toks.split(",")] == rec["tokens"]
+
+
+def test_second_process_decodes_beside_a_live_context(model_fixtures, tmp_path):
+    """Two processes on one GPU: while this process holds a context that has
+    run the persistent decode kernel, the CLI in a child process decodes the
+    same case with the same digest (the kernel's launch must not need a
+    per-device resource that the first process keeps)."""
+    from cis2amd import Cis2Model
+    rec = model_fixtures["tiny-llama"]
+    spec = artifacts.SPECS[rec["spec"]]
+    w = artifacts.Weights(spec, rec["seed"])
+    m = Cis2Model(spec, w, max_pos=len(rec["prompt"]) + rec["gen_toks"])
+    try:
+        assert m.decode(rec["prompt"], rec["gen_toks"])["witness"] == rec["witness"]
+        w.write_dir(str(tmp_path))
+        ids = tmp_path / "ids.txt"
+        ids.write_text("\n".join(str(t) for t in rec["prompt"]) + "\n")
+        r = subprocess.run([CLI, "--weights-dir", str(tmp_path), "--ids", str(ids), "--gen-toks",
+                            str(rec["gen_toks"])], capture_output=True, text=True, timeout=120)
+        assert r.returncode == 0, r.stderr[-2000:]
+        assert "CIS2_REF digest=%s" % rec["witness"] in r.stdout
+        assert m.decode(rec["prompt"], rec["gen_toks"])["witness"] == rec["witness"]
+    finally:
+        m.close()
