@@ -6,9 +6,11 @@
 //
 //   cis2_host --weights-dir DIR --ids FILE [--gen-toks N] [--trace FILE]
 //             [--prompt-idx I] [--reduction sequential|tree] [--sample SEED,T,K,P]
-//             [--verify2]
+//             [--verify2] [--receipt-log FILE]
+//   cis2_host --verify-chain FILE [--receipt-id ID]
 #include "cis2_amd.h"
 #include "cis2_checkpoint.hpp"
+#include "cis2_receipts.hpp"
 #include "cis2_sha256.hpp"
 
 #include <errno.h>
@@ -106,6 +108,10 @@ struct Options {
   // by code/cis2-llm/server/app/runner.py:25-31): --verify2, or this binary
   // invoked under the name cis2-verify2
   bool verify2 = false;
+  // hash-chained receipt log (code/cis2-llm/server/app/receipts.py:31-97):
+  // --receipt-log FILE appends this run's receipt; --verify-chain FILE
+  // [--receipt-id ID] checks a log (through ID) and exits 0 / 1
+  std::string receipt_log, verify_chain, receipt_id;
 };
 
 bool whole_int(const char* t, int* out) {
@@ -152,6 +158,9 @@ std::string parse_options(int argc, char** argv, Options& o) {
                           std::string(v);
        }},
       {"--verify2", false, [](Options& o, const char*) { o.verify2 = true; return std::string(); }},
+      {"--receipt-log", true, [](Options& o, const char* v) { o.receipt_log = v; return std::string(); }},
+      {"--verify-chain", true, [](Options& o, const char* v) { o.verify_chain = v; return std::string(); }},
+      {"--receipt-id", true, [](Options& o, const char* v) { o.receipt_id = v; return std::string(); }},
   };
   for (int i = 1; i < argc; ++i) {
     const Flag* f = nullptr;
@@ -171,6 +180,17 @@ int main(int argc, char** argv) {
   if (const std::string err = parse_options(argc, argv, opt); !err.empty()) {
     fprintf(stderr, "FATAL: %s\n", err.c_str());
     return 2;
+  }
+  if (!opt.verify_chain.empty()) {  // no model, no device: check the log and exit
+    FILE* f = fopen(opt.verify_chain.c_str(), "rb");
+    if (!f) fatal("cannot open " + opt.verify_chain);
+    fclose(f);
+    const std::string text = slurp(opt.verify_chain);
+    const ChainResult r =
+        verify_chain_text(text, opt.receipt_id.empty() ? nullptr : &opt.receipt_id);
+    printf("CIS2_CHAIN %s records=%zu head=%s message=%s\n", r.ok ? "PASS" : "FAIL", r.records,
+           r.last_hash.c_str(), r.message.c_str());
+    return r.ok ? 0 : 1;
   }
   const std::string& ids_path = opt.ids_path;
   const std::string& trace_path = opt.trace_path;
@@ -333,6 +353,45 @@ int main(int argc, char** argv) {
     printf("generated_token_ids=%s\n", ids_list(gen).c_str());
     cis2_ctx_destroy(ctx);
     return 0;
+  }
+  if (!opt.receipt_log.empty()) {
+    uint8_t table[32], invf[32];
+    cis2_digests(ctx, table, invf);
+    const JsonNode* mt = cfgj.member(cfgj.root(), "model_type");
+    std::vector<uint32_t> gen(ids.begin() + (long)prompt.size(), ids.end());
+    std::vector<ReceiptField> f = {
+        {"receipt_id", json_string(new_receipt_id())},
+        {"created", json_string(utc_now_iso())},
+        {"model", json_string("cis2-" + (mt && mt->type == JsonNode::String ? mt->text : "llama") +
+                              "-fp32")},
+        {"cis2_version", json_string(reduction ? "v0.4-candidate-tree" : "v0.3b")},
+        {"reduction_mode", json_string(reduction ? "tree" : "sequential")},
+        {"backend", json_string("gfx950")},
+        {"witness_digest", json_string(hex(wit, 32))},
+        {"argmax_digest", json_string(hex(adig, 32))},
+        {"table_digest", json_string(hex(table, 32))},
+        {"inv_freq_table_digest", json_string(hex(invf, 32))},
+        {"weights_sha256", json_string(hex(hdr, 32))},
+        {"tokenizer_sha256", json_string(hex(hdr + 32, 32))},
+        {"config_sha256", json_string(hex(hdr + 64, 32))},
+        {"prompt_idx", std::to_string(prompt_idx)},
+        {"prompt_token_ids", json_u32_list(prompt)},
+        {"generated_token_ids", json_u32_list(gen)},
+    };
+    if (samp.mode) {
+      uint32_t tb, pb;
+      memcpy(&tb, &samp.temperature, 4);
+      memcpy(&pb, &samp.top_p, 4);
+      char sb[160];
+      snprintf(sb, sizeof sb,
+               "{\"seed\":%llu,\"temperature_bits\":%u,\"top_k\":%u,\"top_p_bits\":%u}",
+               (unsigned long long)samp.seed, tb, samp.top_k, pb);
+      f.emplace_back("sampling", sb);
+    }
+    const auto ar = append_receipt(opt.receipt_log, f);
+    if (!ar.first) fatal("--receipt-log: " + ar.second);
+    fprintf(stderr, "receipt appended to %s: log_hash=%s\n", opt.receipt_log.c_str(),
+            ar.second.c_str());
   }
   for (int s = 0; s < gen_toks; ++s)
     fprintf(stderr, "[run1] step %d: token_id=%u\n", s, ids[prompt.size() + s]);

@@ -28,7 +28,7 @@ struct JsonNode {
   Type type = Null;
   bool flag = false;     // Bool
   double number = 0.0;   // Number: strtod of the lexeme (correctly rounded)
-  std::string text;      // String: decoded UTF-8
+  std::string text;      // String: decoded UTF-8; Number: the lexeme as written
   std::string key;       // member name, when the parent is an Object
   int32_t first = -1;    // first child (Array, Object)
   int32_t next = -1;     // next sibling
@@ -136,7 +136,12 @@ class JsonDoc {
                 st = t == Tok::BeginObject ? FirstKeyOrEnd : Value;
                 break;
               case Tok::Str: v.type = JsonNode::String; v.text = tok_text_; st = after_value(); break;
-              case Tok::Num: v.type = JsonNode::Number; v.number = tok_num_; st = after_value(); break;
+              case Tok::Num:
+                v.type = JsonNode::Number;
+                v.number = tok_num_;
+                v.text = tok_text_;
+                st = after_value();
+                break;
               case Tok::True: v.type = JsonNode::Bool; v.flag = true; st = after_value(); break;
               case Tok::False: v.type = JsonNode::Bool; st = after_value(); break;
               case Tok::Null: st = after_value(); break;
@@ -243,8 +248,8 @@ class JsonDoc {
         if (p_ < e_ && (*p_ == '+' || *p_ == '-')) ++p_;
         if (digits() == 0) fail("malformed number");
       }
-      const std::string lexeme(s, p_);
-      tok_num_ = strtod(lexeme.c_str(), nullptr);
+      tok_text_.assign(s, p_);
+      tok_num_ = strtod(tok_text_.c_str(), nullptr);
     }
     uint32_t hex4() {
       if (e_ - p_ < 4) fail("truncated \\u escape");

@@ -138,3 +138,41 @@ def test_second_process_decodes_beside_a_live_context(model_fixtures, tmp_path):
         assert m.decode(rec["prompt"], rec["gen_toks"])["witness"] == rec["witness"]
     finally:
         m.close()
+
+
+def test_cli_receipt_log(model_fixtures, tmp_path):
+    """--receipt-log appends one hash-chained record per run (the service's
+    log format, code/cis2-llm/server/app/receipts.py:31-97) holding the
+    run's digests; --verify-chain and the Python mirror both accept the log,
+    and a record altered afterwards is reported."""
+    import json
+    from cis2amd import receipts
+    rec = model_fixtures["tiny-llama"]
+    artifacts.Weights(artifacts.SPECS[rec["spec"]], rec["seed"]).write_dir(str(tmp_path))
+    ids = tmp_path / "ids.txt"
+    ids.write_text("\n".join(str(t) for t in rec["prompt"]) + "\n")
+    log = tmp_path / "receipts.jsonl"
+    for _ in range(2):
+        r = subprocess.run([CLI, "--weights-dir", str(tmp_path), "--ids", str(ids), "--gen-toks",
+                            str(rec["gen_toks"]), "--receipt-log", str(log)],
+                           capture_output=True, text=True, timeout=120)
+        assert r.returncode == 0, r.stderr[-2000:]
+        assert "CIS2_REF digest=%s" % rec["witness"] in r.stdout
+    L = receipts.ReceiptLog(log)
+    assert L.verify_chain() == (True, "chain OK")
+    recs = L.records()
+    assert len(recs) == 2 and recs[0]["receipt_id"] != recs[1]["receipt_id"]
+    for x in recs:
+        assert x["witness_digest"] == rec["witness"]
+        assert x["argmax_digest"] == rec["argmax_digest"]
+        assert x["table_digest"] == rec["table_digest"]
+        assert x["prompt_token_ids"] + x["generated_token_ids"] == rec["tokens"]
+        assert x["cis2_version"] == "v0.3b" and x["backend"] == "gfx950"
+    v = subprocess.run([CLI, "--verify-chain", str(log)], capture_output=True, text=True, timeout=60)
+    assert v.returncode == 0 and "CIS2_CHAIN PASS records=2" in v.stdout
+    lines = log.read_text().splitlines()
+    bad = json.loads(lines[0])
+    bad["generated_token_ids"][0] ^= 1
+    log.write_text(json.dumps(bad, sort_keys=True) + "\n" + lines[1] + "\n")
+    v = subprocess.run([CLI, "--verify-chain", str(log)], capture_output=True, text=True, timeout=60)
+    assert v.returncode == 1 and "line 0: log_hash mismatch (tampered record)" in v.stdout
