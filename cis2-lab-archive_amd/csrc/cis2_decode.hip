@@ -93,9 +93,16 @@ __host__ __device__ inline uint32_t att_row_stride(uint32_t pos) {
   return p4 + ((36u - (p4 & 31u)) & 31u);
 }
 
-// LDS floats of the attention task: scores (max_pos + 64) and K, V rows.
+// Row stride (floats) of the attention task's transposed LDS copy of K (one
+// row of head dims per position): hd rounded up to 4, plus 4, so that 16
+// lanes reading 16 bytes each from 16 consecutive rows cover all 64 banks.
+__host__ __device__ inline uint32_t att_k_stride(uint32_t hd) { return ((hd + 3) & ~3u) + 4; }
+
+// LDS floats of the attention task: scores (max_pos + 64), K as rows of
+// positions 0..pos-1 (rounded up to 4) and V as rows of head dims.
 __host__ __device__ inline size_t att_lds_floats(uint32_t hd, uint32_t pos, uint32_t max_pos) {
-  return (size_t)max_pos + 64 + 2 * (size_t)hd * att_row_stride(pos);
+  return (size_t)max_pos + 64 + (size_t)((pos + 3) & ~3u) * att_k_stride(hd) +
+         (size_t)hd * att_row_stride(pos);
 }
 
 // Positions per tile when a head's cached K/V do not fit in LDS: the
@@ -931,33 +938,82 @@ __device__ __forceinline__ void run_qkv(const DecodeArgs& a, uint32_t l, uint32_
 }
 
 // Copies positions [0, pos) of one kv head's cached K and V (both
-// [hd][max_pos] in HBM, written by earlier launches) into LDS rows of
-// stride S: K rows 0..hd-1, then V rows.  Positions up to pos rounded to 4
-// are copied; the ones >= pos are never used.
-__device__ __forceinline__ void prefetch_kv(const DecodeArgs& a, uint32_t l, uint32_t kvh, lf* kl,
-                                            uint32_t S) {
-  const uint32_t hd = a.hd, kq = (a.pos + 3) >> 2, mp4 = a.max_pos >> 2, nrow = 2 * hd;
+// [hd][max_pos] in HBM, written by earlier launches) into LDS: K transposed
+// into rows of KS floats, one per position (kt[j * KS + d] = k_j[d]), V as
+// rows of stride S, one per head dim (vl[d * S + j] = v_j[d]).  Positions up
+// to pos rounded to 4 are copied; the ones >= pos are never used.  The
+// global reads run along positions (16 bytes per thread, 16 in flight).
+__device__ __forceinline__ void prefetch_kv(const DecodeArgs& a, uint32_t l, uint32_t kvh, lf* kt,
+                                            uint32_t KS, lf* vl, uint32_t S) {
+  const uint32_t hd = a.hd, kq = (a.pos + 3) >> 2, mp4 = a.max_pos >> 2, n4 = hd * kq;
   gf4* kc = G4(a.kc0 + (size_t)l * a.cache_stride);
   gf4* kb = kc + (size_t)kvh * hd * mp4;
   gf4* vb = kc + (size_t)a.kvd * mp4 + (size_t)kvh * hd * mp4;
-  lf4* dst = (lf4*)kl;
-  const uint32_t s4 = S >> 2, wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  lf4* v4 = (lf4*)vl;
+  const uint32_t s4 = S >> 2;
   constexpr uint32_t B = 16;
-  for (uint32_t q = lane; q < kq; q += 64) {
-    uint32_t r = wv;
-    for (; r + 4 * (B - 1) < nrow; r += 4 * B) {
-      f4 t[B];
+  for (uint32_t i0 = threadIdx.x; i0 < n4; i0 += B * kThreads) {
+    f4 tk[B], tv[B];
 #pragma unroll
-      for (uint32_t u = 0; u < B; ++u) {
-        const uint32_t rr = r + 4 * u;
-        t[u] = rr < hd ? kb[(size_t)rr * mp4 + q] : vb[(size_t)(rr - hd) * mp4 + q];
+    for (uint32_t u = 0; u < B; ++u) {
+      const uint32_t i = i0 + u * kThreads;
+      if (i < n4) {
+        const uint32_t d = i / kq, q = i - d * kq;
+        tk[u] = kb[(size_t)d * mp4 + q];
+        tv[u] = vb[(size_t)d * mp4 + q];
       }
-#pragma unroll
-      for (uint32_t u = 0; u < B; ++u) dst[(size_t)(r + 4 * u) * s4 + q] = t[u];
     }
-    for (; r < nrow; r += 4)
-      dst[(size_t)r * s4 + q] = r < hd ? kb[(size_t)r * mp4 + q] : vb[(size_t)(r - hd) * mp4 + q];
+#pragma unroll
+    for (uint32_t u = 0; u < B; ++u) {
+      const uint32_t i = i0 + u * kThreads;
+      if (i < n4) {
+        const uint32_t d = i / kq, q = i - d * kq;
+        lf* dst = kt + (size_t)(4 * q) * KS + d;
+        dst[0] = tk[u].x;
+        dst[KS] = tk[u].y;
+        dst[2 * KS] = tk[u].z;
+        dst[3 * KS] = tk[u].w;
+        v4[(size_t)d * s4 + q] = tv[u];
+      }
+    }
   }
+}
+
+// dot(q, k) * 1 over hd head dims in the order TR selects (q and k: LDS,
+// 16-byte aligned, hd a multiple of 4): blocks of 32 products, each summed
+// in order from the running value (dot_seq) or reduced by tree32 and added
+// (dot_tree).  Every product is one rounding, so forming a block's
+// products before its adds gives dot_seq's bits.
+template <bool TR>
+__device__ __forceinline__ float score_dot(const lf* q, const lf* k, uint32_t hd) {
+  const lf4* q4 = (const lf4*)q;
+  const lf4* k4 = (const lf4*)k;
+  float acc = 0.0f;
+  for (uint32_t b = 0; b < hd; b += 32) {
+    float p[32];
+#pragma unroll
+    for (uint32_t g = 0; g < 8; ++g) {
+      const uint32_t d = b + 4 * g;
+      f4 qv = {0.0f, 0.0f, 0.0f, 0.0f}, kv = {0.0f, 0.0f, 0.0f, 0.0f};
+      if (d < hd) {
+        qv = q4[d >> 2];
+        kv = k4[d >> 2];
+      }
+      p[4 * g] = d < hd ? qv.x * kv.x : 0.0f;
+      p[4 * g + 1] = d < hd ? qv.y * kv.y : 0.0f;
+      p[4 * g + 2] = d < hd ? qv.z * kv.z : 0.0f;
+      p[4 * g + 3] = d < hd ? qv.w * kv.w : 0.0f;
+    }
+    if constexpr (TR) {
+      acc = acc + tree32(p);
+    } else {
+      const uint32_t n = hd - b < 32 ? hd - b : 32;
+#pragma unroll
+      for (uint32_t i = 0; i < 32; ++i)
+        if (i < n) acc = acc + p[i];
+    }
+  }
+  return acc;
 }
 
 // Attention for query head h (code/cis2-fp/src/main.rs:415-467).
@@ -1064,6 +1120,98 @@ __device__ __forceinline__ void store_kv_pos(const DecodeArgs& a, uint32_t l, ui
   }
 }
 
+// Orders this wave's LDS writes before its later LDS reads by other lanes
+// (a wave's LDS operations complete in issue order; this keeps the compiler
+// from moving accesses across the point).
+__device__ __forceinline__ void wave_lds_order() {
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+}
+
+// Softmax and V mix of one head by wave 0 alone, after the scores of
+// positions 0..pos are in ss[] (written by the whole workgroup before a
+// barrier): first-wins max (NaN at position 0 wins), pinned exp, the
+// denominator (strict chain, or tree32 blocks folded from 0), a true
+// divide, then lane d's V-mix chain out_d = fold_j (p_j * v_j[d]) over the
+// V rows in LDS (row d at vl + d*S) and this position's own v.  part: tree
+// partials; misc: 4 floats.  The other waves are not involved: no barrier.
+template <bool TR>
+__device__ __forceinline__ void att_tail_wave0(const DecodeArgs& a, gw* out, lf* ss, uint32_t len,
+                                               uint32_t pos, const lf* vl, uint32_t S,
+                                               const lf* vv, lf* part) {
+  const uint32_t lane = threadIdx.x & 63, hd = a.hd;
+  Cand best = {0.0f, UINT32_MAX};
+  for (uint32_t j = lane; j < len; j += 64) {
+    const float v = ss[j];
+    if (v == v) best = cand_pick(best, Cand{v, j});
+  }
+  const Cand b = cand_wave_dpp(best);
+  const float mx = (ss[0] != ss[0] || b.i == UINT32_MAX) ? ss[0] : ss[b.i];
+  for (uint32_t j = lane; j < len; j += 64) {
+    const float dlt = ss[j] - mx;
+    ss[j] = exp_pinned(dlt);
+  }
+  wave_lds_order();
+  float den;
+  if constexpr (TR) {
+    const uint32_t nbk = (len + 31) / 32;
+    for (uint32_t t = lane; t < nbk; t += 64) part[t] = tree_part(ss + 32 * t, len - 32 * t, 1);
+    wave_lds_order();
+    den = chain1(part, nbk, 1, 0.0f);
+  } else {
+    den = chain_vec(ss, len, 0.0f);
+  }
+  for (uint32_t j = lane; j < len; j += 64) {
+    const float pj = ss[j] / den;
+    ss[j] = pj;
+  }
+  wave_lds_order();
+  const lf4* p4 = (const lf4*)ss;
+  const uint32_t ng = pos >> 2;
+  for (uint32_t d = lane; d < hd; d += 64) {
+    const lf4* v4 = (const lf4*)(vl + (size_t)d * S);
+    float acc = 0.0f;
+    uint32_t g = 0;
+    for (; g + 4 <= ng; g += 4) {
+      f4 pv[4], vr[4];
+#pragma unroll
+      for (uint32_t u = 0; u < 4; ++u) {
+        pv[u] = p4[g + u];
+        vr[u] = v4[g + u];
+      }
+#pragma unroll
+      for (uint32_t u = 0; u < 4; ++u) {
+        const float t0 = pv[u].x * vr[u].x;
+        acc = acc + t0;
+        const float t1 = pv[u].y * vr[u].y;
+        acc = acc + t1;
+        const float t2 = pv[u].z * vr[u].z;
+        acc = acc + t2;
+        const float t3 = pv[u].w * vr[u].w;
+        acc = acc + t3;
+      }
+    }
+    for (; g < ng; ++g) {
+      const f4 pv = p4[g], vr = v4[g];
+      const float t0 = pv.x * vr.x;
+      acc = acc + t0;
+      const float t1 = pv.y * vr.y;
+      acc = acc + t1;
+      const float t2 = pv.z * vr.z;
+      acc = acc + t2;
+      const float t3 = pv.w * vr.w;
+      acc = acc + t3;
+    }
+    for (uint32_t j = 4 * ng; j < pos; ++j) {
+      const float t = ss[j] * vl[(size_t)d * S + j];
+      acc = acc + t;
+    }
+    const float t = ss[pos] * vv[d];
+    acc = acc + t;
+    put_word(out + d, acc, a.epoch);
+  }
+}
+
 template <bool TR>
 __device__ __forceinline__ void run_att(const DecodeArgs& a, uint32_t l, uint32_t h, const Lds& s,
                         size_t wfloats) {
@@ -1078,27 +1226,23 @@ __device__ __forceinline__ void run_att(const DecodeArgs& a, uint32_t l, uint32_
   lf* misc = tmp + hd;  // [0] inv, [1] den, [4..] reduction scratch
   AS_LDS uint32_t* red = (AS_LDS uint32_t*)(misc + 4);
   lf* ss = s.w;  // scores / probabilities
-  lf* kl = ss + a.max_pos + 64;
-  const uint32_t S = att_row_stride(pos);
-  lf* vl = kl + (size_t)hd * S;
-  const bool in_lds = att_lds_floats(hd, pos, a.max_pos) <= wfloats;
+  lf* kt = ss + a.max_pos + 64;  // K: one row of KS floats per cached position
+  const uint32_t S = att_row_stride(pos), KS = att_k_stride(hd);
+  lf* vl = kt + (size_t)((pos + 3) & ~3u) * KS;  // V: one row of S floats per head dim
+  const bool in_lds = hd % 4 == 0 && att_lds_floats(hd, pos, a.max_pos) <= wfloats;
   stamp(a, l, P_ATT, h, 0);
-  if (in_lds) prefetch_kv(a, l, kvh, kl, S);
+  if (in_lds) prefetch_kv(a, l, kvh, kt, KS, vl, S);
   att_head_inputs<TR>(a, l, h, qv, tmp, misc);
   stamp(a, l, P_ATT, h, 1);
   if (h % group == 0) store_kv_pos(a, l, kvh, kv, vv);  // one writer per kv head
   // scores_j = dot_seq(q, k_j) * scale (main.rs:440-445)
   if (in_lds) {
-    // products q[d] * k_j[d] in place (row d scaled by q[d]); tmp = q * k_pos
-    const uint32_t kq = (pos + 3) >> 2, s4 = S >> 2;
-    scale_rows_by_row((lf4*)kl, s4, hd, kq, qv);
-    for (uint32_t d = threadIdx.x; d < hd; d += kThreads) tmp[d] = qv[d] * kv[d];
-    __syncthreads();
+    // the lane of position j forms q[d] * k_j[d] from its K row and adds
+    // them in order (or by tree32 blocks)
     for (uint32_t j = threadIdx.x; j < len; j += kThreads) {
-      const lf* p = j < pos ? kl + j : tmp;
-      const uint32_t st = j < pos ? S : 1u;
-      const float acc = TR ? tree_col(p, hd, st, 0.0f) : chain1(p, hd, st, 0.0f);
-      ss[j] = acc * a.scale;
+      const lf* kr = j < pos ? kt + (size_t)j * KS : kv;
+      const float sj = score_dot<TR>(qv, kr, hd) * a.scale;
+      ss[j] = sj;
     }
   } else {
     // The cached K/V do not fit in LDS: stream tiles of TP positions.  Per
@@ -1123,23 +1267,21 @@ __device__ __forceinline__ void run_att(const DecodeArgs& a, uint32_t l, uint32_
     if (threadIdx.x == 0)
       ss[pos] = (TR ? tree_col(tmp, hd, 1, 0.0f) : chain1(tmp, hd, 1, 0.0f)) * a.scale;
   }
+  if (in_lds) {
+    // the scores are in ss; wave 0 finishes the head (tree partials in the
+    // K region, which no one reads any more)
+    __syncthreads();
+    stamp(a, l, P_ATT, h, 3);
+    if (threadIdx.x < 64) att_tail_wave0<TR>(a, ac.att + (size_t)h * hd, ss, len, pos, vl, S, vv, kt);
+    __syncthreads();
+    stamp(a, l, P_ATT, h, 2);
+    return;
+  }
   __syncthreads();
-  softmax_lds<TR>(ss, len, ss + a.max_pos + 64, misc, red);  // tree partials in the K region
+  softmax_lds<TR>(ss, len, ss + a.max_pos + 64, misc, red);
   stamp(a, l, P_ATT, h, 3);
   // V mix out_d = fold_j (p_j * v_j[d]) (main.rs:454-463)
-  if (in_lds) {
-    const uint32_t kq = (pos + 3) >> 2, s4 = S >> 2;
-    lf4* v4 = (lf4*)vl;
-    const lf4* p4 = (const lf4*)ss;
-    scale_rows_by_col(v4, s4, hd, kq, p4);
-    __syncthreads();
-    for (uint32_t d = threadIdx.x; d < hd; d += kThreads) {
-      float acc = chain_vec(vl + (size_t)d * S, pos, 0.0f);
-      float p = ss[pos] * vv[d];
-      acc = acc + p;
-      put_word(ac.att + (size_t)h * hd + d, acc, a.epoch);
-    }
-  } else {
+  {
     // Tiles of TP positions: products p_j * v_j[d] in place, then lane d
     // continues its one left-to-right chain over the tile.
     const uint32_t TP = att_tile_positions(hd, a.max_pos, wfloats), TS = TP + 4;
@@ -1723,7 +1865,9 @@ size_t decode_act_floats(uint32_t H, uint32_t I, uint32_t qd, uint32_t kvd) {
 bool decode_att_ok(const DecodeArgs& a) {
   const size_t wfloats = decode_wregion_bytes(a) / 4;
   if (a.att_split) return a.att_tp >= 32 && a.nh % a.nkv == 0;
-  return att_lds_floats(a.hd, a.max_pos, a.max_pos) <= wfloats ||
+  // the one-task form keeps K and V in LDS when they fit (head_dim a
+  // multiple of 4), else streams tiles of at least 32 positions
+  return (a.hd % 4 == 0 && att_lds_floats(a.hd, a.max_pos, a.max_pos) <= wfloats) ||
          att_tile_positions(a.hd, a.max_pos, wfloats) >= 32;
 }
 
