@@ -86,6 +86,13 @@ int orc_fpenv_pin(void) {
   return 0;
 }
 
+/* Clears FTZ|DAZ on the calling thread (the default IEEE environment), so a
+ * test process can run code that needs subnormals after the oracle pinned
+ * its thread; every oracle entry pins again on its next call. */
+void orc_fpenv_release(void) {
+  _mm_setcsr(_mm_getcsr() & ~((1u << 15) | (1u << 6)));
+}
+
 /* ======================================================================
  * Integer/rounding helpers without libm.
  * Saturating casts: Rust `as` semantics, code/cis2-fp/src/math.rs:167-225

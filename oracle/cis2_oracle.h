@@ -38,6 +38,7 @@ extern "C" {
 /* Pins MXCSR FTZ|DAZ on the calling thread, reads it back and runs the
  * two adversarial probes.  Returns 0 on success. */
 int orc_fpenv_pin(void);
+void orc_fpenv_release(void);
 
 /* ---- scalar pinned math ---------------------------------------------- */
 enum { ORC_FN_EXP = 0, ORC_FN_SIN = 1, ORC_FN_COS = 2, ORC_FN_LN = 3,

@@ -91,6 +91,20 @@ def lib():
     return _o
 
 
+def fpenv_release():
+    """Give the calling thread back the default FP environment (subnormals
+    kept) if the oracle pinned FTZ|DAZ on it; returns whether it had."""
+    if _o is None:
+        return False
+    _o.orc_fpenv_release()
+    return True
+
+
+def fpenv_repin():
+    if _o is not None and _o.orc_fpenv_pin() != 0:
+        raise RuntimeError("oracle FTZ/DAZ pin failed")
+
+
 def ref_math():
     """The reference's own cis2_math.h compiled here (None if not built)."""
     if not os.path.exists(REF_MATH_PATH):

@@ -23,6 +23,18 @@ CLI = os.path.join(ROOT, "cis2-lab-archive_amd", "bin", "cis2_host")
 INC = os.path.join(ROOT, "cis2-lab-archive_amd", "csrc")
 
 
+@pytest.fixture(autouse=True)
+def ieee_fpenv():
+    """Canonical JSON of subnormal floats needs the default FP environment:
+    an oracle test that ran earlier in this process left FTZ|DAZ pinned on
+    the main thread."""
+    import _oracle
+    had = _oracle.fpenv_release()
+    yield
+    if had:
+        _oracle.fpenv_repin()
+
+
 @pytest.fixture(scope="module")
 def harness(tmp_path_factory):
     gxx = shutil.which("g++")
