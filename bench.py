@@ -65,6 +65,8 @@ NORM_BYTES = 4 * 61 * 576
 KV_BYTES_PER_POS = 4 * 2 * 192 * 30
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "k_decode_smollm2_pmc.txt")
 GEMV_STREAM_FILE = os.path.join(ROOT, "profiles", "k_gemv_many_1536x576_stream.txt")
+LM_HEAD_FILE = os.path.join(ROOT, "profiles", "k_gemv_lm_head_49152x576.txt")
+GEMV_ONE_FILE = os.path.join(ROOT, "profiles", "k_gemv_pipe_1536x576.txt")
 
 
 def decode_bytes(pos):
@@ -99,15 +101,40 @@ def gemv_roofline(M=1536, K=576, copies=128, iters=4096):
     ms_b = plan.time_batch(copies, 32)
     achieved_b = copies * algo_bytes / (ms_b * 1e-3) / 1e9
     plan.close()
+    lm = lm_head_roofline(K=K)
     return {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
-            "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-            "kernel": "k_gemv %dx%d strict order" % (M, K), "us_per_launch": round(ms * 1e3, 3),
+            "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": measured_traffic(GEMV_ONE_FILE) if (M, K) == (1536, 576) else None,
+            "kernel": "k_gemv_pipe<16, %d>: one %dx%d GEMV per launch" % (K, M, K),
+            "us_per_launch": round(ms * 1e3, 3),
             "algorithmic_bytes": algo_bytes,
             "stream": {"gemvs_per_launch": copies, "us_per_launch": round(ms_b * 1e3, 2),
                        "achieved": round(achieved_b, 2), "frac": round(achieved_b / HBM_PEAK_GBS, 4),
                        "traffic": measured_traffic(GEMV_STREAM_FILE) if copies == 128 else None,
                        "kernel": "k_gemv_many: %d independent %dx%d GEMVs per launch"
-                                 % (copies, M, K)}}
+                                 % (copies, M, K)},
+            "lm_head": lm}
+
+
+def lm_head_roofline(M=49152, K=576, copies=3, iters=64):
+    """The one bs=1 GEMV wide enough to stream at HBM rate: the SmolLM2-135M
+    LM head, 49152x576 strict order (113 MB of fp32 weights), one GEMV per
+    launch, rotating through `copies` replicas (340 MB > the 256 MB Infinity
+    Cache), timed with HIP events on the plan's stream."""
+    from cis2amd import GemvPlan, artifacts
+    W = artifacts.gen_f32(SEED, 3, M * K, 0.02).reshape(M, K)
+    plan = GemvPlan(W, copies=copies)
+    plan.time(8)
+    ms = plan.time(iters)
+    plan.close()
+    algo = 4 * M * K + 4 * K + 4 * M
+    achieved = algo / (ms * 1e-3) / 1e9
+    return {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": measured_traffic(LM_HEAD_FILE),
+            "kernel": "k_gemv_many<16, 576> (one %dx%d GEMV per launch, %d row blocks)"
+                      % (M, K, (M + 15) // 16),
+            "us_per_launch": round(ms * 1e3, 3), "algorithmic_bytes": algo}
 
 
 def host_cpu():
@@ -340,6 +367,8 @@ def main():
     ap.add_argument("--no-roofline", action="store_true")
     ap.add_argument("--no-batch", action="store_true", help="skip the batched-decode sizes")
     ap.add_argument("--no-qwen3", action="store_true", help="skip the Qwen3 4096+256 run")
+    ap.add_argument("--gemv-only", action="store_true",
+                    help="only the strict-order GEMV rooflines (config 1, the stream, the LM head)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 512 MiB device-to-device copy (counter calibration)")
     a = ap.parse_args()
@@ -354,6 +383,9 @@ def main():
         torch.cuda.synchronize()
         log("copied 3 x %d bytes" % (4 * n))
         print(json.dumps({"copy_bytes": 4 * n, "copies": 3}), flush=True)
+        return
+    if a.gemv_only:
+        print(json.dumps({"gemv_config1": gemv_roofline()}), flush=True)
         return
     if a.gpus != 1:
         print("bench.py: one GPU only (the pinned-order decode is not sharded across GPUs); "

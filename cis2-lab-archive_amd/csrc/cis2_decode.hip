@@ -406,6 +406,17 @@ __device__ __forceinline__ void prefetch_rows_async(const float* W, uint32_t R, 
 // s_waitcnt vmcnt(0) (expcnt, lgkmcnt fields at their maxima: no wait).
 __device__ __forceinline__ void wait_vm0() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
+// Workgroup barrier for LDS data only: waits for this wave's LDS
+// operations, not for its outstanding global loads (HIP's __syncthreads
+// waits for those too).  The empty asm statements keep the compiler from
+// moving memory accesses across the barrier.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
 // Row block blk of two matrices of the same shape, back to back in LDS.
 __device__ __forceinline__ void prefetch_rows2(const float* A, const float* B, uint32_t R,
                                                uint32_t K, uint32_t blk, lf* dst) {
@@ -589,7 +600,7 @@ __device__ __forceinline__ float gemv_lds_t(lf* W, const lf* x, uint32_t K, uint
   const uint32_t bf4 = KG * R, nins = (KG + GP - 1) / GP;
   const uint32_t r = lane < R ? lane : R - 1;
   prod_ins<R>(W4, x4, bf4, nb, KG, 0, nins / NC, wv, kThreads / 64, pad);
-  __syncthreads();
+  lds_barrier();
   float acc = 0.0f;
   for (uint32_t c = 0; c < NC; ++c) {
     const uint32_t i0 = nins * c / NC, i1 = nins * (c + 1) / NC;
@@ -600,7 +611,7 @@ __device__ __forceinline__ float gemv_lds_t(lf* W, const lf* x, uint32_t K, uint
       prod_ins<R>(W4, x4, bf4, nb, KG, i1, nins * (c + 2) / NC, wv - nb, kThreads / 64 - nb,
                   pad);
     }
-    __syncthreads();
+    lds_barrier();
   }
   return acc;
 }
@@ -688,12 +699,12 @@ __device__ __forceinline__ float gemv_tree_t(uint32_t Rr, lf* W, const lf* x, ui
     }
     ((lf*)p)[0] = tree32(lv);
   }
-  __syncthreads();
+  lds_barrier();
   float acc = 0.0f;
   if (wv < nb)
     acc = chain1((const lf*)(W4 + (size_t)wv * bf4 + (lane < Rv ? lane : Rv - 1)), KB, 32 * Rv,
                  0.0f);
-  __syncthreads();
+  lds_barrier();
   return acc;
 }
 
@@ -1780,6 +1791,102 @@ void k_gemv_blk(const float* __restrict__ W, const float* __restrict__ x, float*
   if (threadIdx.x < R && row < M) GW(y)[row] = acc;
 }
 
+// s_waitcnt vmcnt(n) for a run-time n.  n is clamped to the counter's 63:
+// once every load has been issued at most 63 are outstanding, and they are
+// the newest ones, so when more than 63 loads followed the ones waited for,
+// those have completed.
+__device__ __forceinline__ void wait_vmcnt(uint32_t n) {
+  switch (n < 63u ? n : 63u) {
+#define CIS2_VMW(k) \
+  case k:           \
+    __builtin_amdgcn_s_waitcnt(0x0F70 | ((k) & 15) | (((k) >> 4) << 14)); \
+    break;
+    CIS2_VMW(0) CIS2_VMW(1) CIS2_VMW(2) CIS2_VMW(3) CIS2_VMW(4) CIS2_VMW(5) CIS2_VMW(6)
+    CIS2_VMW(7) CIS2_VMW(8) CIS2_VMW(9) CIS2_VMW(10) CIS2_VMW(11) CIS2_VMW(12) CIS2_VMW(13)
+    CIS2_VMW(14) CIS2_VMW(15) CIS2_VMW(16) CIS2_VMW(17) CIS2_VMW(18) CIS2_VMW(19) CIS2_VMW(20)
+    CIS2_VMW(21) CIS2_VMW(22) CIS2_VMW(23) CIS2_VMW(24) CIS2_VMW(25) CIS2_VMW(26) CIS2_VMW(27)
+    CIS2_VMW(28) CIS2_VMW(29) CIS2_VMW(30) CIS2_VMW(31) CIS2_VMW(32) CIS2_VMW(33) CIS2_VMW(34)
+    CIS2_VMW(35) CIS2_VMW(36) CIS2_VMW(37) CIS2_VMW(38) CIS2_VMW(39) CIS2_VMW(40) CIS2_VMW(41)
+    CIS2_VMW(42) CIS2_VMW(43) CIS2_VMW(44) CIS2_VMW(45) CIS2_VMW(46) CIS2_VMW(47) CIS2_VMW(48)
+    CIS2_VMW(49) CIS2_VMW(50) CIS2_VMW(51) CIS2_VMW(52) CIS2_VMW(53) CIS2_VMW(54) CIS2_VMW(55)
+    CIS2_VMW(56) CIS2_VMW(57) CIS2_VMW(58) CIS2_VMW(59) CIS2_VMW(60) CIS2_VMW(61) CIS2_VMW(62)
+    default: __builtin_amdgcn_s_waitcnt(0x0F70 | 15 | (3 << 14)); break;
+#undef CIS2_VMW
+  }
+}
+
+// 16-byte global->LDS loads (global_load_lds_dwordx4) of the 64-slot runs
+// [64 ins, 64 ins + 64) of src into the same slots of dst, for ins = i0 + w,
+// i0 + w + nw, ... < i1.  Every run is one wave instruction and lane l
+// always writes slot 64 ins + l, so dst needs 63 slots of room past n4;
+// lanes past n4 read slot n4 - 1 (no lane is skipped, so the count of
+// load instructions is exact).  Returns that count (wave-uniform).
+__device__ __forceinline__ uint32_t load_runs(gf4* src, lf4* dst, uint32_t n4, uint32_t i0,
+                                              uint32_t i1, uint32_t w, uint32_t nw) {
+  const uint32_t lane = threadIdx.x & 63;
+  uint32_t cnt = 0;
+  for (uint32_t ins = i0 + w; ins < i1; ins += nw) {
+    const uint32_t s0 = ins * 64;
+    __builtin_amdgcn_global_load_lds((const AS_GLB void*)(src + min(s0 + lane, n4 - 1)),
+                                     (AS_LDS void*)(dst + s0), 16, 0, 0);
+    ++cnt;
+  }
+  return cnt;
+}
+
+// The lone GEMV, pipelined (the standalone plan's kernel for K fixed at
+// compile time): every wave issues, right at the start and in chunk order,
+// the loads of exactly the W slots its own product instructions multiply,
+// straight into LDS, so no wave waits for another wave's loads and the
+// chain starts one HBM round trip after the launch instead of after the
+// whole block has arrived.  Product instruction ins covers the 64 16-byte
+// slots [64 ins, 64 ins + 64) of the block (group ins*GP + l/R, row l%R, as
+// in prod_ins).  x is loaded by all waves first.  Chunk 0's instructions are
+// spread over all four waves, later chunks over waves 1-3.  After chunk 0's
+// products, lane r of wave 0 adds row r's products of chunk c strictly in
+// order while waves 1-3 form chunk c+1's.
+template <uint32_t R, uint32_t K>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void k_gemv_pipe(const float* __restrict__ W, const float* __restrict__ x, float* y, uint32_t M) {
+  constexpr uint32_t NC = 4, GP = 64 / R, NW = kThreads / 64, KG = K / 4;
+  constexpr uint32_t NINS = (KG + GP - 1) / GP, N4 = KG * R;
+  static_assert(K % 4 == 0 && 64 % R == 0, "shape");
+  extern __shared__ f4 lds_dyn[];
+  lf4* w4 = (lf4*)lds_dyn;   // the block, then 64 slots of room
+  lf4* xs = w4 + N4 + 64;    // x, then 64 slots of room
+  lf4* pad = xs + KG + 64;   // prod_ins's idle-lane slots
+  const uint32_t b = blockIdx.x;
+  const uint32_t wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  gf4* src = G4(W + (size_t)b * R * K);
+  uint32_t cnt[NC];
+  cnt[0] = load_runs(G4(x), xs, KG, 0, (KG + 63) / 64, wv, NW);
+  cnt[0] += load_runs(src, w4, N4, 0, NINS / NC, wv, NW);
+  for (uint32_t c = 1; c < NC; ++c)
+    cnt[c] = wv == 0 ? 0u : load_runs(src, w4, N4, NINS * c / NC, NINS * (c + 1) / NC, wv - 1,
+                                      NW - 1);
+  wait_vmcnt(cnt[1] + cnt[2] + cnt[3]);
+  lds_barrier();
+  prod_ins<R>(w4, xs, N4, 1, KG, 0, NINS / NC, wv, NW, pad);
+  lds_barrier();
+  const uint32_t lane = threadIdx.x & 63, r = lane < R ? lane : R - 1;
+  float acc = 0.0f;
+  for (uint32_t c = 0; c < NC; ++c) {
+    const uint32_t i0 = NINS * c / NC, i1 = NINS * (c + 1) / NC;
+    if (wv == 0) {
+      const uint32_t g0 = i0 * GP, g1 = min(i1 * GP, KG);
+      acc = chain4<8>(w4 + (size_t)g0 * R + r, g1 - g0, R, acc);
+    } else if (c + 1 < NC) {
+      uint32_t later = 0;
+      for (uint32_t c2 = c + 2; c2 < NC; ++c2) later += cnt[c2];
+      wait_vmcnt(later);
+      prod_ins<R>(w4, xs, N4, 1, KG, i1, NINS * (c + 2) / NC, wv - 1, NW - 1, pad);
+    }
+    lds_barrier();
+  }
+  const uint32_t row = b * R + threadIdx.x;
+  if (threadIdx.x < R && row < M) GW(y)[row] = acc;
+}
+
 // A batch of n independent GEMVs in one launch (gridDim.y = n): GEMV i is
 // y_i = W_c x_i with W_c the replica c = (first + i) % copies, x_i at
 // x + i*K, y_i at y + i*M.  The block's work is k_gemv_blk's; several
@@ -1823,14 +1930,26 @@ static hipError_t launch_gemv_blk_t(const float* W, const float* x, float* y, ui
   return hipGetLastError();
 }
 
+template <uint32_t R, uint32_t K>
+static hipError_t launch_gemv_pipe_t(const float* W, const float* x, float* y, uint32_t M,
+                                     hipStream_t s) {
+  const size_t lds = ((size_t)R * K + K + 3 * 256) * 4;  // block, x, 64 slots after each, pad
+  hipError_t e = ensure_dynamic_lds(reinterpret_cast<const void*>(&k_gemv_pipe<R, K>), lds);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL((k_gemv_pipe<R, K>), dim3((M + R - 1) / R), dim3(kThreads), lds, s, W, x, y,
+                     M);
+  return hipGetLastError();
+}
+
 hipError_t launch_gemv_blk(const float* W, const float* x, float* y, uint32_t M, uint32_t K,
                            uint32_t R, hipStream_t s) {
   const size_t lds = gemv_blk_lds_bytes(K, R);
   if (K % 4 || lds > 160 * 1024 - 64) return hipErrorInvalidValue;
   // the hidden size of SmolLM2-135M (K = 576: the 1536x576 up-projection)
   // compiled with K fixed; any other K at run time
-  if (R == 16) return K == 576 ? launch_gemv_blk_t<16, 576>(W, x, y, M, K, lds, s)
-                               : launch_gemv_blk_t<16, 0>(W, x, y, M, K, lds, s);
+  if (R == 16 && K == 576) return launch_gemv_pipe_t<16, 576>(W, x, y, M, s);
+  if (R == 16 && K == 1536) return launch_gemv_pipe_t<16, 1536>(W, x, y, M, s);
+  if (R == 16) return launch_gemv_blk_t<16, 0>(W, x, y, M, K, lds, s);
   if (R == 32) return K == 576 ? launch_gemv_blk_t<32, 576>(W, x, y, M, K, lds, s)
                                : launch_gemv_blk_t<32, 0>(W, x, y, M, K, lds, s);
   return hipErrorInvalidValue;

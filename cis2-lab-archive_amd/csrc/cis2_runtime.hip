@@ -157,6 +157,9 @@ struct cis2_ctx {
 constexpr size_t kProfMax = 65536;
 // Rows per block of the standalone GEMV plan's layout (one workgroup each).
 constexpr uint32_t kPlanR = 16;
+// Above this many row blocks (two per CU on MI355X) a lone GEMV runs on the
+// streaming batch kernel.
+constexpr uint32_t kPlanStreamBlocks = 512;
 
 struct cis2_gemv_plan {
   uint32_t M, K, copies;
@@ -1725,10 +1728,22 @@ int cis2_gemv_plan_create(uint32_t M, uint32_t K, uint32_t copies, const float* 
   return CIS2_OK;
 }
 
+// One GEMV of the plan on replica c.  A matrix of many row blocks (an LM
+// head: more than two blocks per CU) streams through the batch kernel,
+// whose workgroups share CUs so one block's loads overlap another's chains;
+// a smaller one runs the pipelined lone-GEMV kernel, one block per CU.
+static hipError_t plan_launch(cis2_gemv_plan* p, uint32_t c, const float* x, float* y) {
+  const size_t per = blocked_floats(p->M, p->K, kPlanR);
+  if ((p->M + kPlanR - 1) / kPlanR > kPlanStreamBlocks)
+    return launch_gemv_many(p->W, per, p->copies, c % p->copies, 1, x, y, p->M, p->K, kPlanR,
+                            p->st);
+  return launch_gemv_blk(p->W + per * (c % p->copies), x, y, p->M, p->K, kPlanR, p->st);
+}
+
 int cis2_gemv_plan_run(cis2_gemv_plan* p, const float* x, float* y) {
   if (!p || !x || !y) return CIS2_E_ARG;
   hipError_t e = hipMemcpyAsync(p->x, x, (size_t)p->K * sizeof(float), hipMemcpyHostToDevice, p->st);
-  if (e == hipSuccess) e = launch_gemv_blk(p->W, p->x, p->y, p->M, p->K, kPlanR, p->st);
+  if (e == hipSuccess) e = plan_launch(p, 0, p->x, p->y);
   if (e == hipSuccess) e = hipMemcpyAsync(y, p->y, (size_t)p->M * sizeof(float), hipMemcpyDeviceToHost, p->st);
   if (e == hipSuccess) e = hipStreamSynchronize(p->st);
   return e == hipSuccess ? CIS2_OK : CIS2_E_DEVICE;
@@ -1736,13 +1751,11 @@ int cis2_gemv_plan_run(cis2_gemv_plan* p, const float* x, float* y) {
 
 int cis2_gemv_plan_time(cis2_gemv_plan* p, uint32_t iters, float* ms) {
   if (!p || !ms || iters == 0) return CIS2_E_ARG;
-  const size_t per = blocked_floats(p->M, p->K, kPlanR);
   hipError_t e = hipSuccess;
   for (uint32_t i = 0; e == hipSuccess && i < p->copies; ++i)  // warm-up pass
-    e = launch_gemv_blk(p->W + per * i, p->x, p->y, p->M, p->K, kPlanR, p->st);
+    e = plan_launch(p, i, p->x, p->y);
   if (e == hipSuccess) e = hipEventRecord(p->e0, p->st);
-  for (uint32_t i = 0; e == hipSuccess && i < iters; ++i)
-    e = launch_gemv_blk(p->W + per * (i % p->copies), p->x, p->y, p->M, p->K, kPlanR, p->st);
+  for (uint32_t i = 0; e == hipSuccess && i < iters; ++i) e = plan_launch(p, i, p->x, p->y);
   if (e == hipSuccess) e = hipEventRecord(p->e1, p->st);
   if (e == hipSuccess) e = hipEventSynchronize(p->e1);
   float t = 0.0f;

@@ -43,7 +43,7 @@ FMA64 = re.compile(r"^v_fma(c)?_f64$")
 # integer sequences: +-2^32 as an f32 literal, or as the high word of an f64
 INT_LIT32 = re.compile(r"0x[4c]f800000\b")
 INT_LIT64 = re.compile(r"0x[4c]1f00000\b")
-STRICT_ZERO = re.compile(r"(k_gemv_blk|k_gemv_many|4cis26k_gemvE|k_bgemmILb0ELb0E)")
+STRICT_ZERO = re.compile(r"(k_gemv_blk|k_gemv_pipe|k_gemv_many|4cis26k_gemvE|k_bgemmILb0ELb0E)")
 
 
 def tools():

@@ -35,6 +35,20 @@ def test_edge_shapes_match_oracle(M, K):
     assert np.array_equal(GemvPlan(W)(x).view(np.uint32), O.gemv(W, x).view(np.uint32))
 
 
+@pytest.mark.parametrize("M,K", [(49152, 576), (8193, 100), (8208, 576)])
+def test_many_block_gemv_matches_oracle(M, K):
+    """Matrices of more than 512 row blocks (the LM head of the SmolLM2 shape,
+    49152x576) run on the streaming kernel: same bits as the oracle, on every
+    replica."""
+    W = artifacts.gen_f32(20261202, M, M * K, 0.02).reshape(M, K)
+    x = artifacts.gen_f32(20261202, K, K, 1.0)
+    plan = GemvPlan(W, copies=2)
+    ref = O.gemv(W, x).view(np.uint32)
+    assert np.array_equal(plan(x).view(np.uint32), ref)
+    plan.time(3)  # both replicas used
+    assert np.array_equal(plan(x).view(np.uint32), ref)
+
+
 def test_cancellation_order_survives_on_device():
     W = np.array([[1e8, 1.0, -1e8, 0.0], [1e8, -1e8, 1.0, 0.0]], np.float32)
     y = GemvPlan(W)(np.ones(4, np.float32))
