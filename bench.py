@@ -73,6 +73,26 @@ def decode_bytes(pos):
     return GEMV_WEIGHT_BYTES + NORM_BYTES + KV_BYTES_PER_POS * (int(pos) + 1)
 
 
+def spec_bytes(spec):
+    """(weight bytes, KV bytes per cached position) of one decode row of a
+    model: the fp32 GEMV weights of every layer and the LM head, the norm
+    weights (two per layer, the QK norms, the final norm), and the K and V
+    rows one position adds to the cache."""
+    H, I, L = spec.hidden, spec.inter, spec.n_layers
+    qd, kvd = spec.qd, spec.kvd
+    gemv = L * (H * qd + 2 * H * kvd + qd * H + 3 * H * I) + spec.vocab * H
+    norms = L * (2 * H + (2 * spec.hd if spec.qk_norm else 0)) + H
+    return 4 * (gemv + norms), 4 * 2 * kvd * L
+
+
+def roofline_obj(algo_bytes, seconds, kernel, **extra):
+    achieved = algo_bytes / seconds / 1e9
+    r = {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+         "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "kernel": kernel}
+    r.update(extra)
+    return r
+
+
 def measured_traffic(path=TRAFFIC_FILE):
     """HBM bytes per launch (FETCH_SIZE + WRITE_SIZE, copy-calibrated) from a
     committed counter summary, or None."""
@@ -228,6 +248,15 @@ def batch_decode(spec, weights, sizes=(1, 8, 32, 64)):
         tt = time.perf_counter() - t
         rec = {"tok_s": round(B * gen / (tt - tp), 1), "prefill_rows": sum(len(p) for p in P),
                "prefill_s": round(tp, 4), "total_s": round(tt, 4)}
+        if B == max(sizes):
+            # decode steps only: weights once per step for all B rows, each
+            # row's cached K/V at its own position (prompt length + step)
+            wb, kvb = spec_bytes(spec)
+            algo = sum(wb + sum(kvb * (len(p) + st + 1) for p in P) for st in range(gen))
+            rec["roofline"] = roofline_obj(
+                algo, tt - tp, "batched decode step (row GEMMs, row attention, argmax; "
+                "timed by wall clock over the %d decode steps)" % gen,
+                algorithmic_bytes_per_step=int(round(algo / gen)))
         fx = os.path.join(ROOT, "tests", "golden", "batch_set.json")
         if os.path.exists(fx):
             doc = json.load(open(fx))
@@ -255,10 +284,19 @@ def llama_set():
     m = Cis2Model(spec, w, max_pos=pset["hi"] + gen, max_seqs=len(prompts))
     m.decode_batch(prompts[:2], 4)
     t = time.perf_counter()
+    m.decode_batch(prompts, 0)
+    tp = time.perf_counter() - t
+    t = time.perf_counter()
     rows = m.decode_batch(prompts, gen)
     tt = time.perf_counter() - t
+    wb, kvb = spec_bytes(spec)
+    algo = sum(wb + sum(kvb * (len(p) + st + 1) for p in prompts) for st in range(gen))
     rec = {"sequences": len(prompts), "gen_toks": gen, "total_s": round(tt, 4),
-           "tok_s": round(len(prompts) * gen / tt, 1)}
+           "tok_s": round(len(prompts) * gen / tt, 1), "prefill_s": round(tp, 4),
+           "roofline": roofline_obj(
+               algo, tt - tp, "batched decode step over all %d sequences (wall clock over the "
+               "%d decode steps, the prefill-only call's time subtracted)" % (len(prompts), gen),
+               algorithmic_bytes_per_step=int(round(algo / gen)))}
     fx = os.path.join(ROOT, "tests", "golden", "llama160m_set.json")
     if os.path.exists(fx):
         doc = json.load(open(fx))
@@ -283,13 +321,24 @@ def qwen3_long(gen=256, n_prompt=4096, seed=6):
     t = time.perf_counter()
     m.begin(prompt, gen)
     tp = time.perf_counter() - t
+    m.profile(True)
     t = time.perf_counter()
     m.steps(gen)
     td = time.perf_counter() - t
+    m.profile(False)
+    launches, kernel_ms, positions = m.profile_read()
     r = m.end(gen)
     m.close()
     rec = {"prefill_s": round(tp, 4), "prefill_rows_s": round(n_prompt / tp, 1),
            "decode_tok_s": round(gen / td, 2), "witness": r["witness"]}
+    if launches:
+        wb, kvb = spec_bytes(spec)
+        algo = sum(wb + kvb * (int(p) + 1) for p in positions)
+        rec["roofline"] = roofline_obj(
+            algo, kernel_ms * 1e-3, "k_decode (persistent, split attention; HIP events per launch)",
+            launches=launches, us_per_launch=round(kernel_ms * 1e3 / launches, 2),
+            algorithmic_bytes_per_launch=int(round(algo / launches)),
+            positions=[int(positions[0]), int(positions[-1])])
     fx = os.path.join(ROOT, "tests", "golden", "qwen3_fixture.json")
     if os.path.exists(fx):
         ref = json.load(open(fx)).get("qwen3-0.6b-4096")
@@ -367,6 +416,8 @@ def main():
     ap.add_argument("--no-roofline", action="store_true")
     ap.add_argument("--no-batch", action="store_true", help="skip the batched-decode sizes")
     ap.add_argument("--no-qwen3", action="store_true", help="skip the Qwen3 4096+256 run")
+    ap.add_argument("--only", choices=["qwen3", "batch", "llama"], default=None,
+                    help="run one side workload alone and print its JSON (profiling)")
     ap.add_argument("--gemv-only", action="store_true",
                     help="only the strict-order GEMV rooflines (config 1, the stream, the LM head)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -383,6 +434,17 @@ def main():
         torch.cuda.synchronize()
         log("copied 3 x %d bytes" % (4 * n))
         print(json.dumps({"copy_bytes": 4 * n, "copies": 3}), flush=True)
+        return
+    if a.only:
+        from cis2amd import artifacts
+        spec = artifacts.SPECS["smollm2-135m"]
+        if a.only == "qwen3":
+            out = {"qwen3_4096": qwen3_long()}
+        elif a.only == "llama":
+            out = {"llama160m_set": llama_set()}
+        else:
+            out = {"batch_decode": batch_decode(spec, artifacts.Weights(spec, SEED))}
+        print(json.dumps(out), flush=True)
         return
     if a.gemv_only:
         print(json.dumps({"gemv_config1": gemv_roofline()}), flush=True)
