@@ -587,7 +587,7 @@ __device__ __forceinline__ void prod_ins(lf4* W4, const lf4* x4, uint32_t bf4, u
 // form chunk 0, then waves [0, nb) add chunk c (a strict chain per lane,
 // reads kept in flight) while the other waves form chunk c+1.  Returns row
 // `lane` of block `wave` in waves < nb (lanes >= R: row R-1).
-template <uint32_t R>
+template <uint32_t R, uint32_t CD = 8>
 __device__ __forceinline__ float gemv_lds_t(lf* W, const lf* x, uint32_t K, uint32_t nb,
                                             lf4* pad) {
   constexpr uint32_t NC = 4, GP = 64 / R;
@@ -606,7 +606,7 @@ __device__ __forceinline__ float gemv_lds_t(lf* W, const lf* x, uint32_t K, uint
     const uint32_t i0 = nins * c / NC, i1 = nins * (c + 1) / NC;
     if (wv < nb) {
       const uint32_t g0 = i0 * GP, g1 = min(i1 * GP, KG);
-      acc = chain4<8>(W4 + (size_t)wv * bf4 + (size_t)g0 * R + r, g1 - g0, R, acc);
+      acc = chain4<CD>(W4 + (size_t)wv * bf4 + (size_t)g0 * R + r, g1 - g0, R, acc);
     } else if (c + 1 < NC) {
       prod_ins<R>(W4, x4, bf4, nb, KG, i1, nins * (c + 2) / NC, wv - nb, kThreads / 64 - nb,
                   pad);
@@ -646,12 +646,12 @@ __device__ __noinline__ float gemv_lds_generic(uint32_t R, lf* W, const lf* x, u
 // Inlined GEMV for the block heights a call site can see (the persistent
 // kernel's layouts: R = min(32, 36864/K), gate/up R/2); any other height
 // takes the generic out-of-line path.
-template <uint32_t R0, uint32_t... Rs>
+template <uint32_t CD, uint32_t R0, uint32_t... Rs>
 __device__ __forceinline__ float gemv_lds(uint32_t R, lf* W, const lf* x, uint32_t K, uint32_t nb,
                                           lf4* pad) {
-  if (R == R0) return gemv_lds_t<R0>(W, x, K, nb, pad);
+  if (R == R0) return gemv_lds_t<R0, CD>(W, x, K, nb, pad);
   if constexpr (sizeof...(Rs) > 0) {
-    return gemv_lds<Rs...>(R, W, x, K, nb, pad);
+    return gemv_lds<CD, Rs...>(R, W, x, K, nb, pad);
   } else {
     return gemv_lds_generic(R, W, x, K, nb);
   }
@@ -724,14 +724,15 @@ __device__ __forceinline__ float gemv_tree(uint32_t R, lf* W, const lf* x, uint3
   }
 }
 
-// The GEMV of a call site in the reduction order TR selects.
-template <bool TR, uint32_t... Rs>
+// The GEMV of a call site in the reduction order TR selects; CD: reads kept
+// in flight by the sequential order's chain.
+template <bool TR, uint32_t CD, uint32_t... Rs>
 __device__ __forceinline__ float gemv_sel(uint32_t R, lf* W, const lf* x, uint32_t K,
                                           uint32_t nb, lf4* pad) {
   if constexpr (TR) {
     return gemv_tree<Rs...>(R, W, x, K, nb, pad);
   } else {
-    return gemv_lds<Rs...>(R, W, x, K, nb, pad);
+    return gemv_lds<CD, Rs...>(R, W, x, K, nb, pad);
   }
 }
 
@@ -939,7 +940,7 @@ __device__ __forceinline__ void run_qkv(const DecodeArgs& a, uint32_t l, uint32_
   stamp(a, l, P_QKV, t, 1);
   rmsnorm_lds<TR>(x, nw, a.eps, a.H, ln, ln, s_inv);
   stamp(a, l, P_QKV, t, 3);
-  const float acc = gemv_sel<TR, 32>(a.Rq, s.w, ln, a.H, 1, s.pad);
+  const float acc = gemv_sel<TR, 8, 32>(a.Rq, s.w, ln, a.H, 1, s.pad);
   const uint32_t row = g.blk * a.Rq + threadIdx.x;
   if (threadIdx.x < a.Rq && row < g.M) {
     const float r = g.bias ? acc + G(g.bias)[row] : acc;
@@ -1519,7 +1520,7 @@ __device__ __forceinline__ void run_o(const DecodeArgs& a, uint32_t l, uint32_t 
            [=](uint32_t i) { return i < qd ? att + i : hin + (i - qd); });
   }
   stamp(a, l, P_O, t, 1);
-  const float acc = gemv_sel<TR, 32, 18>(a.Ro, s.w, x, qd, 1, s.pad);
+  const float acc = gemv_sel<TR, 8, 32, 18>(a.Ro, s.w, x, qd, 1, s.pad);
   stamp(a, l, P_O, t, 3);
   if (threadIdx.x < nr) put_word(ac.h1 + r0 + threadIdx.x, hres[threadIdx.x] + acc, a.epoch);
   stamp(a, l, P_O, t, 2);
@@ -1542,7 +1543,7 @@ __device__ __forceinline__ void run_gu(const DecodeArgs& a, uint32_t l, uint32_t
   stamp(a, l, P_GU, t, 1);
   rmsnorm_lds<TR>(x, nw, a.eps, a.H, ln, ln, s_inv);
   stamp(a, l, P_GU, t, 3);
-  const float acc = gemv_sel<TR, 16>(a.Rg, s.w, ln, a.H, 2, s.pad);
+  const float acc = gemv_sel<TR, 8, 16>(a.Rg, s.w, ln, a.H, 2, s.pad);
   const uint32_t wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
   if (wv == 0) gx[lane] = acc;
   __syncthreads();
@@ -1571,7 +1572,9 @@ __device__ __forceinline__ void run_d(const DecodeArgs& a, uint32_t l, uint32_t 
   gather(x, I + nr, a.epoch, a.err,
          [=](uint32_t i) { return i < I ? hid + i : h1 + (i - I); });
   stamp(a, l, P_D, t, 1);
-  const float acc = gemv_sel<TR, 32, 24, 12>(a.Rd, s.w, x, I, 1, s.pad);
+  // the 1536- to 3072-long chain keeps 12 reads in flight (8 elsewhere:
+  // deeper rings slowed the shorter GEMVs, measured)
+  const float acc = gemv_sel<TR, 12, 32, 24, 12>(a.Rd, s.w, x, I, 1, s.pad);
   stamp(a, l, P_D, t, 3);
   if (threadIdx.x < nr) put_word(ac.hout + r0 + threadIdx.x, hres[threadIdx.x] + acc, a.epoch);
   stamp(a, l, P_D, t, 2);
@@ -1608,8 +1611,8 @@ __device__ __forceinline__ void run_lm(const DecodeArgs& a, const Lds& s) {
       }
       c = cand_wave_dpp(c);
       if (lane == 0) {
-        st_ag(a.cand + 2 * b, __float_as_uint(c.v));
-        st_ag(a.cand + 2 * b + 1, c.i);
+        __hip_atomic_store((gw*)a.cand + b, ((u64)c.i << 32) | __float_as_uint(c.v),
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
       if (b == 0 && lane == 0) st_ag(a.cand + 2 * a.nl, acc != acc ? 1u : 0u);
     }
@@ -1626,7 +1629,7 @@ __device__ __forceinline__ void run_lm(const DecodeArgs& a, const Lds& s) {
     for (uint32_t b = wg; b < a.nl; b += a.nwg) {
       if (prev != UINT32_MAX) publish(prev, prev_acc);
       if (b + a.nwg < a.nl) prefetch_rows_async(a.lm, a.Rl, a.H, b + a.nwg, nxt);
-      prev_acc = gemv_sel<TR, 32>(a.Rl, cur, hn, a.H, 1, s.pad);
+      prev_acc = gemv_sel<TR, 8, 32>(a.Rl, cur, hn, a.H, 1, s.pad);
       prev = b;
       ++done;
       wait_vm0();
@@ -1642,7 +1645,7 @@ __device__ __forceinline__ void run_lm(const DecodeArgs& a, const Lds& s) {
         prefetch_rows(a.lm, a.Rl, a.H, b, s.w);
         __syncthreads();
       }
-      const float acc = gemv_sel<TR, 32>(a.Rl, s.w, hn, a.H, 1, s.pad);
+      const float acc = gemv_sel<TR, 8, 32>(a.Rl, s.w, hn, a.H, 1, s.pad);
       publish(b, acc);
       ++done;
       __syncthreads();
@@ -1661,10 +1664,19 @@ __device__ __forceinline__ void run_lm(const DecodeArgs& a, const Lds& s) {
   }
   __syncthreads();
   if (!s_last) return;
+  // every block's (value, index) pair as one 64-bit word, eight per thread
+  // in flight
   Cand c = {0.0f, UINT32_MAX};
-  for (uint32_t b = threadIdx.x; b < a.nl; b += kThreads) {
-    Cand o = {__uint_as_float(ld_ag(a.cand + 2 * b)), ld_ag(a.cand + 2 * b + 1)};
-    c = cand_pick(c, o);
+  const gw* cw = (const gw*)a.cand;
+  for (uint32_t b0 = threadIdx.x; b0 < a.nl; b0 += 8 * kThreads) {
+    u64 w[8];
+#pragma unroll
+    for (uint32_t u = 0; u < 8; ++u)
+      if (b0 + u * kThreads < a.nl) w[u] = get_word(cw + b0 + u * kThreads);
+#pragma unroll
+    for (uint32_t u = 0; u < 8; ++u)
+      if (b0 + u * kThreads < a.nl)
+        c = cand_pick(c, Cand{__uint_as_float((uint32_t)w[u]), (uint32_t)(w[u] >> 32)});
   }
   const Cand r = cand_block(c, red);
   if (threadIdx.x == 0) {
