@@ -22,7 +22,7 @@ layer (medians over the middle layers and the recorded launches):
 
 Usage:
   python -m cis2amd.timeline [--spec smollm2-135m] [--reduction 0|1]
-      [--prompt 32] [--steps 24] [--from-pos 40] [--file PATH]
+      [--prompt 32] [--steps 24] [--from-pos 40] [--max-pos N] [--file PATH]
 """
 import argparse
 import os
@@ -36,13 +36,16 @@ PHASES = ["QKV", "ATT", "O", "GU", "D"]
 TICK_US = 0.01  # s_memrealtime: 100 MHz
 
 
-def record(spec_name, reduction, n_prompt, steps, path, seed=20261201):
+def record(spec_name, reduction, n_prompt, steps, path, seed=20261201, max_pos=None):
+    """Decodes `steps` greedy tokens after an `n_prompt`-token prompt with
+    the timeline on; max_pos (default prompt + steps) sizes the context as a
+    longer decode would (the attention plan depends on it)."""
     os.environ["CIS2_TIMELINE"] = path
     from . import Cis2Model, artifacts
     spec = artifacts.SPECS[spec_name]
     w = artifacts.Weights(spec, seed)
     prompt = artifacts.prompt_ids(seed, spec.vocab, n_prompt)
-    m = Cis2Model(spec, w, max_pos=n_prompt + steps, reduction_mode=reduction)
+    m = Cis2Model(spec, w, max_pos=max(max_pos or 0, n_prompt + steps), reduction_mode=reduction)
     try:
         m.begin(prompt, steps)
         m.steps(steps)
@@ -137,10 +140,12 @@ def main(argv=None):
     ap.add_argument("--prompt", type=int, default=32)
     ap.add_argument("--steps", type=int, default=24)
     ap.add_argument("--from-pos", type=int, default=40)
+    ap.add_argument("--max-pos", type=int, default=None,
+                    help="context size (default prompt + steps)")
     ap.add_argument("--file", default=None, help="timeline file (default: a temporary file)")
     a = ap.parse_args(argv)
     path = a.file or os.path.join(tempfile.mkdtemp(prefix="cis2tl_"), "timeline.bin")
-    r = record(a.spec, a.reduction, a.prompt, a.steps, path)
+    r = record(a.spec, a.reduction, a.prompt, a.steps, path, max_pos=a.max_pos)
     print("%s reduction=%d prompt=%d steps=%d witness=%s" % (
         a.spec, a.reduction, a.prompt, a.steps, r["witness"]))
     print(summarize(load(path), a.from_pos))

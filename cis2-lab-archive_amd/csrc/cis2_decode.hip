@@ -1343,9 +1343,9 @@ __device__ __forceinline__ void run_att(const DecodeArgs& a, uint32_t l, uint32_
 template <bool TR>
 __device__ __forceinline__ void run_att_score(const DecodeArgs& a, uint32_t l, uint32_t t,
                                               const Lds& s) {
-  const uint32_t C = a.att_chunks, h = t / C, c = t - h * C;
+  const uint32_t C = a.att_chunks, h = t / C, c = t - h * C, P = a.att_cpos;
   const uint32_t hd = a.hd, group = a.nh / a.nkv, kvh = h / group, pos = a.pos, len = pos + 1;
-  const uint32_t j0 = c * kThreads;
+  const uint32_t j0 = c * P;
   stamp(a, l, P_ATT, t, 0);
   if (j0 >= len) {  // no positions in this chunk yet
     stamp(a, l, P_ATT, t, 1);
@@ -1360,9 +1360,8 @@ __device__ __forceinline__ void run_att_score(const DecodeArgs& a, uint32_t l, u
   lf* misc = tmp + hd;
   att_head_inputs<TR>(a, l, h, qv, tmp, misc);
   stamp(a, l, P_ATT, t, 1);
-  if (pos < j0 + kThreads && h % group == 0) store_kv_pos(a, l, kvh, kv, vv);
-  const uint32_t j = j0 + threadIdx.x;
-  if (j < len) {
+  if (pos < j0 + P && h % group == 0) store_kv_pos(a, l, kvh, kv, vv);
+  for (uint32_t j = j0 + threadIdx.x; j < len && j < j0 + P; j += kThreads) {
     const float* kb = a.kc0 + (size_t)l * a.cache_stride + (size_t)kvh * hd * a.max_pos + j;
     const bool cached = j < pos;
     float acc = 0.0f;
@@ -1488,7 +1487,7 @@ __device__ __forceinline__ void run_att_mix(const DecodeArgs& a, uint32_t l, uin
       }
       if (i + 2 < nt) copy_v_rows(tile(i + 2), vrows, a.max_pos, nd, (i + 2) * TP, tile_n(i + 2), TS);
     }
-    __syncthreads();
+    lds_barrier();  // tile i+2's copy stays in flight (waited for before its products)
   }
   if (threadIdx.x < nd) {
     const float p = ss[pos] * vv[threadIdx.x];
@@ -2008,7 +2007,19 @@ bool decode_att_needs_split(const DecodeArgs& a) {
 
 void decode_att_plan(DecodeArgs& a, bool split) {
   a.att_split = split ? 1u : 0u;
-  a.att_chunks = (a.max_pos + kThreads - 1) / kThreads;
+  // positions per score task: 256 (one per thread) when every head's chunks
+  // fit one per workgroup, else the fewest 64-multiples up to 512 that do
+  // (a workgroup holding two score tasks of a layer would finish its second
+  // one late, and every mix task of the head waits for it)
+  uint32_t cp = kThreads;
+  const uint32_t per_head = a.nh ? a.nwg / a.nh : 0;
+  if (per_head > 0 && a.nh * ((a.max_pos + cp - 1) / cp) > a.nwg) {
+    cp = (a.max_pos + per_head - 1) / per_head;
+    cp = (cp + 63) & ~63u;
+    if (cp > 2 * kThreads) cp = 2 * kThreads;
+  }
+  a.att_cpos = cp;
+  a.att_chunks = (a.max_pos + cp - 1) / cp;
   a.natt_s = a.nh * a.att_chunks;
   a.att_dvc = (a.hd + kAttDV - 1) / kAttDV;
   a.natt_v = a.nh * a.att_dvc;

@@ -55,17 +55,18 @@ struct DecodeArgs {
   uint32_t pos, epoch, lm_epoch, want_logits;
   uint32_t tree;  // 1: v0.4-candidate tree reduction order, 0: sequential
   // Split attention (contexts whose K/V rows do not fit one workgroup's
-  // LDS): the ATT phase runs natt_s = nh * att_chunks score tasks (256
-  // positions each) and then natt_v = nh * att_dvc mix tasks (16 output
-  // dims each, V tiles of att_tp positions); scores pass through scw,
-  // tagged words [L][nh][max_pos] (zeroed at start).
-  uint32_t att_split, att_chunks, natt_s, att_dvc, natt_v, att_tp;
+  // LDS): the ATT phase runs natt_s = nh * att_chunks score tasks
+  // (att_cpos positions each, a multiple of 64 in [256, 512]) and then
+  // natt_v = nh * att_dvc mix tasks (16 output dims each, V tiles of att_tp
+  // positions); scores pass through scw, tagged words [L][nh][max_pos]
+  // (zeroed at start).
+  uint32_t att_split, att_chunks, natt_s, att_dvc, natt_v, att_tp, att_cpos;
   uint64_t* scw;
 };
 
 // Floats (4-byte units) of one layer's tagged activation storage.
 size_t decode_act_floats(uint32_t H, uint32_t I, uint32_t qd, uint32_t kvd);
-constexpr uint32_t kTimelineTasks = 256;
+constexpr uint32_t kTimelineTasks = 512;
 constexpr uint32_t kMaxTasks = 6;       // tasks per workgroup per layer
 constexpr uint16_t kNoTask = 0xFFFF;
 // Phases of a layer, in dependency order.

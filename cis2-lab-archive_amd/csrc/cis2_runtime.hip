@@ -686,37 +686,51 @@ void fold_rows(std::vector<Sha256>& w, const float* logits, const uint32_t* ids,
 }  // namespace
 
 // Spreads the tasks of every phase over the workgroups: each task goes to a
-// workgroup with the fewest tasks so far, preferring one whose last task is
-// not in the phase just before (so its next weight copy has a phase of time
-// to land).  Every list is in phase order, which makes the waits acyclic: a
-// task only waits for tasks of earlier (layer, phase), or, for split
-// attention's mix tasks, for score tasks of the same phase, which come
-// first in every list (lower task indices are assigned first).  False when
-// some workgroup would need more than kMaxTasks or a task index exceeds 12
-// bits.
+// workgroup with the fewest tasks of its phase (a phase with more tasks than
+// workgroups: split attention's score and mix tasks, so that no workgroup
+// runs two score tasks while another runs none), then the fewest tasks so
+// far, preferring one whose previous task is not in the phase just before
+// (so its next weight copy has a phase of time to land; a down task's
+// successor is the next layer's QKV task).  Every list is in phase order,
+// which makes the waits acyclic: a task only waits for tasks of earlier
+// (layer, phase), or, for split attention's mix tasks, for score tasks of
+// the same phase, which come first in every list (lower task indices are
+// assigned first).  False when some workgroup would need more than
+// kMaxTasks or a task index exceeds 12 bits.
 static bool assign_tasks(const DecodeArgs& a, std::vector<uint16_t>& table) {
   const uint32_t natt = a.att_split ? a.natt_s + a.natt_v : a.nh;
   const uint32_t n[kPhases] = {a.nq, natt, a.no, a.ng, a.nd};
   const uint32_t W = a.nwg;
   table.assign((size_t)W * kMaxTasks, kNoTask);
-  std::vector<uint32_t> cnt(W, 0);
+  std::vector<uint32_t> cnt(W, 0), same(W, 0);
   std::vector<int> last(W, -2);
+  std::vector<bool> has_qkv(W, false);
   for (uint32_t p = 0; p < kPhases; ++p) {
     if (n[p] >= 4096) return false;
+    std::fill(same.begin(), same.end(), 0u);
+    auto adjacent = [&](uint32_t w) {
+      return last[w] == (int)p - 1 || (p == kPhaseD && has_qkv[w]);
+    };
     for (uint32_t t = 0; t < n[p]; ++t) {
       uint32_t best = W;
       for (uint32_t w = 0; w < W; ++w) {
         // one task of a phase per workgroup, unless the phase has more
-        // tasks than workgroups (split attention's score and mix tasks)
-        if (cnt[w] >= kMaxTasks || (last[w] == (int)p && n[p] <= W)) continue;
+        // tasks than workgroups
+        if (cnt[w] >= kMaxTasks || (same[w] > 0 && n[p] <= W)) continue;
         if (best == W) { best = w; continue; }
-        const bool adj_w = last[w] == (int)p - 1, adj_b = last[best] == (int)p - 1;
+        if (same[w] != same[best]) {
+          if (same[w] < same[best]) best = w;
+          continue;
+        }
+        const bool adj_w = adjacent(w), adj_b = adjacent(best);
         if (cnt[w] < cnt[best] || (cnt[w] == cnt[best] && !adj_w && adj_b)) best = w;
       }
       if (best == W) return false;
       table[(size_t)best * kMaxTasks + cnt[best]] = (uint16_t)(p << 12 | t);
       ++cnt[best];
+      ++same[best];
       last[best] = (int)p;
+      if (p == kPhaseQKV) has_qkv[best] = true;
     }
   }
   return true;
