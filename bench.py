@@ -418,6 +418,8 @@ def main():
     ap.add_argument("--no-qwen3", action="store_true", help="skip the Qwen3 4096+256 run")
     ap.add_argument("--only", choices=["qwen3", "batch", "llama"], default=None,
                     help="run one side workload alone and print its JSON (profiling)")
+    ap.add_argument("--batch-sizes", default="1,8,32,64",
+                    help="batch sizes of the batched decode (comma-separated)")
     ap.add_argument("--gemv-only", action="store_true",
                     help="only the strict-order GEMV rooflines (config 1, the stream, the LM head)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -443,7 +445,8 @@ def main():
         elif a.only == "llama":
             out = {"llama160m_set": llama_set()}
         else:
-            out = {"batch_decode": batch_decode(spec, artifacts.Weights(spec, SEED))}
+            out = {"batch_decode": batch_decode(spec, artifacts.Weights(spec, SEED),
+                                                sizes=tuple(int(v) for v in a.batch_sizes.split(",")))}
         print(json.dumps(out), flush=True)
         return
     if a.gemv_only:
@@ -537,7 +540,8 @@ def main():
         out["gemv_config1"] = gemv_roofline()
         log("standalone GEMV 1536x576:", out["gemv_config1"])
     if not a.no_batch:
-        out["batch_decode"] = batch_decode(spec, weights)
+        out["batch_decode"] = batch_decode(spec, weights,
+                                           sizes=tuple(int(v) for v in a.batch_sizes.split(",")))
         out["llama160m_set"] = llama_set()
     if not a.no_qwen3:
         out["qwen3_4096"] = qwen3_long()

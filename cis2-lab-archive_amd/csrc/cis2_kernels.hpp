@@ -21,6 +21,8 @@ size_t blocked_floats(uint32_t M, uint32_t K, uint32_t R);
 // table under a lock, so contexts on different devices or host threads each
 // see their own device's setting.
 hipError_t ensure_dynamic_lds(const void* fn, size_t bytes);
+// Compute units of the current device (cached per device, thread-safe).
+int device_cu_count();
 
 // One output segment of a multi-segment GEMV launch.
 struct GemvSeg {

@@ -22,6 +22,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <charconv>
 #include <string>
 #include <utility>
 #include <vector>
@@ -95,15 +96,16 @@ inline std::string quoted_ascii(const std::string& s) {
 
 // Shortest round-trip decimal of a double, laid out as Python's float repr
 // (fixed notation for decimal exponents -4 < e <= 16, else d.ddde+XX).
+// The digits are the shortest string that reads back as x and, among those,
+// the one nearest x (std::to_chars): at 2^-24 that is 5.960464477539063e-08,
+// which is not the correctly rounded 16-digit value (...062e-08 does not
+// read back: below a power of two the neighbouring doubles are closer).
 inline std::string float_repr(double x) {
   if (std::isnan(x)) return "NaN";
   if (std::isinf(x)) return x > 0 ? "Infinity" : "-Infinity";
   char b[64];
-  int prec = 1;
-  for (; prec <= 17; ++prec) {
-    snprintf(b, sizeof b, "%.*e", prec - 1, x);
-    if (strtod(b, nullptr) == x) break;
-  }
+  const auto r = std::to_chars(b, b + sizeof b - 1, x, std::chars_format::scientific);
+  *r.ptr = '\0';
   // b = [-]d.ddde[+-]XX: split the digits and the exponent
   std::string t(b);
   const bool neg = t[0] == '-';

@@ -978,12 +978,11 @@ hipError_t bgemm_configure() {
 // CIS2_BGEMM_CB=1 keeps one batch row per thread on every grid (for A/B
 // timing of the two-row form; the results are the same bits either way).
 static bool bgemm_cb_allowed() {
-  static int allowed = -1;
-  if (allowed < 0) {
+  static const bool allowed = [] {
     const char* e = std::getenv("CIS2_BGEMM_CB");
-    allowed = (e && e[0] == '1' && e[1] == 0) ? 0 : 1;
-  }
-  return allowed == 1;
+    return !(e && e[0] == '1' && e[1] == 0);
+  }();
+  return allowed;
 }
 
 hipError_t launch_bgemm_multi(const BgemmSeg* segs, uint32_t nseg, uint32_t n,
@@ -996,14 +995,7 @@ hipError_t launch_bgemm_multi(const BgemmSeg* segs, uint32_t nseg, uint32_t n,
   }
   const BgemmSeg& s0 = segs[0];
   if (s0.K % 4 || s0.ldx % 4 || s0.R == 0 || s0.R > kT) return hipErrorInvalidValue;
-  static int ncu = 0;
-  if (ncu == 0) {
-    int dev = 0;
-    (void)hipGetDevice(&dev);
-    if (hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-        ncu <= 0)
-      ncu = 256;
-  }
+  const int ncu = device_cu_count();
   BgemmArgs a = {};
   a.blk0[0] = 0;
   for (uint32_t i = 0; i < nseg; ++i) {
@@ -1088,14 +1080,7 @@ hipError_t launch_attention_rows(const float* q, const float* kc, const float* v
   // Few rows (decode steps): one head per workgroup, for the most
   // workgroups.  Many rows: the most heads of one KV head (a divisor of
   // the group) whose LDS fits, so K and V are read once per group.
-  static int ncu = 0;
-  if (ncu == 0) {
-    int dev = 0;
-    (void)hipGetDevice(&dev);
-    if (hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-        ncu <= 0)
-      ncu = 256;
-  }
+  const int ncu = device_cu_count();
   uint32_t hpw = 1;
   if ((uint64_t)rows.n * nkv >= 4 * (uint64_t)ncu) {
     for (uint32_t h = std::min(group, kMaxHeadsPerWg); h > 1; --h)

@@ -192,6 +192,25 @@ def test_canonical_form_equals_python(harness, tmp_path_factory, value):
     assert r.stdout == receipts.canonical(value).decode()
 
 
+def test_canonical_floats_at_power_of_two_boundaries(harness, tmp_path):
+    """Below a power of two the neighbouring doubles are twice as close, so
+    the correctly rounded n-digit decimal can fail to read back while the
+    next one up does (2^-24: 5.960464477539063e-08, not ...0625e-08); every
+    power of two, its neighbours and a few classic cases."""
+    import math
+    vals = []
+    for k in range(-1074, 1024):
+        v = math.ldexp(1.0, k)
+        vals += [v, math.nextafter(v, 0.0), math.nextafter(v, math.inf), -v]
+    vals += [0.1 + 0.2, 1e23, 9007199254740993.0, 5e-324, 2.2250738585072014e-308,
+             1.7976931348623157e308, 1e16, 1e-4, 9.999999999999999e-5, 123456789012345678.0]
+    p = tmp_path / "v.json"
+    p.write_text(json.dumps(vals))
+    r = run(harness, "canon", str(p))
+    assert r.returncode == 0, r.stderr
+    assert r.stdout == receipts.canonical(vals).decode()
+
+
 def test_cli_verify_chain(harness, tmp_path):
     if not os.path.exists(CLI):
         pytest.skip("cis2_host not built")
