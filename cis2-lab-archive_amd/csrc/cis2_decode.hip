@@ -527,6 +527,50 @@ __device__ __forceinline__ float chain_vec(const lf* p, uint32_t n, float acc) {
   return acc;
 }
 
+// chain4's order with reads past the end allowed: the caller keeps D
+// groups of readable LDS after group n-1 (at the same stride), so the ring
+// is refilled unconditionally at fixed offsets (no address arithmetic and
+// no branches per step; the extra reads are never added); the last partial
+// round adds its groups under uniform tests.  n wave-uniform.
+template <uint32_t D = 8>
+__device__ __forceinline__ float chain4s(const lf4* p, uint32_t n, uint32_t st, float acc) {
+  f4 ring[D];
+#pragma unroll
+  for (uint32_t u = 0; u < D; ++u) ring[u] = p[(size_t)u * st];
+  uint32_t g = 0;
+  for (; g + D <= n; g += D) {
+#pragma unroll
+    for (uint32_t u = 0; u < D; ++u) {
+      const f4 v = ring[u];
+      acc = acc + v.x;
+      acc = acc + v.y;
+      acc = acc + v.z;
+      acc = acc + v.w;
+      ring[u] = p[(size_t)(g + u + D) * st];
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+#pragma unroll
+  for (uint32_t u = 0; u + 1 < D; ++u) {
+    if (g + u < n) {
+      const f4 v = ring[u];
+      acc = acc + v.x;
+      acc = acc + v.y;
+      acc = acc + v.z;
+      acc = acc + v.w;
+    }
+  }
+  return acc;
+}
+
+// Strict sum of n contiguous LDS floats (16-byte aligned) with 60 readable
+// floats after them.
+__device__ __forceinline__ float chain_vec_s(const lf* p, uint32_t n, float acc) {
+  acc = chain4s<15>(reinterpret_cast<const lf4*>(p), n >> 2, 1, acc);
+  for (uint32_t i = n & ~3u; i < n; ++i) acc = acc + p[i];
+  return acc;
+}
+
 // ---------------------------------------------------------------------------
 // GEMV on LDS-resident row blocks ([K/4][R][4] floats per block)
 // ---------------------------------------------------------------------------
@@ -741,6 +785,23 @@ __device__ __forceinline__ float tree_part(const lf* p, uint32_t n, uint32_t st)
   float lv[32];
 #pragma unroll
   for (uint32_t i = 0; i < 32; ++i) lv[i] = i < n ? p[(size_t)i * st] : 0.0f;
+  return tree32(lv);
+}
+// tree_part of 32 contiguous 16-byte-aligned floats, the whole block
+// readable (the values past n count as +0).
+__device__ __forceinline__ float tree_part_v(const lf* p, uint32_t n) {
+  float lv[32];
+  const lf4* p4 = (const lf4*)p;
+#pragma unroll
+  for (uint32_t i = 0; i < 8; ++i) {
+    const f4 v = p4[i];
+    lv[4 * i] = v.x;
+    lv[4 * i + 1] = v.y;
+    lv[4 * i + 2] = v.z;
+    lv[4 * i + 3] = v.w;
+  }
+#pragma unroll
+  for (uint32_t i = 0; i < 32; ++i) lv[i] = i < n ? lv[i] : 0.0f;
   return tree32(lv);
 }
 // Tree-order sum over n strided LDS values p[i * st] (scores: one column of
@@ -1140,87 +1201,141 @@ __device__ __forceinline__ void wave_lds_order() {
   __builtin_amdgcn_wave_barrier();
 }
 
-// Softmax and V mix of one head by wave 0 alone, after the scores of
-// positions 0..pos are in ss[] (written by the whole workgroup before a
-// barrier): first-wins max (NaN at position 0 wins), pinned exp, the
-// denominator (strict chain, or tree32 blocks folded from 0), a true
-// divide, then lane d's V-mix chain out_d = fold_j (p_j * v_j[d]) over the
-// V rows in LDS (row d at vl + d*S) and this position's own v.  part: tree
-// partials; misc: 4 floats.  The other waves are not involved: no barrier.
-template <bool TR>
-__device__ __forceinline__ void att_tail_wave0(const DecodeArgs& a, gw* out, lf* ss, uint32_t len,
-                                               uint32_t pos, const lf* vl, uint32_t S,
-                                               const lf* vv, lf* part) {
-  const uint32_t lane = threadIdx.x & 63, hd = a.hd;
-  Cand best = {0.0f, UINT32_MAX};
-  for (uint32_t j = lane; j < len; j += 64) {
-    const float v = ss[j];
-    if (v == v) best = cand_pick(best, Cand{v, j});
+// Softmax and V mix of one head by the whole workgroup, after the scores
+// of positions 0..pos are in ss[] (written before a barrier):
+//  1. every wave finds the maximum over all scores itself (a DPP wave
+//     reduction over the non-NaN scores; a NaN at position 0, or scores
+//     that are all NaN, give NaN): no cross-wave step.  This is the value
+//     of the first maximum; where its bits could differ (+0 against -0),
+//     e_j = exp(s_j - max) does not: both give exp(+-0) = 1;
+//  2. the pinned exp of every position, spread over the block;
+//  3. wave 0 forms the denominator (a strict chain, or tree32 blocks folded
+//     from 0; partials in `part`) into misc[1];
+//  4. the true divide p_j = e_j / den, spread over the block;
+//  5. lane d of the chain waves (one wave per 64 dims) runs the V mix
+//     out_d = fold_j (p_j * v_j[d]) over its cached V row in LDS (row d at
+//     vl + d*S, positions < pos) and then this position's own v: it forms
+//     each product itself, p_j taken by DPP broadcast (row_newbcast) from a
+//     register that holds 16 consecutive probabilities in every 16-lane
+//     row, the next 16 positions' reads in flight.
+// A barrier separates steps 1-4.  hd <= 192.  The chains read up to 60
+// floats past the scores and up to 32 past the last V row (the scores
+// region has 64 spare floats; the vector region follows the V rows).
+// Lane k of this lane's 16-lane row (DPP row_newbcast:k).
+template <uint32_t K>
+__device__ __forceinline__ float bcast16(float v) {
+  return __int_as_float(
+      __builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x150 + (int)K, 0xF, 0xF, false));
+}
+// acc + v[0].x * P_0 + v[0].y * P_1 + ... + v[3].w * P_15 in order (P_k:
+// lane k of this lane's 16-lane row), each product rounded, then the add.
+template <uint32_t K>
+__device__ __forceinline__ void mix_step(float& acc, float P, const f4 (&v)[4]) {
+  const f4 w = v[K / 4];
+  const float x = K % 4 == 0 ? w.x : K % 4 == 1 ? w.y : K % 4 == 2 ? w.z : w.w;
+  const float t = x * bcast16<K>(P);
+  acc = acc + t;
+}
+template <uint32_t K = 0>
+__device__ __forceinline__ void mix16(float& acc, float P, const f4 (&v)[4]) {
+  if constexpr (K < 16) {
+    mix_step<K>(acc, P, v);
+    mix16<K + 1>(acc, P, v);
   }
-  const Cand b = cand_wave_dpp(best);
-  const float mx = (ss[0] != ss[0] || b.i == UINT32_MAX) ? ss[0] : ss[b.i];
-  for (uint32_t j = lane; j < len; j += 64) {
+}
+// The first rem (< 16) steps of mix16.
+template <uint32_t K>
+__device__ __forceinline__ void mix_tail(float& acc, float P, const f4 (&v)[4], uint32_t rem) {
+  if constexpr (K < 15) {
+    if (K < rem) {
+      mix_step<K>(acc, P, v);
+      mix_tail<K + 1>(acc, P, v, rem);
+    }
+  }
+}
+
+template <bool TR>
+__device__ __forceinline__ void att_tail_block(const DecodeArgs& a, gw* out, lf* ss, uint32_t len,
+                                               uint32_t pos, lf* vl, uint32_t S, const lf* vv,
+                                               lf* part, lf* misc) {
+  const uint32_t lane = threadIdx.x & 63, hd = a.hd;
+  const uint32_t wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const float s0 = ss[0];
+  float m = -__builtin_inff();
+  for (uint32_t j0 = 0; j0 < len; j0 += 256) {  // four reads in flight per lane
+    float v[4];
+#pragma unroll
+    for (uint32_t u = 0; u < 4; ++u) {
+      const uint32_t j = j0 + u * 64 + lane;
+      v[u] = j < len ? ss[j] : -__builtin_inff();
+    }
+#pragma unroll
+    for (uint32_t u = 0; u < 4; ++u) m = v[u] > m ? v[u] : m;  // false for NaN
+  }
+  const float mx = s0 != s0 ? s0 : wave_max(m);
+  lds_barrier();
+  for (uint32_t j = threadIdx.x; j < len; j += kThreads) {
     const float dlt = ss[j] - mx;
     ss[j] = exp_pinned(dlt);
   }
-  wave_lds_order();
-  float den;
-  if constexpr (TR) {
-    const uint32_t nbk = (len + 31) / 32;
-    for (uint32_t t = lane; t < nbk; t += 64) part[t] = tree_part(ss + 32 * t, len - 32 * t, 1);
-    wave_lds_order();
-    den = chain1(part, nbk, 1, 0.0f);
-  } else {
-    den = chain_vec(ss, len, 0.0f);
+  lds_barrier();
+  if (wv == 0) {
+    float den;
+    if constexpr (TR) {
+      const uint32_t nbk = (len + 31) / 32;
+      for (uint32_t t = lane; t < nbk; t += 64) part[t] = tree_part_v(ss + 32 * t, len - 32 * t);
+      wave_lds_order();
+      den = chain1(part, nbk, 1, 0.0f);
+    } else {
+      den = chain_vec_s(ss, len, 0.0f);
+    }
+    if (lane == 0) misc[1] = den;
   }
-  for (uint32_t j = lane; j < len; j += 64) {
+  lds_barrier();
+  const float den = misc[1];
+  for (uint32_t j = threadIdx.x; j < len; j += kThreads) {
     const float pj = ss[j] / den;
     ss[j] = pj;
   }
-  wave_lds_order();
-  const lf4* p4 = (const lf4*)ss;
-  const uint32_t ng = pos >> 2;
-  for (uint32_t d = lane; d < hd; d += 64) {
-    const lf4* v4 = (const lf4*)(vl + (size_t)d * S);
+  lds_barrier();
+  const uint32_t ncw = (hd + 63) >> 6, s4 = S >> 2;  // chain waves
+  if (wv < ncw) {  // every lane runs (the broadcasts read whole rows)
+    const uint32_t d = (wv << 6) + lane, dr = d < hd ? d : hd - 1, k = lane & 15;
+    const lf4* vr = (const lf4*)vl + (size_t)dr * s4;
+    const uint32_t nb = pos >> 4;  // whole blocks of 16 positions
     float acc = 0.0f;
-    uint32_t g = 0;
-    for (; g + 4 <= ng; g += 4) {
-      f4 pv[4], vr[4];
+    // two register sets, each block's reads issued one block ahead
+    float PA = ss[k], PB;
+    f4 vA[4], vB[4];
 #pragma unroll
-      for (uint32_t u = 0; u < 4; ++u) {
-        pv[u] = p4[g + u];
-        vr[u] = v4[g + u];
-      }
+    for (uint32_t u = 0; u < 4; ++u) vA[u] = vr[u];
+    uint32_t m = 0;
+    for (; m + 2 <= nb; m += 2) {
+      PB = ss[16 * (m + 1) + k];
 #pragma unroll
-      for (uint32_t u = 0; u < 4; ++u) {
-        const float t0 = pv[u].x * vr[u].x;
-        acc = acc + t0;
-        const float t1 = pv[u].y * vr[u].y;
-        acc = acc + t1;
-        const float t2 = pv[u].z * vr[u].z;
-        acc = acc + t2;
-        const float t3 = pv[u].w * vr[u].w;
-        acc = acc + t3;
-      }
+      for (uint32_t u = 0; u < 4; ++u) vB[u] = vr[4 * (m + 1) + u];
+      mix16(acc, PA, vA);
+      PA = ss[16 * (m + 2) + k];
+#pragma unroll
+      for (uint32_t u = 0; u < 4; ++u) vA[u] = vr[4 * (m + 2) + u];
+      mix16(acc, PB, vB);
     }
-    for (; g < ng; ++g) {
-      const f4 pv = p4[g], vr = v4[g];
-      const float t0 = pv.x * vr.x;
-      acc = acc + t0;
-      const float t1 = pv.y * vr.y;
-      acc = acc + t1;
-      const float t2 = pv.z * vr.z;
-      acc = acc + t2;
-      const float t3 = pv.w * vr.w;
-      acc = acc + t3;
+    if (m < nb) {  // one whole block left
+      PB = ss[16 * (m + 1) + k];
+#pragma unroll
+      for (uint32_t u = 0; u < 4; ++u) vB[u] = vr[4 * (m + 1) + u];
+      mix16(acc, PA, vA);
+      PA = PB;
+#pragma unroll
+      for (uint32_t u = 0; u < 4; ++u) vA[u] = vB[u];
     }
-    for (uint32_t j = 4 * ng; j < pos; ++j) {
-      const float t = ss[j] * vl[(size_t)d * S + j];
+    // the last partial block: positions 16*nb .. pos-1 (uniform tests)
+    mix_tail<0>(acc, PA, vA, pos - 16 * nb);
+    if (d < hd) {
+      const float t = ss[pos] * vv[d];
       acc = acc + t;
+      put_word(out + d, acc, a.epoch);
     }
-    const float t = ss[pos] * vv[d];
-    acc = acc + t;
-    put_word(out + d, acc, a.epoch);
   }
 }
 
@@ -1241,7 +1356,8 @@ __device__ __forceinline__ void run_att(const DecodeArgs& a, uint32_t l, uint32_
   lf* kt = ss + a.max_pos + 64;  // K: one row of KS floats per cached position
   const uint32_t S = att_row_stride(pos), KS = att_k_stride(hd);
   lf* vl = kt + (size_t)((pos + 3) & ~3u) * KS;  // V: one row of S floats per head dim
-  const bool in_lds = hd % 4 == 0 && att_lds_floats(hd, pos, a.max_pos) <= wfloats;
+  const bool in_lds =
+      hd % 4 == 0 && hd <= 192 && att_lds_floats(hd, pos, a.max_pos) <= wfloats;
   stamp(a, l, P_ATT, h, 0);
   if (in_lds) prefetch_kv(a, l, kvh, kt, KS, vl, S);
   att_head_inputs<TR>(a, l, h, qv, tmp, misc);
@@ -1280,11 +1396,11 @@ __device__ __forceinline__ void run_att(const DecodeArgs& a, uint32_t l, uint32_
       ss[pos] = (TR ? tree_col(tmp, hd, 1, 0.0f) : chain1(tmp, hd, 1, 0.0f)) * a.scale;
   }
   if (in_lds) {
-    // the scores are in ss; wave 0 finishes the head (tree partials in the
-    // K region, which no one reads any more)
+    // the scores are in ss; the block finishes the head (tree partials in
+    // the K region, which no one reads any more)
     __syncthreads();
     stamp(a, l, P_ATT, h, 3);
-    if (threadIdx.x < 64) att_tail_wave0<TR>(a, ac.att + (size_t)h * hd, ss, len, pos, vl, S, vv, kt);
+    att_tail_block<TR>(a, ac.att + (size_t)h * hd, ss, len, pos, vl, S, vv, kt, misc);
     __syncthreads();
     stamp(a, l, P_ATT, h, 2);
     return;
@@ -1731,6 +1847,9 @@ void k_decode(DecodeArgs a) {
   s.v = s.w + wbytes / 4;
   s.pad = (lf4*)(s.v + decode_vec_floats(a));
   const uint32_t wg = blockIdx.x;
+  // profiling: workgroup entry and exit in the layer-0 LM slots (the LM
+  // phase stamps the last layer's)
+  if (a.L > 1) stamp(a, 0, P_LM, wg, 0);
   // this workgroup's tasks (the same in every layer), in phase order
   uint32_t task[kMaxTasks];
   uint32_t ntask = 0;
@@ -1771,6 +1890,7 @@ void k_decode(DecodeArgs a) {
     }
   }
   if (a.want_logits) run_lm<TR>(a, s);
+  if (a.L > 1) stamp(a, 0, P_LM, wg, 2);
 }
 
 // ---------------------------------------------------------------------------
@@ -1997,7 +2117,8 @@ bool decode_att_ok(const DecodeArgs& a) {
   if (a.att_split) return a.att_tp >= 32 && a.nh % a.nkv == 0;
   // the one-task form keeps K and V in LDS when they fit (head_dim a
   // multiple of 4), else streams tiles of at least 32 positions
-  return (a.hd % 4 == 0 && att_lds_floats(a.hd, a.max_pos, a.max_pos) <= wfloats) ||
+  return (a.hd % 4 == 0 && a.hd <= 192 &&
+          att_lds_floats(a.hd, a.max_pos, a.max_pos) <= wfloats) ||
          att_tile_positions(a.hd, a.max_pos, wfloats) >= 32;
 }
 

@@ -113,26 +113,34 @@ __device__ __forceinline__ float rsqrt_cr(float x) {
 
 // Exponent-field scaling (code/cis2-fp/src/math.rs:206-225): underflow is
 // +0 for either sign, overflow a signed infinity.
+// Written as selects (the same value as testing the cases in turn: zero,
+// underflow, overflow, in range) so that a loop over it does not branch.
 __device__ __forceinline__ float ldexp_bits(float y, int32_t k) {
-  if (y == 0.0f) return y;
-  uint32_t b = bf(y);
-  int32_t e = (int32_t)((b >> 23) & 0xFFu) + k;
-  if (e <= 0) return 0.0f;
-  if (e >= 0xFF) return (b >> 31) ? fb(0xFF800000u) : fb(0x7F800000u);
-  return fb((b & 0x807FFFFFu) | ((uint32_t)e << 23));
+  const uint32_t b = bf(y);
+  const int32_t e = (int32_t)((b >> 23) & 0xFFu) + k;
+  const float ov = (b >> 31) ? fb(0xFF800000u) : fb(0x7F800000u);
+  const float in = fb((b & 0x807FFFFFu) | ((uint32_t)e << 23));
+  const float r = e <= 0 ? 0.0f : (e >= 0xFF ? ov : in);
+  return y == 0.0f ? y : r;
 }
 
-// exp (code/cis2-fp/src/math.rs:167-204; spec §6.2).
+// exp (code/cis2-fp/src/math.rs:167-204; spec §6.2).  The main path runs
+// on every lane, with 0 standing in for the special inputs (NaN, x > 88,
+// x < -88) whose results are selected at the end: the same bits as
+// returning early, without divergent branches in a loop over positions.
+// On the main path |z0| < 128, where floor_f32 and sat_i32 reduce to the
+// truncating conversion (and its correction) used here.
 __device__ __forceinline__ float exp_pinned(float x) {
   x = daz(x);
-  if (x != x) return fb(kQNaN);
-  if (x > 88.0f) return fb(0x7F800000u);
-  if (x < -88.0f) return 0.0f;
-  float t = x * fb(kExpLog2e);
+  const bool nan = x != x, hi = x > 88.0f, lo = x < -88.0f;
+  const float xr = (nan || hi || lo) ? 0.0f : x;
+  float t = xr * fb(kExpLog2e);
   float z0 = t + 0.5f;
-  float k = floor_f32(z0);
+  const int32_t zi = (int32_t)z0;
+  float k = (float)zi;
+  if (z0 < k) k = k - 1.0f;
   float kc1 = k * fb(kExpC1);
-  float r0 = x - kc1;
+  float r0 = xr - kc1;
   float kc2 = k * fb(kExpC2);
   float r = r0 - kc2;
   float r2 = r * r;
@@ -146,7 +154,11 @@ __device__ __forceinline__ float exp_pinned(float x) {
   float pr2 = p * r2;
   float s = pr2 + r;
   float y = s + 1.0f;
-  return ldexp_bits(y, sat_i32(k));
+  float e = ldexp_bits(y, (int32_t)k);
+  e = lo ? 0.0f : e;
+  e = hi ? fb(0x7F800000u) : e;
+  e = nan ? fb(kQNaN) : e;
+  return e;
 }
 
 // Octant reduction in binary64 (code/cis2-fp/src/math.rs:248-264).
