@@ -386,18 +386,24 @@ def sampled_decode(spec, weights, prompt):
 def tree_decode(spec, weights, prompt, gen=256):
     """The same greedy workload in the v0.4-candidate tree reduction order
     (reduction_mode 1, the reference's -DCIS2_REDUCTION_TREE build): tok/s
-    over steps 17..256 and the witness against the reference driver's
+    over steps 17..256, the kernel time per launch (HIP events around each
+    launch on its stream) and the witness against the reference driver's
     tree-order fixture."""
     from cis2amd import Cis2Model
     m = Cis2Model(spec, weights, max_pos=len(prompt) + gen, reduction_mode=1)
     m.begin(prompt, gen)
     m.steps(16)
+    m.profile(True)
     t = time.perf_counter()
     m.steps(gen - 16)
     dt = time.perf_counter() - t
+    m.profile(False)
+    launches, kernel_ms, _ = m.profile_read()
     r = m.end(gen)
     m.close()
     rec = {"tok_s": round((gen - 16) / dt, 1), "witness": r["witness"]}
+    if launches:
+        rec["us_per_launch"] = round(kernel_ms * 1e3 / launches, 2)
     fx = os.path.join(ROOT, "tests", "golden", "model_fixtures.json")
     if os.path.exists(fx):
         ref = json.load(open(fx)).get("smollm2-135m-tree")
