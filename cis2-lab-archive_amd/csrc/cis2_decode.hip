@@ -157,6 +157,7 @@ __host__ __device__ inline size_t decode_wregion_bytes(const DecodeArgs& a) {
   m = m > g ? m : g;
   m = m > d ? m : d;
   m = m > lm ? m : lm;
+  m = m > a.wslot ? m : a.wslot;
   // Attention: scores always in LDS; K/V rows in LDS for the positions that
   // fit in 150 KiB, read from HBM beyond that.
   size_t att = att_lds_floats(a.hd, a.max_pos, a.max_pos);
@@ -981,14 +982,14 @@ __device__ __forceinline__ QkvGeom qkv_geom(const DecodeArgs& a, const LayerW& L
 // One row block of q, k or v: input_layernorm, GEMV, bias (main.rs:405-413).
 template <bool TR>
 __device__ __forceinline__ void run_qkv(const DecodeArgs& a, uint32_t l, uint32_t t, const Lds& s,
-                                       uint32_t tok) {
+                                       uint32_t tok, lf* wl, bool pre) {
   const LayerW Lw = a.layers[l];
   const Act ac = act_of(a, l);
   const QkvGeom g = qkv_geom(a, Lw, ac, t);
   lf* x = s.v;
   lf* ln = s.v + a.H;
   lf* s_inv = s.v + 2 * a.H;
-  prefetch_rows(g.W, a.Rq, a.H, g.blk, s.w);
+  if (!pre) prefetch_rows(g.W, a.Rq, a.H, g.blk, wl);
   const NormW nw = load_normw(Lw.ln1, a.H);
   stamp(a, l, P_QKV, t, 0);
   if (l == 0) {
@@ -1001,7 +1002,7 @@ __device__ __forceinline__ void run_qkv(const DecodeArgs& a, uint32_t l, uint32_
   stamp(a, l, P_QKV, t, 1);
   rmsnorm_lds<TR>(x, nw, a.eps, a.H, ln, ln, s_inv);
   stamp(a, l, P_QKV, t, 3);
-  const float acc = gemv_sel<TR, 8, 32>(a.Rq, s.w, ln, a.H, 1, s.pad);
+  const float acc = gemv_sel<TR, 8, 32, 8>(a.Rq, wl, ln, a.H, 1, s.pad);
   const uint32_t row = g.blk * a.Rq + threadIdx.x;
   if (threadIdx.x < a.Rq && row < g.M) {
     const float r = g.bias ? acc + G(g.bias)[row] : acc;
@@ -1616,13 +1617,13 @@ __device__ __forceinline__ void run_att_mix(const DecodeArgs& a, uint32_t l, uin
 // o_proj block + residual h1 = h + o (main.rs:470-472).
 template <bool TR>
 __device__ __forceinline__ void run_o(const DecodeArgs& a, uint32_t l, uint32_t t, const Lds& s,
-                                     uint32_t tok) {
+                                     uint32_t tok, lf* wl, bool pre) {
   const LayerW Lw = a.layers[l];
   const Act ac = act_of(a, l);
   const uint32_t qd = a.qd, r0 = t * a.Ro, nr = min(a.Ro, a.H - r0);
   lf* x = s.v;        // attention output [qd]
   lf* hres = x + qd;  // this block's residual rows [nr]
-  prefetch_rows(Lw.wo, a.Ro, qd, t, s.w);
+  if (!pre) prefetch_rows(Lw.wo, a.Ro, qd, t, wl);
   stamp(a, l, P_O, t, 0);
   if (l == 0) {
     gf* e = G(a.embed) + (size_t)tok * a.H + r0;
@@ -1635,7 +1636,7 @@ __device__ __forceinline__ void run_o(const DecodeArgs& a, uint32_t l, uint32_t 
            [=](uint32_t i) { return i < qd ? att + i : hin + (i - qd); });
   }
   stamp(a, l, P_O, t, 1);
-  const float acc = gemv_sel<TR, 8, 32, 18>(a.Ro, s.w, x, qd, 1, s.pad);
+  const float acc = gemv_sel<TR, 8, 32, 18, 8>(a.Ro, wl, x, qd, 1, s.pad);
   stamp(a, l, P_O, t, 3);
   if (threadIdx.x < nr) put_word(ac.h1 + r0 + threadIdx.x, hres[threadIdx.x] + acc, a.epoch);
   stamp(a, l, P_O, t, 2);
@@ -1644,21 +1645,22 @@ __device__ __forceinline__ void run_o(const DecodeArgs& a, uint32_t l, uint32_t 
 // gate/up block (wave 0 gate rows, wave 1 up rows) after
 // post_attention_layernorm; hid = silu(gate) * up (main.rs:478-487).
 template <bool TR>
-__device__ __forceinline__ void run_gu(const DecodeArgs& a, uint32_t l, uint32_t t, const Lds& s) {
+__device__ __forceinline__ void run_gu(const DecodeArgs& a, uint32_t l, uint32_t t, const Lds& s,
+                                      lf* wl, bool pre) {
   const LayerW Lw = a.layers[l];
   const Act ac = act_of(a, l);
   lf* x = s.v;
   lf* ln = x + a.H;
   lf* gx = ln + a.H;  // 64 floats: gate results
   lf* s_inv = gx + 64;
-  prefetch_rows2(Lw.wg, Lw.wu, a.Rg, a.H, t, s.w);
+  if (!pre) prefetch_rows2(Lw.wg, Lw.wu, a.Rg, a.H, t, wl);
   const NormW nw = load_normw(Lw.ln2, a.H);
   stamp(a, l, P_GU, t, 0);
   gather_vec(x, ac.h1, a.H, a);
   stamp(a, l, P_GU, t, 1);
   rmsnorm_lds<TR>(x, nw, a.eps, a.H, ln, ln, s_inv);
   stamp(a, l, P_GU, t, 3);
-  const float acc = gemv_sel<TR, 8, 16>(a.Rg, s.w, ln, a.H, 2, s.pad);
+  const float acc = gemv_sel<TR, 8, 16, 8>(a.Rg, wl, ln, a.H, 2, s.pad);
   const uint32_t wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
   if (wv == 0) gx[lane] = acc;
   __syncthreads();
@@ -1674,13 +1676,14 @@ __device__ __forceinline__ void run_gu(const DecodeArgs& a, uint32_t l, uint32_t
 
 // down block + residual h_next = h1 + down (main.rs:489-491).
 template <bool TR>
-__device__ __forceinline__ void run_d(const DecodeArgs& a, uint32_t l, uint32_t t, const Lds& s) {
+__device__ __forceinline__ void run_d(const DecodeArgs& a, uint32_t l, uint32_t t, const Lds& s,
+                                     lf* wl, bool pre) {
   const LayerW Lw = a.layers[l];
   const Act ac = act_of(a, l);
   const uint32_t I = a.I, r0 = t * a.Rd, nr = min(a.Rd, a.H - r0);
   lf* x = s.v;       // hid [I]
   lf* hres = x + I;  // residual rows [nr]
-  prefetch_rows(Lw.wd, a.Rd, I, t, s.w);
+  if (!pre) prefetch_rows(Lw.wd, a.Rd, I, t, wl);
   stamp(a, l, P_D, t, 0);
   const gw* h1 = ac.h1 + r0;
   const gw* hid = ac.hid;
@@ -1689,7 +1692,7 @@ __device__ __forceinline__ void run_d(const DecodeArgs& a, uint32_t l, uint32_t 
   stamp(a, l, P_D, t, 1);
   // the 1536- to 3072-long chain keeps 12 reads in flight (8 elsewhere:
   // deeper rings slowed the shorter GEMVs, measured)
-  const float acc = gemv_sel<TR, 12, 32, 24, 12>(a.Rd, s.w, x, I, 1, s.pad);
+  const float acc = gemv_sel<TR, 12, 32, 24, 12, 8>(a.Rd, wl, x, I, 1, s.pad);
   stamp(a, l, P_D, t, 3);
   if (threadIdx.x < nr) put_word(ac.hout + r0 + threadIdx.x, hres[threadIdx.x] + acc, a.epoch);
   stamp(a, l, P_D, t, 2);
@@ -1801,6 +1804,43 @@ __device__ __forceinline__ void run_lm(const DecodeArgs& a, const Lds& s) {
   stamp(a, L - 1, P_LM, wg, 3);
 }
 
+// Floats of a task's weight blocks in LDS (attention: none).
+__device__ __forceinline__ uint32_t task_wfloats(const DecodeArgs& a, uint32_t ph) {
+  switch (ph) {
+    case P_QKV: return a.Rq * a.H;
+    case P_O: return a.Ro * a.qd;
+    case P_GU: return 2 * a.Rg * a.H;
+    case P_D: return a.Rd * a.I;
+    default: return 0;
+  }
+}
+// Loads of layer l's weight blocks of a workgroup's tasks into their LDS
+// slots (global_load_lds, nothing waited for: the tasks' gathers wait for
+// every earlier load before their barrier).
+__device__ __forceinline__ void load_task_weights(const DecodeArgs& a, uint32_t l,
+                                                  const uint32_t* task, uint32_t ntask,
+                                                  const uint32_t* woff, const Lds& s) {
+  const LayerW Lw = a.layers[l];
+  for (uint32_t i = 0; i < ntask; ++i) {
+    const uint32_t ph = task[i] >> 12, t = task[i] & 0xFFFu;
+    lf* wl = s.w + woff[i];
+    switch (ph) {
+      case P_QKV: {
+        const QkvGeom g = qkv_geom(a, Lw, act_of(a, l), t);
+        prefetch_rows_async(g.W, a.Rq, a.H, g.blk, wl);
+        break;
+      }
+      case P_O: prefetch_rows_async(Lw.wo, a.Ro, a.qd, t, wl); break;
+      case P_GU:
+        prefetch_rows_async(Lw.wg, a.Rg, a.H, t, wl);
+        prefetch_rows_async(Lw.wu, a.Rg, a.H, t, wl + a.Rg * a.H);
+        break;
+      case P_D: prefetch_rows_async(Lw.wd, a.Rd, a.I, t, wl); break;
+      default: break;
+    }
+  }
+}
+
 // One 256-thread workgroup per CU (the LDS footprint allows no second one),
 // so one wave per SIMD: the compiler may use the whole register file.
 // Model shapes compiled with their dimensions and row-block heights as
@@ -1812,7 +1852,7 @@ struct KShape {
 };
 constexpr KShape kShapes[] = {
     {0, 0, 0, 0, 0, 0, 0, 0, 0},
-    {576, 1536, 576, 64, 32, 32, 16, 24, 32},     // SmolLM2-135M
+    {576, 1536, 576, 64, 8, 8, 8, 8, 32},         // SmolLM2-135M
     {768, 3072, 768, 64, 32, 32, 16, 12, 32},     // llama-160m
     {1024, 3072, 2048, 128, 32, 18, 16, 12, 32},  // Qwen3-0.6B
 };
@@ -1863,6 +1903,27 @@ void k_decode(DecodeArgs a) {
       reads_tok |= ph == P_QKV || ph == P_O;  // the layer-0 tasks that read the embedding row
     }
   }
+  // Workgroups without an attention task keep every task's weight blocks
+  // in a slot of their own and load the next layer's after their last task
+  // of a layer (layer 0's at the start), so no task waits for its weights;
+  // a workgroup with an attention task loads each block at its task's start.
+  uint32_t woff[kMaxTasks];
+  bool slots = true;
+  {
+    uint32_t tot = 0;
+#pragma unroll
+    for (uint32_t i = 0; i < kMaxTasks; ++i) {
+      woff[i] = tot;
+      if (i < ntask) {
+        const uint32_t ph = task[i] >> 12;
+        if (ph == P_ATT) slots = false;
+        tot += task_wfloats(a, ph);
+        if (tot % 4) slots = false;  // slots start 16-byte aligned
+      }
+    }
+    if ((size_t)tot * 4 > wbytes) slots = false;
+  }
+  if (slots) load_task_weights(a, 0, task, ntask, woff, s);
   uint32_t tok = 0;
   if (reads_tok) {
     tok = *(const AS_GLB uint32_t*)a.tok_in;
@@ -1874,20 +1935,22 @@ void k_decode(DecodeArgs a) {
   for (uint32_t l = 0; l < a.L; ++l) {
     for (uint32_t i = 0; i < ntask; ++i) {
       const uint32_t ph = task[i] >> 12, t = task[i] & 0xFFFu;
+      lf* wl = slots ? s.w + woff[i] : s.w;
       switch (ph) {
-        case P_QKV: run_qkv<TR>(a, l, t, s, tok); break;
+        case P_QKV: run_qkv<TR>(a, l, t, s, tok, wl, slots); break;
         case P_ATT:
           if (!a.att_split) run_att<TR>(a, l, t, s, wbytes / 4);
           else if (t < a.natt_s) run_att_score<TR>(a, l, t, s);
           else run_att_mix<TR>(a, l, t - a.natt_s, s);
           break;
-        case P_O: run_o<TR>(a, l, t, s, tok); break;
-        case P_GU: run_gu<TR>(a, l, t, s); break;
-        case P_D: run_d<TR>(a, l, t, s); break;
+        case P_O: run_o<TR>(a, l, t, s, tok, wl, slots); break;
+        case P_GU: run_gu<TR>(a, l, t, s, wl, slots); break;
+        case P_D: run_d<TR>(a, l, t, s, wl, slots); break;
         default: break;
       }
       __syncthreads();
     }
+    if (slots && l + 1 < a.L) load_task_weights(a, l + 1, task, ntask, woff, s);
   }
   if (a.want_logits) run_lm<TR>(a, s);
   if (a.L > 1) stamp(a, 0, P_LM, wg, 2);

@@ -62,6 +62,9 @@ struct DecodeArgs {
   // (zeroed at start).
   uint32_t att_split, att_chunks, natt_s, att_dvc, natt_v, att_tp, att_cpos;
   uint64_t* scw;
+  // floats of the largest set of weight blocks one workgroup without an
+  // attention task keeps in LDS (one slot per task; 0: none kept)
+  uint32_t wslot;
 };
 
 // Floats (4-byte units) of one layer's tagged activation storage.

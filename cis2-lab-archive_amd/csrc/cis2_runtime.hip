@@ -736,6 +736,30 @@ static bool assign_tasks(const DecodeArgs& a, std::vector<uint16_t>& table) {
   return true;
 }
 
+// Floats of the largest set of weight blocks a workgroup without an
+// attention task keeps in LDS (the persistent kernel's per-task slots).
+static uint32_t task_slot_floats(const DecodeArgs& a, const std::vector<uint16_t>& table) {
+  uint64_t best = 0;
+  for (size_t w = 0; w * kMaxTasks < table.size(); ++w) {
+    uint64_t tot = 0;
+    bool att = false;
+    for (uint32_t i = 0; i < kMaxTasks; ++i) {
+      const uint16_t v = table[w * kMaxTasks + i];
+      if (v == kNoTask) break;
+      switch (v >> 12) {
+        case kPhaseQKV: tot += (uint64_t)a.Rq * a.H; break;
+        case kPhaseATT: att = true; break;
+        case kPhaseO: tot += (uint64_t)a.Ro * a.qd; break;
+        case kPhaseGU: tot += 2ull * a.Rg * a.H; break;
+        case kPhaseD: tot += (uint64_t)a.Rd * a.I; break;
+        default: break;
+      }
+    }
+    if (!att && tot > best) best = tot;
+  }
+  return best > UINT32_MAX ? UINT32_MAX : (uint32_t)best;
+}
+
 extern "C" {
 
 const char* cis2_strerror(int code) {
@@ -902,7 +926,10 @@ int cis2_ctx_create(const cis2_config* cfg, cis2_ctx** out) {
     const char* pf = getenv("CIS2_PREFILL");
     c->seq_prefill = pf && !strcmp(pf, "seq");
     DecodeArgs& a = c->dargs;
-    auto plan = [&](uint32_t cap) {
+    // cap: the largest block height; small: GEMV blocks of at most 8 rows
+    // (gate/up 8 each) and 32-row LM blocks, taken when every GEMV phase
+    // still has at most one task per workgroup
+    auto plan = [&](uint32_t cap, bool small) {
       memset(&a, 0, sizeof a);
       a.H = H; a.I = I; a.V = V; a.L = f.n_layers; a.nh = f.n_heads; a.nkv = f.n_kv_heads;
       a.hd = f.head_dim; a.qd = c->qd; a.kvd = c->kvd; a.max_pos = f.max_pos;
@@ -911,6 +938,13 @@ int cis2_ctx_create(const cis2_config* cfg, cis2_ctx** out) {
       a.Rg = rows_per_block(H, cap) / 2 > 0 ? rows_per_block(H, cap) / 2 : 1;
       a.Rd = rows_per_block(I, cap);
       a.Rl = rows_per_block(H, cap);
+      if (small) {
+        a.Rq = rows_per_block(H, 8);
+        a.Ro = rows_per_block(c->qd, 8);
+        a.Rg = rows_per_block(H, 16) / 2 > 0 ? rows_per_block(H, 16) / 2 : 1;
+        a.Rd = rows_per_block(I, 8);
+        a.Rl = rows_per_block(H, 32);
+      }
       a.nq_q = (c->qd + a.Rq - 1) / a.Rq;
       a.nq_k = (c->kvd + a.Rq - 1) / a.Rq;
       a.nq = a.nq_q + 2 * a.nq_k;
@@ -932,13 +966,17 @@ int cis2_ctx_create(const cis2_config* cfg, cis2_ctx** out) {
       decode_att_plan(a, pa && !strcmp(pa, "split")  ? true
                          : pa && !strcmp(pa, "one") ? false
                                                     : decode_att_needs_split(a));
+      if (small && (a.nq > a.nwg || a.no > a.nwg || a.ng > a.nwg || a.nd > a.nwg)) return false;
+      if (!assign_tasks(a, c->wg_tasks)) return false;
       // dynamic LDS plus the kernel's static LDS (a few words) within one CU
+      const size_t cap_lds = lds > 0 && (size_t)lds < 160 * 1024 ? (size_t)lds : 160 * 1024;
+      a.wslot = task_slot_floats(a, c->wg_tasks);
+      if (decode_lds_bytes(a) + 64 > cap_lds) a.wslot = 0;  // slots where they fit only
       const size_t need_lds = decode_lds_bytes(a) + 64;
-      return assign_tasks(a, c->wg_tasks) && lds > 0 && need_lds <= (size_t)lds &&
-             need_lds <= 160 * 1024 && a.hd <= 256 &&  // RoPE: one pair per thread
+      return lds > 0 && need_lds <= cap_lds && a.hd <= 256 &&  // RoPE: one pair per thread
              decode_att_ok(a);
     };
-    c->fast_ok = plan(32) || plan(64);
+    c->fast_ok = plan(32, true) || plan(32, false) || plan(64, false);
     if (c->fast_ok) {  // every workgroup resident at once, or the per-op path
       bool res = false;
       if (decode_coresident(a, c->ncu, &res) != hipSuccess || !res) c->fast_ok = false;
@@ -995,6 +1033,12 @@ int cis2_ctx_create(const cis2_config* cfg, cis2_ctx** out) {
         c->tline = static_cast<uint64_t*>(p);
         (void)hipMemset(c->tline, 0, n * 8);
         c->tline_file = fopen(tl, "wb");
+        // the task table beside it (<file>.tasks: nwg rows of kMaxTasks
+        // phase << 12 | task words, 0xFFFF ends a row)
+        if (FILE* tf = fopen((std::string(tl) + ".tasks").c_str(), "wb")) {
+          fwrite(c->wg_tasks.data(), sizeof(uint16_t), c->wg_tasks.size(), tf);
+          fclose(tf);
+        }
       }
     }
   }
