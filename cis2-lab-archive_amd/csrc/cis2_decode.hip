@@ -1002,7 +1002,7 @@ __device__ __forceinline__ void run_qkv(const DecodeArgs& a, uint32_t l, uint32_
   stamp(a, l, P_QKV, t, 1);
   rmsnorm_lds<TR>(x, nw, a.eps, a.H, ln, ln, s_inv);
   stamp(a, l, P_QKV, t, 3);
-  const float acc = gemv_sel<TR, 8, 32, 8>(a.Rq, wl, ln, a.H, 1, s.pad);
+  const float acc = gemv_sel<TR, 8, 32, 8, 16>(a.Rq, wl, ln, a.H, 1, s.pad);
   const uint32_t row = g.blk * a.Rq + threadIdx.x;
   if (threadIdx.x < a.Rq && row < g.M) {
     const float r = g.bias ? acc + G(g.bias)[row] : acc;
@@ -1853,8 +1853,8 @@ struct KShape {
 constexpr KShape kShapes[] = {
     {0, 0, 0, 0, 0, 0, 0, 0, 0},
     {576, 1536, 576, 64, 8, 8, 8, 8, 32},         // SmolLM2-135M
-    {768, 3072, 768, 64, 32, 32, 16, 12, 32},     // llama-160m
-    {1024, 3072, 2048, 128, 32, 18, 16, 12, 32},  // Qwen3-0.6B
+    {768, 3072, 768, 64, 16, 8, 16, 8, 32},       // llama-160m
+    {1024, 3072, 2048, 128, 16, 8, 16, 8, 32},    // Qwen3-0.6B
 };
 
 __host__ __device__ inline bool shape_matches(const DecodeArgs& a, const KShape& k) {

@@ -939,11 +939,19 @@ int cis2_ctx_create(const cis2_config* cfg, cis2_ctx** out) {
       a.Rd = rows_per_block(I, cap);
       a.Rl = rows_per_block(H, cap);
       if (small) {
-        a.Rq = rows_per_block(H, 8);
-        a.Ro = rows_per_block(c->qd, 8);
-        a.Rg = rows_per_block(H, 16) / 2 > 0 ? rows_per_block(H, 16) / 2 : 1;
-        a.Rd = rows_per_block(I, 8);
+        // the smallest of 8, 16, 32 rows that keeps the phase at one task
+        // per workgroup (and the block within rows_per_block's bound)
+        auto pick = [&](uint32_t M, uint32_t K, uint32_t mats) {
+          for (uint32_t r = 8; r <= 32; r *= 2)
+            if ((M + r - 1) / r <= c->ncu && r * mats <= rows_per_block(K, 64)) return r;
+          return 0u;
+        };
+        a.Rq = pick(c->qd + 2 * c->kvd, H, 1);
+        a.Ro = pick(H, c->qd, 1);
+        a.Rg = pick(I, H, 2);
+        a.Rd = pick(H, I, 1);
         a.Rl = rows_per_block(H, 32);
+        if (!a.Rq || !a.Ro || !a.Rg || !a.Rd) return false;
       }
       a.nq_q = (c->qd + a.Rq - 1) / a.Rq;
       a.nq_k = (c->kvd + a.Rq - 1) / a.Rq;
