@@ -283,4 +283,29 @@ __device__ __forceinline__ float tree32(float (&l)[32]) {
   return l[0];
 }
 
+// Cross-lane moves within a wave64 (DPP): row_shr:n inside 16-lane rows and
+// the broadcasts of lane 15 / lane 31 into later rows; lanes without a
+// source keep `old`.  A max (min) scan with shifts 1, 2, 4, 8 leaves each
+// row's extreme in its lane 15, the two broadcasts carry them to lane 63.
+template <int CTRL, int ROWMASK>
+__device__ __forceinline__ uint32_t dpp_move(uint32_t old, uint32_t src) {
+  return (uint32_t)__builtin_amdgcn_update_dpp((int)old, (int)src, CTRL, ROWMASK, 0xF, false);
+}
+template <int CTRL, int ROWMASK>
+__device__ __forceinline__ float max_step(float x) {
+  const uint32_t u = __float_as_uint(x);
+  const float y = __uint_as_float(dpp_move<CTRL, ROWMASK>(u, u));
+  return y > x ? y : x;
+}
+// Largest value over the wave (inputs NaN-free), in every lane.
+__device__ __forceinline__ float wave_max(float x) {
+  x = max_step<0x111, 0xF>(x);
+  x = max_step<0x112, 0xF>(x);
+  x = max_step<0x114, 0xF>(x);
+  x = max_step<0x118, 0xF>(x);
+  x = max_step<0x142, 0xA>(x);
+  x = max_step<0x143, 0xC>(x);
+  return __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(x), 63));
+}
+
 }  // namespace cis2

@@ -8,6 +8,7 @@
 #include "cis2_kernels.hpp"
 
 #include <algorithm>
+#include <type_traits>
 #include <cstdlib>
 
 namespace cis2 {
@@ -54,8 +55,9 @@ constexpr uint32_t kBgemmLdsBig = 150 * 1024;
 // chains per thread over W and W2 (gate and up) and stores
 // silu(gate) * up (main.rs:484-487).  NORM applies the RMSNorm of each X row
 // first (main.rs:245-260): the row's squares are summed in one strict chain
-// (or tree32 blocks) from 0 while the first chunk's loads are in flight,
-// inv = 1/sqrt(sum/K + eps), and each staged element becomes (x*inv)*w[k].
+// (or tree32 blocks) from 0 over the row as staged in LDS (a first pass over
+// the chunks when the row spans several), inv = 1/sqrt(sum/K + eps), and
+// each staged element becomes (x*inv)*w[k].
 // ---------------------------------------------------------------------------
 constexpr uint32_t kMaxSegs = 3;
 struct BgemmArgs {
@@ -67,18 +69,16 @@ struct BgemmArgs {
   float eps;
 };
 
-// RMSNorm factor of one row of K floats (K % 4 == 0), read from global
-// memory 16 loads ahead of the chain.
-__device__ float row_inv_rms(const float* x, uint32_t K, float eps, bool tree) {
-  const v4* x4 = reinterpret_cast<const v4*>(x);
-  const uint32_t K4 = K / 4;
-  float acc = 0.0f;
+// Sum of squares of q4 16-byte groups, continuing the strict chain acc (or
+// adding one tree32 per 8 groups, the last block zero-padded), read from
+// LDS or global memory.
+__device__ __forceinline__ float sumsq_groups(const v4* x4, uint32_t q4, float acc, bool tree) {
   if (tree) {
-    for (uint32_t q0 = 0; q0 < K4; q0 += 8) {
+    for (uint32_t q0 = 0; q0 < q4; q0 += 8) {
       float l[32];
 #pragma unroll
       for (uint32_t i = 0; i < 8; ++i) {
-        const v4 v = q0 + i < K4 ? x4[q0 + i] : v4{0.0f, 0.0f, 0.0f, 0.0f};
+        const v4 v = q0 + i < q4 ? x4[q0 + i] : v4{0.0f, 0.0f, 0.0f, 0.0f};
         l[4 * i] = v.x * v.x;
         l[4 * i + 1] = v.y * v.y;
         l[4 * i + 2] = v.z * v.z;
@@ -87,23 +87,9 @@ __device__ float row_inv_rms(const float* x, uint32_t K, float eps, bool tree) {
       acc = acc + tree32(l);
     }
   } else {
-    constexpr uint32_t B = 16;
-    uint32_t q0 = 0;
-    for (; q0 + B <= K4; q0 += B) {
-      v4 v[B];
-#pragma unroll
-      for (uint32_t i = 0; i < B; ++i) v[i] = x4[q0 + i];
-#pragma unroll
-      for (uint32_t i = 0; i < B; ++i) {
-        float sq;
-        sq = v[i].x * v[i].x; acc = acc + sq;
-        sq = v[i].y * v[i].y; acc = acc + sq;
-        sq = v[i].z * v[i].z; acc = acc + sq;
-        sq = v[i].w * v[i].w; acc = acc + sq;
-      }
-    }
-    for (; q0 < K4; ++q0) {
-      const v4 v = x4[q0];
+#pragma unroll 8
+    for (uint32_t q = 0; q < q4; ++q) {
+      const v4 v = x4[q];
       float sq;
       sq = v.x * v.x; acc = acc + sq;
       sq = v.y * v.y; acc = acc + sq;
@@ -111,7 +97,11 @@ __device__ float row_inv_rms(const float* x, uint32_t K, float eps, bool tree) {
       sq = v.w * v.w; acc = acc + sq;
     }
   }
-  const float mean = acc / (float)K;
+  return acc;
+}
+// RMSNorm factor from a row's sum of squares over K elements.
+__device__ __forceinline__ float inv_rms_of(float sumsq, uint32_t K, float eps) {
+  const float mean = sumsq / (float)K;
   const float arg = mean + eps;
   return rsqrt_cr(arg);
 }
@@ -131,22 +121,16 @@ __global__ __launch_bounds__(256) void k_bgemm(BgemmArgs a) {
   const uint32_t qmax = KC / 4, xs4 = qmax + 1;  // padded X rows: no bank aliasing
   v4* Ws = sm;                                   // [q4][R] (DUAL: then W2's at Ws + qmax * R)
   v4* Xs = sm + (size_t)(DUAL ? 2 : 1) * qmax * R;
+  v4* NWs = Xs + (size_t)NB * xs4;               // NORM: the chunk's norm weights
   const v4* Wg = reinterpret_cast<const v4*>(g.W + (size_t)blk * R * K);
   const v4* Wg2 = DUAL ? reinterpret_cast<const v4*>(a.W2 + (size_t)blk * R * K) : nullptr;
   float acc[CB], acc2[CB];
 #pragma unroll
   for (uint32_t c = 0; c < CB; ++c) acc[c] = acc2[c] = 0.0f;
-  for (uint32_t k0 = 0; k0 < K; k0 += KC) {
-    const uint32_t q4 = std::min(KC, K - k0) / 4, g0 = k0 / 4;
-    // every load of the chunk in flight at once, straight into LDS; each
-    // wave instruction fills 64 consecutive 16-byte slots
-    const uint32_t nw4 = q4 * R;
-    for (uint32_t i0 = wv * 64; i0 < nw4; i0 += kT)
-      if (i0 + lane < nw4) lds_load16(Wg + (size_t)g0 * R + i0 + lane, Ws + i0);
-    if (DUAL) {
-      for (uint32_t i0 = wv * 64; i0 < nw4; i0 += kT)
-        if (i0 + lane < nw4) lds_load16(Wg2 + (size_t)g0 * R + i0 + lane, Ws + qmax * R + i0);
-    }
+  // the chunk's X rows (and norm weights), every load in flight at once,
+  // straight into LDS; each wave instruction fills 64 consecutive 16-byte
+  // slots
+  auto stage_x = [&](uint32_t g0, uint32_t q4, bool with_nw) {
     const uint32_t pieces = (q4 + 63) / 64;
     for (uint32_t j = wv; j < NB * pieces; j += kT / 64) {
       const uint32_t bx = j / pieces, q0 = (j - bx * pieces) * 64;
@@ -154,16 +138,48 @@ __global__ __launch_bounds__(256) void k_bgemm(BgemmArgs a) {
       const v4* xr = reinterpret_cast<const v4*>(g.X + (size_t)row * g.ldx) + g0 + q0;
       if (q0 + lane < q4) lds_load16(xr + lane, Xs + bx * xs4 + q0);
     }
-    if (NORM && k0 == 0 && t < NB)
-      s_inv[t] = row_inv_rms(g.X + (size_t)std::min(b0 + t, a.n - 1) * g.ldx, K, a.eps, a.tree);
+    if (NORM && with_nw) {
+      const v4* nw4p = reinterpret_cast<const v4*>(a.nw) + g0;
+      for (uint32_t i0 = wv * 64; i0 < q4; i0 += kT)
+        if (i0 + lane < q4) lds_load16(nw4p + i0 + lane, NWs + i0);
+    }
+  };
+  // RMSNorm of the staged rows: one lane per batch row continues its
+  // sum-of-squares chain over each chunk from LDS.  Rows longer than one
+  // chunk take a first pass over their chunks before the GEMM's.
+  float ssq = 0.0f;
+  if (NORM && K > KC) {
+    for (uint32_t k0 = 0; k0 < K; k0 += KC) {
+      const uint32_t q4 = std::min(KC, K - k0) / 4;
+      stage_x(k0 / 4, q4, false);
+      wait_vm0();
+      __syncthreads();
+      if (t < NB) ssq = sumsq_groups(Xs + t * xs4, q4, ssq, a.tree);
+      __syncthreads();
+    }
+    if (t < NB) s_inv[t] = inv_rms_of(ssq, K, a.eps);
+  }
+  for (uint32_t k0 = 0; k0 < K; k0 += KC) {
+    const uint32_t q4 = std::min(KC, K - k0) / 4, g0 = k0 / 4;
+    const uint32_t nw4 = q4 * R;
+    for (uint32_t i0 = wv * 64; i0 < nw4; i0 += kT)
+      if (i0 + lane < nw4) lds_load16(Wg + (size_t)g0 * R + i0 + lane, Ws + i0);
+    if (DUAL) {
+      for (uint32_t i0 = wv * 64; i0 < nw4; i0 += kT)
+        if (i0 + lane < nw4) lds_load16(Wg2 + (size_t)g0 * R + i0 + lane, Ws + qmax * R + i0);
+    }
+    stage_x(g0, q4, true);
     wait_vm0();
     __syncthreads();
     if (NORM) {
-      const v4* nw4p = reinterpret_cast<const v4*>(a.nw) + g0;
+      if (K <= KC) {
+        if (t < NB) s_inv[t] = inv_rms_of(sumsq_groups(Xs + t * xs4, q4, 0.0f, a.tree), K, a.eps);
+        __syncthreads();
+      }
       for (uint32_t i = t; i < NB * q4; i += kT) {
         const uint32_t bx = i / q4, q = i - bx * q4;
         const float inv = s_inv[bx];
-        const v4 x = Xs[bx * xs4 + q], w = nw4p[q];
+        const v4 x = Xs[bx * xs4 + q], w = NWs[q];
         v4 y;
         float sx;
         sx = x.x * inv; y.x = sx * w.x;
@@ -572,6 +588,379 @@ __global__ __launch_bounds__(kAttT) void k_attention_rows(const float* __restric
   }
 }
 
+// Strict sums over LDS with a ring of 16-byte reads in flight; the caller
+// keeps D groups of readable LDS after the last one, so the ring is refilled
+// unconditionally at fixed offsets (the extra reads are never used) and the
+// last partial round adds its groups under uniform tests.  n wave-uniform.
+//   chain_lds_s:  acc + x[0] + x[1] + ... + x[n-1]
+//   mix_lds_s:    acc + p[0]*v[0] + ... + p[n-1]*v[n-1]
+// x, p and v 16-byte aligned.
+template <uint32_t D>
+__device__ __forceinline__ float chain_lds_s(const float* x, uint32_t n, float acc) {
+  const v4* x4 = reinterpret_cast<const v4*>(x);
+  const uint32_t ng = n / 4;
+  v4 ring[D];
+#pragma unroll
+  for (uint32_t u = 0; u < D; ++u) ring[u] = x4[u];
+  uint32_t g = 0;
+  for (; g + D <= ng; g += D) {
+#pragma unroll
+    for (uint32_t u = 0; u < D; ++u) {
+      const v4 r = ring[u];
+      acc = acc + r.x;
+      acc = acc + r.y;
+      acc = acc + r.z;
+      acc = acc + r.w;
+      ring[u] = x4[g + u + D];
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+#pragma unroll
+  for (uint32_t u = 0; u + 1 < D; ++u) {
+    if (g + u < ng) {
+      const v4 r = ring[u];
+      acc = acc + r.x;
+      acc = acc + r.y;
+      acc = acc + r.z;
+      acc = acc + r.w;
+    }
+  }
+  for (uint32_t j = 4 * ng; j < n; ++j) acc = acc + x[j];
+  return acc;
+}
+template <uint32_t D>
+__device__ __forceinline__ float mix_lds_s(const float* p, const float* v, uint32_t n, float acc) {
+  const v4* p4 = reinterpret_cast<const v4*>(p);
+  const v4* v4p = reinterpret_cast<const v4*>(v);
+  const uint32_t ng = n / 4;
+  v4 rp[D], rv[D];
+#pragma unroll
+  for (uint32_t u = 0; u < D; ++u) {
+    rp[u] = p4[u];
+    rv[u] = v4p[u];
+  }
+  auto step = [&](const v4& a, const v4& b) {
+    float pr;
+    pr = a.x * b.x; acc = acc + pr;
+    pr = a.y * b.y; acc = acc + pr;
+    pr = a.z * b.z; acc = acc + pr;
+    pr = a.w * b.w; acc = acc + pr;
+  };
+  uint32_t g = 0;
+  for (; g + D <= ng; g += D) {
+#pragma unroll
+    for (uint32_t u = 0; u < D; ++u) {
+      step(rp[u], rv[u]);
+      rp[u] = p4[g + u + D];
+      rv[u] = v4p[g + u + D];
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+#pragma unroll
+  for (uint32_t u = 0; u + 1 < D; ++u)
+    if (g + u < ng) step(rp[u], rv[u]);
+  for (uint32_t j = 4 * ng; j < n; ++j) {
+    const float pr = p[j] * v[j];
+    acc = acc + pr;
+  }
+  return acc;
+}
+// Readable floats the decode-rows attention keeps after its LDS regions.
+constexpr uint32_t kKvSlack = 64;
+
+// acc + p[0] + ... + p[n-1], strictly left to right (16-byte LDS reads,
+// eight of them per batch).
+__device__ __forceinline__ float chain_lds(const float* p, uint32_t n, float acc) {
+  const v4* p4 = reinterpret_cast<const v4*>(p);
+  uint32_t j = 0;
+  for (; j + 32 <= n; j += 32) {
+    v4 e[8];
+#pragma unroll
+    for (uint32_t u = 0; u < 8; ++u) e[u] = p4[j / 4 + u];
+#pragma unroll
+    for (uint32_t u = 0; u < 8; ++u) {
+      acc = acc + e[u].x;
+      acc = acc + e[u].y;
+      acc = acc + e[u].z;
+      acc = acc + e[u].w;
+    }
+  }
+  for (; j < n; ++j) acc = acc + p[j];
+  return acc;
+}
+
+// ---------------------------------------------------------------------------
+// Attention of decode rows (few rows, one per sequence): one workgroup of
+// kKvT threads per (row, KV head) takes the HPW = nh / nkv query heads of
+// that KV head, with the per-row kernel's arithmetic in the same order
+// (scores d ascending, dot_seq or tree32 blocks, first-wins maximum, pinned
+// exp, strict or tree denominator, true divide, V-mix j ascending;
+// code/cis2-fp/src/main.rs:429-467, math.rs:425-465), so every output has
+// the per-row kernel's bits.
+//   scores:  a thread takes two adjacent positions per round (8-byte K
+//            loads, 64 d per batch in flight), one chain per (position,
+//            head);
+//   V rows:  then copied into LDS with global_load_lds by every wave, in
+//            chunks of C <= 256 positions over two buffers (row stride
+//            C + 4 floats: lane d's 16-byte reads fall in distinct banks);
+//            the softmax's barriers wait for LDS only, so the copies land
+//            meanwhile; a buffer is refilled two chunks ahead while the
+//            V-mix runs over the other;
+//   softmax: the maximum with DPP, exp, the HPW denominators on HPW waves
+//            at once (a ring of LDS reads), the divide;
+//   V-mix:   HPW * HD / 64 waves, lane = d, each product formed with p_j
+//            taken by DPP broadcast (row_newbcast) from a register holding
+//            16 consecutive probabilities in every 16-lane row, the next 16
+//            positions' reads in flight.
+// LDS (floats): q [HPW][HD], scores [HPW][ls], tree partials [HPW][nbs]
+// (rounded up to 4), V [2][HD][C + 4], kKvSlack readable floats (the read
+// rings run up to 56 floats past a row's end).
+// ---------------------------------------------------------------------------
+constexpr uint32_t kKvT = 512;
+typedef float v2 __attribute__((ext_vector_type(2)));
+
+// s_waitcnt lgkmcnt(0), then s_barrier: LDS written before it is visible
+// after it; global loads in flight stay in flight.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_s_waitcnt(0xC07F);
+  __builtin_amdgcn_s_barrier();
+}
+// Lane k of this lane's 16-lane row (DPP row_newbcast:k).
+template <uint32_t K>
+__device__ __forceinline__ float bcast16(float v) {
+  return __int_as_float(
+      __builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x150 + (int)K, 0xF, 0xF, false));
+}
+// acc + P_0 * v[0].x + P_1 * v[0].y + ... + P_15 * v[3].w in order (P_k:
+// lane k of this lane's 16-lane row), each product rounded, then the add.
+template <uint32_t K = 0>
+__device__ __forceinline__ void mix16(float& acc, float P, const v4 (&v)[4]) {
+  if constexpr (K < 16) {
+    const v4 w = v[K / 4];
+    const float x = K % 4 == 0 ? w.x : K % 4 == 1 ? w.y : K % 4 == 2 ? w.z : w.w;
+    const float t = bcast16<K>(P) * x;
+    acc = acc + t;
+    mix16<K + 1>(acc, P, v);
+  }
+}
+// The first rem (< 16) steps of mix16.
+template <uint32_t K = 0>
+__device__ __forceinline__ void mix16_part(float& acc, float P, const v4 (&v)[4], uint32_t rem) {
+  if constexpr (K < 15) {
+    if (K < rem) {
+      const v4 w = v[K / 4];
+      const float x = K % 4 == 0 ? w.x : K % 4 == 1 ? w.y : K % 4 == 2 ? w.z : w.w;
+      const float t = bcast16<K>(P) * x;
+      acc = acc + t;
+      mix16_part<K + 1>(acc, P, v, rem);
+    }
+  }
+}
+// acc + p[0]*v[0] + ... + p[n-1]*v[n-1] in order; p and v in LDS, 16-byte
+// aligned, 16 readable floats past n; two register sets, each block of 16
+// positions read one block ahead.  n wave-uniform.
+__device__ __forceinline__ float mix_dpp(const float* p, const float* v, uint32_t n, float acc) {
+  const uint32_t k = threadIdx.x & 15, nb = n >> 4;
+  const v4* v4p = reinterpret_cast<const v4*>(v);
+  float PA = p[k], PB;
+  v4 vA[4], vB[4];
+#pragma unroll
+  for (uint32_t u = 0; u < 4; ++u) vA[u] = v4p[u];
+  uint32_t m = 0;
+  for (; m + 2 <= nb; m += 2) {
+    PB = p[16 * (m + 1) + k];
+#pragma unroll
+    for (uint32_t u = 0; u < 4; ++u) vB[u] = v4p[4 * (m + 1) + u];
+    mix16(acc, PA, vA);
+    PA = p[16 * (m + 2) + k];
+#pragma unroll
+    for (uint32_t u = 0; u < 4; ++u) vA[u] = v4p[4 * (m + 2) + u];
+    mix16(acc, PB, vB);
+  }
+  if (m < nb) {  // one whole block left
+    PB = p[16 * (m + 1) + k];
+#pragma unroll
+    for (uint32_t u = 0; u < 4; ++u) vB[u] = v4p[4 * (m + 1) + u];
+    mix16(acc, PA, vA);
+    PA = PB;
+#pragma unroll
+    for (uint32_t u = 0; u < 4; ++u) vA[u] = vB[u];
+  }
+  mix16_part(acc, PA, vA, n - 16 * nb);
+  return acc;
+}
+
+template <uint32_t HPW, uint32_t HD>
+__global__ __launch_bounds__(kKvT) void k_attention_kv(const float* __restrict__ q,
+                                                     const float* __restrict__ kc,
+                                                     const float* __restrict__ vc,
+                                                     RowsDesc rows, uint32_t nh,
+                                                     uint32_t max_pos, uint64_t seq_stride,
+                                                     float scale, float* out, uint32_t tree,
+                                                     uint32_t ls, uint32_t C) {
+  constexpr uint32_t NW = kKvT / 64, WPH = HD / 64, CW = HPW * WPH;
+  static_assert(HD % 64 == 0 && CW <= NW, "chain waves");
+  extern __shared__ v4 sh4[];
+  float* sh = reinterpret_cast<float*>(sh4);
+  __shared__ float s_red[NW][HPW];
+  __shared__ float s_den[HPW];
+  const uint32_t r = blockIdx.x, kvh = blockIdx.y, qh0 = kvh * HPW, t = threadIdx.x;
+  const uint32_t wv = __builtin_amdgcn_readfirstlane(t >> 6), lane = t & 63;
+  const uint32_t pos = rows.pos[r], len = pos + 1, S = C + 4;
+  const uint32_t nbs = (ls + 31) / 32, len4 = (len + 3) & ~3u;
+  const size_t sb = (size_t)rows.seq[r] * seq_stride;
+  const float* kb = kc + sb + (size_t)kvh * HD * max_pos;
+  const float* vb = vc + sb + (size_t)kvh * HD * max_pos;
+  float* sq = sh;
+  float* ssb = sq + HPW * HD;
+  float* partb = ssb + HPW * ls;
+  float* VL = partb + ((HPW * nbs + 3) & ~3u);
+  const uint32_t nch = (len + C - 1) / C;
+  // chunk ch of V row d into buffer ch % 2: one wave instruction (C <= 256
+  // positions), lanes past the chunk or the row's end idle
+  auto stage_row = [&](uint32_t ch, uint32_t d) {
+    const uint32_t o = lane * 4, j = ch * C + o;
+    if (o < C && j < len4)
+      lds_load16(reinterpret_cast<const v4*>(vb + (size_t)d * max_pos + j),
+                 reinterpret_cast<v4*>(VL + (size_t)(ch & 1) * HD * S + (size_t)d * S));
+  };
+  const float* qv = q + (size_t)r * nh * HD + (size_t)qh0 * HD;
+  for (uint32_t i = t; i < HPW * HD; i += kKvT) sq[i] = qv[i];
+  lds_barrier();
+  // scores: thread t takes positions jp, jp + 1 (jp = 2 * (t + k * kKvT);
+  // len4 <= max_pos, so a pair below len4 stays in the row)
+  for (uint32_t jp = 2 * t; jp < len; jp += 2 * kKvT) {
+    float acc[2][HPW];
+#pragma unroll
+    for (uint32_t p = 0; p < 2; ++p)
+#pragma unroll
+      for (uint32_t h = 0; h < HPW; ++h) acc[p][h] = 0.0f;
+#pragma unroll
+    for (uint32_t d0 = 0; d0 < HD; d0 += 64) {
+      v2 kv[64];
+#pragma unroll
+      for (uint32_t i = 0; i < 64; ++i)
+        kv[i] = *reinterpret_cast<const v2*>(kb + (size_t)(d0 + i) * max_pos + jp);
+      if (tree) {
+#pragma unroll
+        for (uint32_t b0 = 0; b0 < 64; b0 += 32)
+#pragma unroll
+          for (uint32_t p = 0; p < 2; ++p)
+#pragma unroll
+            for (uint32_t h = 0; h < HPW; ++h) {
+              float l[32];
+#pragma unroll
+              for (uint32_t i = 0; i < 32; ++i)
+                l[i] = sq[h * HD + d0 + b0 + i] * (p ? kv[b0 + i].y : kv[b0 + i].x);
+              acc[p][h] = acc[p][h] + tree32(l);
+            }
+      } else {
+#pragma unroll
+        for (uint32_t i = 0; i < 64; ++i)
+#pragma unroll
+          for (uint32_t h = 0; h < HPW; ++h) {
+            const float qd = sq[h * HD + d0 + i];
+            float pr;
+            pr = qd * kv[i].x; acc[0][h] = acc[0][h] + pr;
+            pr = qd * kv[i].y; acc[1][h] = acc[1][h] + pr;
+          }
+      }
+    }
+#pragma unroll
+    for (uint32_t p = 0; p < 2; ++p)
+      if (jp + p < len)
+#pragma unroll
+        for (uint32_t h = 0; h < HPW; ++h) ssb[h * ls + jp + p] = acc[p][h] * scale;
+  }
+  // the V copies of chunks 0 and 1, spread over the waves
+  for (uint32_t d = wv; d < HD; d += NW) {
+    stage_row(0, d);
+    if (nch > 1) stage_row(1, d);
+  }
+  lds_barrier();
+  // maximum per head: the largest non-NaN score (its value does not depend
+  // on which of equal scores is first: exp(s - (+0)) = exp(s - (-0))), a NaN
+  // score at 0 wins
+  {
+    float m[HPW];
+#pragma unroll
+    for (uint32_t h = 0; h < HPW; ++h) m[h] = -__builtin_huge_valf();
+    for (uint32_t j = t; j < len; j += kKvT)
+#pragma unroll
+      for (uint32_t h = 0; h < HPW; ++h) {
+        const float v = ssb[h * ls + j];
+        m[h] = v > m[h] ? v : m[h];
+      }
+#pragma unroll
+    for (uint32_t h = 0; h < HPW; ++h) {
+      m[h] = wave_max(m[h]);
+      if (lane == 0) s_red[wv][h] = m[h];
+    }
+    lds_barrier();
+#pragma unroll
+    for (uint32_t h = 0; h < HPW; ++h) {
+      float mx = s_red[0][h];
+#pragma unroll
+      for (uint32_t w = 1; w < NW; ++w) mx = s_red[w][h] > mx ? s_red[w][h] : mx;
+      const float s0 = ssb[h * ls];
+      m[h] = s0 != s0 ? s0 : mx;
+    }
+    for (uint32_t j = t; j < len; j += kKvT)
+#pragma unroll
+      for (uint32_t h = 0; h < HPW; ++h) {
+        const float dlt = ssb[h * ls + j] - m[h];
+        ssb[h * ls + j] = exp_pinned(dlt);
+      }
+  }
+  lds_barrier();
+  const uint32_t nb = (len + 31) / 32;
+  if (tree) {
+    for (uint32_t i = t; i < HPW * nb; i += kKvT) {
+      const uint32_t h = i / nb, tb = i - h * nb;
+      const float* ss = ssb + h * ls;
+      float l[32];
+#pragma unroll
+      for (uint32_t k = 0; k < 32; ++k) l[k] = 32 * tb + k < len ? ss[32 * tb + k] : 0.0f;
+      partb[h * nbs + tb] = tree32(l);
+    }
+    lds_barrier();
+  }
+  // denominators: wave h sums head h (every lane the same chain)
+  if (wv < HPW) {
+    const float acc = tree ? chain_lds_s<14>(partb + wv * nbs, nb, 0.0f)
+                           : chain_lds_s<14>(ssb + wv * ls, len, 0.0f);
+    if (lane == 0) s_den[wv] = acc;
+  }
+  lds_barrier();
+#pragma unroll
+  for (uint32_t h = 0; h < HPW; ++h) {
+    const float den = s_den[h];
+    for (uint32_t j = t; j < len; j += kKvT) {
+      const float pj = ssb[h * ls + j] / den;
+      ssb[h * ls + j] = pj;
+    }
+  }
+  // V-mix over the staged chunks
+  const uint32_t h = wv / WPH, d = (wv - h * WPH) * 64 + lane;
+  const float* ps = ssb + (size_t)(wv < CW ? h : 0) * ls;
+  float acc = 0.0f;
+  for (uint32_t ch = 0; ch < nch; ++ch) {
+    // chunk ch's copies (issued after the scores or two chunks back) have
+    // landed and every wave is done with chunk ch - 1, whose buffer takes
+    // chunk ch + 1 (copied by the waves without a chain)
+    wait_vm0();
+    __syncthreads();
+    if (wv >= CW && ch > 0 && ch + 1 < nch)
+      for (uint32_t dd = wv - CW; dd < HD; dd += NW - CW) stage_row(ch + 1, dd);
+    if (wv < CW) {
+      const uint32_t jc = ch * C;
+      acc = mix_dpp(ps + jc, VL + (size_t)(ch & 1) * HD * S + (size_t)d * S,
+                    std::min(C, len - jc), acc);
+    }
+  }
+  if (wv < CW) out[(size_t)r * nh * HD + (size_t)(qh0 + h) * HD + d] = acc;
+}
+
 // ---------------------------------------------------------------------------
 // Attention of prefill rows in tiles.  A tile is up to kAttQT rows of one
 // sequence at consecutive positions p0 .. p0+nr-1 (built on the host); a
@@ -616,27 +1005,6 @@ struct AttTileCfg {
   static_assert(P * TK % 1024 == 0 && P * HD % 1024 == 0, "thread blocking");
   static_assert(P <= 64, "one denominator lane per pair in wave 0");
 };
-
-// acc + p[0] + ... + p[n-1], strictly left to right (16-byte LDS reads,
-// eight of them per batch).
-__device__ __forceinline__ float chain_lds(const float* p, uint32_t n, float acc) {
-  const v4* p4 = reinterpret_cast<const v4*>(p);
-  uint32_t j = 0;
-  for (; j + 32 <= n; j += 32) {
-    v4 e[8];
-#pragma unroll
-    for (uint32_t u = 0; u < 8; ++u) e[u] = p4[j / 4 + u];
-#pragma unroll
-    for (uint32_t u = 0; u < 8; ++u) {
-      acc = acc + e[u].x;
-      acc = acc + e[u].y;
-      acc = acc + e[u].z;
-      acc = acc + e[u].w;
-    }
-  }
-  for (; j < n; ++j) acc = acc + p[j];
-  return acc;
-}
 
 // n positions of `rows` rows (row stride `gstride` floats in global memory,
 // starting at src) into LDS rows of stride `lstride` at dst, 16 bytes per
@@ -959,15 +1327,23 @@ hipError_t launch_bgemm_t(const BgemmArgs& a, dim3 grid, size_t lds, hipStream_t
   return hipGetLastError();
 }
 
-// The LDS limit of every k_bgemm variant, set at the first launch of any
-// (so that no attribute call happens later, e.g. inside a graph capture).
-hipError_t bgemm_configure() {
-  const void* fns[6] = {reinterpret_cast<const void*>(&k_bgemm<false, false, 1>),
-                        reinterpret_cast<const void*>(&k_bgemm<false, true, 1>),
-                        reinterpret_cast<const void*>(&k_bgemm<true, false, 1>),
-                        reinterpret_cast<const void*>(&k_bgemm<true, true, 1>),
-                        reinterpret_cast<const void*>(&k_bgemm<false, false, 2>),
-                        reinterpret_cast<const void*>(&k_bgemm<true, false, 2>)};
+// The LDS limit of every k_bgemm and k_attention_kv variant, set at the
+// first launch of any (a forward launches a GEMM before its first
+// attention), so that no attribute call happens later, e.g. inside a graph
+// capture.
+hipError_t rows_configure() {
+  const void* fns[12] = {reinterpret_cast<const void*>(&k_bgemm<false, false, 1>),
+                         reinterpret_cast<const void*>(&k_bgemm<false, true, 1>),
+                         reinterpret_cast<const void*>(&k_bgemm<true, false, 1>),
+                         reinterpret_cast<const void*>(&k_bgemm<true, true, 1>),
+                         reinterpret_cast<const void*>(&k_bgemm<false, false, 2>),
+                         reinterpret_cast<const void*>(&k_bgemm<true, false, 2>),
+                         reinterpret_cast<const void*>(&k_attention_kv<1, 64>),
+                         reinterpret_cast<const void*>(&k_attention_kv<2, 64>),
+                         reinterpret_cast<const void*>(&k_attention_kv<3, 64>),
+                         reinterpret_cast<const void*>(&k_attention_kv<4, 64>),
+                         reinterpret_cast<const void*>(&k_attention_kv<1, 128>),
+                         reinterpret_cast<const void*>(&k_attention_kv<2, 128>)};
   for (const void* f : fns) {
     hipError_t e = ensure_dynamic_lds(f, kBgemmLdsBig);
     if (e != hipSuccess) return e;
@@ -990,7 +1366,7 @@ hipError_t launch_bgemm_multi(const BgemmSeg* segs, uint32_t nseg, uint32_t n,
   if (n == 0) return hipSuccess;
   if (nseg == 0 || nseg > kMaxSegs || (o.W2 && nseg != 1)) return hipErrorInvalidValue;
   {
-    hipError_t e = bgemm_configure();
+    hipError_t e = rows_configure();
     if (e != hipSuccess) return e;
   }
   const BgemmSeg& s0 = segs[0];
@@ -1026,14 +1402,16 @@ hipError_t launch_bgemm_multi(const BgemmSeg* segs, uint32_t nseg, uint32_t n,
   // (fewer K chunks, each a full round trip); larger grids keep two
   // workgroups per CU, so that up to two per CU all run at once
   const uint32_t budget = wgs <= (uint64_t)ncu ? kBgemmLdsBig : kBgemmLds;
-  // largest chunk (a multiple of 32 k) whose W slices and X rows fit
-  const uint32_t q_fit = (budget / 16 - NB) / (S * s0.R + NB);
+  // largest chunk (a multiple of 32 k) whose W slices, X rows and norm
+  // weights fit
+  const uint32_t NW = o.norm_w ? 1 : 0;
+  const uint32_t q_fit = (budget / 16 - NB) / (S * s0.R + NB + NW);
   uint32_t KC = (q_fit * 4) & ~31u;
   if (KC == 0) return hipErrorInvalidValue;
   const uint32_t K32 = (s0.K + 31) & ~31u;
   if (KC > K32) KC = K32;
   a.KC = KC;
-  const size_t lds = ((size_t)(KC / 4) * s0.R * S + (size_t)NB * (KC / 4 + 1)) * 16;
+  const size_t lds = ((size_t)(KC / 4) * (s0.R * S + NW) + (size_t)NB * (KC / 4 + 1)) * 16;
   const dim3 grid(a.blk0[nseg], (n + NB - 1) / NB);
   if (CB == 2) return o.W2 ? launch_bgemm_t<true, false, 2>(a, grid, lds, st)
                            : launch_bgemm_t<false, false, 2>(a, grid, lds, st);
@@ -1067,6 +1445,16 @@ hipError_t launch_rope_store_rows(float* q, float* k, const float* v, const floa
   return hipGetLastError();
 }
 
+// CIS2_ATT_KV=0 keeps decode rows on the one-head-per-workgroup kernel;
+// CIS2_ATT_KV=<n> caps the V chunk at n positions (rounded down to a
+// multiple of 64), so that short rows run through the chunk ring too.  For
+// A/B timing and tests: the results are the same bits either way.
+static size_t kv_attention_cap() {
+  const char* e = std::getenv("CIS2_ATT_KV");
+  if (!e || !*e) return SIZE_MAX;
+  return (size_t)std::strtoul(e, nullptr, 10) / 64 * 64;
+}
+
 hipError_t launch_attention_rows(const float* q, const float* kc, const float* vc,
                                  RowsDesc rows, uint32_t max_len, uint32_t nh, uint32_t nkv,
                                  uint32_t hd, uint32_t max_pos, uint64_t seq_stride, float scale,
@@ -1077,12 +1465,51 @@ hipError_t launch_attention_rows(const float* q, const float* kc, const float* v
   const uint32_t group = nh / nkv;
   const size_t hd4 = ((size_t)hd + 3) / 4 * 4, ls = ((size_t)max_len + 3) / 4 * 4;
   auto lds_of = [&](uint32_t hpw) { return hpw * (hd4 + ls + (ls + 31) / 32) * sizeof(float); };
-  // Few rows (decode steps): one head per workgroup, for the most
-  // workgroups.  Many rows: the most heads of one KV head (a divisor of
-  // the group) whose LDS fits, so K and V are read once per group.
   const int ncu = device_cu_count();
+  const uint64_t wgs_kv = (uint64_t)rows.n * nkv;
+  const uint32_t tr = tree ? 1u : 0u, ls32 = (uint32_t)ls;
+  // Few rows (decode steps), head_dim 64 or 128: one workgroup per (row, KV
+  // head) with the V rows staged in LDS, in chunks of C positions (two
+  // buffers: the longest row in one pass of each when they fit).  A grid of
+  // at most one workgroup per CU may take most of the LDS, larger ones half.
+  if (wgs_kv < 4 * (uint64_t)ncu && (hd == 64 || hd == 128) && group * hd <= 256) {
+    hipError_t e = rows_configure();
+    if (e != hipSuccess) return e;
+    const size_t nbs = (ls + 31) / 32;
+    const size_t fixed = (group * hd + group * ls + ((group * nbs + 3) & ~(size_t)3)) * 4;
+    const size_t budget = wgs_kv <= (uint64_t)ncu ? kBgemmLdsBig : kBgemmLds;
+    const size_t c_need = std::min<size_t>((((size_t)max_len + 1) / 2 + 63) & ~(size_t)63, 256);
+    size_t c_fit = 0;
+    if (budget > fixed + kKvSlack * 4 + 8 * hd * 68)
+      c_fit = ((budget - fixed - kKvSlack * 4) / (8 * hd) - 4) & ~(size_t)63;
+    const size_t C = std::min(std::min(c_need, c_fit), kv_attention_cap());
+    if (C >= 64) {
+      const size_t shmem = fixed + 2 * hd * (C + 4) * 4 + kKvSlack * 4;
+      const dim3 grid(rows.n, nkv);
+      const uint32_t c32 = (uint32_t)C;
+#define CIS2_ATT_KV(H, D)                                                                      \
+  hipLaunchKernelGGL((k_attention_kv<H, D>), grid, dim3(kKvT), shmem, st, q, kc, vc, rows, nh, \
+                     max_pos, seq_stride, scale, out, tr, ls32, c32)
+      if (hd == 64) {
+        switch (group) {
+          case 1: CIS2_ATT_KV(1, 64); break;
+          case 2: CIS2_ATT_KV(2, 64); break;
+          case 3: CIS2_ATT_KV(3, 64); break;
+          default: CIS2_ATT_KV(4, 64);
+        }
+      } else {
+        if (group == 1) CIS2_ATT_KV(1, 128);
+        else CIS2_ATT_KV(2, 128);
+      }
+#undef CIS2_ATT_KV
+      return hipGetLastError();
+    }
+  }
+  // Otherwise, few rows: one head per workgroup, for the most workgroups.
+  // Many rows: the most heads of one KV head (a divisor of the group) whose
+  // LDS fits, so K and V are read once per group.
   uint32_t hpw = 1;
-  if ((uint64_t)rows.n * nkv >= 4 * (uint64_t)ncu) {
+  if (wgs_kv >= 4 * (uint64_t)ncu) {
     for (uint32_t h = std::min(group, kMaxHeadsPerWg); h > 1; --h)
       if (group % h == 0 && lds_of(h) <= 60 * 1024) {
         hpw = h;
@@ -1092,7 +1519,6 @@ hipError_t launch_attention_rows(const float* q, const float* kc, const float* v
   const size_t shmem = lds_of(hpw);
   if (shmem > 60 * 1024) return hipErrorInvalidValue;
   const dim3 grid(rows.n, nh / hpw);
-  const uint32_t tr = tree ? 1u : 0u, ls32 = (uint32_t)ls;
   switch (hpw) {
     case 4:
       hipLaunchKernelGGL(k_attention_rows<4>, grid, dim3(kAttT), shmem, st, q, kc, vc, rows, nh,

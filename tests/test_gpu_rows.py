@@ -150,6 +150,31 @@ def test_decode_batch_ragged_equals_bs1(B, graph, mode):
         assert np.array_equal(rows[i]["ids"], s["ids"])
 
 
+@pytest.mark.parametrize("cap", ["", "64"])
+@pytest.mark.parametrize("mode", [0, 1])
+@pytest.mark.parametrize("name", ["smollm2-4l", "tiny-wide"])
+def test_decode_batch_kv_head_attention(name, mode, cap):
+    """Decode rows of head_dim 64 and 128 attend one workgroup per (row, KV
+    head), the V rows staged in LDS in chunks; CIS2_ATT_KV=64 caps a chunk
+    at 64 positions, so the rows of up to 200 + 12 positions run through the
+    two-buffer ring.  Each row equals its bs=1 decode and the run with one
+    head per workgroup (CIS2_ATT_KV=0)."""
+    spec = artifacts.SPECS[name]
+    w = artifacts.Weights(spec, 7)
+    prompts = [artifacts.set_prompt(7, i, spec.vocab, 1, 200, 11) for i in range(3)]
+    gen = 12
+    m = Cis2Model(spec, w, max_pos=200 + gen, max_seqs=3, reduction_mode=mode)
+    rows = _with_env("CIS2_ATT_KV", cap, lambda: m.decode_batch(prompts, gen)) if cap else \
+        m.decode_batch(prompts, gen)
+    old = _with_env("CIS2_ATT_KV", "0", lambda: m.decode_batch(prompts, gen))
+    solo = Cis2Model(spec, w, max_pos=200 + gen, reduction_mode=mode)
+    for i, p in enumerate(prompts):
+        s = solo.decode(p, gen, step_digests=False)
+        assert rows[i]["witness"] == s["witness"] == old[i]["witness"], i
+        assert rows[i]["argmax_digest"] == s["argmax_digest"], i
+        assert np.array_equal(rows[i]["ids"], s["ids"]), i
+
+
 @pytest.mark.parametrize("name", ["smollm2-135m", "smollm2-135m-tree"])
 def test_rows_many_rows_gqa_grouped_attention(name, model_fixtures):
     """Enough rows that the attention groups the query heads of one KV head
