@@ -36,6 +36,12 @@ __device__ __forceinline__ void lds_load16(const v4* src, v4* dst_wave) {
 }
 // s_waitcnt vmcnt(0) (expcnt, lgkmcnt fields at their maxima: no wait).
 __device__ __forceinline__ void wait_vm0() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+// Lane k of this lane's 16-lane row (DPP row_newbcast:k).
+template <uint32_t K>
+__device__ __forceinline__ float bcast16(float v) {
+  return __int_as_float(
+      __builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x150 + (int)K, 0xF, 0xF, false));
+}
 // LDS per batched-GEMM workgroup: two workgroups fit one CU; small grids
 // may use one workgroup's worth of almost all of it.
 constexpr uint32_t kBgemmLds = 78 * 1024;
@@ -131,8 +137,12 @@ __global__ __launch_bounds__(256) void k_bgemm(BgemmArgs a) {
   // straight into LDS; each wave instruction fills 64 consecutive 16-byte
   // slots
   auto stage_x = [&](uint32_t g0, uint32_t q4, bool with_nw) {
-    const uint32_t pieces = (q4 + 63) / 64;
-    for (uint32_t j = wv; j < NB * pieces; j += kT / 64) {
+    const uint32_t pieces = (q4 + 63) / 64, nx = NB * pieces;
+    // workgroups start at different rows: the grid's requests for the
+    // shared X rows spread over the cache channels
+    const uint32_t rot = (blockIdx.x * 5) % nx;
+    for (uint32_t j0 = wv; j0 < nx; j0 += kT / 64) {
+      const uint32_t j = j0 + rot < nx ? j0 + rot : j0 + rot - nx;
       const uint32_t bx = j / pieces, q0 = (j - bx * pieces) * 64;
       const uint32_t row = std::min(b0 + bx, a.n - 1);
       const v4* xr = reinterpret_cast<const v4*>(g.X + (size_t)row * g.ldx) + g0 + q0;
@@ -318,6 +328,275 @@ __global__ __launch_bounds__(256) void k_bgemm(BgemmArgs a) {
       }
       g.Y[(size_t)row * g.ldy + m] = y;
     }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Batched GEMM in tiles of 16 outputs x 16 batch rows (sequential order, W
+// in blocks of R = 8 or 16 rows): a workgroup owns 16 consecutive outputs m
+// (16 / R blocks of W) and 16 batch rows; lane l of wave w computes output
+// (row 4w + l/16, column l%16) as one strict chain acc + W[m][k] * X[b][k],
+// k ascending (code/cis2-fp/src/main.rs:228-243, math.rs:40-48), the bits
+// of k_bgemm.  A 16-lane row of a wave shares one batch row: each lane
+// reads 4 consecutive k of X per 16-byte LDS read (the row: 64 k), and a
+// chain takes X[b][k] from lane (k/4) % 16 of its row by DPP broadcast
+// (row_newbcast) inside the multiply; the chains' LDS reads are the W groups
+// (a ring of D reads ahead) and one X read per 64 k, where k_bgemm's lanes
+// read an X group per 4 k.  NORM: each 16-lane row computes its row's
+// inverse RMS from the staged X (the squares' sum in one strict chain, the
+// partial sums broadcast the same way), and the chain scales each X read,
+// (x * inv) * w[k], before use.  Operands go through registers per K chunk:
+// every load of the chunk in flight, then the LDS writes.
+// LDS (16-byte groups): W blocks [16/R][q4max * R + 8] (the pad keeps the
+// two blocks' reads in distinct banks), W2 the same (DUAL), norm weights
+// [q4max], X [16][q4max + 1], then b16_slack(R) readable groups (the
+// rings read up to 23 W groups, at stride R, and 31 X groups past a
+// chunk's end; the values are never used).
+// ---------------------------------------------------------------------------
+inline uint32_t b16_slack(uint32_t R) { return 24 * R + 64; }
+
+// Steps G .. 15 of a 16-group block starting at group q: ring slot G % D
+// holds W group q + G (refilled with q + G + D), xq is this lane's X group
+// q + (lane % 16); X[b][4(q + G) + j] is component j of lane G's xq.
+template <bool DUAL, uint32_t D, uint32_t G = 0>
+__device__ __forceinline__ void b16_block(float& acc, float& acc2, const v4& xq, v4 (&rw)[D],
+                                          v4 (&rw2)[D], const v4* wp, const v4* wp2, uint32_t R,
+                                          uint32_t q) {
+  if constexpr (G < 16) {
+    const v4 w = rw[G % D];
+    const float x0 = bcast16<G>(xq.x), x1 = bcast16<G>(xq.y);
+    const float x2 = bcast16<G>(xq.z), x3 = bcast16<G>(xq.w);
+    float p;
+    p = x0 * w.x; acc = acc + p;
+    p = x1 * w.y; acc = acc + p;
+    p = x2 * w.z; acc = acc + p;
+    p = x3 * w.w; acc = acc + p;
+    if (DUAL) {
+      const v4 w2 = rw2[G % D];
+      p = x0 * w2.x; acc2 = acc2 + p;
+      p = x1 * w2.y; acc2 = acc2 + p;
+      p = x2 * w2.z; acc2 = acc2 + p;
+      p = x3 * w2.w; acc2 = acc2 + p;
+    }
+    rw[G % D] = wp[(size_t)(q + G + D) * R];
+    if (DUAL) rw2[G % D] = wp2[(size_t)(q + G + D) * R];
+    __builtin_amdgcn_sched_barrier(0);
+    b16_block<DUAL, D, G + 1>(acc, acc2, xq, rw, rw2, wp, wp2, R, q);
+  }
+}
+// The first nt (< 16) steps of b16_block.
+template <bool DUAL, uint32_t D, uint32_t G = 0>
+__device__ __forceinline__ void b16_tail(float& acc, float& acc2, const v4& xq, v4 (&rw)[D],
+                                         v4 (&rw2)[D], const v4* wp, const v4* wp2, uint32_t R,
+                                         uint32_t q, uint32_t nt) {
+  if constexpr (G < 15) {
+    if (G < nt) {
+      const v4 w = rw[G % D];
+      const float x0 = bcast16<G>(xq.x), x1 = bcast16<G>(xq.y);
+      const float x2 = bcast16<G>(xq.z), x3 = bcast16<G>(xq.w);
+      float p;
+      p = x0 * w.x; acc = acc + p;
+      p = x1 * w.y; acc = acc + p;
+      p = x2 * w.z; acc = acc + p;
+      p = x3 * w.w; acc = acc + p;
+      if (DUAL) {
+        const v4 w2 = rw2[G % D];
+        p = x0 * w2.x; acc2 = acc2 + p;
+        p = x1 * w2.y; acc2 = acc2 + p;
+        p = x2 * w2.z; acc2 = acc2 + p;
+        p = x3 * w2.w; acc2 = acc2 + p;
+      }
+      rw[G % D] = wp[(size_t)(q + G + D) * R];
+      if (DUAL) rw2[G % D] = wp2[(size_t)(q + G + D) * R];
+      __builtin_amdgcn_sched_barrier(0);
+      b16_tail<DUAL, D, G + 1>(acc, acc2, xq, rw, rw2, wp, wp2, R, q, nt);
+    }
+  }
+}
+// Sum of squares of n groups x4[0 .. n-1] continuing acc, strict order:
+// blocks of 8 groups, the next block's squares formed between this block's
+// adds (x4 in LDS with 16 readable groups past n).
+template <uint32_t U = 0>
+__device__ __forceinline__ void sq_step(float& acc, float (&s)[8][4], const v4* x4, uint32_t gn) {
+  if constexpr (U < 8) {
+    const v4 v = x4[gn + U];
+    acc = acc + s[U][0];
+    s[U][0] = v.x * v.x;
+    acc = acc + s[U][1];
+    s[U][1] = v.y * v.y;
+    acc = acc + s[U][2];
+    s[U][2] = v.z * v.z;
+    acc = acc + s[U][3];
+    s[U][3] = v.w * v.w;
+    sq_step<U + 1>(acc, s, x4, gn);
+  }
+}
+__device__ __forceinline__ float sumsq_pipe(const v4* x4, uint32_t n, float acc) {
+  float s[8][4];
+#pragma unroll
+  for (uint32_t u = 0; u < 8; ++u) {
+    const v4 v = x4[u];
+    s[u][0] = v.x * v.x;
+    s[u][1] = v.y * v.y;
+    s[u][2] = v.z * v.z;
+    s[u][3] = v.w * v.w;
+  }
+  uint32_t g = 0;
+  for (; g + 8 < n; g += 8) sq_step(acc, s, x4, g + 8);
+#pragma unroll
+  for (uint32_t u = 0; u < 8; ++u)
+    if (g + u < n) {
+      acc = acc + s[u][0];
+      acc = acc + s[u][1];
+      acc = acc + s[u][2];
+      acc = acc + s[u][3];
+    }
+  return acc;
+}
+
+template <bool DUAL, bool NORM>
+__global__ __launch_bounds__(256) void k_bgemm16(BgemmArgs a) {
+  extern __shared__ v4 sm[];
+  constexpr uint32_t D = 8;  // W groups read ahead (a divisor of 16: the ring slot of
+                             // group q + G is G % D for every block start q)
+  uint32_t si = 0;
+  if (a.nseg > 1 && blockIdx.x >= a.blk0[1]) si = (a.nseg > 2 && blockIdx.x >= a.blk0[2]) ? 2 : 1;
+  const BgemmSeg g = si == 0 ? a.s[0] : (si == 1 ? a.s[1] : a.s[2]);
+  const uint32_t R = g.R, KC = a.KC, K = g.K, nblk = 16 / R;
+  const uint32_t tile = blockIdx.x - a.blk0[si], b0 = blockIdx.y * 16, t = threadIdx.x;
+  const uint32_t wv = __builtin_amdgcn_readfirstlane(t >> 6), lane = t & 63;
+  const uint32_t c = lane & 15, bb = wv * 4 + (lane >> 4);  // output column, batch row
+  const uint32_t qmax = KC / 4, xs4 = qmax + 1, BS = qmax * R + 8;
+  v4* Ws = sm;                                   // [nblk][BS]
+  v4* W2s = Ws + (size_t)nblk * BS;              // DUAL
+  v4* NWs = W2s + (DUAL ? (size_t)nblk * BS : 0);  // NORM: the chunk's norm weights
+  v4* Xs = NWs + (NORM ? qmax : 0);              // [16][xs4]
+  const v4* Wg = reinterpret_cast<const v4*>(g.W + (size_t)tile * 16 * K);
+  const v4* Wg2 = DUAL ? reinterpret_cast<const v4*>(a.W2 + (size_t)tile * 16 * K) : nullptr;
+  // A chunk's operands (groups g0 .. g0+q4-1): per round, a thread loads up
+  // to 8 W (and 8 W2) groups of the tile's blocks, the X groups of 4 rows
+  // (wave w: rows 4w .. 4w+3, lanes over the groups) and one norm weight
+  // group, all in flight, then writes them.
+  auto stage = [&](uint32_t g0, uint32_t q4, bool with_w) {
+    constexpr uint32_t WB = 8, XP = 4;
+    const uint32_t nwb = q4 * R, nw = with_w ? nblk * nwb : 0, pieces = (q4 + 63) / 64;
+    for (uint32_t rd = 0; rd == 0 || rd * 256 * WB < nw; ++rd) {
+      v4 tw[WB], tw2[WB], tx[4][XP], tn;
+#pragma unroll
+      for (uint32_t u = 0; u < WB; ++u) {
+        const uint32_t i = (rd * WB + u) * 256 + t;
+        if (i < nw) {
+          const uint32_t cb = i >= nwb ? 1 : 0, j = i - cb * nwb;
+          tw[u] = Wg[(size_t)cb * R * K / 4 + (size_t)g0 * R + j];
+          if (DUAL) tw2[u] = Wg2[(size_t)cb * R * K / 4 + (size_t)g0 * R + j];
+        }
+      }
+      if (rd == 0) {
+#pragma unroll
+        for (uint32_t j = 0; j < 4; ++j) {
+          const uint32_t bx = wv * 4 + j, row = std::min(b0 + bx, a.n - 1);
+          const v4* xr = reinterpret_cast<const v4*>(g.X + (size_t)row * g.ldx) + g0;
+#pragma unroll
+          for (uint32_t pc = 0; pc < XP; ++pc) {
+            const uint32_t q = pc * 64 + lane;
+            if (pc < pieces && q < q4) tx[j][pc] = xr[q];
+          }
+        }
+        if (NORM && with_w && t < q4) tn = reinterpret_cast<const v4*>(a.nw)[g0 + t];
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (uint32_t u = 0; u < WB; ++u) {
+        const uint32_t i = (rd * WB + u) * 256 + t;
+        if (i < nw) {
+          const uint32_t cb = i >= nwb ? 1 : 0, j = i - cb * nwb;
+          Ws[cb * BS + j] = tw[u];
+          if (DUAL) W2s[cb * BS + j] = tw2[u];
+        }
+      }
+      if (rd == 0) {
+#pragma unroll
+        for (uint32_t j = 0; j < 4; ++j) {
+          const uint32_t bx = wv * 4 + j;
+#pragma unroll
+          for (uint32_t pc = 0; pc < XP; ++pc) {
+            const uint32_t q = pc * 64 + lane;
+            if (pc < pieces && q < q4) Xs[bx * xs4 + q] = tx[j][pc];
+          }
+        }
+        if (NORM && with_w && t < q4) NWs[t] = tn;
+      }
+    }
+  };
+  // RMSNorm: the 16 lanes of a batch row chain its squares (strict order)
+  // over each staged chunk (16-byte reads, the same address across the
+  // row's lanes); rows longer than one chunk take a first pass over their
+  // chunks before the GEMM's.
+  const v4* xrow = Xs + bb * xs4;
+  const v4* xr = xrow + c;
+  auto sumsq_chunk = [&](uint32_t q4, float acc0) { return sumsq_pipe(xrow, q4, acc0); };
+  float inv = 0.0f;
+  if (NORM && K > KC) {
+    float ssq = 0.0f;
+    for (uint32_t k0 = 0; k0 < K; k0 += KC) {
+      const uint32_t q4 = std::min(KC, K - k0) / 4;
+      stage(k0 / 4, q4, false);
+      __syncthreads();
+      ssq = sumsq_chunk(q4, ssq);
+      __syncthreads();
+    }
+    inv = inv_rms_of(ssq, K, a.eps);
+  }
+  float acc = 0.0f, acc2 = 0.0f;
+  const uint32_t cb = c / R, r = c - cb * R;
+  const v4* wp = Ws + cb * BS + r;
+  const v4* wp2 = W2s + cb * BS + r;
+  for (uint32_t k0 = 0; k0 < K; k0 += KC) {
+    const uint32_t q4 = std::min(KC, K - k0) / 4;
+    stage(k0 / 4, q4, true);
+    __syncthreads();
+    if (NORM && K <= KC) inv = inv_rms_of(sumsq_chunk(q4, 0.0f), K, a.eps);
+    // this lane's X group of a block, scaled for NORM
+    auto xget = [&](uint32_t q) {
+      v4 x = xr[q];
+      if (NORM) {
+        const v4 w = NWs[q + c];
+        float sx;
+        sx = x.x * inv; x.x = sx * w.x;
+        sx = x.y * inv; x.y = sx * w.y;
+        sx = x.z * inv; x.z = sx * w.z;
+        sx = x.w * inv; x.w = sx * w.w;
+      }
+      return x;
+    };
+    v4 rw[D], rw2[D];
+#pragma unroll
+    for (uint32_t u = 0; u < D; ++u) {
+      rw[u] = wp[(size_t)u * R];
+      if (DUAL) rw2[u] = wp2[(size_t)u * R];
+    }
+    v4 xq = xget(0);
+    uint32_t q = 0;
+    for (; q + 16 <= q4; q += 16) {
+      const v4 xn = xget(q + 16);  // the next block's X (past the end: unused)
+      b16_block<DUAL, D>(acc, acc2, xq, rw, rw2, wp, wp2, R, q);
+      xq = xn;
+    }
+    if (q < q4) b16_tail<DUAL, D>(acc, acc2, xq, rw, rw2, wp, wp2, R, q, q4 - q);
+    __syncthreads();
+  }
+  const uint32_t m = tile * 16 + c, row = b0 + bb;
+  if (row < a.n && m < g.M) {
+    float y = acc;
+    if (DUAL) {
+      const float sg = silu_pinned(acc);
+      y = sg * acc2;
+    } else if (g.epi == kEpiBias) {
+      y = acc + g.add[m];
+    } else if (g.epi == kEpiResidual) {
+      y = g.add[(size_t)row * g.ldadd + m] + acc;
+    }
+    g.Y[(size_t)row * g.ldy + m] = y;
   }
 }
 
@@ -724,12 +1003,6 @@ typedef float v2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_s_waitcnt(0xC07F);
   __builtin_amdgcn_s_barrier();
-}
-// Lane k of this lane's 16-lane row (DPP row_newbcast:k).
-template <uint32_t K>
-__device__ __forceinline__ float bcast16(float v) {
-  return __int_as_float(
-      __builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x150 + (int)K, 0xF, 0xF, false));
 }
 // acc + P_0 * v[0].x + P_1 * v[0].y + ... + P_15 * v[3].w in order (P_k:
 // lane k of this lane's 16-lane row), each product rounded, then the add.
@@ -1332,7 +1605,11 @@ hipError_t launch_bgemm_t(const BgemmArgs& a, dim3 grid, size_t lds, hipStream_t
 // attention), so that no attribute call happens later, e.g. inside a graph
 // capture.
 hipError_t rows_configure() {
-  const void* fns[12] = {reinterpret_cast<const void*>(&k_bgemm<false, false, 1>),
+  const void* fns[16] = {reinterpret_cast<const void*>(&k_bgemm<false, false, 1>),
+                         reinterpret_cast<const void*>(&k_bgemm16<false, false>),
+                         reinterpret_cast<const void*>(&k_bgemm16<false, true>),
+                         reinterpret_cast<const void*>(&k_bgemm16<true, false>),
+                         reinterpret_cast<const void*>(&k_bgemm16<true, true>),
                          reinterpret_cast<const void*>(&k_bgemm<false, true, 1>),
                          reinterpret_cast<const void*>(&k_bgemm<true, false, 1>),
                          reinterpret_cast<const void*>(&k_bgemm<true, true, 1>),
@@ -1361,6 +1638,59 @@ static bool bgemm_cb_allowed() {
   return allowed;
 }
 
+// CIS2_BGEMM16=0 keeps every batched GEMM on k_bgemm (for A/B timing; the
+// results are the same bits either way).
+static bool bgemm16_allowed() {
+  const char* e = std::getenv("CIS2_BGEMM16");
+  return !(e && e[0] == '0' && e[1] == 0);
+}
+
+// k_bgemm16 for sequential-order GEMMs whose W blocks have 8 or 16 rows and
+// whose segments are whole 16-output tiles.
+static hipError_t launch_bgemm16(const BgemmSeg* segs, uint32_t nseg, uint32_t n,
+                                 const BgemmOpts& o, int ncu, hipStream_t st) {
+  const BgemmSeg& s0 = segs[0];
+  BgemmArgs a = {};
+  a.blk0[0] = 0;
+  for (uint32_t i = 0; i < nseg; ++i) {
+    a.s[i] = segs[i];
+    a.blk0[i + 1] = a.blk0[i] + segs[i].M / 16;
+  }
+  for (uint32_t i = nseg; i < kMaxSegs; ++i) {
+    a.s[i] = s0;
+    a.blk0[i + 1] = a.blk0[nseg];
+  }
+  a.nseg = nseg;
+  a.n = n;
+  a.TB = 16;
+  a.tree = 0;
+  a.W2 = o.W2;
+  a.nw = o.norm_w;
+  a.eps = o.eps;
+  const uint32_t S = o.W2 ? 2 : 1, NW = o.norm_w ? 1 : 0, nblk = 16 / s0.R;
+  const uint64_t wgs = (uint64_t)a.blk0[nseg] * ((n + 15) / 16);
+  const uint32_t budget = wgs <= (uint64_t)ncu ? kBgemmLdsBig : kBgemmLds;
+  // LDS groups: S * nblk * (q * R + 8) + NW * q + 16 * (q + 1) + slack
+  const uint32_t fixed = 8 * S * nblk + 16 + b16_slack(s0.R);
+  const uint32_t q_fit = (budget / 16 - fixed) / (16 * S + NW + 16);
+  uint32_t KC = std::min((q_fit * 4) & ~31u, 1024u);
+  if (KC == 0) return hipErrorInvalidValue;
+  const uint32_t K32 = (s0.K + 31) & ~31u;
+  if (KC > K32) KC = K32;
+  a.KC = KC;
+  const size_t q = KC / 4;
+  const size_t lds =
+      ((size_t)S * nblk * (q * s0.R + 8) + NW * q + 16 * (q + 1) + b16_slack(s0.R)) * 16;
+  const dim3 grid(a.blk0[nseg], (n + 15) / 16);
+  if (o.W2)
+    hipLaunchKernelGGL((o.norm_w ? k_bgemm16<true, true> : k_bgemm16<true, false>), grid,
+                       dim3(kT), lds, st, a);
+  else
+    hipLaunchKernelGGL((o.norm_w ? k_bgemm16<false, true> : k_bgemm16<false, false>), grid,
+                       dim3(kT), lds, st, a);
+  return hipGetLastError();
+}
+
 hipError_t launch_bgemm_multi(const BgemmSeg* segs, uint32_t nseg, uint32_t n,
                               const BgemmOpts& o, hipStream_t st) {
   if (n == 0) return hipSuccess;
@@ -1372,6 +1702,13 @@ hipError_t launch_bgemm_multi(const BgemmSeg* segs, uint32_t nseg, uint32_t n,
   const BgemmSeg& s0 = segs[0];
   if (s0.K % 4 || s0.ldx % 4 || s0.R == 0 || s0.R > kT) return hipErrorInvalidValue;
   const int ncu = device_cu_count();
+  {
+    bool tiles = !o.tree && (s0.R == 8 || s0.R == 16) && bgemm16_allowed();
+    for (uint32_t i = 0; i < nseg && tiles; ++i)
+      tiles = segs[i].M % 16 == 0 && segs[i].R == s0.R && segs[i].K == s0.K &&
+              segs[i].X == s0.X && segs[i].ldx == s0.ldx;
+    if (tiles) return launch_bgemm16(segs, nseg, n, o, ncu, st);
+  }
   BgemmArgs a = {};
   a.blk0[0] = 0;
   for (uint32_t i = 0; i < nseg; ++i) {
