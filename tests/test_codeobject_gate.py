@@ -16,7 +16,7 @@ each kernel is checked:
     0x5f7ffffc, FMAs with a +-2^32 literal or a zero multiplicand; the f64 ->
     integer split with a -2^32 literal), which carry no float data;
   - the pure reduction kernels (the standalone GEMVs, the per-op GEMV, the
-    row GEMM without norm or gate) contain no FMA and no divide at all;
+    row GEMMs without norm or gate) contain no FMA and no divide at all;
   - no scalar-cache writes of any kind (stores, atomics, write-back).
 
 The per-kernel FMA accounting is printed (pytest -s)."""
@@ -43,7 +43,7 @@ FMA64 = re.compile(r"^v_fma(c)?_f64$")
 # integer sequences: +-2^32 as an f32 literal, or as the high word of an f64
 INT_LIT32 = re.compile(r"0x[4c]f800000\b")
 INT_LIT64 = re.compile(r"0x[4c]1f00000\b")
-STRICT_ZERO = re.compile(r"(k_gemv_blk|k_gemv_pipe|k_gemv_many|4cis26k_gemvE|k_bgemmILb0ELb0E)")
+STRICT_ZERO = re.compile(r"(k_gemv_blk|k_gemv_pipe|k_gemv_many|4cis26k_gemvE|k_bgemmILb0ELb0E|k_bgemm16ILb0ELb0E)")
 
 
 def tools():
