@@ -1045,6 +1045,14 @@ __device__ __forceinline__ float chain_lds(const float* p, uint32_t n, float acc
 // ---------------------------------------------------------------------------
 constexpr uint32_t kKvT = 512;
 typedef float v2 __attribute__((ext_vector_type(2)));
+// RoPE inputs of the fused form: the rows' raw k and v ([n][nkv][hd]) and
+// the cos/sin table ([max_pos][hd/2][2]).
+struct KvFuse {
+  const float* k;
+  const float* v;
+  const float* rope_cs;
+  uint32_t nkv;
+};
 
 // s_waitcnt lgkmcnt(0), then s_barrier: LDS written before it is visible
 // after it; global loads in flight stay in flight.
@@ -1111,14 +1119,13 @@ __device__ __forceinline__ float mix_dpp(const float* p, const float* v, uint32_
   return acc;
 }
 
-template <uint32_t HPW, uint32_t HD>
+template <uint32_t HPW, uint32_t HD, bool FUSE>
 __global__ __launch_bounds__(kKvT) void k_attention_kv(const float* __restrict__ q,
-                                                     const float* __restrict__ kc,
-                                                     const float* __restrict__ vc,
-                                                     RowsDesc rows, uint32_t nh,
-                                                     uint32_t max_pos, uint64_t seq_stride,
-                                                     float scale, float* out, uint32_t tree,
-                                                     uint32_t ls, uint32_t C) {
+                                                     float* kc, float* vc, RowsDesc rows,
+                                                     uint32_t nh, uint32_t max_pos,
+                                                     uint64_t seq_stride, float scale,
+                                                     float* out, uint32_t tree, uint32_t ls,
+                                                     uint32_t C, KvFuse fz) {
   constexpr uint32_t NW = kKvT / 64, WPH = HD / 64, CW = HPW * WPH;
   static_assert(HD % 64 == 0 && CW <= NW, "chain waves");
   extern __shared__ v4 sh4[];
@@ -1128,15 +1135,20 @@ __global__ __launch_bounds__(kKvT) void k_attention_kv(const float* __restrict__
   const uint32_t r = blockIdx.x, kvh = blockIdx.y, qh0 = kvh * HPW, t = threadIdx.x;
   const uint32_t wv = __builtin_amdgcn_readfirstlane(t >> 6), lane = t & 63;
   const uint32_t pos = rows.pos[r], len = pos + 1, S = C + 4;
-  const uint32_t nbs = (ls + 31) / 32, len4 = (len + 3) & ~3u;
+  // FUSE: position pos comes from this launch (its K and V from LDS), the
+  // caches serve positions 0 .. pos-1
+  const uint32_t lc = FUSE ? pos : len;
+  const uint32_t nbs = (ls + 31) / 32, len4 = (lc + 3) & ~3u;
   const size_t sb = (size_t)rows.seq[r] * seq_stride;
-  const float* kb = kc + sb + (size_t)kvh * HD * max_pos;
-  const float* vb = vc + sb + (size_t)kvh * HD * max_pos;
+  float* kb = kc + sb + (size_t)kvh * HD * max_pos;
+  float* vb = vc + sb + (size_t)kvh * HD * max_pos;
   float* sq = sh;
-  float* ssb = sq + HPW * HD;
+  float* kself = sq + HPW * HD;  // FUSE: this position's rotated k and its v
+  float* vself = kself + HD;
+  float* ssb = vself + HD;
   float* partb = ssb + HPW * ls;
   float* VL = partb + ((HPW * nbs + 3) & ~3u);
-  const uint32_t nch = (len + C - 1) / C;
+  const uint32_t nch = (lc + C - 1) / C;
   // chunk ch of V row d into buffer ch % 2: one wave instruction (C <= 256
   // positions), lanes past the chunk or the row's end idle
   auto stage_row = [&](uint32_t ch, uint32_t d) {
@@ -1146,11 +1158,67 @@ __global__ __launch_bounds__(kKvT) void k_attention_kv(const float* __restrict__
                  reinterpret_cast<v4*>(VL + (size_t)(ch & 1) * HD * S + (size_t)d * S));
   };
   const float* qv = q + (size_t)r * nh * HD + (size_t)qh0 * HD;
-  for (uint32_t i = t; i < HPW * HD; i += kKvT) sq[i] = qv[i];
+  if constexpr (FUSE) {
+    // RoPE at pos of the HPW query heads and of KV head kvh, in
+    // k_rope_store_rows's order (o1 = x1*c + (-x2)*s, o2 = x2*c + x1*s); the
+    // rotated k and the raw v also into the caches at pos
+    constexpr uint32_t half = HD / 2;
+    const float* cs = fz.rope_cs + (size_t)pos * half * 2;
+    const float* kin = fz.k + (size_t)r * fz.nkv * HD + (size_t)kvh * HD;
+    const float* vin = fz.v + (size_t)r * fz.nkv * HD + (size_t)kvh * HD;
+    for (uint32_t i = t; i < (HPW + 1) * half; i += kKvT) {
+      const uint32_t h = i / half, ii = i - h * half;
+      const float* src = h < HPW ? qv + (size_t)h * HD : kin;
+      const float cv = cs[2 * ii], sv = cs[2 * ii + 1];
+      const float x1 = src[ii], x2 = src[ii + half];
+      const float t1 = x1 * cv;
+      const float nx2 = -x2;
+      const float t2 = nx2 * sv;
+      const float t3 = x2 * cv;
+      const float t4 = x1 * sv;
+      const float o1 = t1 + t2, o2 = t3 + t4;
+      if (h < HPW) {
+        sq[h * HD + ii] = o1;
+        sq[h * HD + ii + half] = o2;
+      } else {
+        kself[ii] = o1;
+        kself[ii + half] = o2;
+        kb[(size_t)ii * max_pos + pos] = o1;
+        kb[(size_t)(ii + half) * max_pos + pos] = o2;
+      }
+    }
+    for (uint32_t d = t; d < HD; d += kKvT) {
+      const float vv = vin[d];
+      vself[d] = vv;
+      vb[(size_t)d * max_pos + pos] = vv;
+    }
+  } else {
+    for (uint32_t i = t; i < HPW * HD; i += kKvT) sq[i] = qv[i];
+  }
   lds_barrier();
+  // FUSE: position pos's scores from the rotated k in LDS, one lane per head
+  if (FUSE && t < HPW) {
+    float acc = 0.0f;
+    if (tree) {
+#pragma unroll
+      for (uint32_t d0 = 0; d0 < HD; d0 += 32) {
+        float l[32];
+#pragma unroll
+        for (uint32_t i = 0; i < 32; ++i) l[i] = sq[t * HD + d0 + i] * kself[d0 + i];
+        acc = acc + tree32(l);
+      }
+    } else {
+      for (uint32_t d = 0; d < HD; ++d) {
+        const float pr = sq[t * HD + d] * kself[d];
+        acc = acc + pr;
+      }
+    }
+    ssb[t * ls + pos] = acc * scale;
+  }
   // scores: thread t takes positions jp, jp + 1 (jp = 2 * (t + k * kKvT);
-  // len4 <= max_pos, so a pair below len4 stays in the row)
-  for (uint32_t jp = 2 * t; jp < len; jp += 2 * kKvT) {
+  // len4 <= max_pos, so a pair below len4 stays in the row; a pair's
+  // second position past the cached ones is computed and dropped)
+  for (uint32_t jp = 2 * t; jp < lc; jp += 2 * kKvT) {
     float acc[2][HPW];
 #pragma unroll
     for (uint32_t p = 0; p < 2; ++p)
@@ -1189,7 +1257,7 @@ __global__ __launch_bounds__(kKvT) void k_attention_kv(const float* __restrict__
     }
 #pragma unroll
     for (uint32_t p = 0; p < 2; ++p)
-      if (jp + p < len)
+      if (jp + p < lc)
 #pragma unroll
         for (uint32_t h = 0; h < HPW; ++h) ssb[h * ls + jp + p] = acc[p][h] * scale;
   }
@@ -1276,8 +1344,14 @@ __global__ __launch_bounds__(kKvT) void k_attention_kv(const float* __restrict__
     if (wv < CW) {
       const uint32_t jc = ch * C;
       acc = mix_dpp(ps + jc, VL + (size_t)(ch & 1) * HD * S + (size_t)d * S,
-                    std::min(C, len - jc), acc);
+                    std::min(C, lc - jc), acc);
     }
+  }
+  wait_vm0();  // no copy still in flight when the workgroup ends (lc = 0)
+  if (FUSE && nch == 0) __syncthreads();  // the divide's p_pos, with no chunk loop
+  if (FUSE && wv < CW) {
+    const float pr = ps[pos] * vself[d];
+    acc = acc + pr;
   }
   if (wv < CW) out[(size_t)r * nh * HD + (size_t)(qh0 + h) * HD + d] = acc;
 }
@@ -1653,7 +1727,7 @@ hipError_t launch_bgemm_t(const BgemmArgs& a, dim3 grid, size_t lds, hipStream_t
 // attention), so that no attribute call happens later, e.g. inside a graph
 // capture.
 hipError_t rows_configure() {
-  const void* fns[16] = {reinterpret_cast<const void*>(&k_bgemm<false, false, 1>),
+  const void* fns[22] = {reinterpret_cast<const void*>(&k_bgemm<false, false, 1>),
                          reinterpret_cast<const void*>(&k_bgemm16<false, false>),
                          reinterpret_cast<const void*>(&k_bgemm16<false, true>),
                          reinterpret_cast<const void*>(&k_bgemm16<true, false>),
@@ -1663,12 +1737,18 @@ hipError_t rows_configure() {
                          reinterpret_cast<const void*>(&k_bgemm<true, true, 1>),
                          reinterpret_cast<const void*>(&k_bgemm<false, false, 2>),
                          reinterpret_cast<const void*>(&k_bgemm<true, false, 2>),
-                         reinterpret_cast<const void*>(&k_attention_kv<1, 64>),
-                         reinterpret_cast<const void*>(&k_attention_kv<2, 64>),
-                         reinterpret_cast<const void*>(&k_attention_kv<3, 64>),
-                         reinterpret_cast<const void*>(&k_attention_kv<4, 64>),
-                         reinterpret_cast<const void*>(&k_attention_kv<1, 128>),
-                         reinterpret_cast<const void*>(&k_attention_kv<2, 128>)};
+                         reinterpret_cast<const void*>(&k_attention_kv<1, 64, false>),
+                         reinterpret_cast<const void*>(&k_attention_kv<2, 64, false>),
+                         reinterpret_cast<const void*>(&k_attention_kv<3, 64, false>),
+                         reinterpret_cast<const void*>(&k_attention_kv<4, 64, false>),
+                         reinterpret_cast<const void*>(&k_attention_kv<1, 128, false>),
+                         reinterpret_cast<const void*>(&k_attention_kv<2, 128, false>),
+                         reinterpret_cast<const void*>(&k_attention_kv<1, 64, true>),
+                         reinterpret_cast<const void*>(&k_attention_kv<2, 64, true>),
+                         reinterpret_cast<const void*>(&k_attention_kv<3, 64, true>),
+                         reinterpret_cast<const void*>(&k_attention_kv<4, 64, true>),
+                         reinterpret_cast<const void*>(&k_attention_kv<1, 128, true>),
+                         reinterpret_cast<const void*>(&k_attention_kv<2, 128, true>)};
   for (const void* f : fns) {
     hipError_t e = ensure_dynamic_lds(f, kBgemmLdsBig);
     if (e != hipSuccess) return e;
@@ -1840,6 +1920,90 @@ static size_t kv_attention_cap() {
   return (size_t)std::strtoul(e, nullptr, 10) / 64 * 64;
 }
 
+// Decode rows (rows x kv heads < 4 x CUs), head_dim 64 or 128: one
+// workgroup per (row, KV head) with the V rows staged in LDS, in chunks of C
+// positions (two buffers: the longest row in one pass of each when they
+// fit).  A grid of at most one workgroup per CU may take most of the LDS,
+// larger ones half.  C = 0: another kernel.
+struct KvPlan {
+  size_t C = 0, shmem = 0;
+  uint32_t group = 0, ls = 0;
+};
+static hipError_t kv_plan(uint32_t n, uint32_t nh, uint32_t nkv, uint32_t hd, uint32_t max_len,
+                          KvPlan* p) {
+  *p = KvPlan{};
+  if (nkv == 0 || nh % nkv) return hipErrorInvalidValue;
+  const uint32_t group = nh / nkv;
+  const int ncu = device_cu_count();
+  const uint64_t wgs_kv = (uint64_t)n * nkv;
+  if (!(wgs_kv < 4 * (uint64_t)ncu && (hd == 64 || hd == 128) && group * hd <= 256))
+    return hipSuccess;
+  hipError_t e = rows_configure();
+  if (e != hipSuccess) return e;
+  const size_t ls = ((size_t)max_len + 3) / 4 * 4, nbs = (ls + 31) / 32;
+  const size_t fixed =
+      (group * hd + 2 * hd + group * ls + ((group * nbs + 3) & ~(size_t)3)) * 4;
+  const size_t budget = wgs_kv <= (uint64_t)ncu ? kBgemmLdsBig : kBgemmLds;
+  const size_t c_need =
+      std::min<size_t>((((size_t)max_len + 1) / 2 + 63) & ~(size_t)63, 256);
+  size_t c_fit = 0;
+  if (budget > fixed + kKvSlack * 4 + 8 * hd * 68)
+    c_fit = ((budget - fixed - kKvSlack * 4) / (8 * hd) - 4) & ~(size_t)63;
+  const size_t C = std::min(std::min(c_need, c_fit), kv_attention_cap());
+  if (C < 64) return hipSuccess;
+  p->C = C;
+  p->shmem = fixed + 2 * hd * (C + 4) * 4 + kKvSlack * 4;
+  p->group = group;
+  p->ls = (uint32_t)ls;
+  return hipSuccess;
+}
+static hipError_t launch_kv(const KvPlan& kp, bool fuse, const float* q, float* kc, float* vc,
+                            RowsDesc rows, uint32_t nh, uint32_t hd, uint32_t max_pos,
+                            uint64_t seq_stride, float scale, float* out, bool tree,
+                            const KvFuse& fz, hipStream_t st) {
+  const dim3 grid(rows.n, nh / kp.group);
+  const uint32_t tr = tree ? 1u : 0u, c32 = (uint32_t)kp.C;
+#define CIS2_ATT_KV(H, D)                                                                     \
+  do {                                                                                        \
+    if (fuse)                                                                                 \
+      hipLaunchKernelGGL((k_attention_kv<H, D, true>), grid, dim3(kKvT), kp.shmem, st, q, kc, \
+                         vc, rows, nh, max_pos, seq_stride, scale, out, tr, kp.ls, c32, fz);  \
+    else                                                                                      \
+      hipLaunchKernelGGL((k_attention_kv<H, D, false>), grid, dim3(kKvT), kp.shmem, st, q,    \
+                         kc, vc, rows, nh, max_pos, seq_stride, scale, out, tr, kp.ls, c32,   \
+                         fz);                                                                 \
+  } while (0)
+  if (hd == 64) {
+    switch (kp.group) {
+      case 1: CIS2_ATT_KV(1, 64); break;
+      case 2: CIS2_ATT_KV(2, 64); break;
+      case 3: CIS2_ATT_KV(3, 64); break;
+      default: CIS2_ATT_KV(4, 64);
+    }
+  } else {
+    if (kp.group == 1) CIS2_ATT_KV(1, 128);
+    else CIS2_ATT_KV(2, 128);
+  }
+#undef CIS2_ATT_KV
+  return hipGetLastError();
+}
+
+hipError_t launch_rope_attention_rows(const float* q, const float* k, const float* v,
+                                      const float* rope_cs, RowsDesc rows, uint32_t max_len,
+                                      uint32_t nh, uint32_t nkv, uint32_t hd, uint32_t max_pos,
+                                      float* kc, float* vc, uint64_t seq_stride, float scale,
+                                      float* out, bool tree, hipStream_t st) {
+  if (rows.n == 0) return hipSuccess;
+  if (max_len == 0 || max_len > max_pos || max_pos % 4 || hd % 2) return hipErrorInvalidValue;
+  KvPlan kp;
+  hipError_t e = kv_plan(rows.n, nh, nkv, hd, max_len, &kp);
+  if (e != hipSuccess) return e;
+  if (!kp.C) return hipErrorNotSupported;
+  const KvFuse fz{k, v, rope_cs, nkv};
+  return launch_kv(kp, true, q, kc, vc, rows, nh, hd, max_pos, seq_stride, scale, out, tree, fz,
+                   st);
+}
+
 hipError_t launch_attention_rows(const float* q, const float* kc, const float* vc,
                                  RowsDesc rows, uint32_t max_len, uint32_t nh, uint32_t nkv,
                                  uint32_t hd, uint32_t max_pos, uint64_t seq_stride, float scale,
@@ -1853,42 +2017,12 @@ hipError_t launch_attention_rows(const float* q, const float* kc, const float* v
   const int ncu = device_cu_count();
   const uint64_t wgs_kv = (uint64_t)rows.n * nkv;
   const uint32_t tr = tree ? 1u : 0u, ls32 = (uint32_t)ls;
-  // Few rows (decode steps), head_dim 64 or 128: one workgroup per (row, KV
-  // head) with the V rows staged in LDS, in chunks of C positions (two
-  // buffers: the longest row in one pass of each when they fit).  A grid of
-  // at most one workgroup per CU may take most of the LDS, larger ones half.
-  if (wgs_kv < 4 * (uint64_t)ncu && (hd == 64 || hd == 128) && group * hd <= 256) {
-    hipError_t e = rows_configure();
+  {
+    KvPlan kp;
+    hipError_t e = kv_plan(rows.n, nh, nkv, hd, max_len, &kp);
     if (e != hipSuccess) return e;
-    const size_t nbs = (ls + 31) / 32;
-    const size_t fixed = (group * hd + group * ls + ((group * nbs + 3) & ~(size_t)3)) * 4;
-    const size_t budget = wgs_kv <= (uint64_t)ncu ? kBgemmLdsBig : kBgemmLds;
-    const size_t c_need = std::min<size_t>((((size_t)max_len + 1) / 2 + 63) & ~(size_t)63, 256);
-    size_t c_fit = 0;
-    if (budget > fixed + kKvSlack * 4 + 8 * hd * 68)
-      c_fit = ((budget - fixed - kKvSlack * 4) / (8 * hd) - 4) & ~(size_t)63;
-    const size_t C = std::min(std::min(c_need, c_fit), kv_attention_cap());
-    if (C >= 64) {
-      const size_t shmem = fixed + 2 * hd * (C + 4) * 4 + kKvSlack * 4;
-      const dim3 grid(rows.n, nkv);
-      const uint32_t c32 = (uint32_t)C;
-#define CIS2_ATT_KV(H, D)                                                                      \
-  hipLaunchKernelGGL((k_attention_kv<H, D>), grid, dim3(kKvT), shmem, st, q, kc, vc, rows, nh, \
-                     max_pos, seq_stride, scale, out, tr, ls32, c32)
-      if (hd == 64) {
-        switch (group) {
-          case 1: CIS2_ATT_KV(1, 64); break;
-          case 2: CIS2_ATT_KV(2, 64); break;
-          case 3: CIS2_ATT_KV(3, 64); break;
-          default: CIS2_ATT_KV(4, 64);
-        }
-      } else {
-        if (group == 1) CIS2_ATT_KV(1, 128);
-        else CIS2_ATT_KV(2, 128);
-      }
-#undef CIS2_ATT_KV
-      return hipGetLastError();
-    }
+    if (kp.C) return launch_kv(kp, false, q, const_cast<float*>(kc), const_cast<float*>(vc),
+                               rows, nh, hd, max_pos, seq_stride, scale, out, tree, KvFuse{}, st);
   }
   // Otherwise, few rows: one head per workgroup, for the most workgroups.
   // Many rows: the most heads of one KV head (a divisor of the group) whose

@@ -71,6 +71,17 @@ hipError_t launch_attention_rows(const float* q, const float* kc, const float* v
                                  RowsDesc rows, uint32_t max_len, uint32_t nh, uint32_t nkv,
                                  uint32_t hd, uint32_t max_pos, uint64_t seq_stride, float scale,
                                  float* out, bool tree, hipStream_t st);
+// Rows of distinct sequences (decode steps): launch_rope_store_rows and
+// launch_attention_rows in one launch, with the same bits and the same cache
+// writes, when the shape takes the one-workgroup-per-(row, KV head)
+// attention (head_dim 64 or 128, rows x kv heads < 4 x CUs);
+// hipErrorNotSupported otherwise, with nothing launched.  q, k and v are
+// the rows' un-rotated projections (q and k are not rotated in place).
+hipError_t launch_rope_attention_rows(const float* q, const float* k, const float* v,
+                                      const float* rope_cs, RowsDesc rows, uint32_t max_len,
+                                      uint32_t nh, uint32_t nkv, uint32_t hd, uint32_t max_pos,
+                                      float* kc, float* vc, uint64_t seq_stride, float scale,
+                                      float* out, bool tree, hipStream_t st);
 // Prefill attention in tiles: rows row0 .. row0+nr-1 (nr <= 16) are rows of
 // sequence seq at positions p0 .. p0+nr-1; each tile's rows get the same
 // bits as launch_attention_rows gives them (sequential order only), with

@@ -489,8 +489,11 @@ constexpr uint32_t kFuseNormRows = 256;
 // other buffers of at least nl rows.
 // ntiles > 0: the attention runs over the ntiles tiles in c->rows.tiles
 // (runs of rows of one sequence at consecutive positions).
+// one_per_seq: every row belongs to a different sequence (decode steps), so
+// RoPE and the cache store may run inside the attention launch.
 int forward_rows(cis2_ctx* c, uint32_t n, const uint32_t* d_tok, uint32_t max_len, uint32_t nl,
-                 float* logits = nullptr, uint32_t* arg = nullptr, uint32_t ntiles = 0) {
+                 float* logits = nullptr, uint32_t* arg = nullptr, uint32_t ntiles = 0,
+                 bool one_per_seq = false) {
   const cis2_config& f = c->cfg;
   RowsBuf& b = c->rows;
   const uint32_t H = f.hidden, I = f.inter, hd = f.head_dim, QD = c->qd, KV = c->kvd;
@@ -528,18 +531,29 @@ int forward_rows(cis2_ctx* c, uint32_t n, const uint32_t* d_tok, uint32_t max_le
     LAUNCH(launch_bgemm_multi(qkv, 3, n, o1, s), "rows qkv");
     if (Ly.qn) LAUNCH(launch_rmsnorm(b.q, Ly.qn, f.eps, hd, n * f.n_heads, b.q, s, tree), "rows q_norm");
     if (Ly.kn) LAUNCH(launch_rmsnorm(b.k, Ly.kn, f.eps, hd, n * f.n_kv_heads, b.k, s, tree), "rows k_norm");
-    LAUNCH(launch_rope_store_rows(b.q, b.k, b.v, c->rope_cs, rd, f.n_heads, f.n_kv_heads, hd,
-                                  f.max_pos, kc, vc, seq_stride, s),
-           "rows rope");
-    if (ntiles)
-      LAUNCH(launch_attention_tiles(b.q, kc, vc, b.tiles, ntiles, max_len, f.n_heads,
-                                    f.n_kv_heads, hd, f.max_pos, seq_stride, c->scale, b.att,
-                                    b.ascr, s),
-             "rows attention tiles");
-    else
-      LAUNCH(launch_attention_rows(b.q, kc, vc, rd, max_len, f.n_heads, f.n_kv_heads, hd,
-                                   f.max_pos, seq_stride, c->scale, b.att, tree, s),
-             "rows attention");
+    // decode steps: RoPE and the cache store inside the attention launch
+    // when its shape allows (hipErrorNotSupported: nothing launched)
+    hipError_t fe = hipErrorNotSupported;
+    if (one_per_seq && !ntiles)
+      fe = launch_rope_attention_rows(b.q, b.k, b.v, c->rope_cs, rd, max_len, f.n_heads,
+                                      f.n_kv_heads, hd, f.max_pos, kc, vc, seq_stride, c->scale,
+                                      b.att, tree, s);
+    if (fe != hipErrorNotSupported) {
+      LAUNCH(fe, "rows rope + attention");
+    } else {
+      LAUNCH(launch_rope_store_rows(b.q, b.k, b.v, c->rope_cs, rd, f.n_heads, f.n_kv_heads, hd,
+                                    f.max_pos, kc, vc, seq_stride, s),
+             "rows rope");
+      if (ntiles)
+        LAUNCH(launch_attention_tiles(b.q, kc, vc, b.tiles, ntiles, max_len, f.n_heads,
+                                      f.n_kv_heads, hd, f.max_pos, seq_stride, c->scale, b.att,
+                                      b.ascr, s),
+               "rows attention tiles");
+      else
+        LAUNCH(launch_attention_rows(b.q, kc, vc, rd, max_len, f.n_heads, f.n_kv_heads, hd,
+                                     f.max_pos, seq_stride, c->scale, b.att, tree, s),
+               "rows attention");
+    }
     const BgemmSeg so{Ly.wo, H, QD, c->Ro, b.att, QD, b.h2, H, b.h, H, kEpiResidual};
     LAUNCH(launch_bgemm(so, n, tree, s), "rows o_proj");
     std::swap(b.h, b.h2);
@@ -642,7 +656,10 @@ int forward_rows_host(cis2_ctx* c, uint32_t n, const uint32_t* seq, const uint32
   uint32_t ntiles = 0;
   r = plan_tiles(c, n, seq, pos, max_len, &ntiles);
   if (r) return r;
-  return forward_rows(c, n, b.tok, max_len, nl, nullptr, nullptr, ntiles);
+  std::vector<uint32_t> ss(seq, seq + n);
+  std::sort(ss.begin(), ss.end());
+  const bool one_per_seq = std::adjacent_find(ss.begin(), ss.end()) == ss.end();
+  return forward_rows(c, n, b.tok, max_len, nl, nullptr, nullptr, ntiles, one_per_seq);
 }
 
 // Checks a row set: sequence and position ranges, token ranges, and no two
@@ -1517,7 +1534,7 @@ static int decode_steps(cis2_ctx* c, uint32_t G, const uint32_t* lens, const uin
          "rows upload");
   // one pass into buffer j: tokens from buffer 1 - j
   auto pass = [&](uint32_t j) -> int {
-    int r = forward_rows(c, G, argb[1 - j], max_len, G, logb[j], argb[j]);
+    int r = forward_rows(c, G, argb[1 - j], max_len, G, logb[j], argb[j], 0, true);
     if (r) return r;
     HIPCHK(c, launch_advance_rows(rb.pos, G, c->st), "rows advance");
     return CIS2_OK;
