@@ -141,7 +141,8 @@ __host__ __device__ inline uint32_t att_mix_tile_positions(uint32_t max_pos, siz
 __host__ __device__ inline size_t decode_vec_floats(const DecodeArgs& a) {
   size_t vec = 2 * (size_t)a.H + 64 + 64;                          // QKV, GU, LM
   const size_t vo = (size_t)a.qd + a.Ro, vd = (size_t)a.I + a.Rd;  // O, D
-  const size_t va = 4 * (size_t)a.hd + 64;                         // ATT
+  const size_t ng = a.nkv ? a.nh / a.nkv : 1;                      // ATT (score task)
+  const size_t va = (2 * ng + 4) * a.hd + 64;
   vec = vec > vo ? vec : vo;
   vec = vec > vd ? vec : vd;
   vec = vec > va ? vec : va;
@@ -1477,16 +1478,100 @@ __device__ __forceinline__ void run_att(const DecodeArgs& a, uint32_t l, uint32_
   stamp(a, l, P_ATT, h, 2);
 }
 
+// The inputs of kv head kvh's score task, in LDS: the G = nh/nkv query
+// heads of the group at qv[g*hd ..), the kv head's k at qv[G*hd ..) and v
+// after it; Qwen3's per-head QK-norm (after bias, before RoPE;
+// labs/w1x-qwen3/scripts/qwen3-port.diff:66-80) and RoPE rotate-half of
+// every q head and k (main.rs:285-307): o1 = x1*c + (-x2)*s,
+// o2 = x2*c + x1*s.  The G+1 sums of squares run as separate chains, one
+// per wave.  cs: hd floats (this position's cos/sin pairs), tmp: (G+1)*hd
+// floats, misc: 64.  Ends with a barrier.
+template <bool TR>
+__device__ __forceinline__ void att_group_inputs(const DecodeArgs& a, uint32_t l, uint32_t kvh,
+                                                 lf* qv, lf* cs, lf* tmp, lf* misc) {
+  const LayerW Lw = a.layers[l];
+  const Act ac = act_of(a, l);
+  const uint32_t hd = a.hd, ng = a.nh / a.nkv, nv = ng + 1, half = hd / 2;
+  NormW nq, nk;
+  if (Lw.qn) nq = load_normw(Lw.qn, hd);
+  if (Lw.kn) nk = load_normw(Lw.kn, hd);
+  float csv = 0.0f;
+  if (threadIdx.x < hd) csv = G(a.rope_cs)[(size_t)a.pos * hd + threadIdx.x];
+  const uint32_t nq_w = ng * hd;
+  gather(qv, (ng + 2) * hd, a.epoch, a.err, [=](uint32_t i) {
+    return i < nq_w ? ac.q + (size_t)kvh * nq_w + i
+                    : (i < nq_w + hd ? ac.k : ac.v) + (size_t)kvh * hd + (i - nq_w) % hd;
+  });
+  if (threadIdx.x < hd) cs[threadIdx.x] = csv;
+  if (Lw.qn || Lw.kn) {  // rmsnorm of each vector that has weights
+    const uint32_t nb = (hd + 31) / 32;
+    if constexpr (TR) {
+      for (uint32_t t = threadIdx.x; t < nv * nb; t += kThreads) {
+        const uint32_t v = t / nb, b = t - v * nb;
+        const lf* x = qv + (size_t)v * hd + 32 * b;
+        float lv[32];
+#pragma unroll
+        for (uint32_t i = 0; i < 32; ++i) {
+          const float xv = 32 * b + i < hd ? x[i] : 0.0f;
+          lv[i] = xv * xv;
+        }
+        tmp[t] = tree32(lv);
+      }
+    } else {
+      for (uint32_t i = threadIdx.x; i < nv * hd; i += kThreads) {
+        const float xv = qv[i];
+        tmp[i] = xv * xv;
+      }
+    }
+    __syncthreads();
+    for (uint32_t v = threadIdx.x >> 6; v < nv; v += kThreads / 64) {
+      const float acc = TR ? chain1(tmp + (size_t)v * nb, nb, 1, 0.0f)
+                           : chain_vec(tmp + (size_t)v * hd, hd, 0.0f);
+      float mean = acc / (float)hd;
+      float arg = mean + a.eps;
+      float inv = rsqrt_cr(arg);
+      if ((threadIdx.x & 63) == 0) misc[v] = inv;
+    }
+    __syncthreads();
+    for (uint32_t v = 0; v < nv; ++v) {
+      const float inv = misc[v];
+      const float* wg = v < ng ? Lw.qn : Lw.kn;
+      if (!wg) continue;
+      for (uint32_t i = threadIdx.x; i < hd; i += kThreads) {
+        const float wv = i < kThreads ? (v < ng ? nq.v[0] : nk.v[0]) : G(wg)[i];
+        float sx = qv[(size_t)v * hd + i] * inv;
+        qv[(size_t)v * hd + i] = sx * wv;
+      }
+    }
+  }
+  __syncthreads();
+  for (uint32_t idx = threadIdx.x; idx < nv * half; idx += kThreads) {
+    const uint32_t v = idx / half, i = idx - v * half;
+    lf* hv = qv + (size_t)v * hd;
+    float c = cs[2 * i], sn = cs[2 * i + 1];
+    float x1 = hv[i], x2 = hv[i + half];
+    float t1 = x1 * c;
+    float nx2 = -x2;
+    float t2 = nx2 * sn;
+    float t3 = x2 * c;
+    float t4 = x1 * sn;
+    hv[i] = t1 + t2;
+    hv[i + half] = t3 + t4;
+  }
+  __syncthreads();
+}
+
 // ---------------------------------------------------------------------------
 // Split attention, for contexts whose K/V rows do not fit one workgroup's
 // LDS.  The phase's tasks are natt_s score tasks and then natt_v mix tasks
 // (every workgroup runs its score tasks before its mix tasks, so waits stay
 // acyclic):
-//   score task (h, c): positions c*256 .. c*256+255 of query head h; thread
-//     j loads its column k_j[0..hd) straight from the cache, 64 loads in
-//     flight, and forms dot_seq(q, k_j) (or dot_tree) * scale, published as
-//     a tagged word; the chunk holding `pos` uses this position's own k and
-//     (for the first head of a kv group) stores k and v into the caches.
+//   score task (kvh, c): positions c*P .. c*P+P-1 of every query head of kv
+//     head kvh; thread j loads its column k_j[0..hd) straight from the
+//     cache once for all the group's heads (128 dims at a time) and forms
+//     dot_seq(q, k_j) (or dot_tree) * scale per head, each published as a
+//     tagged word; the chunk holding `pos` uses this position's own k and
+//     stores k and v into the caches.
 //   mix task (h, dc): output dims d0 = dc*16 .. d0+15 of head h: gathers all
 //     of the head's scores, runs the softmax (the same order as one task),
 //     then lane d of wave 0 continues its one left-to-right V-mix chain over
@@ -1496,12 +1581,59 @@ __device__ __forceinline__ void run_att(const DecodeArgs& a, uint32_t l, uint32_
 // Each head's K and V are read by many workgroups at once instead of
 // streaming through one.
 // ---------------------------------------------------------------------------
+constexpr uint32_t kScoreKB = 128;  // K dims a score thread holds in registers
+
+// acc0 (and acc1 when `two`) continue over q0[i] * k[i] (q1[i] * k[i]),
+// i < nd: one left-to-right chain per head (dot_seq, math.rs:56-62) or
+// tree32 blocks folded in order (dot_tree, math.rs:75-93).  The products of
+// one 16-dim slice at a time are formed ahead of the chain's adds.
+template <bool TR>
+__device__ __forceinline__ void score_chains(const lf* q0, const lf* q1, bool two,
+                                             const float (&k)[kScoreKB], uint32_t nd,
+                                             float& acc0, float& acc1) {
+  if constexpr (TR) {
+#pragma unroll
+    for (uint32_t b = 0; b < kScoreKB; b += 32) {
+      if (b < nd) {
+        float l32[32];
+#pragma unroll
+        for (uint32_t i = 0; i < 32; ++i) l32[i] = b + i < nd ? q0[b + i] * k[b + i] : 0.0f;
+        acc0 = acc0 + tree32(l32);
+        if (two) {
+#pragma unroll
+          for (uint32_t i = 0; i < 32; ++i) l32[i] = b + i < nd ? q1[b + i] * k[b + i] : 0.0f;
+          acc1 = acc1 + tree32(l32);
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  } else {
+#pragma unroll
+    for (uint32_t b = 0; b < kScoreKB; b += 16) {
+      if (b < nd) {
+#pragma unroll
+        for (uint32_t i = b; i < b + 16; ++i) {
+          if (i < nd) {
+            const float p = q0[i] * k[i];
+            acc0 = acc0 + p;
+            if (two) {
+              const float p1 = q1[i] * k[i];
+              acc1 = acc1 + p1;
+            }
+          }
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+}
+
 template <bool TR>
 __device__ __forceinline__ void run_att_score(const DecodeArgs& a, uint32_t l, uint32_t t,
                                               const Lds& s) {
-  const uint32_t C = a.att_chunks, h = t / C, c = t - h * C, P = a.att_cpos;
-  const uint32_t hd = a.hd, group = a.nh / a.nkv, kvh = h / group, pos = a.pos, len = pos + 1;
-  const uint32_t j0 = c * P;
+  const uint32_t C = a.att_chunks, kvh = t / C, c = t - kvh * C, P = a.att_cpos;
+  const uint32_t hd = a.hd, ng = a.nh / a.nkv, pos = a.pos, len = pos + 1;
+  const uint32_t j0 = c * P, jend = min(len, j0 + P);
   stamp(a, l, P_ATT, t, 0);
   if (j0 >= len) {  // no positions in this chunk yet
     stamp(a, l, P_ATT, t, 1);
@@ -1509,45 +1641,55 @@ __device__ __forceinline__ void run_att_score(const DecodeArgs& a, uint32_t l, u
     stamp(a, l, P_ATT, t, 2);
     return;
   }
-  lf* qv = s.v;
-  lf* kv = qv + hd;
+  lf* qv = s.v;                  // the group's q heads [ng][hd]
+  lf* kv = qv + (size_t)ng * hd;  // this position's k, then v
   lf* vv = kv + hd;
-  lf* tmp = vv + hd;
-  lf* misc = tmp + hd;
-  att_head_inputs<TR>(a, l, h, qv, tmp, misc);
-  stamp(a, l, P_ATT, t, 1);
-  if (pos < j0 + P && h % group == 0) store_kv_pos(a, l, kvh, kv, vv);
-  for (uint32_t j = j0 + threadIdx.x; j < len && j < j0 + P; j += kThreads) {
-    const float* kb = a.kc0 + (size_t)l * a.cache_stride + (size_t)kvh * hd * a.max_pos + j;
-    const bool cached = j < pos;
-    float acc = 0.0f;
-    for (uint32_t d0 = 0; d0 < hd; d0 += 64) {
-      const uint32_t nd = min(64u, hd - d0);
-      float k[64];
+  lf* cs = vv + hd;                     // cos/sin pairs [hd]
+  lf* tmp = cs + hd;                    // [(ng+1)*hd]
+  lf* misc = tmp + (size_t)(ng + 1) * hd;
+  // kv head kvh's K rows as a buffer: one per-thread offset (the position)
+  // and a scalar offset per dim keep the column's loads off the vector
+  // registers' address pairs (reads past the rows return 0)
+  const __amdgpu_buffer_rsrc_t kbuf = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(a.kc0 + (size_t)l * a.cache_stride + (size_t)kvh * hd * a.max_pos), (short)0,
+      (int)(hd * a.max_pos * 4), 0x00020000);
+  constexpr uint32_t kNone = UINT32_MAX;
+  float k[kScoreKB];
+  uint32_t held = kNone;  // first dim of the K block in k[] for position jt
+  uint32_t jt = j0 + threadIdx.x;
+  auto load_k = [&](uint32_t d0) {
+    const uint32_t nd = min(kScoreKB, hd - d0);
+    if (jt < pos) {
 #pragma unroll
-      for (uint32_t i = 0; i < 64; ++i)
-        if (i < nd) k[i] = cached ? kb[(size_t)(d0 + i) * a.max_pos] : kv[d0 + i];
-      if (TR) {
+      for (uint32_t i = 0; i < kScoreKB; ++i)
+        if (i < nd)
+          k[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                              kbuf, jt * 4, (d0 + i) * a.max_pos * 4, 0));
+    } else {
 #pragma unroll
-        for (uint32_t b = 0; b < 64; b += 32) {
-          if (b < nd) {
-            float l32[32];
-#pragma unroll
-            for (uint32_t i = 0; i < 32; ++i) l32[i] = b + i < nd ? qv[d0 + b + i] * k[b + i] : 0.0f;
-            acc = acc + tree32(l32);
-          }
-        }
-      } else {
-#pragma unroll
-        for (uint32_t i = 0; i < 64; ++i) {
-          if (i < nd) {
-            const float p = qv[d0 + i] * k[i];
-            acc = acc + p;
-          }
-        }
-      }
+      for (uint32_t i = 0; i < kScoreKB; ++i)
+        if (i < nd) k[i] = kv[d0 + i];
     }
-    put_word((gw*)a.scw + ((size_t)l * a.nh + h) * a.max_pos + j, acc * a.scale, a.epoch);
+    held = d0;
+  };
+  att_group_inputs<TR>(a, l, kvh, qv, cs, tmp, misc);
+  stamp(a, l, P_ATT, t, 1);
+  if (pos < j0 + P) store_kv_pos(a, l, kvh, kv, vv);
+  gw* sc = (gw*)a.scw + ((size_t)l * a.nh + (size_t)kvh * ng) * a.max_pos;
+  for (; jt < jend; jt += kThreads) {
+    for (uint32_t g0 = 0; g0 < ng; g0 += 2) {
+      const bool two = g0 + 1 < ng;
+      float a0 = 0.0f, a1 = 0.0f;
+      for (uint32_t d0 = 0; d0 < hd; d0 += kScoreKB) {
+        const uint32_t nd = min(kScoreKB, hd - d0);
+        if (held != d0) load_k(d0);
+        score_chains<TR>(qv + (size_t)g0 * hd + d0, qv + (size_t)(g0 + 1) * hd + d0, two, k, nd,
+                         a0, a1);
+      }
+      put_word(sc + (size_t)g0 * a.max_pos + jt, a0 * a.scale, a.epoch);
+      if (two) put_word(sc + (size_t)(g0 + 1) * a.max_pos + jt, a1 * a.scale, a.epoch);
+    }
+    held = kNone;
   }
   stamp(a, l, P_ATT, t, 3);
   stamp(a, l, P_ATT, t, 2);
@@ -2216,7 +2358,7 @@ size_t decode_act_floats(uint32_t H, uint32_t I, uint32_t qd, uint32_t kvd) {
 
 bool decode_att_ok(const DecodeArgs& a) {
   const size_t wfloats = decode_wregion_bytes(a) / 4;
-  if (a.att_split) return a.att_tp >= 32 && a.nh % a.nkv == 0;
+  if (a.att_split) return a.att_tp >= 32 && a.nh % a.nkv == 0 && a.nh / a.nkv < 64;
   // the one-task form keeps K and V in LDS when they fit (head_dim a
   // multiple of 4), else streams tiles of at least 32 positions
   return (a.hd % 4 == 0 && a.hd <= 192 &&
@@ -2230,20 +2372,21 @@ bool decode_att_needs_split(const DecodeArgs& a) {
 
 void decode_att_plan(DecodeArgs& a, bool split) {
   a.att_split = split ? 1u : 0u;
-  // positions per score task: 256 (one per thread) when every head's chunks
-  // fit one per workgroup, else the fewest 64-multiples up to 512 that do
-  // (a workgroup holding two score tasks of a layer would finish its second
-  // one late, and every mix task of the head waits for it)
+  // positions per score task (one kv head's query heads): 256 (one per
+  // thread) when every kv head's chunks fit one per workgroup, else the
+  // fewest 64-multiples up to 512 that do (a workgroup holding two score
+  // tasks of a layer would finish its second one late, and every mix task
+  // of the group waits for it)
   uint32_t cp = kThreads;
-  const uint32_t per_head = a.nh ? a.nwg / a.nh : 0;
-  if (per_head > 0 && a.nh * ((a.max_pos + cp - 1) / cp) > a.nwg) {
-    cp = (a.max_pos + per_head - 1) / per_head;
+  const uint32_t per_kv = a.nkv ? a.nwg / a.nkv : 0;
+  if (per_kv > 0 && a.nkv * ((a.max_pos + cp - 1) / cp) > a.nwg) {
+    cp = (a.max_pos + per_kv - 1) / per_kv;
     cp = (cp + 63) & ~63u;
     if (cp > 2 * kThreads) cp = 2 * kThreads;
   }
   a.att_cpos = cp;
   a.att_chunks = (a.max_pos + cp - 1) / cp;
-  a.natt_s = a.nh * a.att_chunks;
+  a.natt_s = a.nkv * a.att_chunks;
   a.att_dvc = (a.hd + kAttDV - 1) / kAttDV;
   a.natt_v = a.nh * a.att_dvc;
   a.att_tp = att_mix_tile_positions(a.max_pos, decode_wregion_bytes(a) / 4);

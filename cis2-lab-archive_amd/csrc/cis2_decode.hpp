@@ -55,8 +55,9 @@ struct DecodeArgs {
   uint32_t pos, epoch, lm_epoch, want_logits;
   uint32_t tree;  // 1: v0.4-candidate tree reduction order, 0: sequential
   // Split attention (contexts whose K/V rows do not fit one workgroup's
-  // LDS): the ATT phase runs natt_s = nh * att_chunks score tasks
-  // (att_cpos positions each, a multiple of 64 in [256, 512]) and then
+  // LDS): the ATT phase runs natt_s = nkv * att_chunks score tasks (all
+  // query heads of one kv head over att_cpos positions, a multiple of 64 in
+  // [256, 512]) and then
   // natt_v = nh * att_dvc mix tasks (16 output dims each, V tiles of att_tp
   // positions); scores pass through scw, tagged words [L][nh][max_pos]
   // (zeroed at start).

@@ -999,6 +999,8 @@ int cis2_ctx_create(const cis2_config* cfg, cis2_ctx** out) {
       if (decode_lds_bytes(a) + 64 > cap_lds) a.wslot = 0;  // slots where they fit only
       const size_t need_lds = decode_lds_bytes(a) + 64;
       return lds > 0 && need_lds <= cap_lds && a.hd <= 256 &&  // RoPE: one pair per thread
+             // split attention's score tasks address a kv head's K rows as one buffer
+             (!a.att_split || (uint64_t)a.hd * a.max_pos * 4 <= 0x7FFFFFFFu) &&
              decode_att_ok(a);
     };
     c->fast_ok = plan(32, true) || plan(32, false) || plan(64, false);

@@ -55,3 +55,25 @@ def test_split_and_one_task_step_digests_agree(model_fixtures):
     b = build(rec, "one").decode(rec["prompt"], 64)
     assert a["step_digests"] == b["step_digests"]
     assert a["witness"] == b["witness"]
+
+
+@pytest.mark.parametrize("n_heads,n_kv,mode", [(6, 2, 0), (6, 2, 1), (10, 2, 0)])
+def test_split_score_groups_match_one_task(n_heads, n_kv, mode):
+    """Score tasks cover all query heads of a kv head (pairs of heads, then
+    a lone head for odd groups) with Qwen3's per-head QK-norm: both forms
+    give the same per-step logits for groups of 3 and 5."""
+    import numpy as np
+    spec = artifacts.ModelSpec(f"tiny-g{n_heads // n_kv}", 96, 128, 2, n_heads, n_kv, 300, 1e-6,
+                               1000000.0, True, head_dim=32, qk_norm=True)
+    w = artifacts.Weights(spec, 7)
+    prompt = np.arange(1, 20, dtype=np.uint32)
+    out = []
+    for att in ("split", "one"):
+        os.environ["CIS2_ATT"] = att
+        try:
+            m = Cis2Model(spec, w, max_pos=64, reduction_mode=mode)
+        finally:
+            del os.environ["CIS2_ATT"]
+        out.append(m.decode(prompt, 40))
+    assert list(out[0]["ids"]) == list(out[1]["ids"])
+    assert out[0]["step_digests"] == out[1]["step_digests"]
