@@ -1,5 +1,6 @@
 """Split attention in the persistent decode kernel: the ATT phase as score
-tasks (256 positions each, columns read straight from the K cache) and mix
+tasks (256 positions of all query heads of one kv head each, columns read
+straight from the K cache) and mix
 tasks (16 output dims each: softmax, then the V-mix chain over V tiles
 streamed into LDS).  It is chosen when a head's K/V rows do not fit one
 workgroup (Qwen3 at 4352 positions, the 1200-position tree case);
