@@ -85,6 +85,9 @@ class Checkpoint {
     uint64_t first = 0, last = 0;  // byte range [first, last) of the data section
   };
 
+  // Largest header the reader accepts (safetensors writers stay below it).
+  static constexpr uint64_t kMaxHeaderBytes = 100ull << 20;
+
   Checkpoint() = default;
   Checkpoint(const Checkpoint&) = delete;
   Checkpoint& operator=(const Checkpoint&) = delete;
@@ -109,6 +112,9 @@ class Checkpoint {
     uint64_t hlen = 0;
     for (int i = 7; i >= 0; --i) hlen = hlen << 8 | len8[i];
     if (hlen > size_ - 8) fatal("safetensors: header length beyond the end of the file");
+    // the header is read whole before it is parsed: refuse a declared length
+    // beyond what any writer produces before allocating it
+    if (hlen > kMaxHeaderBytes) fatal("safetensors: header length above the 100 MiB limit");
     std::string text((size_t)hlen, '\0');
     if (hlen && fread(&text[0], 1, (size_t)hlen, fp_) != hlen)
       fatal("safetensors: short read of the header");

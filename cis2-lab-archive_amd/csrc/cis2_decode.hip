@@ -406,7 +406,14 @@ __device__ __forceinline__ void prefetch_rows_async(const float* W, uint32_t R, 
   }
 }
 // s_waitcnt vmcnt(0) (expcnt, lgkmcnt fields at their maxima: no wait).
-__device__ __forceinline__ void wait_vm0() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+// The builtin is a side effect without a memory operand, so the empty asm
+// statements pin the LDS accesses of the caller (the reads of rows that
+// this wave's global_load_lds copies filled) after it.
+__device__ __forceinline__ void wait_vm0() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0x0F70);
+  asm volatile("" ::: "memory");
+}
 
 // Workgroup barrier for LDS data only: waits for this wave's LDS
 // operations, not for its outstanding global loads (HIP's __syncthreads
@@ -1649,7 +1656,10 @@ __device__ __forceinline__ void run_att_score(const DecodeArgs& a, uint32_t l, u
   lf* misc = tmp + (size_t)(ng + 1) * hd;
   // kv head kvh's K rows as a buffer: one per-thread offset (the position)
   // and a scalar offset per dim keep the column's loads off the vector
-  // registers' address pairs (reads past the rows return 0)
+  // registers' address pairs.  With stride 0 the hardware range check
+  // covers the per-thread offset only, not the per-dim scalar one, so the
+  // loads stay in bounds by their guards: jt < pos < max_pos, d0 + i < hd,
+  // and the host's hd * max_pos * 4 <= 2^31 - 1 check.
   const __amdgpu_buffer_rsrc_t kbuf = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(a.kc0 + (size_t)l * a.cache_stride + (size_t)kvh * hd * a.max_pos), (short)0,
       (int)(hd * a.max_pos * 4), 0x00020000);

@@ -340,7 +340,8 @@ int check_err_flag(cis2_ctx* c) {
   uint32_t e = 0;
   HIPCHK(c, hipMemcpy(&e, c->d_err, 4, hipMemcpyDeviceToHost), "error flag");
   if (e) {
-    (void)hipMemset(c->d_err, 0, 4);
+    (void)hipMemsetAsync(c->d_err, 0, 4, c->st);
+    (void)hipStreamSynchronize(c->st);
     if (e & 2u)
       return fail(c, CIS2_E_DEVICE,
                   "persistent decode kernel: a phase wait hit its spin cap "
@@ -884,11 +885,11 @@ int cis2_ctx_create(const cis2_config* cfg, cis2_ctx** out) {
   c->allocs.push_back(tp);
   c->d_tok = static_cast<uint32_t*>(tp);
   c->d_err = c->d_tok + 2;
-  (void)hipMemset(tp, 0, 16);
+  (void)hipMemsetAsync(tp, 0, 16, c->st);
   if (hipMalloc(&tp, 16) != hipSuccess) { cis2_ctx_destroy(c); return CIS2_E_OOM; }
   c->allocs.push_back(tp);
   c->d_tok2 = static_cast<uint32_t*>(tp);
-  (void)hipMemset(tp, 0, 16);
+  (void)hipMemsetAsync(tp, 0, 16, c->st);
   if (!(c->logits2 = dalloc(c, V))) { cis2_ctx_destroy(c); return CIS2_E_OOM; }
   if (hipMalloc(&tp, (size_t)f.max_pos * sizeof(uint32_t)) != hipSuccess) {
     cis2_ctx_destroy(c);
@@ -896,7 +897,7 @@ int cis2_ctx_create(const cis2_config* cfg, cis2_ctx** out) {
   }
   c->allocs.push_back(tp);
   c->d_prompt = static_cast<uint32_t*>(tp);
-  (void)hipMemset(c->kv, 0, (size_t)f.max_seqs * f.n_layers * 2 * c->kvd * f.max_pos * sizeof(float));
+  (void)hipMemsetAsync(c->kv, 0, (size_t)f.max_seqs * f.n_layers * 2 * c->kvd * f.max_pos * sizeof(float), c->st);
   // Pinned inv_freq and rotation table; theta narrowed to f32 once
   // (code/cis2-fp/src/main.rs:849-858).
   if (launch_rope_table((float)f.rope_theta, f.head_dim, f.max_pos, c->inv_freq, c->rope_cs,
@@ -1026,8 +1027,8 @@ int cis2_ctx_create(const cis2_config* cfg, cis2_ctx** out) {
     }
     c->allocs.push_back(p);
     c->counters = static_cast<uint32_t*>(p);
-    (void)hipMemset(c->counters, 0, cnt_n * 4);
-    (void)hipMemset(c->act, 0, act_f * sizeof(float));  // tag 0: never a launch epoch
+    (void)hipMemsetAsync(c->counters, 0, cnt_n * 4, c->st);
+    (void)hipMemsetAsync(c->act, 0, act_f * sizeof(float), c->st);  // tag 0: never a launch epoch
     if (hipMalloc(&p, ((size_t)2 * a.nl + 4) * 4) != hipSuccess) {
       cis2_ctx_destroy(c);
       return CIS2_E_OOM;
@@ -1050,7 +1051,7 @@ int cis2_ctx_create(const cis2_config* cfg, cis2_ctx** out) {
         return CIS2_E_OOM;
       }
       c->allocs.push_back(p);
-      (void)hipMemset(p, 0, nw * 8);  // tag 0: never a launch epoch
+      (void)hipMemsetAsync(p, 0, nw * 8, c->st);  // tag 0: never a launch epoch
       a.scw = static_cast<uint64_t*>(p);
     }
     if (const char* tl = getenv("CIS2_TIMELINE")) {
@@ -1058,7 +1059,7 @@ int cis2_ctx_create(const cis2_config* cfg, cis2_ctx** out) {
       if (hipMalloc(&p, n * 8) == hipSuccess) {
         c->allocs.push_back(p);
         c->tline = static_cast<uint64_t*>(p);
-        (void)hipMemset(c->tline, 0, n * 8);
+        (void)hipMemsetAsync(c->tline, 0, n * 8, c->st);
         c->tline_file = fopen(tl, "wb");
         // the task table beside it (<file>.tasks: nwg rows of kMaxTasks
         // phase << 12 | task words, 0xFFFF ends a row)
@@ -1068,6 +1069,12 @@ int cis2_ctx_create(const cis2_config* cfg, cis2_ctx** out) {
         }
       }
     }
+  }
+  // every zero fill above runs on the context's stream (which does not
+  // synchronize with the null stream): complete before the first launch
+  if (hipStreamSynchronize(c->st) != hipSuccess) {
+    cis2_ctx_destroy(c);
+    return CIS2_E_DEVICE;
   }
   build_registry(c);
   *out = c;
@@ -1305,6 +1312,10 @@ int cis2_sample_logits_noalloc(cis2_ctx* c, const float* logits_dev, uint32_t n,
   const uint32_t V = c->cfg.vocab;
   if (V > kNoAllocMaxVocab)
     return fail(c, CIS2_E_ARG, "vocabulary exceeds the no-allocation scratch (262144 entries)");
+  std::mutex* mu = sample_scratch_lock(c->dev);
+  if (!mu) return fail(c, CIS2_E_DEVICE, "device index out of range");
+  // one draw at a time per GPU: the scratch is shared by every context there
+  std::lock_guard<std::mutex> hold(*mu);
   SampleBufs b;
   uint32_t* err = nullptr;
   HIPCHK(c, sample_scratch_bufs(c->dev, V, &b, &err), "sampler scratch");

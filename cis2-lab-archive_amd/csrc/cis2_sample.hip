@@ -419,6 +419,7 @@ static_assert(kScratchWords * 8 == kNoAllocScratchBytes, "scratch size as declar
 constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mu;
 void* g_scratch_dev[kMaxDevices];  // this GPU's address of `scratch`, or null
+std::mutex g_scratch_use[kMaxDevices];  // held by a draw for its whole use of the scratch
 }  // namespace
 
 static __device__ __align__(256) uint64_t scratch[kScratchWords];
@@ -436,6 +437,10 @@ hipError_t sample_scratch_init() {
   if (!ptr) return hipErrorInvalidSymbol;
   g_scratch_dev[dev] = ptr;
   return hipSuccess;
+}
+
+std::mutex* sample_scratch_lock(int dev) {
+  return dev >= 0 && dev < kMaxDevices ? &g_scratch_use[dev] : nullptr;
 }
 
 hipError_t sample_scratch_bufs(int dev, uint32_t V, SampleBufs* b, uint32_t** err) {

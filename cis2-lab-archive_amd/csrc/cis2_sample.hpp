@@ -5,6 +5,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <mutex>
+
 namespace cis2 {
 
 struct SampleParams {
@@ -46,6 +48,10 @@ constexpr size_t kNoAllocScratchBytes =
 // Resolves the current GPU's copy of the scratch array (once per device,
 // with that device current).  Called at context creation.
 hipError_t sample_scratch_init();
+// The lock a draw holds from clearing the error flag until its results are
+// back, so that draws from several host threads on one GPU take turns with
+// the shared scratch (null for a device index out of range).
+std::mutex* sample_scratch_lock(int dev);
 // The sampler buffers and the error-flag word carved out of GPU dev's
 // scratch for a vocabulary of V (<= kNoAllocMaxVocab).  No allocation.
 hipError_t sample_scratch_bufs(int dev, uint32_t V, SampleBufs* b, uint32_t** err);

@@ -184,9 +184,11 @@ int cis2_sample_logits(cis2_ctx *ctx, const float *logits_host, uint32_t n,
  * nothing: its scratch is one static array per GPU of 5,244,992 bytes
  * (two sort-key arrays, the f32 terms, candidates, flags), which serves
  * vocabularies up to 262,144 (larger: CIS2_E_ARG) and is held until the
- * process ends.  Every call on a GPU shares that GPU's array, so calls that
- * overlap on one GPU (two contexts on two host threads) race.  Blocks until
- * the draws are done; a NaN logit gives CIS2_E_NUMERIC. */
+ * process ends.  Every call on a GPU shares that GPU's array: a call holds
+ * a per-GPU lock from clearing its error flag until its results are back,
+ * so calls from several host threads on one GPU take turns (each process
+ * has its own array).  Blocks until the draws are done; a NaN logit gives
+ * CIS2_E_NUMERIC. */
 int cis2_sample_logits_noalloc(cis2_ctx *ctx, const float *logits_dev, uint32_t n,
                                const uint32_t *steps, uint32_t *ids_dev, uint32_t *nkeep_dev);
 

@@ -168,3 +168,23 @@ def test_reader_under_sanitizers(model_dir, tmp_path):
             assert r.returncode == 2 and "FATAL:" in r.stderr, what
         else:
             assert r.returncode == 0, what
+
+
+def test_cli_refuses_oversized_header_before_reading_it(model_dir, tmp_path):
+    """A (sparse) file whose header-length field claims 150 MiB, which the
+    file does hold: refused by the 100 MiB cap before the header is
+    allocated or read, not after a 150 MiB allocation."""
+    if not os.path.exists(CLI):
+        pytest.skip("cis2_host not built")
+    w = tmp_path / "w"
+    w.mkdir()
+    for f in ("config.json", "tokenizer.json"):
+        shutil.copy(model_dir / f, w / f)
+    hlen = 150 << 20
+    with open(w / "model.safetensors", "wb") as f:
+        f.write(struct.pack("<Q", hlen) + b"{")
+        f.truncate(8 + hlen + 64)  # sparse: no disk blocks behind the claim
+    r = subprocess.run([CLI, "--weights-dir", str(w), "--ids", str(model_dir / "ids.txt"),
+                        "--gen-toks", "1"], capture_output=True, text=True, timeout=30)
+    assert r.returncode == 2, r.stderr[-300:]
+    assert "FATAL: safetensors: header length above the 100 MiB limit" in r.stderr

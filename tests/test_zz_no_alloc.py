@@ -150,3 +150,42 @@ def test_noalloc_error_paths():
         assert e.value.code == -1
     finally:
         mb.close()
+
+
+def test_noalloc_two_threads_take_turns():
+    """Two contexts on one GPU, each driven by its own host thread, draw
+    through the shared scratch at the same time; the per-GPU lock makes them
+    take turns, so every draw equals its context's allocating draw."""
+    import threading
+
+    rng = np.random.default_rng(99)
+    jobs = []
+    for V, seed in ((49152, 11), (30000, 12)):
+        spec = tiny_with_vocab(V)
+        m = Cis2Model(spec, artifacts.Weights(spec, 5), max_pos=8)
+        m.set_sampling(seed, 0.8, 40, 0.95)
+        rows = logit_rows(rng, V, 3)
+        steps = [int(x) for x in rng.integers(0, 2**32, 3)]
+        jobs.append((m, rows, steps, m.sample_logits(rows, steps)))
+    errors = []
+
+    def worker(m, rows, steps, want):
+        try:
+            for _ in range(20):
+                ids, nk = draw_noalloc(m, rows, steps)
+                assert list(ids) == [int(x) for x in want[0]]
+                assert list(nk) == [int(x) for x in want[1]]
+        except BaseException as e:  # reported by the main thread
+            errors.append(e)
+
+    threads = [threading.Thread(target=worker, args=j) for j in jobs]
+    try:
+        for t in threads:
+            t.start()
+        for t in threads:
+            t.join(timeout=120)
+        assert not any(t.is_alive() for t in threads), "a drawing thread did not finish"
+        assert not errors, errors[0]
+    finally:
+        for m, *_ in jobs:
+            m.close()
