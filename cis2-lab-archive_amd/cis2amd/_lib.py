@@ -80,6 +80,7 @@ SIGNATURES = {
     "cis2_profile": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int]),
     "cis2_profile_read": (ctypes.c_int, [ctypes.c_void_p, c_u64p, ctypes.POINTER(ctypes.c_double),
                                          c_u32p, ctypes.c_uint64]),
+    "cis2_recoveries": (ctypes.c_int, [ctypes.c_void_p, c_u32p]),
     "cis2_gemv_plan_create": (ctypes.c_int, [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32,
                                              c_fp, ctypes.POINTER(ctypes.c_void_p)]),
     "cis2_gemv_plan_run": (ctypes.c_int, [ctypes.c_void_p, c_fp, c_fp]),

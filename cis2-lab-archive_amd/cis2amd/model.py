@@ -83,6 +83,13 @@ class Cis2Model:
         k = int(n[0])
         return k, float(ms[0]), pos[:min(k, cap)].copy()
 
+    def recoveries(self):
+        """Steps whose persistent launch hit its bounded wait and were
+        recomputed on the per-op path (cis2_recoveries)."""
+        n = np.zeros(1, dtype=np.uint32)
+        check(_lib.lib().cis2_recoveries(self.ctx, _ptr(n, _lib.c_u32p)), self.ctx)
+        return int(n[0])
+
     def forward_token(self, pos, tok, seq=0):
         """One forward pass; returns (logits float32[vocab], argmax id)."""
         V = self.spec.vocab

@@ -57,7 +57,6 @@ __device__ __forceinline__ AS_GLB float* GW(float* p) { return (AS_GLB float*)p;
 __device__ __forceinline__ AS_GLB uint32_t* GU(uint32_t* p) { return (AS_GLB uint32_t*)p; }
 
 constexpr uint32_t kThreads = 256;
-constexpr uint32_t kSpinCap = 1u << 24;  // ~0.5 s of s_sleep(1)
 
 enum { P_QKV = kPhaseQKV, P_ATT = kPhaseATT, P_O = kPhaseO, P_GU = kPhaseGU, P_D = kPhaseD,
        P_LM = 5 };
@@ -201,7 +200,7 @@ __device__ __forceinline__ void stamp(const DecodeArgs& a, uint32_t l, uint32_t 
 // vectors are gathered in slices.
 template <class F>
 __device__ __forceinline__ void gather(lf* dst, uint32_t n, uint32_t epoch, uint32_t* err,
-                                       F addr) {
+                                       uint32_t cap, F addr) {
   constexpr int M = 12;
   for (uint32_t base = 0; base < n; base += M * kThreads) {
     u64 w[M];
@@ -222,7 +221,7 @@ __device__ __forceinline__ void gather(lf* dst, uint32_t n, uint32_t epoch, uint
       __builtin_amdgcn_s_sleep(1);
       ++spins;
       if ((spins & 255u) == 0 && ld_ag(err) != 0u) break;  // another task failed
-      if (spins > kSpinCap) {
+      if (spins > cap) {  // a.spin_cap: about 0.5 s by default
         raise_err(err, 2u);
         break;
       }
@@ -238,7 +237,7 @@ __device__ __forceinline__ void gather(lf* dst, uint32_t n, uint32_t epoch, uint
 
 __device__ __forceinline__ void gather_vec(lf* dst, const gw* src, uint32_t n,
                                            const DecodeArgs& a) {
-  gather(dst, n, a.epoch, a.err, [=](uint32_t i) { return src + i; });
+  gather(dst, n, a.epoch, a.err, a.spin_cap, [=](uint32_t i) { return src + i; });
 }
 
 // Copies n4 f4 (element i from src(i), global memory) to dst[i] with up to
@@ -1163,7 +1162,7 @@ __device__ __forceinline__ void att_head_inputs(const DecodeArgs& a, uint32_t l,
     rc = cs[2 * i];
     rsn = cs[2 * i + 1];
   }
-  gather(qv, 3 * hd, a.epoch, a.err, [=](uint32_t i) {
+  gather(qv, 3 * hd, a.epoch, a.err, a.spin_cap, [=](uint32_t i) {
     const uint32_t seg = i >= hd ? (i >= 2 * hd ? 2u : 1u) : 0u, d = i - seg * hd;
     return seg == 0 ? ac.q + (size_t)h * hd + d
                     : (seg == 1 ? ac.k : ac.v) + (size_t)kvh * hd + d;
@@ -1505,7 +1504,7 @@ __device__ __forceinline__ void att_group_inputs(const DecodeArgs& a, uint32_t l
   float csv = 0.0f;
   if (threadIdx.x < hd) csv = G(a.rope_cs)[(size_t)a.pos * hd + threadIdx.x];
   const uint32_t nq_w = ng * hd;
-  gather(qv, (ng + 2) * hd, a.epoch, a.err, [=](uint32_t i) {
+  gather(qv, (ng + 2) * hd, a.epoch, a.err, a.spin_cap, [=](uint32_t i) {
     return i < nq_w ? ac.q + (size_t)kvh * nq_w + i
                     : (i < nq_w + hd ? ac.k : ac.v) + (size_t)kvh * hd + (i - nq_w) % hd;
   });
@@ -1768,10 +1767,10 @@ __device__ __forceinline__ void run_att_mix(const DecodeArgs& a, uint32_t l, uin
     if (nt > 0) copy_v_rows(tile(0), vrows, a.max_pos, nd, 0, tile_n(0), TS);
     if (nt > 1) copy_v_rows(tile(1), vrows, a.max_pos, nd, TP, tile_n(1), TS);
   }
-  gather(ss, len, a.epoch, a.err, [=](uint32_t i) {
+  gather(ss, len, a.epoch, a.err, a.spin_cap, [=](uint32_t i) {
     return (const gw*)a.scw + ((size_t)l * a.nh + h) * a.max_pos + i;
   });
-  gather(vv, nd, a.epoch, a.err, [=](uint32_t i) { return ac.v + (size_t)kvh * hd + d0 + i; });
+  gather(vv, nd, a.epoch, a.err, a.spin_cap, [=](uint32_t i) { return ac.v + (size_t)kvh * hd + d0 + i; });
   stamp(a, l, P_ATT, t, 1);
   __syncthreads();
   softmax_lds<TR>(ss, len, part, misc, red);
@@ -1823,7 +1822,7 @@ __device__ __forceinline__ void run_o(const DecodeArgs& a, uint32_t l, uint32_t 
   } else {
     const gw* hin = act_of(a, l - 1).hout + r0;
     const gw* att = ac.att;
-    gather(x, qd + nr, a.epoch, a.err,
+    gather(x, qd + nr, a.epoch, a.err, a.spin_cap,
            [=](uint32_t i) { return i < qd ? att + i : hin + (i - qd); });
   }
   stamp(a, l, P_O, t, 1);
@@ -1878,7 +1877,7 @@ __device__ __forceinline__ void run_d(const DecodeArgs& a, uint32_t l, uint32_t 
   stamp(a, l, P_D, t, 0);
   const gw* h1 = ac.h1 + r0;
   const gw* hid = ac.hid;
-  gather(x, I + nr, a.epoch, a.err,
+  gather(x, I + nr, a.epoch, a.err, a.spin_cap,
          [=](uint32_t i) { return i < I ? hid + i : h1 + (i - I); });
   stamp(a, l, P_D, t, 1);
   // the 1536- to 3072-long chain keeps 12 reads in flight (8 elsewhere:

@@ -22,6 +22,8 @@ inline uint32_t rows_per_block(uint32_t K, uint32_t cap = 64) {
   return r > cap ? cap : (r < 1 ? 1 : r);
 }
 
+constexpr uint32_t kDefaultSpinCap = 1u << 24;
+
 struct DecodeArgs {
   const LayerW* layers;  // device array [L]
   const float* embed;    // row-major [V][H]
@@ -37,6 +39,10 @@ struct DecodeArgs {
   uint32_t* tok_in;      // token of this position
   uint32_t* tok_out;     // argmax written here (may alias tok_in)
   uint32_t* err;
+  // Sleeps a phase wait may take before it raises error bit 2 and gives up
+  // (kDefaultSpinCap, about 0.5 s; a test can set a tiny cap to make the
+  // waits give up while every workgroup still exits normally).
+  uint32_t spin_cap;
   // Optional per-task timestamps (s_memrealtime, 100 MHz), null when off:
   // [(l * 6 + phase) * 64 + task] * 4 words: wait start, wait end, done,
   // and a mid-point (after RMSNorm for QKV/GU, after the GEMV for O/D,

@@ -8,10 +8,14 @@
 #include "cis2_sample.hpp"
 #include "cis2_sha256.hpp"
 
+#include <errno.h>
+#include <fcntl.h>
 #include <hip/hip_runtime.h>
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
+#include <sys/file.h>
+#include <unistd.h>
 
 #include <algorithm>
 #include <map>
@@ -139,6 +143,17 @@ struct cis2_ctx {
   uint32_t* cand = nullptr;
   uint32_t epoch = 0, lm_epoch = 0;
   DecodeArgs dargs;
+  // Persistent launches of this GPU are taken one session at a time across
+  // processes: an exclusive flock on <dir>/cis2amd-<pci bus id>.lock, held
+  // from the first persistent launch of a session until its end
+  // (CIS2_DECODE_LOCK=0: never taken; CIS2_LOCK_DIR: the directory, /tmp by
+  // default).  -1: not held.
+  int lock_fd = -1;
+  bool lock_off = false;
+  std::string lock_path;
+  // steps whose persistent launch hit the spin cap and were recomputed on the
+  // per-op path (cis2_recoveries)
+  uint32_t recoveries = 0;
   uint64_t* tline = nullptr;  // CIS2_TIMELINE=<file>: per-task timestamps of every launch
   FILE* tline_file = nullptr;
   std::vector<uint16_t> wg_tasks;  // [nwg][kMaxTasks] task table of the persistent kernel
@@ -349,6 +364,42 @@ int check_err_flag(cis2_ctx* c) {
     if (e & 0x100u) return fail(c, CIS2_E_NUMERIC, "NaN among logits / temperature in a sampled draw");
     return fail(c, CIS2_E_RANGE, "token id out of range on the device");
   }
+  return CIS2_OK;
+}
+
+// The GPU's persistent-decode lock (see cis2_ctx::lock_fd): taken before
+// the first persistent launch of a session, kept until decode_unlock.  A
+// second process (or context) decoding on the same GPU waits here instead
+// of launching a grid that would share the CUs with this one (its
+// workgroups could then wait on each other until the spin cap).  A lock
+// that cannot be taken (unwritable directory) is skipped: the spin-cap
+// recovery still keeps such runs correct.
+static void decode_lock(cis2_ctx* c) {
+  if (c->lock_off || c->lock_fd >= 0) return;
+  const int fd = open(c->lock_path.c_str(), O_RDWR | O_CREAT | O_CLOEXEC, 0666);
+  if (fd < 0) return;
+  while (flock(fd, LOCK_EX) != 0) {
+    if (errno != EINTR) {
+      close(fd);
+      return;
+    }
+  }
+  c->lock_fd = fd;
+}
+static void decode_unlock(cis2_ctx* c) {
+  if (c->lock_fd < 0) return;
+  close(c->lock_fd);
+  c->lock_fd = -1;
+}
+
+// Waits for every queued launch and copy, then clears the device error
+// word; *bits receives what it held.
+static int drain_and_clear_err(cis2_ctx* c, uint32_t* bits) {
+  HIPCHK(c, hipStreamSynchronize(c->st), "drain");
+  if (c->cs) HIPCHK(c, hipStreamSynchronize(c->cs), "drain copies");
+  HIPCHK(c, hipMemcpy(bits, c->d_err, 4, hipMemcpyDeviceToHost), "error flag");
+  HIPCHK(c, hipMemsetAsync(c->d_err, 0, 4, c->st), "error flag clear");
+  HIPCHK(c, hipStreamSynchronize(c->st), "error flag clear");
   return CIS2_OK;
 }
 
@@ -802,6 +853,8 @@ const char* cis2_last_error(const cis2_ctx* ctx) { return ctx ? ctx->err.c_str()
 void cis2_ctx_destroy(cis2_ctx* c) {
   if (!c) return;
   if (c->st) (void)hipStreamSynchronize(c->st);
+  if (c->cs) (void)hipStreamSynchronize(c->cs);
+  if (c->lock_fd >= 0) close(c->lock_fd);  // closing the descriptor releases the flock
   for (void* p : c->allocs) (void)hipFree(p);
   for (void* p : c->rows.mem) (void)hipFree(p);
   for (void* p : c->rows.lmem) (void)hipFree(p);
@@ -941,6 +994,17 @@ int cis2_ctx_create(const cis2_config* cfg, cis2_ctx** out) {
     c->ncu = (uint32_t)ncu;
     const char* pe = getenv("CIS2_PATH");
     c->force_ops = pe && !strcmp(pe, "ops");
+    const char* pl = getenv("CIS2_DECODE_LOCK");
+    c->lock_off = pl && !strcmp(pl, "0");
+    {
+      char bus[64] = {0};
+      if (hipDeviceGetPCIBusId(bus, (int)sizeof bus - 1, dev) != hipSuccess || !bus[0])
+        snprintf(bus, sizeof bus, "dev%d", dev);
+      for (char* q = bus; *q; ++q)
+        if (*q == ':' || *q == '/' || *q == '.') *q = '_';
+      const char* ld = getenv("CIS2_LOCK_DIR");
+      c->lock_path = std::string(ld && *ld ? ld : "/tmp") + "/cis2amd-" + bus + ".lock";
+    }
     const char* pf = getenv("CIS2_PREFILL");
     c->seq_prefill = pf && !strcmp(pf, "seq");
     DecodeArgs& a = c->dargs;
@@ -986,6 +1050,11 @@ int cis2_ctx_create(const cis2_config* cfg, cis2_ctx** out) {
       a.rope_cs = c->rope_cs;
       a.logits = c->logits;
       a.err = c->d_err;
+      a.spin_cap = kDefaultSpinCap;
+      if (const char* sc = getenv("CIS2_SPIN_CAP")) {
+        const unsigned long v = strtoul(sc, nullptr, 10);
+        if (v >= 1 && v <= kDefaultSpinCap) a.spin_cap = (uint32_t)v;
+      }
       // attention split over score and mix tasks when a head's K/V rows at
       // max_pos do not fit one workgroup (CIS2_ATT=split / one: forced)
       const char* pa = getenv("CIS2_ATT");
@@ -1155,6 +1224,12 @@ int cis2_profile(cis2_ctx* c, int on) {
   return CIS2_OK;
 }
 
+int cis2_recoveries(cis2_ctx* c, uint32_t* count) {
+  if (!c || !count) return CIS2_E_ARG;
+  *count = c->recoveries;
+  return CIS2_OK;
+}
+
 int cis2_profile_read(cis2_ctx* c, uint64_t* launches, double* total_ms, uint32_t* positions,
                       uint64_t cap) {
   if (!c || !launches || !total_ms) return CIS2_E_ARG;
@@ -1201,17 +1276,32 @@ int cis2_forward(cis2_ctx* c, uint32_t n, const uint32_t* seq, const uint32_t* p
              "argmax copy");
     return check_err_flag(c);
   }
+  const bool held = c->lock_fd >= 0;  // a decode session of this context holds the lock
   for (uint32_t i = 0; i < n; ++i) {
     if (seq[i] >= c->cfg.max_seqs) return fail(c, CIS2_E_ARG, "sequence index out of range");
     if (pos[i] >= c->cfg.max_pos) return fail(c, CIS2_E_RANGE, "position beyond max_pos");
     if (tok[i] >= c->cfg.vocab) return fail(c, CIS2_E_RANGE, "token id >= vocab");
     HIPCHK(c, hipMemcpyAsync(c->d_tok, &tok[i], 4, hipMemcpyHostToDevice, c->st), "token");
-    if (use_fast(c)) {
+    bool ops = !use_fast(c);
+    if (!ops) {
+      decode_lock(c);
       r = forward_fast(c, seq[i], pos[i], c->d_tok, true);
       if (r) return r;
       HIPCHK(c, hipMemcpyAsync(c->d_tok + 1, c->d_tok, 4, hipMemcpyDeviceToDevice, c->st),
              "argmax copy");
-    } else {
+      // a persistent launch that hit the spin cap: this row again on the
+      // per-op path (it rewrites the position's K/V rows in every layer)
+      uint32_t bits = 0;
+      r = drain_and_clear_err(c, &bits);
+      if (r) return r;
+      if (bits & ~2u) HIPCHK(c, hipMemcpy(c->d_err, &bits, 4, hipMemcpyHostToDevice), "error flag");
+      if (bits & 2u) {
+        c->recoveries++;
+        ops = true;
+        HIPCHK(c, hipMemcpyAsync(c->d_tok, &tok[i], 4, hipMemcpyHostToDevice, c->st), "token");
+      }
+    }
+    if (ops) {
       r = forward_one(c, seq[i], pos[i], c->d_tok, true);
       if (r) return r;
       if (argmax_out) LAUNCH(launch_argmax(c->logits, c->cfg.vocab, c->d_tok + 1, c->st), "argmax");
@@ -1224,6 +1314,7 @@ int cis2_forward(cis2_ctx* c, uint32_t n, const uint32_t* seq, const uint32_t* p
     if (argmax_out)
       HIPCHK(c, hipMemcpy(&argmax_out[i], c->d_tok + 1, 4, hipMemcpyDeviceToHost), "argmax copy");
   }
+  if (!held) decode_unlock(c);
   return check_err_flag(c);
 }
 
@@ -1338,12 +1429,18 @@ int cis2_sample_logits_noalloc(cis2_ctx* c, const float* logits_dev, uint32_t n,
 // host enqueues step s, then folds step s - (kRing-1) while the GPU runs:
 // argmax and the next token stay on the device, the logits stream to a
 // pinned ring slot with an event per slot.
+// Internal return of fold_step: the step's logits came from a persistent
+// launch that hit the spin cap (recover_step redoes it).
+constexpr int kNeedsRecovery = 1000;
+
 static int fold_step(cis2_ctx* c) {
   Session& S = c->sess;
   const uint32_t V = c->cfg.vocab;
   const uint32_t step = S.folded;
   const int slot = step % kRing;
   HIPCHK(c, hipEventSynchronize(c->ring_ev[slot]), "ring wait");
+  // the error word as it stood after the pass that produced these logits
+  if (S.fast && (c->ring_tok[slot * 2 + 1] & 2u)) return kNeedsRecovery;
   const float* lg = c->ring + (size_t)slot * V;
   const uint32_t nid = c->ring_tok[slot * 2];
   S.w.update(lg, (size_t)V * sizeof(float));
@@ -1352,6 +1449,35 @@ static int fold_step(cis2_ctx* c) {
   S.ids[S.n_prompt + step] = nid;
   S.folded++;
   return CIS2_OK;
+}
+
+// Step `step`'s logits came from a persistent launch that hit the spin cap
+// (its grid was not all resident at once: another process's work held
+// CUs).  Every later launch of the session read a token that launch never
+// wrote, so all of them are discarded: once the queues are drained and the
+// error word cleared, the position before `step` is recomputed on the
+// per-op path (same arithmetic, so the same bits; it rewrites that
+// position's K/V rows in every layer), and the session continues from
+// `step` on the per-op path, which recomputes every later position as it
+// re-enqueues it.
+static int recover_step(cis2_ctx* c, uint32_t step) {
+  Session& S = c->sess;
+  uint32_t bits = 0;
+  int r = drain_and_clear_err(c, &bits);
+  if (r) return r;
+  if (bits & ~2u)
+    return fail(c, (bits & 0x100u) ? CIS2_E_NUMERIC : CIS2_E_RANGE,
+                "device error during a recovered decode step");
+  S.fast = false;
+  c->recoveries++;
+  const uint32_t pos = S.n_prompt + step - 1;  // step >= 1: step 0 comes from the prefill
+  HIPCHK(c, hipMemcpyAsync(c->d_tok, &S.ids[pos], 4, hipMemcpyHostToDevice, c->st), "token");
+  r = forward_one(c, S.seq, pos, c->d_tok, true);
+  if (r) return r;
+  HIPCHK(c, hipStreamSynchronize(c->st), "recovery sync");
+  S.enqueued = step;
+  S.folded = step;
+  return check_err_flag(c);
 }
 
 int cis2_decode_begin(cis2_ctx* c, uint32_t seq, const uint32_t* prompt, uint32_t n_prompt,
@@ -1366,6 +1492,7 @@ int cis2_decode_begin(cis2_ctx* c, uint32_t seq, const uint32_t* prompt, uint32_
   if (r) return r;
   r = cis2_reset_seq(c, seq);
   if (r) return r;
+  decode_unlock(c);  // a session left without cis2_decode_end
   Session& S = c->sess;
   S = Session();
   S.seq = seq;
@@ -1383,6 +1510,7 @@ int cis2_decode_begin(cis2_ctx* c, uint32_t seq, const uint32_t* prompt, uint32_
   HIPCHK(c, hipMemcpy(c->d_prompt, prompt, (size_t)n_prompt * 4, hipMemcpyHostToDevice),
          "prompt upload");
   S.fast = use_fast(c);
+  if (S.fast) decode_lock(c);
   if (n_prompt > 1 && !c->trace && !c->seq_prefill) {
     // all prompt positions in one row-batched pass (bit-identical to the
     // position-by-position prefill); the last row's logits and argmax go
@@ -1398,10 +1526,24 @@ int cis2_decode_begin(cis2_ctx* c, uint32_t seq, const uint32_t* prompt, uint32_
     HIPCHK(c, hipMemcpyAsync(c->d_tok, c->rows.arg, 4, hipMemcpyDeviceToDevice, c->st),
            "prefill argmax");
   } else {
-    for (uint32_t p = 0; p < n_prompt; ++p) {
-      r = S.fast ? forward_fast(c, seq, p, c->d_prompt + p, p + 1 == n_prompt)
-                 : forward_one(c, seq, p, c->d_prompt + p, p + 1 == n_prompt);
+    for (int pass = 0; pass < 2; ++pass) {
+      for (uint32_t p = 0; p < n_prompt; ++p) {
+        r = S.fast ? forward_fast(c, seq, p, c->d_prompt + p, p + 1 == n_prompt)
+                   : forward_one(c, seq, p, c->d_prompt + p, p + 1 == n_prompt);
+        if (r) return r;
+      }
+      if (!S.fast) break;
+      // a persistent prefill launch that hit the spin cap: the whole prompt
+      // again on the per-op path (each position rewrites its K/V rows)
+      uint32_t bits = 0;
+      r = drain_and_clear_err(c, &bits);
       if (r) return r;
+      if (!(bits & 2u)) {
+        if (bits) HIPCHK(c, hipMemcpy(c->d_err, &bits, 4, hipMemcpyHostToDevice), "error flag");
+        break;
+      }
+      S.fast = false;
+      c->recoveries++;
     }
   }
   HIPCHK(c, hipStreamSynchronize(c->st), "prefill sync");
@@ -1415,58 +1557,93 @@ int cis2_decode_steps(cis2_ctx* c, uint32_t n) {
   if (!S.active) return fail(c, CIS2_E_ARG, "no decode session");
   if ((uint64_t)S.enqueued + n > S.max_steps) return fail(c, CIS2_E_RANGE, "steps beyond max_steps");
   const uint32_t V = c->cfg.vocab;
+  const uint32_t target = S.enqueued + n;
   hipStream_t s = c->st;
-  int r;
-  // Persistent-kernel steps alternate between two logit buffers and two
-  // token slots: step t's logits and token (set t % 2) are copied to the
-  // host ring on the copy stream while pass t (which writes set (t+1) % 2)
-  // runs; pass t waits only for the copy of step t-1, whose set it
-  // overwrites.  The per-op path keeps one set and copies in stream order.
-  const bool alt = S.fast && !c->trace;
-  if (alt && !c->cs)
+  int r = CIS2_OK;
+  if (S.fast && !c->trace && !c->cs)
     HIPCHK(c, hipStreamCreateWithFlags(&c->cs, hipStreamNonBlocking), "copy stream");
-  for (uint32_t i = 0; i < n; ++i) {
-    const uint32_t step = S.enqueued;
-    const int slot = step % kRing;
-    if (step >= S.folded + kRing) {  // slot reuse: fold what it held first
-      r = fold_step(c);
-      if (r) return r;
-    }
-    const bool odd = alt && (step & 1);
-    float* lcur = odd ? c->logits2 : c->logits;
-    float* lnext = alt ? (odd ? c->logits : c->logits2) : c->logits;
-    uint32_t* tcur = odd ? c->d_tok2 : c->d_tok;
-    uint32_t* tnext = alt ? (odd ? c->d_tok : c->d_tok2) : c->d_tok;
-    // the persistent kernel already left the argmax of these logits in the
-    // token slot; a sampled draw replaces it (generation step = this step)
-    if (c->samp_on)
-      LAUNCH(launch_sample(lcur, V, c->samp, step, c->sbuf, tcur, c->d_err, s), "sample");
-    else if (!S.fast)
-      LAUNCH(launch_argmax(c->logits, V, c->d_tok, s), "argmax");
-    hipStream_t cp = alt ? c->cs : s;
-    if (alt) {
-      HIPCHK(c, hipEventRecord(c->ring_ready[slot], s), "step event");
-      HIPCHK(c, hipStreamWaitEvent(cp, c->ring_ready[slot], 0), "copy wait");
-    }
-    HIPCHK(c, hipMemcpyAsync(c->ring + (size_t)slot * V, lcur, (size_t)V * sizeof(float),
-                             hipMemcpyDeviceToHost, cp),
-           "logits d2h");
-    HIPCHK(c, hipMemcpyAsync(c->ring_tok + slot * 2, tcur, 4, hipMemcpyDeviceToHost, cp),
-           "token d2h");
-    HIPCHK(c, hipEventRecord(c->ring_ev[slot], cp), "ring event");
-    if (alt && step > 0)  // set (step+1) % 2 held step-1's results: copied by now
-      HIPCHK(c, hipStreamWaitEvent(s, c->ring_ev[(step - 1) % kRing], 0), "set reuse wait");
-    r = S.fast ? forward_fast(c, S.seq, S.n_prompt + step, tcur, true, lnext, tnext)
-               : forward_one(c, S.seq, S.n_prompt + step, c->d_tok, true);
-    if (r) return r;
-    S.enqueued++;
-  }
-  while (S.folded < S.enqueued) {
+  // one fold: 0 folded, 1 a recovery reset the session to an earlier step
+  // (the loops restart from there), -1 error (in r)
+  auto fold = [&]() -> int {
     r = fold_step(c);
-    if (r) return r;
+    if (r == kNeedsRecovery) {
+      r = recover_step(c, S.folded);
+      return r ? -1 : 1;
+    }
+    return r ? -1 : 0;
+  };
+  while (true) {
+    bool restart = false;
+    while (S.enqueued < target && !restart) {
+      // Persistent-kernel steps alternate between two logit buffers and two
+      // token slots: step t's logits and token (set t % 2) are copied to the
+      // host ring on the copy stream while pass t (which writes set
+      // (t+1) % 2) runs; pass t waits only for the copy of step t-1, whose
+      // set it overwrites.  The per-op path keeps one set and copies in
+      // stream order.
+      const bool alt = S.fast && !c->trace;
+      const uint32_t step = S.enqueued;
+      const int slot = step % kRing;
+      if (step >= S.folded + kRing) {  // slot reuse: fold what it held first
+        const int f = fold();
+        if (f < 0) return r;
+        if (f > 0) {
+          restart = true;
+          break;
+        }
+      }
+      const bool odd = alt && (step & 1);
+      float* lcur = odd ? c->logits2 : c->logits;
+      float* lnext = alt ? (odd ? c->logits : c->logits2) : c->logits;
+      uint32_t* tcur = odd ? c->d_tok2 : c->d_tok;
+      uint32_t* tnext = alt ? (odd ? c->d_tok : c->d_tok2) : c->d_tok;
+      // the persistent kernel already left the argmax of these logits in the
+      // token slot; a sampled draw replaces it (generation step = this step)
+      if (c->samp_on)
+        LAUNCH(launch_sample(lcur, V, c->samp, step, c->sbuf, tcur, c->d_err, s), "sample");
+      else if (!S.fast)
+        LAUNCH(launch_argmax(c->logits, V, c->d_tok, s), "argmax");
+      hipStream_t cp = alt ? c->cs : s;
+      if (alt) {
+        HIPCHK(c, hipEventRecord(c->ring_ready[slot], s), "step event");
+        HIPCHK(c, hipStreamWaitEvent(cp, c->ring_ready[slot], 0), "copy wait");
+      }
+      HIPCHK(c, hipMemcpyAsync(c->ring + (size_t)slot * V, lcur, (size_t)V * sizeof(float),
+                               hipMemcpyDeviceToHost, cp),
+             "logits d2h");
+      HIPCHK(c, hipMemcpyAsync(c->ring_tok + slot * 2, tcur, 4, hipMemcpyDeviceToHost, cp),
+             "token d2h");
+      // the error word after the pass that produced these logits
+      HIPCHK(c, hipMemcpyAsync(c->ring_tok + slot * 2 + 1, c->d_err, 4, hipMemcpyDeviceToHost,
+                               cp),
+             "error d2h");
+      HIPCHK(c, hipEventRecord(c->ring_ev[slot], cp), "ring event");
+      if (alt && step > 0)  // set (step+1) % 2 held step-1's results: copied by now
+        HIPCHK(c, hipStreamWaitEvent(s, c->ring_ev[(step - 1) % kRing], 0), "set reuse wait");
+      r = S.fast ? forward_fast(c, S.seq, S.n_prompt + step, tcur, true, lnext, tnext)
+                 : forward_one(c, S.seq, S.n_prompt + step, c->d_tok, true);
+      if (r) return r;
+      S.enqueued++;
+    }
+    while (!restart && S.folded < S.enqueued) {
+      const int f = fold();
+      if (f < 0) return r;
+      restart = f > 0;
+    }
+    if (restart) continue;
+    HIPCHK(c, hipStreamSynchronize(s), "decode sync");
+    if (S.fast && S.enqueued > 0) {
+      // the last pass (whose logits the next call folds) hit the spin cap
+      uint32_t e = 0;
+      HIPCHK(c, hipMemcpy(&e, c->d_err, 4, hipMemcpyDeviceToHost), "error flag");
+      if (e & 2u) {
+        r = recover_step(c, S.enqueued);
+        if (r) return r;
+        continue;  // S.enqueued == target: the loops fall through to here
+      }
+    }
+    return check_err_flag(c);
   }
-  HIPCHK(c, hipStreamSynchronize(s), "decode sync");
-  return check_err_flag(c);
 }
 
 int cis2_decode_end(cis2_ctx* c, uint32_t* out_ids, uint8_t witness[32],
@@ -1479,6 +1656,7 @@ int cis2_decode_end(cis2_ctx* c, uint32_t* out_ids, uint8_t witness[32],
     if (r) return r;
   }
   S.active = false;
+  decode_unlock(c);
   const uint32_t total = S.n_prompt + S.enqueued;
   S.w.finish(witness);
   Sha256 a;
@@ -1497,6 +1675,8 @@ int cis2_decode(cis2_ctx* c, uint32_t seq, const uint32_t* prompt, uint32_t n_pr
   if (!r) r = cis2_decode_steps(c, gen_toks);
   if (!r) r = cis2_decode_end(c, out_ids, witness, argmax_digest, step_digests);
   c->sess.active = false;
+  if (c->st) (void)hipStreamSynchronize(c->st);
+  decode_unlock(c);
   return r;
 }
 

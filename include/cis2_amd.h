@@ -236,6 +236,21 @@ int cis2_profile(cis2_ctx *ctx, int on);
 int cis2_profile_read(cis2_ctx *ctx, uint64_t *launches, double *total_ms, uint32_t *positions,
                       uint64_t cap);
 
+/* ---- Sharing the GPU (no counterpart in the reference: its decode is one
+ * CPU process) ---------------------------------------------------------------
+ * The persistent decode kernel needs its whole grid resident at once.  Its
+ * launches are therefore taken one decode session at a time per GPU, across
+ * processes: an exclusive flock on CIS2_LOCK_DIR (default /tmp)/cis2amd-<pci
+ * bus id>.lock is held from a session's first persistent launch
+ * (cis2_decode_begin) until cis2_decode_end (cis2_forward: for the call);
+ * CIS2_DECODE_LOCK=0 turns it off.  Should a launch still find CUs held by
+ * other work and hit its bounded wait (the spin cap, about 0.5 s; the
+ * CIS2_SPIN_CAP environment variable at context creation sets it in sleeps),
+ * the step is recomputed on the per-op path with the same bits and the
+ * session continues there.  *count receives how many steps of this context
+ * were recovered so. */
+int cis2_recoveries(cis2_ctx *ctx, uint32_t *count);
+
 /* ---- Standalone pinned-order GEMV (the 4-row-interleaved reference kernel
  * of labs/rust-5, whose bits equal matvec/dot_seq: src/main.rs:228-243,
  * math.rs:40-48) --------------------------------------------------------- */
