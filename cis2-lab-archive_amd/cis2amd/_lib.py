@@ -94,6 +94,7 @@ SIGNATURES = {
     "cis2_math_chunk_hashes": (ctypes.c_int, [ctypes.c_int, ctypes.c_uint32, ctypes.c_uint32, c_u64p]),
     "cis2_div_map": (ctypes.c_int, [c_fp, c_fp, c_fp, ctypes.c_uint64]),
     "cis2_fpenv_probe": (ctypes.c_int, [c_u32p]),
+    "cis2_wait_probe": (ctypes.c_int, [c_u32p]),
 }
 
 _lib = None

@@ -324,6 +324,14 @@ def fpenv_probe():
     return int(out[0]), int(out[1])
 
 
+def wait_probe():
+    """(wrong registers after 128 vector loads and one vmcnt(0) wait, wrong
+    words after 40 LDS reads and one lgkmcnt(0) wait): cis2_wait_probe."""
+    out = np.zeros(2, dtype=np.uint32)
+    check(_lib.lib().cis2_wait_probe(_ptr(out, _lib.c_u32p)))
+    return int(out[0]), int(out[1])
+
+
 def sha256(data):
     buf = bytes(data)
     out = _u8buf(32)

@@ -9,6 +9,7 @@
 #include <map>
 #include <mutex>
 #include <utility>
+#include <vector>
 
 #include <float.h>
 #include <string.h>
@@ -537,6 +538,99 @@ hipError_t launch_fpenv_probe(uint32_t* out, hipStream_t s) {
   }
   if (e == hipSuccess) e = hipStreamSynchronize(s);
   (void)hipFree(din);
+  return e;
+}
+
+// ---------------------------------------------------------------------------
+// Wait-counter capacity probes (verification only).  One wave issues N
+// vector loads (global_load_dword) or N LDS reads (ds_read_b128) into N
+// distinct registers with no wait in between (inline asm: the compiler adds
+// none), then one s_waitcnt vmcnt(0) / lgkmcnt(0), then stores every
+// register.  The counters' fields hold 63 and 15 operations; the decode
+// kernel's score tasks keep 64 (head_dim 64) or 128 (head_dim 128) loads
+// per thread in flight and rely on the hardware holding further issue at
+// the field's maximum rather than losing count.  A wrong value here would
+// mean a wait can return while more operations are in flight than the
+// field holds.  N stays small enough that no destination register is
+// spilled or moved before the wait (checked on the built code object).
+// ---------------------------------------------------------------------------
+typedef float pf4 __attribute__((ext_vector_type(4)));
+constexpr int kProbeVm = 128, kProbeLds = 40;
+// element of `in` that vector load I of lane l reads (16384 floats)
+__host__ __device__ constexpr uint32_t probe_vm_index(int I, uint32_t lane) {
+  return (uint32_t)(I / 8) * 1024u + lane + (uint32_t)(I % 8) * 64u;
+}
+template <int I, int N>
+__device__ __forceinline__ void probe_vm_issue(float (&r)[N], const float* base) {
+  if constexpr (I < N) {
+    asm volatile("global_load_dword %0, %1, off offset:%2"
+                 : "=&v"(r[I])
+                 : "v"(base + (I / 8) * 1024), "i"((I % 8) * 256)
+                 : "memory");
+    probe_vm_issue<I + 1, N>(r, base);
+  }
+}
+__global__ __launch_bounds__(64) void k_probe_vm(const float* in, float* out) {
+  const uint32_t lane = threadIdx.x;
+  float r[kProbeVm];
+  probe_vm_issue<0, kProbeVm>(r, in + lane);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+  for (int i = 0; i < kProbeVm; ++i) out[i * 64 + lane] = r[i];
+}
+template <int I, int N>
+__device__ __forceinline__ void probe_lds_issue(pf4 (&r)[N], uint32_t addr) {
+  if constexpr (I < N) {
+    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=&v"(r[I]) : "v"(addr), "i"(I * 1024)
+                 : "memory");
+    probe_lds_issue<I + 1, N>(r, addr);
+  }
+}
+__global__ __launch_bounds__(64) void k_probe_lds(const pf4* in, pf4* out) {
+  __shared__ pf4 lds[kProbeLds * 64];
+  const uint32_t lane = threadIdx.x;
+  for (uint32_t i = lane; i < kProbeLds * 64; i += 64) lds[i] = in[i];
+  __syncthreads();
+  pf4 r[kProbeLds];
+  // LDS byte offset of slot `lane`; load I reads slot I * 64 + lane
+  const uint32_t addr = (uint32_t)(size_t)((__attribute__((address_space(3))) pf4*)lds + lane);
+  probe_lds_issue<0, kProbeLds>(r, addr);
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+  for (int i = 0; i < kProbeLds; ++i) out[i * 64 + lane] = r[i];
+}
+
+hipError_t run_wait_probes(uint32_t bad[2]) {
+  const size_t nvm = 16384, nlds = (size_t)kProbeLds * 64;
+  std::vector<float> hin(nvm);
+  for (size_t i = 0; i < nvm; ++i) hin[i] = (float)i;
+  float *din = nullptr, *dout = nullptr;
+  hipError_t e = hipMalloc(&din, nvm * 4);
+  if (e == hipSuccess) e = hipMalloc(&dout, (size_t)kProbeVm * 64 * 4);
+  if (e == hipSuccess) e = hipMemcpy(din, hin.data(), nvm * 4, hipMemcpyHostToDevice);
+  std::vector<float> hout((size_t)kProbeVm * 64);
+  bad[0] = bad[1] = 0;
+  if (e == hipSuccess) {
+    hipLaunchKernelGGL(k_probe_vm, dim3(1), dim3(64), 0, 0, din, dout);
+    e = hipGetLastError();
+  }
+  if (e == hipSuccess) e = hipMemcpy(hout.data(), dout, hout.size() * 4, hipMemcpyDeviceToHost);
+  if (e == hipSuccess)
+    for (int i = 0; i < kProbeVm; ++i)
+      for (uint32_t l = 0; l < 64; ++l)
+        if (hout[(size_t)i * 64 + l] != hin[probe_vm_index(i, l)]) ++bad[0];
+  // LDS: f4 slot j holds (4j, 4j+1, 4j+2, 4j+3); the first nlds slots of hin
+  if (e == hipSuccess) {
+    hipLaunchKernelGGL(k_probe_lds, dim3(1), dim3(64), 0, 0, reinterpret_cast<const pf4*>(din),
+                       reinterpret_cast<pf4*>(dout));
+    e = hipGetLastError();
+  }
+  if (e == hipSuccess) e = hipMemcpy(hout.data(), dout, nlds * 16, hipMemcpyDeviceToHost);
+  if (e == hipSuccess)
+    for (size_t j = 0; j < nlds * 4; ++j)
+      if (hout[j] != hin[j]) ++bad[1];
+  if (din) (void)hipFree(din);
+  if (dout) (void)hipFree(dout);
   return e;
 }
 

@@ -78,6 +78,11 @@ hipError_t launch_rope_table(float theta_f32, uint32_t hd, uint32_t max_pos,
                              float* inv_freq, float* rope_cs, hipStream_t s);
 // Device FTZ/DAZ probes: out[0] = bits(2^-126 * 1e-10), out[1] = bits(denorm + 0).
 hipError_t launch_fpenv_probe(uint32_t* out, hipStream_t s);
+// Wait-counter capacity probes (verification): bad[0] = wrong registers after
+// 128 vector loads and one vmcnt(0) wait, bad[1] = wrong words after 40 LDS
+// reads and one lgkmcnt(0) wait (both 0 on hardware that holds issue at the
+// counters' maxima).
+hipError_t run_wait_probes(uint32_t bad[2]);
 // Exhaustive-sweep helper: per-chunk order-free hash of fn over the input
 // bit patterns [first, first + count).
 hipError_t launch_math_hash(int fn, uint32_t first, uint32_t count,

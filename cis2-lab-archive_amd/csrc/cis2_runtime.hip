@@ -2155,6 +2155,11 @@ int cis2_div_map(const float* a, const float* b, float* out, uint64_t n) {
 
 void cis2_sha256(const void* data, uint64_t n, uint8_t out[32]) { sha256(data, n, out); }
 
+int cis2_wait_probe(uint32_t bad[2]) {
+  if (!bad) return CIS2_E_ARG;
+  return run_wait_probes(bad) == hipSuccess ? CIS2_OK : CIS2_E_DEVICE;
+}
+
 int cis2_fpenv_probe(uint32_t out[2]) {
   if (!out) return CIS2_E_ARG;
   uint32_t* d = nullptr;

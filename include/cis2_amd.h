@@ -291,6 +291,14 @@ int cis2_math_chunk_hashes(int fn, uint32_t c0, uint32_t nchunks, uint64_t *out)
 int cis2_div_map(const float *a, const float *b, float *out, uint64_t n);
 /* Device FTZ/DAZ probes: bits of 2^-126*1e-10 and of (2^-149 + 0.0). */
 int cis2_fpenv_probe(uint32_t out[2]);
+/* Wait-counter capacity probes (verification; no counterpart in the
+ * reference): bad[0] receives the wrong registers after one wave issues 128
+ * vector loads and then a single s_waitcnt vmcnt(0), bad[1] the wrong words
+ * after 40 LDS reads and a single lgkmcnt(0).  The counters' fields hold 63
+ * and 15 operations; the decode kernel keeps up to 128 loads per thread in
+ * flight, which is exact only if the hardware holds further issue at a
+ * field's maximum: both counts are then 0. */
+int cis2_wait_probe(uint32_t bad[2]);
 
 #ifdef __cplusplus
 }

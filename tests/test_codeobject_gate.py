@@ -140,6 +140,40 @@ def test_fma_only_in_divide_and_sqrt_expansions(code):
     assert not bad, bad
 
 
+def test_wait_probes_issue_every_load_before_one_wait(code):
+    """The wait-counter probes (cis2_wait_probe) test the hardware only if
+    the built code issues all 128 vector loads (40 LDS reads) back to back,
+    waits once, and never copies or spills a destination register before
+    that wait (such a copy would read the register before its load lands)."""
+    fns = code["cis2_kernels"]
+    for tag, load, wait, n in (("k_probe_vm", "global_load_dword", "vmcnt(0)", 128),
+                               ("k_probe_lds", "ds_read_b128", "lgkmcnt(0)", 40)):
+        name = [f for f in fns if tag in f]
+        assert len(name) == 1, tag
+        ins = fns[name[0]]
+        first = next(i for i, (op, _) in enumerate(ins) if op == load)
+        end = next(i for i, (op, a) in enumerate(ins) if i > first and op == "s_waitcnt")
+        assert wait in ins[end][1], (tag, ins[end])
+        between = ins[first:end]
+        assert [op for op, _ in between].count(load) == n, tag
+
+        def regs(text):
+            out = set()
+            for a, b in re.findall(r"\bv\[(\d+):(\d+)\]", text):
+                out.update(range(int(a), int(b) + 1))
+            out.update(int(r) for r in re.findall(r"\bv(\d+)\b", text))
+            return out
+
+        dest = set()
+        for op, a in between:
+            if op == load:
+                dest |= regs(a.split(",")[0])
+        for op, a in between:
+            if op != load:  # nothing reads, copies or overwrites a register in flight
+                assert not (regs(a) & dest), (tag, op, a)
+        assert not any(op.startswith(("scratch_", "v_accvgpr")) for op, _ in ins), tag
+
+
 def test_pure_reduction_kernels_have_no_fma(code):
     seen = 0
     for obj in code.values():

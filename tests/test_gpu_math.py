@@ -18,6 +18,15 @@ def test_device_fpenv_probes():
     assert M.fpenv_probe() == (0, 0)
 
 
+def test_wait_counters_cover_more_operations_than_their_fields():
+    """One wave issues 128 vector loads (the vmcnt field holds 63) or 40 LDS
+    reads (lgkmcnt: 15) and waits once for zero: every register holds its
+    load's value, so the hardware holds issue at a field's maximum.  The
+    decode kernel's score tasks keep 64 or 128 loads per thread in flight
+    and rely on this."""
+    assert M.wait_probe() == (0, 0)
+
+
 @pytest.mark.parametrize("fn", FNS)
 def test_exhaustive_all_inputs(fn, math_fixture):
     got = M.device_math_chunk_hashes(fn)
