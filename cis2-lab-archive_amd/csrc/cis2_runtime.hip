@@ -766,6 +766,18 @@ void fold_rows(std::vector<Sha256>& w, const float* logits, const uint32_t* ids,
 // the same phase, which come first in every list (lower task indices are
 // assigned first).  False when some workgroup would need more than
 // kMaxTasks or a task index exceeds 12 bits.
+// XCDs of the MI355X (8 chiplets of 32 CUs, each with its own L2).
+constexpr uint32_t kXcds = 8;
+// The kv head whose cached K/V rows attention task t reads: task h of the
+// one-task form is query head h; in the split form the score tasks are
+// (kv head, chunk) and the mix tasks (query head, dim slice).
+static uint32_t att_kv_head(const DecodeArgs& a, uint32_t t) {
+  const uint32_t group = a.nh / a.nkv;
+  if (!a.att_split) return t / group;
+  if (t < a.natt_s) return t / a.att_chunks;
+  return (t - a.natt_s) / a.att_dvc / group;
+}
+
 static bool assign_tasks(const DecodeArgs& a, std::vector<uint16_t>& table) {
   const uint32_t natt = a.att_split ? a.natt_s + a.natt_v : a.nh;
   const uint32_t n[kPhases] = {a.nq, natt, a.no, a.ng, a.nd};
@@ -781,6 +793,12 @@ static bool assign_tasks(const DecodeArgs& a, std::vector<uint16_t>& table) {
       return last[w] == (int)p - 1 || (p == kPhaseD && has_qkv[w]);
     };
     for (uint32_t t = 0; t < n[p]; ++t) {
+      // attention tasks of one kv head go to one XCD (workgroups are
+      // dispatched to the XCDs round-robin: workgroup w runs on XCD
+      // w % kXcds), so the tasks that read the same cached K and V rows
+      // share that XCD's L2 and the rows come from HBM about once
+      const int pref = p == kPhaseATT ? (int)(att_kv_head(a, t) % kXcds) : -1;
+      auto on_pref = [&](uint32_t w) { return pref >= 0 && (int)(w % kXcds) == pref; };
       uint32_t best = W;
       for (uint32_t w = 0; w < W; ++w) {
         // one task of a phase per workgroup, unless the phase has more
@@ -789,6 +807,10 @@ static bool assign_tasks(const DecodeArgs& a, std::vector<uint16_t>& table) {
         if (best == W) { best = w; continue; }
         if (same[w] != same[best]) {
           if (same[w] < same[best]) best = w;
+          continue;
+        }
+        if (on_pref(w) != on_pref(best)) {
+          if (on_pref(w)) best = w;
           continue;
         }
         const bool adj_w = adjacent(w), adj_b = adjacent(best);
