@@ -1892,6 +1892,88 @@ __device__ __forceinline__ void run_d(const DecodeArgs& a, uint32_t l, uint32_t 
 // copied before the wait), per-block argmax candidates; the workgroup whose
 // blocks complete the set reduces the candidates to the next token id
 // (strict >, first maximum wins, NaN at index 0 wins; main.rs:1161-1169).
+// Sequential-order LM head with every lane on a row: lane r of half-wave
+// h of wave w takes row r of this workgroup's block 8j + 2w + h in round j
+// (blocks b = wg, wg + nwg, ...; 32 rows each) and runs that row's strict
+// chain acc + W[row][k] * hn[k], k ascending, with its own products, the
+// weights streamed from HBM straight into registers (a ring of kLmRing
+// 16-byte groups in flight per lane) and hn read from LDS (one broadcast
+// read per four k).  No product pass, no LDS staging of weights and no
+// barrier inside the loop, so all four waves keep HBM reads in flight.  The
+// ring's first loads are issued before the final norm, whose gather hides
+// their latency.  Needs 32-row blocks and K a multiple of 4 * kLmRing.
+constexpr uint32_t kLmRing = 16;
+struct LmRows {
+  uint32_t nbw, total, slot, r;  // blocks of this workgroup, steps, block slot, row
+  f4 ring[kLmRing];
+};
+__device__ __forceinline__ gf4* lm_row_addr(const DecodeArgs& a, const LmRows& m, uint32_t t) {
+  const uint32_t KG = a.H >> 2, rd = t / KG, g = t - rd * KG;
+  uint32_t i = rd * 8 + m.slot;
+  if (i >= m.nbw) i = m.nbw - 1;  // idle lanes stream a valid block (never published)
+  const uint32_t b = blockIdx.x + i * a.nwg;
+  return G4(a.lm) + ((size_t)b * KG + g) * 32 + m.r;
+}
+__device__ __forceinline__ void lm_rows_start(const DecodeArgs& a, LmRows& m) {
+  const uint32_t wg = blockIdx.x, lane = threadIdx.x & 63;
+  m.nbw = wg < a.nl ? (a.nl - 1 - wg) / a.nwg + 1 : 0;
+  m.total = ((m.nbw + 7) / 8) * (a.H >> 2);
+  m.slot = (threadIdx.x >> 6) * 2 + (lane >> 5);
+  m.r = lane & 31;
+  if (m.nbw == 0) return;
+#pragma unroll
+  for (uint32_t u = 0; u < kLmRing; ++u) m.ring[u] = *lm_row_addr(a, m, u);
+}
+// The rows' chains, logits and per-block candidates; returns the number of
+// blocks this workgroup published.
+__device__ __forceinline__ uint32_t lm_rows_run(const DecodeArgs& a, LmRows& m, const lf* hn) {
+  const uint32_t KG = a.H >> 2, lane = threadIdx.x & 63;
+  if (m.nbw == 0) return 0;
+  AS_GLB float* logits = GW(a.logits);
+  const lf4* hn4 = (const lf4*)hn;
+  float acc = 0.0f;
+  for (uint32_t t0 = 0; t0 < m.total; t0 += kLmRing) {
+    const uint32_t g0 = t0 % KG;
+#pragma unroll
+    for (uint32_t u = 0; u < kLmRing; ++u) {
+      const f4 w = m.ring[u];
+      const f4 xv = hn4[g0 + u];
+      float p;
+      p = w.x * xv.x;
+      acc = acc + p;
+      p = w.y * xv.y;
+      acc = acc + p;
+      p = w.z * xv.z;
+      acc = acc + p;
+      p = w.w * xv.w;
+      acc = acc + p;
+      if (t0 + u + kLmRing < m.total) m.ring[u] = *lm_row_addr(a, m, t0 + u + kLmRing);
+    }
+    if (g0 + kLmRing == KG) {  // a round ends: publish every lane's row
+      const uint32_t i = (t0 / KG) * 8 + m.slot;
+      const bool live = i < m.nbw;
+      const uint32_t b = blockIdx.x + i * a.nwg, row = b * 32 + m.r;
+      Cand c = {0.0f, UINT32_MAX};
+      if (live && row < a.V) {
+        logits[row] = acc;
+        if (acc == acc) c = Cand{acc, row};
+      }
+      if (live && row == 0) st_ag(a.cand + 2 * a.nl, acc != acc ? 1u : 0u);
+#pragma unroll
+      for (uint32_t h = 0; h < 2; ++h) {  // the candidate of each half-wave's block
+        const Cand ch = cand_wave_dpp((lane >> 5) == h ? c : Cand{0.0f, UINT32_MAX});
+        const uint32_t ih = (t0 / KG) * 8 + (threadIdx.x >> 6) * 2 + h;
+        if (lane == 0 && ih < m.nbw)
+          __hip_atomic_store((gw*)a.cand + blockIdx.x + ih * a.nwg,
+                             ((u64)ch.i << 32) | __float_as_uint(ch.v), __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+      }
+      acc = 0.0f;
+    }
+  }
+  return m.nbw;
+}
+
 template <bool TR>
 __device__ __forceinline__ void run_lm(const DecodeArgs& a, const Lds& s) {
   const uint32_t L = a.L, wg = blockIdx.x;
@@ -1900,7 +1982,10 @@ __device__ __forceinline__ void run_lm(const DecodeArgs& a, const Lds& s) {
   lf* hn = x + a.H;
   lf* misc = hn + a.H;
   AS_LDS uint32_t* red = (AS_LDS uint32_t*)(misc + 4);
-  if (wg < a.nl) prefetch_rows(a.lm, a.Rl, a.H, wg, s.w);
+  const bool rows = !TR && a.Rl == 32 && a.H % (4 * kLmRing) == 0;
+  LmRows lr;
+  if (rows) lm_rows_start(a, lr);
+  else if (wg < a.nl) prefetch_rows(a.lm, a.Rl, a.H, wg, s.w);
   const NormW nw = load_normw(a.fnorm, a.H);
   stamp(a, L - 1, P_LM, wg, 0);
   gather_vec(x, act_of(a, L - 1).hout, a.H, a);
@@ -1908,6 +1993,7 @@ __device__ __forceinline__ void run_lm(const DecodeArgs& a, const Lds& s) {
   rmsnorm_lds<TR>(x, nw, a.eps, a.H, hn, hn, misc);
   AS_GLB float* logits = GW(a.logits);
   uint32_t done = 0;
+  if (rows) done = lm_rows_run(a, lr, hn);
   // logits and argmax candidate of block b (wave 0)
   auto publish = [&](uint32_t b, float acc) {
     if (wv == 0) {
@@ -1926,7 +2012,8 @@ __device__ __forceinline__ void run_lm(const DecodeArgs& a, const Lds& s) {
     }
   };
   const size_t blkf = (size_t)a.Rl * a.H;
-  if (2 * blkf * 4 <= decode_wregion_bytes(a)) {
+  if (rows) {
+  } else if (2 * blkf * 4 <= decode_wregion_bytes(a)) {
     // two LDS buffers: block b + nwg streams in while block b is computed;
     // block b's results are published after the wait, so the wait covers
     // only loads and stores issued one GEMV earlier

@@ -6,6 +6,7 @@
 #include "cis2_device_math.hpp"
 #include "cis2_kernels.hpp"
 
+#include <algorithm>
 #include <map>
 #include <mutex>
 #include <utility>
@@ -601,20 +602,26 @@ __global__ __launch_bounds__(64) void k_probe_lds(const pf4* in, pf4* out) {
 }
 
 hipError_t run_wait_probes(uint32_t bad[2]) {
+  // input: 16384 floats (the vector probe's largest index, probe_vm_index(127, 63),
+  // is 15871; the LDS probe reads the first kProbeLds * 64 16-byte slots);
+  // output: the larger of the two probes' results (128 x 64 floats, 40 x 64 x 4)
   const size_t nvm = 16384, nlds = (size_t)kProbeLds * 64;
+  const size_t nout = std::max((size_t)kProbeVm * 64, nlds * 4);
+  static_assert(probe_vm_index(kProbeVm - 1, 63) < 16384, "vector probe input");
+  static_assert(kProbeLds * 64 * 4 <= 16384, "LDS probe input");
   std::vector<float> hin(nvm);
   for (size_t i = 0; i < nvm; ++i) hin[i] = (float)i;
   float *din = nullptr, *dout = nullptr;
   hipError_t e = hipMalloc(&din, nvm * 4);
-  if (e == hipSuccess) e = hipMalloc(&dout, (size_t)kProbeVm * 64 * 4);
+  if (e == hipSuccess) e = hipMalloc(&dout, nout * 4);
   if (e == hipSuccess) e = hipMemcpy(din, hin.data(), nvm * 4, hipMemcpyHostToDevice);
-  std::vector<float> hout((size_t)kProbeVm * 64);
+  std::vector<float> hout(nout);
   bad[0] = bad[1] = 0;
   if (e == hipSuccess) {
     hipLaunchKernelGGL(k_probe_vm, dim3(1), dim3(64), 0, 0, din, dout);
     e = hipGetLastError();
   }
-  if (e == hipSuccess) e = hipMemcpy(hout.data(), dout, hout.size() * 4, hipMemcpyDeviceToHost);
+  if (e == hipSuccess) e = hipMemcpy(hout.data(), dout, (size_t)kProbeVm * 64 * 4, hipMemcpyDeviceToHost);
   if (e == hipSuccess)
     for (int i = 0; i < kProbeVm; ++i)
       for (uint32_t l = 0; l < 64; ++l)
