@@ -6,8 +6,15 @@
 //
 //   cis2_host --weights-dir DIR --ids FILE [--gen-toks N] [--trace FILE]
 //             [--prompt-idx I] [--reduction sequential|tree] [--sample SEED,T,K,P]
-//             [--verify2] [--receipt-log FILE]
+//             [--verify2] [--receipt-log FILE] [--layer-digests]
 //   cis2_host --verify-chain FILE [--receipt-id ID]
+//
+// Debug surface of the reference CLI (code/cis2-fp/src/main.rs:315-335,
+// 355-529, 1099-1212), none of it part of CIS2_REF: --layer-digests prints
+// LAYER_DIGEST lines for the last prompt position; CIS2_DUMP_LAYERS (any
+// value) prints CIS2_DUMP lines on stderr for the last prompt position and
+// the first generated one; CIS2_DUMP_STEP0_LOGITS / CIS2_DUMP_LASTSTEP_LOGITS
+// name files that receive the step-0 and the final step's fp32 logits.
 #include "cis2_amd.h"
 #include "cis2_checkpoint.hpp"
 #include "cis2_receipts.hpp"
@@ -48,6 +55,31 @@ std::string ids_list(const std::vector<uint32_t>& v) {
 struct TraceSink {
   FILE* fp = nullptr;
 };
+
+// The ops of one forward pass that the debug surface reports, as the
+// reference's trace names them, with the digests a capture pass recorded.
+struct Capture {
+  uint32_t pos_lo = 0, pos_hi = 0;  // positions kept: [pos_lo, pos_hi]
+  struct Line {
+    int pos, layer;
+    std::string op, sha;
+  };
+  std::vector<Line> lines;
+};
+void capture_cb(int pos, int layer, const char* op, const uint8_t sha[32], void* user) {
+  Capture* c = static_cast<Capture*>(user);
+  if (pos < (int)c->pos_lo || pos > (int)c->pos_hi) return;
+  const std::string o = op;
+  if (o == "embedding" || o == "resid1" || o == "resid2" || o == "final_norm" || o == "logits")
+    c->lines.push_back({pos, layer, o, hex(sha, 32)});
+}
+
+// Raw little-endian fp32 values to a file (the reference's logit dumps).
+void write_f32(const std::string& path, const std::vector<float>& v) {
+  FILE* f = fopen(path.c_str(), "wb");
+  if (!f || fwrite(v.data(), 4, v.size(), f) != v.size()) fatal("write " + path);
+  fclose(f);
+}
 void trace_cb(int pos, int layer, const char* op, const uint8_t sha[32], void* user) {
   TraceSink* t = static_cast<TraceSink*>(user);
   fprintf(t->fp, "pos=%d layer=%d op=%s sha256=%s\n", pos, layer, op, hex(sha, 32).c_str());
@@ -112,6 +144,9 @@ struct Options {
   // --receipt-log FILE appends this run's receipt; --verify-chain FILE
   // [--receipt-id ID] checks a log (through ID) and exits 0 / 1
   std::string receipt_log, verify_chain, receipt_id;
+  // --layer-digests (code/cis2-fp/src/main.rs:743-751): LAYER_DIGEST lines of
+  // the last prompt position's forward pass
+  bool layer_digests = false;
 };
 
 bool whole_int(const char* t, int* out) {
@@ -158,6 +193,7 @@ std::string parse_options(int argc, char** argv, Options& o) {
                           std::string(v);
        }},
       {"--verify2", false, [](Options& o, const char*) { o.verify2 = true; return std::string(); }},
+      {"--layer-digests", false, [](Options& o, const char*) { o.layer_digests = true; return std::string(); }},
       {"--receipt-log", true, [](Options& o, const char* v) { o.receipt_log = v; return std::string(); }},
       {"--verify-chain", true, [](Options& o, const char* v) { o.verify_chain = v; return std::string(); }},
       {"--receipt-id", true, [](Options& o, const char* v) { o.receipt_id = v; return std::string(); }},
@@ -319,6 +355,48 @@ int main(int argc, char** argv) {
   fprintf(stderr, "[prompt %d] token ids (%zu toks): %s\n", prompt_idx, prompt.size(),
           ids_list(prompt).c_str());
 
+  // Debug capture (the reference's --layer-digests and CIS2_DUMP_LAYERS):
+  // one traced pass of the prompt (and the first generated step for the
+  // dump), before the decode; the per-op path it runs gives the decode's
+  // bits.  Its digests are printed where the reference prints them: the
+  // LAYER_DIGEST lines before any other stdout line, the CIS2_DUMP lines on
+  // stderr.
+  const bool dump_layers = getenv("CIS2_DUMP_LAYERS") != nullptr && !verify2;
+  Capture cap;
+  if ((opt.layer_digests || dump_layers) && !verify2) {
+    const uint32_t last = (uint32_t)prompt.size() - 1;
+    const uint32_t extra = dump_layers && gen_toks > 0 ? 1u : 0u;
+    cap.pos_lo = last;
+    cap.pos_hi = last + extra;
+    cis2_trace_enable(ctx, capture_cb, &cap);
+    std::vector<uint32_t> cids(prompt.size() + extra);
+    uint8_t cw[32], ca[32];
+    rc = cis2_decode(ctx, 0, prompt.data(), (uint32_t)prompt.size(), extra, hdr, cids.data(), cw,
+                     ca, nullptr);
+    cis2_trace_enable(ctx, nullptr, nullptr);
+    if (rc) fatal(std::string("debug capture: ") + cis2_last_error(ctx));
+    if (opt.layer_digests)
+      for (const Capture::Line& l : cap.lines) {
+        if (l.pos != (int)last) continue;
+        if (l.op == "embedding") printf("LAYER_DIGEST embed %s\n", l.sha.c_str());
+        else if (l.op == "resid2") printf("LAYER_DIGEST block_%d %s\n", l.layer, l.sha.c_str());
+        else if (l.op == "final_norm") printf("LAYER_DIGEST final_norm %s\n", l.sha.c_str());
+        else if (l.op == "logits") printf("LAYER_DIGEST logits %s\n", l.sha.c_str());
+      }
+    if (dump_layers)
+      for (const Capture::Line& l : cap.lines) {
+        std::string layer, field;
+        if (l.op == "embedding") layer = "embed", field = "token_embedding";
+        else if (l.op == "resid1") layer = "block" + std::to_string(l.layer), field = "post_attention_hidden";
+        else if (l.op == "resid2") layer = "block" + std::to_string(l.layer), field = "post_mlp_hidden";
+        else if (l.op == "final_norm") layer = "final_norm", field = "final_norm_output";
+        else layer = "logits", field = "pre_argmax_logits";
+        fprintf(stderr, "CIS2_DUMP layer=%s field=%s pos=%d digest=%s\n", layer.c_str(),
+                field.c_str(), l.pos, l.sha.c_str());
+      }
+    fflush(stdout);
+  }
+
   TraceSink sink;
   if (!trace_path.empty()) {
     sink.fp = fopen(trace_path.c_str(), "wb");
@@ -331,6 +409,25 @@ int main(int argc, char** argv) {
                    ids.data(), wit, adig, nullptr);
   if (rc) fatal(std::string("decode: ") + cis2_last_error(ctx));
   if (sink.fp) fclose(sink.fp);
+  cis2_trace_enable(ctx, nullptr, nullptr);
+  // the reference's logit dumps (main.rs:1145-1160, 1197-1212): step 0's
+  // logits (the last prompt position's forward pass) and the final step's
+  // (the forward pass of the last generated id); each pass is recomputed
+  // from the decode's K/V cache with the same bits and rewrites its own
+  // position only
+  auto dump_logits = [&](const char* env, uint32_t pos, uint32_t tok, const char* what) {
+    const char* path = getenv(env);
+    if (!path || verify2) return;
+    std::vector<float> lg(cfg.vocab);
+    uint32_t seq = 0, am = 0;
+    rc = cis2_forward(ctx, 1, &seq, &pos, &tok, lg.data(), &am);
+    if (rc) fatal(std::string(env) + ": " + cis2_last_error(ctx));
+    write_f32(path, lg);
+    fprintf(stderr, "[debug] wrote %s logits (%zu f32 values) to %s\n", what, lg.size(), path);
+  };
+  dump_logits("CIS2_DUMP_STEP0_LOGITS", (uint32_t)prompt.size() - 1, prompt.back(), "step-0");
+  dump_logits("CIS2_DUMP_LASTSTEP_LOGITS", (uint32_t)prompt.size() + gen_toks - 1,
+              ids[prompt.size() + gen_toks - 1], "final-step");
   if (verify2) {
     // section 12.4: the whole decode twice in one process, identical results
     // (verify2/src/main.rs:446-477), then the verifier's five lines

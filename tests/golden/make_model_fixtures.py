@@ -98,7 +98,26 @@ def run_case(name):
             data = open(tpath, "rb").read()
             rec["trace_sha256"] = hashlib.sha256(data).hexdigest()
             rec["trace_lines"] = data.count(b"\n")
+            rec["layer_digests"] = layer_digest_lines(data.decode(), len(prompt) - 1)
         return name, rec
+
+
+def layer_digest_lines(trace_text, pos):
+    """The LAYER_DIGEST lines the reference CLI's --layer-digests prints for
+    the forward pass at `pos` (code/cis2-fp/src/main.rs:382-384, 496-501,
+    509-514, 525-527), from the same pass's trace lines: the embedding, each
+    block's output (resid2), the final norm, the logits."""
+    t = {}
+    for line in trace_text.splitlines():
+        m = re.match(r"pos=(-?\d+) layer=(-?\d+) op=(\S+) sha256=([0-9a-f]{64})$", line)
+        if m and int(m.group(1)) == pos:
+            t[(int(m.group(2)), m.group(3))] = m.group(4)
+    out = ["LAYER_DIGEST embed %s" % t[(-1, "embedding")]]
+    n_layers = len([k for k in t if k[1] == "resid2"])
+    out += ["LAYER_DIGEST block_%d %s" % (li, t[(li, "resid2")]) for li in range(n_layers)]
+    out += ["LAYER_DIGEST final_norm %s" % t[(-1, "final_norm")],
+            "LAYER_DIGEST logits %s" % t[(-1, "logits")]]
+    return out
 
 
 def main():

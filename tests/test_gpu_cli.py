@@ -176,3 +176,99 @@ def test_cli_receipt_log(model_fixtures, tmp_path):
     log.write_text(json.dumps(bad, sort_keys=True) + "\n" + lines[1] + "\n")
     v = subprocess.run([CLI, "--verify-chain", str(log)], capture_output=True, text=True, timeout=60)
     assert v.returncode == 1 and "line 0: log_hash mismatch (tampered record)" in v.stdout
+
+
+def _trace_lines(path):
+    """{(pos, layer, op): sha} of a --trace file."""
+    out = {}
+    for line in path.read_text().splitlines():
+        m = re.match(r"pos=(-?\d+) layer=(-?\d+) op=(\S+) sha256=([0-9a-f]{64})$", line)
+        assert m, line
+        out[(int(m.group(1)), int(m.group(2)), m.group(3))] = m.group(4)
+    return out
+
+
+@pytest.mark.parametrize("name", ["tiny-llama", "tiny-qwen3-tree", "smollm2-short"])
+def test_cli_layer_digests_and_layer_dumps(name, model_fixtures, tmp_path):
+    """--layer-digests (main.rs:743-751, 382-384, 496-501, 509-514, 525-527)
+    prints LAYER_DIGEST lines for the last prompt position: the embedding,
+    each block's output (the trace's resid2), the final norm and the
+    logits; CIS2_DUMP_LAYERS prints CIS2_DUMP lines (main.rs:326-335) for
+    that position and the first generated one.  Both are checked against
+    the --trace file of the same run, which is itself byte-equal to the
+    reference driver's trace (trace_sha256); the decode's digests are
+    unchanged."""
+    rec = model_fixtures[name]
+    spec = artifacts.SPECS[rec["spec"]]
+    artifacts.Weights(spec, rec["seed"]).write_dir(str(tmp_path))
+    ids = tmp_path / "ids.txt"
+    ids.write_text("\n".join(str(t) for t in rec["prompt"]) + "\n")
+    trace = tmp_path / "trace.txt"
+    mode = rec.get("reduction", "sequential")
+    env = dict(os.environ, CIS2_DUMP_LAYERS="1")
+    r = subprocess.run([CLI, "--weights-dir", str(tmp_path), "--ids", str(ids), "--gen-toks",
+                        str(rec["gen_toks"]), "--trace", str(trace), "--reduction", mode,
+                        "--layer-digests"], capture_output=True, text=True, timeout=300, env=env)
+    assert r.returncode == 0, r.stderr[-2000:]
+    assert hashlib.sha256(trace.read_bytes()).hexdigest() == rec["trace_sha256"]
+    assert "CIS2_REF digest=%s" % rec["witness"] in r.stdout
+    t = _trace_lines(trace)
+    last = len(rec["prompt"]) - 1
+    want = ["LAYER_DIGEST embed %s" % t[(last, -1, "embedding")]]
+    want += ["LAYER_DIGEST block_%d %s" % (li, t[(last, li, "resid2")])
+             for li in range(spec.n_layers)]
+    want += ["LAYER_DIGEST final_norm %s" % t[(last, -1, "final_norm")],
+             "LAYER_DIGEST logits %s" % t[(last, -1, "logits")]]
+    got = [l for l in r.stdout.splitlines() if l.startswith("LAYER_DIGEST")]
+    assert got == want
+    assert got == rec["layer_digests"]  # read from the reference driver's trace
+    assert r.stdout.splitlines()[:len(want)] == want  # before every other stdout line
+    dumps = [l for l in r.stderr.splitlines() if l.startswith("CIS2_DUMP ")]
+    want_d = []
+    for pos in (last, last + 1):
+        want_d.append("CIS2_DUMP layer=embed field=token_embedding pos=%d digest=%s"
+                      % (pos, t[(pos, -1, "embedding")]))
+        for li in range(spec.n_layers):
+            want_d.append("CIS2_DUMP layer=block%d field=post_attention_hidden pos=%d digest=%s"
+                          % (li, pos, t[(pos, li, "resid1")]))
+            want_d.append("CIS2_DUMP layer=block%d field=post_mlp_hidden pos=%d digest=%s"
+                          % (li, pos, t[(pos, li, "resid2")]))
+        want_d.append("CIS2_DUMP layer=final_norm field=final_norm_output pos=%d digest=%s"
+                      % (pos, t[(pos, -1, "final_norm")]))
+        want_d.append("CIS2_DUMP layer=logits field=pre_argmax_logits pos=%d digest=%s"
+                      % (pos, t[(pos, -1, "logits")]))
+    assert dumps == want_d
+
+
+@pytest.mark.parametrize("name", ["tiny-qwen3", "smollm2-short"])
+def test_cli_logit_dumps_match_oracle(name, model_fixtures, tmp_path):
+    """CIS2_DUMP_STEP0_LOGITS / CIS2_DUMP_LASTSTEP_LOGITS (main.rs:1145-1160,
+    1197-1212): raw little-endian fp32 files of step 0's logits and the
+    final generated step's, bit-equal to the oracle's forward passes at
+    those positions."""
+    import numpy as np
+
+    import _oracle as O
+    rec = model_fixtures[name]
+    spec = artifacts.SPECS[rec["spec"]]
+    w = artifacts.Weights(spec, rec["seed"])
+    w.write_dir(str(tmp_path))
+    ids = tmp_path / "ids.txt"
+    ids.write_text("\n".join(str(t) for t in rec["prompt"]) + "\n")
+    s0, sl = tmp_path / "step0.f32", tmp_path / "last.f32"
+    env = dict(os.environ, CIS2_DUMP_STEP0_LOGITS=str(s0), CIS2_DUMP_LASTSTEP_LOGITS=str(sl))
+    r = subprocess.run([CLI, "--weights-dir", str(tmp_path), "--ids", str(ids), "--gen-toks",
+                        str(rec["gen_toks"])], capture_output=True, text=True, timeout=300, env=env)
+    assert r.returncode == 0, r.stderr[-2000:]
+    assert "CIS2_REF digest=%s" % rec["witness"] in r.stdout
+    assert "[debug] wrote step-0 logits (%d f32 values) to %s" % (spec.vocab, s0) in r.stderr
+    assert "[debug] wrote final-step logits (%d f32 values) to %s" % (spec.vocab, sl) in r.stderr
+    toks = rec["tokens"]
+    n = len(rec["prompt"])
+    o = O.OracleModel(spec, w, max_pos=n + rec["gen_toks"])
+    lg = None
+    for p in range(n + rec["gen_toks"]):
+        lg = o.forward(p, toks[p])
+        if p == n - 1:
+            assert s0.read_bytes() == lg.astype(np.float32).tobytes()
+    assert sl.read_bytes() == lg.astype(np.float32).tobytes()

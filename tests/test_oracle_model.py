@@ -108,3 +108,35 @@ def test_tree_mode_models_match_reference(name, model_fixtures):
     res, _ = run_tree(rec)
     assert list(res["ids"]) == rec["tokens"]
     assert res["witness"] == rec["witness"]
+
+
+def _layer_digest_lines(lines, pos):
+    """LAYER_DIGEST lines (the reference CLI's --layer-digests, main.rs:382-384,
+    496-501, 509-514, 525-527) of the pass at `pos`, from its trace lines."""
+    t = {}
+    for line in lines:
+        p, layer, op, sha = line.split()
+        if int(p.split("=")[1]) == pos:
+            t[(int(layer.split("=")[1]), op.split("=")[1])] = sha.split("=")[1]
+    n = len([k for k in t if k[1] == "resid2"])
+    return (["LAYER_DIGEST embed %s" % t[(-1, "embedding")]] +
+            ["LAYER_DIGEST block_%d %s" % (i, t[(i, "resid2")]) for i in range(n)] +
+            ["LAYER_DIGEST final_norm %s" % t[(-1, "final_norm")],
+             "LAYER_DIGEST logits %s" % t[(-1, "logits")]])
+
+
+@pytest.mark.parametrize("name", FAST + ["tiny-qwen3-tree"])
+def test_layer_digests_match_reference_trace(name, model_fixtures):
+    """The per-layer digests of the last prompt position (each block's output
+    = the trace's resid2 line) computed by the oracle equal the ones read
+    from the reference driver's own trace (layer_digests, recorded by
+    make_model_fixtures.py); the GPU CLI's --layer-digests lines are checked
+    against the same fixture."""
+    rec = model_fixtures[name]
+    if rec.get("reduction") == "tree":
+        _, lines = run_tree(rec, trace=True)
+    else:
+        _, _, _, lines = run(rec, trace=True)
+    got = _layer_digest_lines(lines, len(rec["prompt"]) - 1)
+    assert got == rec["layer_digests"]
+    assert len(got) == artifacts.SPECS[rec["spec"]].n_layers + 3
