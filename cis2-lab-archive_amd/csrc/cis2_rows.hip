@@ -1727,7 +1727,7 @@ hipError_t launch_bgemm_t(const BgemmArgs& a, dim3 grid, size_t lds, hipStream_t
 // attention), so that no attribute call happens later, e.g. inside a graph
 // capture.
 hipError_t rows_configure() {
-  const void* fns[22] = {reinterpret_cast<const void*>(&k_bgemm<false, false, 1>),
+  const void* fns[20] = {reinterpret_cast<const void*>(&k_bgemm<false, false, 1>),
                          reinterpret_cast<const void*>(&k_bgemm16<false, false>),
                          reinterpret_cast<const void*>(&k_bgemm16<false, true>),
                          reinterpret_cast<const void*>(&k_bgemm16<true, false>),
@@ -1740,13 +1740,11 @@ hipError_t rows_configure() {
                          reinterpret_cast<const void*>(&k_attention_kv<1, 64, false>),
                          reinterpret_cast<const void*>(&k_attention_kv<2, 64, false>),
                          reinterpret_cast<const void*>(&k_attention_kv<3, 64, false>),
-                         reinterpret_cast<const void*>(&k_attention_kv<4, 64, false>),
                          reinterpret_cast<const void*>(&k_attention_kv<1, 128, false>),
                          reinterpret_cast<const void*>(&k_attention_kv<2, 128, false>),
                          reinterpret_cast<const void*>(&k_attention_kv<1, 64, true>),
                          reinterpret_cast<const void*>(&k_attention_kv<2, 64, true>),
                          reinterpret_cast<const void*>(&k_attention_kv<3, 64, true>),
-                         reinterpret_cast<const void*>(&k_attention_kv<4, 64, true>),
                          reinterpret_cast<const void*>(&k_attention_kv<1, 128, true>),
                          reinterpret_cast<const void*>(&k_attention_kv<2, 128, true>)};
   for (const void* f : fns) {
@@ -1936,7 +1934,10 @@ static hipError_t kv_plan(uint32_t n, uint32_t nh, uint32_t nkv, uint32_t hd, ui
   const uint32_t group = nh / nkv;
   const int ncu = device_cu_count();
   const uint64_t wgs_kv = (uint64_t)n * nkv;
-  if (!(wgs_kv < 4 * (uint64_t)ncu && (hd == 64 || hd == 128) && group * hd <= 256))
+  // instances for groups of up to 3 heads at head_dim 64 and 2 at 128 (a
+  // group of 4 at head_dim 64 needed more registers than a wave has and
+  // spilled to scratch; such models take the per-row kernel)
+  if (!(wgs_kv < 4 * (uint64_t)ncu && ((hd == 64 && group <= 3) || (hd == 128 && group <= 2))))
     return hipSuccess;
   hipError_t e = rows_configure();
   if (e != hipSuccess) return e;
@@ -1977,8 +1978,7 @@ static hipError_t launch_kv(const KvPlan& kp, bool fuse, const float* q, float* 
     switch (kp.group) {
       case 1: CIS2_ATT_KV(1, 64); break;
       case 2: CIS2_ATT_KV(2, 64); break;
-      case 3: CIS2_ATT_KV(3, 64); break;
-      default: CIS2_ATT_KV(4, 64);
+      default: CIS2_ATT_KV(3, 64);
     }
   } else {
     if (kp.group == 1) CIS2_ATT_KV(1, 128);

@@ -140,6 +140,30 @@ def test_fma_only_in_divide_and_sqrt_expansions(code):
     assert not bad, bad
 
 
+def test_no_kernel_spills_vector_registers(tmp_path):
+    """Every kernel keeps its values in registers: no VGPR spills to scratch
+    (code-object metadata .vgpr_spill_count).  Spill code is where this
+    compiler was caught reloading a partly spilled register tuple into the
+    wrong register, and a chain kernel fully unrolled under register
+    pressure is what spills."""
+    tools()
+    bad = []
+    for name in OBJECTS:
+        disassemble(name, str(tmp_path))  # unbundles <name>.co into tmp_path
+        co = os.path.join(str(tmp_path), name + ".co")
+        r = subprocess.run([os.path.join(LLVM, "llvm-readelf"), "--notes", co], check=True,
+                           capture_output=True, text=True)
+        kern = None
+        for line in r.stdout.splitlines():
+            m = re.match(r"\s*\.name:\s+(\S+)", line)
+            if m:
+                kern = m.group(1)
+            m = re.match(r"\s*\.vgpr_spill_count:\s+(\d+)", line)
+            if m and int(m.group(1)) != 0:
+                bad.append((name, kern, int(m.group(1))))
+    assert not bad, bad
+
+
 def test_wait_probes_issue_every_load_before_one_wait(code):
     """The wait-counter probes (cis2_wait_probe) test the hardware only if
     the built code issues all 128 vector loads (40 LDS reads) back to back,

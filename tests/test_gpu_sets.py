@@ -64,3 +64,41 @@ def test_batch_stress_rows_match_reference_and_smaller_batch():
         assert small[i]["witness"] == rows[i]["witness"]
         assert small[i]["argmax_digest"] == rows[i]["argmax_digest"]
         assert np.array_equal(small[i]["ids"], rows[i]["ids"])
+
+
+@pytest.mark.parametrize("B", [1, 32])
+def test_batch_stress_b1_b32_match_reference(B):
+    """The batch-stress sequences decoded B at a time (B = 1 and B = 32, the
+    bench's other batch sizes), every row against the reference driver's
+    digests: B = 1 over sequences 0..3 one by one, B = 32 over 32..63."""
+    pset = artifacts.BATCH_SET
+    cases = load_set("batch_set.json", pset)
+    spec = artifacts.SPECS[pset["spec"]]
+    prompts = artifacts.set_prompts(pset)
+    gen = pset["gen_toks"]
+    m = Cis2Model(spec, artifacts.Weights(spec, pset["seed"]), max_pos=pset["hi"] + gen,
+                  max_seqs=B)
+    first, count = (0, 4) if B == 1 else (32, 32)
+    rows = []
+    for s in range(first, first + count, B):
+        rows += m.decode_batch(prompts[s:s + B], gen)
+    bad = [first + i for i, r in enumerate(rows)
+           if [r["witness"], r["argmax_digest"]] != cases[str(first + i)]]
+    assert not bad, "rows whose digests differ from the reference: %s" % bad
+    m.close()
+
+
+def test_llama160m_300_prompts_as_one_batch():
+    """Config 3 as the bench runs it: all 300 llama-160m prompts in one
+    cis2_decode_batch call (300 KV-cache slots), every sequence's digests
+    equal to the reference driver's."""
+    pset = artifacts.LLAMA_SET
+    cases = load_set("llama160m_set.json", pset)
+    spec = artifacts.SPECS[pset["spec"]]
+    prompts = artifacts.set_prompts(pset)
+    m = Cis2Model(spec, artifacts.Weights(spec, pset["seed"]),
+                  max_pos=pset["hi"] + pset["gen_toks"], max_seqs=len(prompts))
+    rows = m.decode_batch(prompts, pset["gen_toks"])
+    bad = [i for i, r in enumerate(rows) if [r["witness"], r["argmax_digest"]] != cases[str(i)]]
+    assert not bad, "sequences whose digests differ from the reference: %s" % bad[:20]
+    m.close()
