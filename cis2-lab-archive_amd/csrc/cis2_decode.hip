@@ -51,6 +51,17 @@ typedef const AS_GLB float gf;
 typedef const AS_GLB f4 gf4;
 typedef AS_GLB u64 gw;
 
+// threadIdx.x through an opaque copy: values derived from it are formed
+// where they are used instead of being hoisted out of the layer loop and
+// kept live for the whole persistent kernel (which otherwise runs out of
+// registers and spills).  gather_map alone keeps threadIdx.x: its word
+// offsets, hoisted, gave the fewest registers of the variants compiled.
+__device__ __forceinline__ uint32_t tid_x() {
+  uint32_t t = threadIdx.x;
+  asm volatile("" : "+v"(t));
+  __builtin_assume(t < 256u);  // every kernel here runs 256-thread workgroups
+  return t;
+}
 __device__ __forceinline__ gf* G(const float* p) { return (gf*)p; }
 __device__ __forceinline__ gf4* G4(const float* p) { return (gf4*)p; }
 __device__ __forceinline__ AS_GLB float* GW(float* p) { return (AS_GLB float*)p; }
@@ -119,20 +130,32 @@ __host__ __device__ inline uint32_t att_tile_positions(uint32_t hd, uint32_t max
 
 // Split attention: output dims per mix task, and the floats of the tree
 // partials that follow the scores (one per 32 positions, rounded to 16 B).
-constexpr uint32_t kAttDV = 16;
+constexpr uint32_t kAttDV = 8;
 __host__ __device__ inline size_t att_part_floats(uint32_t max_pos) {
   return ((size_t)max_pos / 32 + 1 + 3) & ~(size_t)3;
 }
-// Positions per V tile of a mix task: the largest multiple of 32 whose
-// three [kAttDV][TP+4] tiles fit beside the scores and partials; 0 if < 32.
-__host__ __device__ inline uint32_t att_mix_tile_positions(uint32_t max_pos, size_t wfloats) {
+// A mix task's LDS in the weight region (floats): its head's scores
+// ([max_pos + 64]), their tree partials, then a ring of nr V tiles
+// ([16][tp + 4], the products formed in place).  The plan takes a ring of
+// 4 tiles (two in flight beyond the tile in use and the one being
+// formed), else 3, with the largest tile (a multiple of 32, at most 1024
+// positions) that fits.  tp = 0: no plan fits.
+__host__ __device__ inline void att_mix_plan(uint32_t max_pos, size_t wfloats, uint32_t* tp,
+                                             uint32_t* nr) {
+  *tp = 0;
+  *nr = 0;
   const size_t used = (size_t)max_pos + 64 + att_part_floats(max_pos);
-  const size_t room = wfloats > used ? wfloats - used : 0;
-  const size_t per = room / (3 * kAttDV);
-  if (per < 36) return 0;
-  size_t tp = (per - 4) & ~(size_t)31;
-  if (tp > 2048) tp = 2048;
-  return (uint32_t)tp;
+  if (wfloats <= used) return;
+  const size_t room = wfloats - used;
+  for (uint32_t r = 4; r >= 3; --r) {
+    const size_t ts = room / ((size_t)r * kAttDV);
+    if (ts < 36) continue;
+    size_t t = (ts - 4) & ~(size_t)31;
+    if (t > 1024) t = 1024;
+    *tp = (uint32_t)t;
+    *nr = r;
+    return;
+  }
 }
 
 // Floats of the vector region (input vectors and scratch of every role),
@@ -190,18 +213,51 @@ __device__ __forceinline__ void put_word(gw* p, float v, uint32_t epoch) {
 
 __device__ __forceinline__ void stamp(const DecodeArgs& a, uint32_t l, uint32_t ph, uint32_t t,
                                       uint32_t slot) {
-  if (a.tline && threadIdx.x == 0 && t < kTimelineTasks)
+  if (a.tline && tid_x() == 0 && t < kTimelineTasks)
     ((AS_GLB uint64_t*)a.tline)[(((size_t)l * 6 + ph) * kTimelineTasks + t) * 4 + slot] =
         __builtin_amdgcn_s_memrealtime();
 }
 
+// s_waitcnt vmcnt(0) (expcnt, lgkmcnt fields at their maxima: no wait).
+// The builtin is a side effect without a memory operand, so the empty asm
+// statements pin the LDS accesses of the caller (the reads of rows that
+// this wave's global_load_lds copies filled) after it.
+__device__ __forceinline__ void wait_vm0() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0x0F70);
+  asm volatile("" ::: "memory");
+}
+
+// s_waitcnt vmcnt(n) for a run-time n.  n is clamped to the counter's 63:
+// once every load has been issued at most 63 are outstanding, and they are
+// the newest ones, so when more than 63 loads followed the ones waited for,
+// those have completed.
+__device__ __forceinline__ void wait_vmcnt(uint32_t n) {
+  switch (n < 63u ? n : 63u) {
+#define CIS2_VMW(k) \
+  case k:           \
+    __builtin_amdgcn_s_waitcnt(0x0F70 | ((k) & 15) | (((k) >> 4) << 14)); \
+    break;
+    CIS2_VMW(0) CIS2_VMW(1) CIS2_VMW(2) CIS2_VMW(3) CIS2_VMW(4) CIS2_VMW(5) CIS2_VMW(6)
+    CIS2_VMW(7) CIS2_VMW(8) CIS2_VMW(9) CIS2_VMW(10) CIS2_VMW(11) CIS2_VMW(12) CIS2_VMW(13)
+    CIS2_VMW(14) CIS2_VMW(15) CIS2_VMW(16) CIS2_VMW(17) CIS2_VMW(18) CIS2_VMW(19) CIS2_VMW(20)
+    CIS2_VMW(21) CIS2_VMW(22) CIS2_VMW(23) CIS2_VMW(24) CIS2_VMW(25) CIS2_VMW(26) CIS2_VMW(27)
+    CIS2_VMW(28) CIS2_VMW(29) CIS2_VMW(30) CIS2_VMW(31) CIS2_VMW(32) CIS2_VMW(33) CIS2_VMW(34)
+    CIS2_VMW(35) CIS2_VMW(36) CIS2_VMW(37) CIS2_VMW(38) CIS2_VMW(39) CIS2_VMW(40) CIS2_VMW(41)
+    CIS2_VMW(42) CIS2_VMW(43) CIS2_VMW(44) CIS2_VMW(45) CIS2_VMW(46) CIS2_VMW(47) CIS2_VMW(48)
+    CIS2_VMW(49) CIS2_VMW(50) CIS2_VMW(51) CIS2_VMW(52) CIS2_VMW(53) CIS2_VMW(54) CIS2_VMW(55)
+    CIS2_VMW(56) CIS2_VMW(57) CIS2_VMW(58) CIS2_VMW(59) CIS2_VMW(60) CIS2_VMW(61) CIS2_VMW(62)
+    default: __builtin_amdgcn_s_waitcnt(0x0F70 | 15 | (3 << 14)); break;
+#undef CIS2_VMW
+  }
+}
+
 // Waits until the n tagged words addr(0..n-1) carry `epoch` and copies their
-// values to dst[0..n-1].  Up to 12 words in flight per thread; longer
+// values to dst(0..n-1).  Up to M words in flight per thread; longer
 // vectors are gathered in slices.
-template <class F>
-__device__ __forceinline__ void gather(lf* dst, uint32_t n, uint32_t epoch, uint32_t* err,
-                                       uint32_t cap, F addr) {
-  constexpr int M = 12;
+template <int M = 12, class F, class D>
+__device__ __forceinline__ void gather_map(uint32_t n, uint32_t epoch, uint32_t* err,
+                                           uint32_t cap, F addr, D dst) {
   for (uint32_t base = 0; base < n; base += M * kThreads) {
     u64 w[M];
     uint32_t spins = 0;
@@ -229,10 +285,20 @@ __device__ __forceinline__ void gather(lf* dst, uint32_t n, uint32_t epoch, uint
 #pragma unroll
     for (int u = 0; u < M; ++u) {
       const uint32_t i = base + threadIdx.x + u * kThreads;
-      if (i < n) dst[i] = __uint_as_float((uint32_t)w[u]);
+      if (i < n) *dst(i) = __uint_as_float((uint32_t)w[u]);
     }
   }
+  // every global_load_lds copy this wave issued before (weight blocks, K
+  // or V tiles) has landed in LDS too: loads complete in issue order, and
+  // the wait makes that explicit for waves that polled no word
+  wait_vm0();
   __syncthreads();
+}
+// The same into dst[0..n-1].
+template <class F>
+__device__ __forceinline__ void gather(lf* dst, uint32_t n, uint32_t epoch, uint32_t* err,
+                                       uint32_t cap, F addr) {
+  gather_map(n, epoch, err, cap, addr, [=](uint32_t i) { return dst + i; });
 }
 
 __device__ __forceinline__ void gather_vec(lf* dst, const gw* src, uint32_t n,
@@ -246,7 +312,7 @@ __device__ __forceinline__ void gather_vec(lf* dst, const gw* src, uint32_t n,
 template <class F>
 __device__ __forceinline__ void copy_to_lds(lf4* dst, uint32_t n4, F src) {
   constexpr uint32_t B = 36;
-  for (uint32_t i = threadIdx.x; i < n4; i += B * kThreads) {
+  for (uint32_t i = tid_x(); i < n4; i += B * kThreads) {
     f4 t[B];
 #pragma unroll
     for (uint32_t u = 0; u < B; ++u)
@@ -262,7 +328,7 @@ __device__ __forceinline__ void copy_to_lds(lf4* dst, uint32_t n4, F src) {
 template <class F, class G>
 __device__ __forceinline__ void copy_map(uint32_t n4, F src, G dst) {
   constexpr uint32_t B = 16;
-  for (uint32_t i = threadIdx.x; i < n4; i += B * kThreads) {
+  for (uint32_t i = tid_x(); i < n4; i += B * kThreads) {
     f4 t[B];
 #pragma unroll
     for (uint32_t u = 0; u < B; ++u)
@@ -306,7 +372,7 @@ __device__ __forceinline__ void scale_rows(lf4* rows, uint32_t s4, uint32_t nrow
   if (nq >= 48) {
     // long rows: lanes take the groups of a row (most lanes busy), waves take
     // rows wv, wv + 4, ...; 8 rows' groups and factors are read first
-    const uint32_t wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const uint32_t wv = tid_x() >> 6, lane = tid_x() & 63;
     constexpr uint32_t RB = 8;
     for (uint32_t q = lane; q < nq; q += 64) {
       f4 cq = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -343,7 +409,7 @@ __device__ __forceinline__ void scale_rows(lf4* rows, uint32_t s4, uint32_t nrow
   // short rows: items over all threads
   const uint32_t total = nrows * nq;
   constexpr uint32_t B = 4;
-  for (uint32_t i0 = threadIdx.x; i0 < total; i0 += B * kThreads) {
+  for (uint32_t i0 = tid_x(); i0 < total; i0 += B * kThreads) {
     f4 v[B], c[B];
     uint32_t off[B];
 #pragma unroll
@@ -396,22 +462,13 @@ __device__ __forceinline__ void prefetch_rows(const float* W, uint32_t R, uint32
 __device__ __forceinline__ void prefetch_rows_async(const float* W, uint32_t R, uint32_t K,
                                                     uint32_t blk, lf* dst) {
   const uint32_t n4 = R * K / 4;
-  const uint32_t wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const uint32_t wv = __builtin_amdgcn_readfirstlane(tid_x() >> 6), lane = tid_x() & 63;
   gf4* src = G4(W + (size_t)blk * R * K);
   for (uint32_t i0 = wv * 64; i0 < n4; i0 += kThreads) {  // i0: wave-uniform
     if (i0 + lane < n4)
       __builtin_amdgcn_global_load_lds((const AS_GLB void*)(src + i0 + lane),
                                        (AS_LDS void*)((lf4*)dst + i0), 16, 0, 0);
   }
-}
-// s_waitcnt vmcnt(0) (expcnt, lgkmcnt fields at their maxima: no wait).
-// The builtin is a side effect without a memory operand, so the empty asm
-// statements pin the LDS accesses of the caller (the reads of rows that
-// this wave's global_load_lds copies filled) after it.
-__device__ __forceinline__ void wait_vm0() {
-  asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_waitcnt(0x0F70);
-  asm volatile("" ::: "memory");
 }
 
 // Workgroup barrier for LDS data only: waits for this wave's LDS
@@ -423,16 +480,6 @@ __device__ __forceinline__ void lds_barrier() {
   asm volatile("" ::: "memory");
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
-}
-
-// Row block blk of two matrices of the same shape, back to back in LDS.
-__device__ __forceinline__ void prefetch_rows2(const float* A, const float* B, uint32_t R,
-                                               uint32_t K, uint32_t blk, lf* dst) {
-  const size_t blkf = (size_t)R * K;
-  const uint32_t n4 = (uint32_t)(blkf / 4);
-  gf4* sa = G4(A + blk * blkf);
-  gf4* sb = G4(B + blk * blkf);
-  copy_to_lds((lf4*)dst, 2 * n4, [=](uint32_t i) { return i < n4 ? sa + i : sb + (i - n4); });
 }
 
 // ---------------------------------------------------------------------------
@@ -656,7 +703,7 @@ __device__ __forceinline__ void prod_ins(lf4* W4, const lf4* x4, uint32_t bf4, u
                                          uint32_t KG, uint32_t i0, uint32_t i1, uint32_t w,
                                          uint32_t nw, lf4* pad) {
   constexpr uint32_t GP = 64 / R, B = PROD_BATCH;
-  const uint32_t lane = threadIdx.x & 63;
+  const uint32_t lane = tid_x() & 63;
   const uint32_t lg = lane / R, lr = lane - (lane / R) * R;
   const bool live = lane < GP * R;
   for (uint32_t b = 0; b < nb; ++b) {
@@ -701,9 +748,9 @@ __device__ __forceinline__ float gemv_lds_t(lf* W, const lf* x, uint32_t K, uint
                                             lf4* pad) {
   constexpr uint32_t NC = 4, GP = 64 / R;
   // sizes are wave-uniform: keep them (and every bound derived from them) scalar
-  const uint32_t KG = __builtin_amdgcn_readfirstlane(K >> 2), lane = threadIdx.x & 63;
+  const uint32_t KG = __builtin_amdgcn_readfirstlane(K >> 2), lane = tid_x() & 63;
   nb = __builtin_amdgcn_readfirstlane(nb);
-  const uint32_t wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint32_t wv = __builtin_amdgcn_readfirstlane(tid_x() >> 6);
   lf4* W4 = (lf4*)W;
   const lf4* x4 = (const lf4*)x;
   const uint32_t bf4 = KG * R, nins = (KG + GP - 1) / GP;
@@ -732,11 +779,11 @@ __device__ __forceinline__ float gemv_lds_t(lf* W, const lf* x, uint32_t K, uint
 
 // Same order for any other block height (runtime stride, no overlap).
 __device__ float gemv_lds_any(uint32_t R, lf* W, const lf* x, uint32_t K, uint32_t nb) {
-  const uint32_t KG = K >> 2, wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const uint32_t KG = K >> 2, wv = tid_x() >> 6, lane = tid_x() & 63;
   lf4* W4 = (lf4*)W;
   const lf4* x4 = (const lf4*)x;
   const uint32_t bf4 = KG * R;
-  for (uint32_t i = threadIdx.x; i < nb * bf4; i += kThreads) {
+  for (uint32_t i = tid_x(); i < nb * bf4; i += kThreads) {
     const f4 xv = x4[(i % bf4) / R];
     f4 w = W4[i];
     w.x = w.x * xv.x;
@@ -783,14 +830,14 @@ template <uint32_t R>
 __device__ __forceinline__ float gemv_tree_t(uint32_t Rr, lf* W, const lf* x, uint32_t K,
                                              uint32_t nb, lf4* pad) {
   const uint32_t Rv = R ? R : Rr;
-  const uint32_t KG = __builtin_amdgcn_readfirstlane(K >> 2), lane = threadIdx.x & 63;
+  const uint32_t KG = __builtin_amdgcn_readfirstlane(K >> 2), lane = tid_x() & 63;
   nb = __builtin_amdgcn_readfirstlane(nb);
-  const uint32_t wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint32_t wv = __builtin_amdgcn_readfirstlane(tid_x() >> 6);
   lf4* W4 = (lf4*)W;
   const lf4* x4 = (const lf4*)x;
   const uint32_t bf4 = KG * Rv;
   const uint32_t KB = (KG + 7) / 8, items = nb * KB * Rv;
-  for (uint32_t it = threadIdx.x; it < items; it += kThreads) {
+  for (uint32_t it = tid_x(); it < items; it += kThreads) {
     const uint32_t r = it % Rv, q = it / Rv, kb = q % KB, b = q / KB;
     lf4* p = W4 + (size_t)b * bf4 + (size_t)kb * 8 * Rv + r;
     const lf4* xp = x4 + (size_t)kb * 8;
@@ -884,7 +931,7 @@ __device__ __forceinline__ float tree_col(const lf* p, uint32_t n, uint32_t st, 
 // RMSNorm of an LDS vector (code/cis2-fp/src/main.rs:245-260): squares
 // into `tmp`, one strict chain in wave 0, mean by a true divide,
 // inv = 1/sqrt(mean + eps), out = (x*inv)*w.  `out` may alias `tmp` or x.
-// The norm weights a thread scales with (elements threadIdx.x + 256u) are
+// The norm weights a thread scales with (elements tid_x() + 256u) are
 // loaded into registers before the input is waited for (load_normw), so the
 // scaling pass after the chain reads no global memory (n <= 1024; longer
 // vectors read the tail from global memory).
@@ -899,7 +946,7 @@ __device__ __forceinline__ NormW load_normw(const float* w_, uint32_t n) {
   gf* w = G(w_);
 #pragma unroll
   for (uint32_t u = 0; u < kNormRegs; ++u) {
-    const uint32_t i = threadIdx.x + u * kThreads;
+    const uint32_t i = tid_x() + u * kThreads;
     r.v[u] = i < n ? w[i] : 0.0f;
   }
   return r;
@@ -911,7 +958,7 @@ __device__ __forceinline__ void rmsnorm_lds(const lf* x, const NormW& w, float e
                                             lf* tmp, lf* out, lf* s_inv) {
   const uint32_t nb = (n + 31) / 32;
   if constexpr (TR) {
-    for (uint32_t t = threadIdx.x; t < nb; t += kThreads) {
+    for (uint32_t t = tid_x(); t < nb; t += kThreads) {
       float lv[32];
 #pragma unroll
       for (uint32_t i = 0; i < 32; ++i) {
@@ -921,30 +968,30 @@ __device__ __forceinline__ void rmsnorm_lds(const lf* x, const NormW& w, float e
       tmp[t] = tree32(lv);
     }
   } else {
-    for (uint32_t i = threadIdx.x; i < n; i += kThreads) {
+    for (uint32_t i = tid_x(); i < n; i += kThreads) {
       float v = x[i];
       tmp[i] = v * v;
     }
   }
   __syncthreads();
-  if (threadIdx.x < 64) {
+  if (tid_x() < 64) {
     const float acc = TR ? chain1(tmp, nb, 1, 0.0f) : chain_vec(tmp, n, 0.0f);
     float mean = acc / (float)n;
     float arg = mean + eps;
     float inv = rsqrt_cr(arg);
-    if (threadIdx.x == 0) *s_inv = inv;
+    if (tid_x() == 0) *s_inv = inv;
   }
   __syncthreads();
   const float inv = *s_inv;
 #pragma unroll
   for (uint32_t u = 0; u < kNormRegs; ++u) {
-    const uint32_t i = threadIdx.x + u * kThreads;
+    const uint32_t i = tid_x() + u * kThreads;
     if (i < n) {
       float sx = x[i] * inv;
       out[i] = sx * w.v[u];
     }
   }
-  for (uint32_t i = threadIdx.x + kNormRegs * kThreads; i < n; i += kThreads) {
+  for (uint32_t i = tid_x() + kNormRegs * kThreads; i < n; i += kThreads) {
     float sx = x[i] * inv;
     out[i] = sx * G(w.g)[i];
   }
@@ -989,9 +1036,9 @@ __device__ __forceinline__ Cand cand_wave_dpp(Cand c) {
 // Block-wide pick over the 4 waves' candidates (scratch: 8 words in LDS).
 __device__ __forceinline__ Cand cand_block(Cand c, AS_LDS uint32_t* red) {
   c = cand_wave_dpp(c);
-  if ((threadIdx.x & 63) == 0) {
-    red[2 * (threadIdx.x >> 6)] = __float_as_uint(c.v);
-    red[2 * (threadIdx.x >> 6) + 1] = c.i;
+  if ((tid_x() & 63) == 0) {
+    red[2 * (tid_x() >> 6)] = __float_as_uint(c.v);
+    red[2 * (tid_x() >> 6) + 1] = c.i;
   }
   __syncthreads();
   Cand b = {__uint_as_float(red[0]), red[1]};
@@ -1035,12 +1082,12 @@ __device__ __forceinline__ void run_qkv(const DecodeArgs& a, uint32_t l, uint32_
   lf* x = s.v;
   lf* ln = s.v + a.H;
   lf* s_inv = s.v + 2 * a.H;
-  if (!pre) prefetch_rows(g.W, a.Rq, a.H, g.blk, wl);
+  if (!pre) prefetch_rows_async(g.W, a.Rq, a.H, g.blk, wl);
   const NormW nw = load_normw(Lw.ln1, a.H);
   stamp(a, l, P_QKV, t, 0);
   if (l == 0) {
     gf* e = G(a.embed) + (size_t)tok * a.H;
-    for (uint32_t i = threadIdx.x; i < a.H; i += kThreads) x[i] = e[i];
+    for (uint32_t i = tid_x(); i < a.H; i += kThreads) x[i] = e[i];
     __syncthreads();
   } else {
     gather_vec(x, act_of(a, l - 1).hout, a.H, a);
@@ -1049,8 +1096,8 @@ __device__ __forceinline__ void run_qkv(const DecodeArgs& a, uint32_t l, uint32_
   rmsnorm_lds<TR>(x, nw, a.eps, a.H, ln, ln, s_inv);
   stamp(a, l, P_QKV, t, 3);
   const float acc = gemv_sel<TR, 8, 32, 8, 16>(a.Rq, wl, ln, a.H, 1, s.pad);
-  const uint32_t row = g.blk * a.Rq + threadIdx.x;
-  if (threadIdx.x < a.Rq && row < g.M) {
+  const uint32_t row = g.blk * a.Rq + tid_x();
+  if (tid_x() < a.Rq && row < g.M) {
     const float r = g.bias ? acc + G(g.bias)[row] : acc;
     put_word(g.out + row, r, a.epoch);
   }
@@ -1072,7 +1119,7 @@ __device__ __forceinline__ void prefetch_kv(const DecodeArgs& a, uint32_t l, uin
   lf4* v4 = (lf4*)vl;
   const uint32_t s4 = S >> 2;
   constexpr uint32_t B = 16;
-  for (uint32_t i0 = threadIdx.x; i0 < n4; i0 += B * kThreads) {
+  for (uint32_t i0 = tid_x(); i0 < n4; i0 += B * kThreads) {
     f4 tk[B], tv[B];
 #pragma unroll
     for (uint32_t u = 0; u < B; ++u) {
@@ -1156,8 +1203,8 @@ __device__ __forceinline__ void att_head_inputs(const DecodeArgs& a, uint32_t l,
   // cos/sin of this position for the pair this thread rotates (hd <= 256)
   const uint32_t half = hd / 2;
   float rc = 0.0f, rsn = 0.0f;
-  if (threadIdx.x < 2 * half) {
-    const uint32_t i = threadIdx.x < half ? threadIdx.x : threadIdx.x - half;
+  if (tid_x() < 2 * half) {
+    const uint32_t i = tid_x() < half ? tid_x() : tid_x() - half;
     gf* cs = G(a.rope_cs) + (size_t)pos * half * 2;
     rc = cs[2 * i];
     rsn = cs[2 * i + 1];
@@ -1169,8 +1216,8 @@ __device__ __forceinline__ void att_head_inputs(const DecodeArgs& a, uint32_t l,
   });
   if (Lw.qn) rmsnorm_lds<TR>(qv, nq, a.eps, hd, tmp, qv, misc);
   if (Lw.kn) rmsnorm_lds<TR>(kv, nk, a.eps, hd, tmp, kv, misc);
-  if (threadIdx.x < 2 * half) {
-    const uint32_t idx = threadIdx.x;
+  if (tid_x() < 2 * half) {
+    const uint32_t idx = tid_x();
     lf* hv = idx < half ? qv : kv;
     uint32_t i = idx < half ? idx : idx - half;
     float c = rc, sn = rsn;
@@ -1195,34 +1242,34 @@ template <bool TR>
 __device__ __forceinline__ void softmax_lds(lf* ss, uint32_t len, lf* part, lf* misc,
                                             AS_LDS uint32_t* red) {
   Cand best = {0.0f, UINT32_MAX};
-  for (uint32_t j = threadIdx.x; j < len; j += kThreads) {
+  for (uint32_t j = tid_x(); j < len; j += kThreads) {
     float v = ss[j];
     if (v == v) best = cand_pick(best, Cand{v, j});
   }
   const Cand b = cand_block(best, red);
   // the first maximum's own bits (a NaN at position 0 wins outright)
   const float mx = (ss[0] != ss[0] || b.i == UINT32_MAX) ? ss[0] : ss[b.i];
-  for (uint32_t j = threadIdx.x; j < len; j += kThreads) {
+  for (uint32_t j = tid_x(); j < len; j += kThreads) {
     float dlt = ss[j] - mx;
     ss[j] = exp_pinned(dlt);
   }
   __syncthreads();
   if constexpr (TR) {
     const uint32_t nbk = (len + 31) / 32;
-    for (uint32_t t = threadIdx.x; t < nbk; t += kThreads)
+    for (uint32_t t = tid_x(); t < nbk; t += kThreads)
       part[t] = tree_part(ss + 32 * t, len - 32 * t, 1);
     __syncthreads();
-    if (threadIdx.x < 64) {
+    if (tid_x() < 64) {
       const float acc = chain1(part, nbk, 1, 0.0f);
-      if (threadIdx.x == 0) misc[1] = acc;
+      if (tid_x() == 0) misc[1] = acc;
     }
-  } else if (threadIdx.x < 64) {
+  } else if (tid_x() < 64) {
     const float acc = chain_vec(ss, len, 0.0f);
-    if (threadIdx.x == 0) misc[1] = acc;
+    if (tid_x() == 0) misc[1] = acc;
   }
   __syncthreads();
   const float den = misc[1];
-  for (uint32_t j = threadIdx.x; j < len; j += kThreads) {
+  for (uint32_t j = tid_x(); j < len; j += kThreads) {
     float pj = ss[j] / den;
     ss[j] = pj;
   }
@@ -1234,7 +1281,7 @@ __device__ __forceinline__ void store_kv_pos(const DecodeArgs& a, uint32_t l, ui
                                              const lf* kv, const lf* vv) {
   AS_GLB float* kc = GW(a.kc0 + (size_t)l * a.cache_stride);
   AS_GLB float* vc = GW(a.vc0 + (size_t)l * a.cache_stride);
-  for (uint32_t d = threadIdx.x; d < a.hd; d += kThreads) {
+  for (uint32_t d = tid_x(); d < a.hd; d += kThreads) {
     kc[((size_t)kvh * a.hd + d) * a.max_pos + a.pos] = kv[d];
     vc[((size_t)kvh * a.hd + d) * a.max_pos + a.pos] = vv[d];
   }
@@ -1305,8 +1352,8 @@ template <bool TR>
 __device__ __forceinline__ void att_tail_block(const DecodeArgs& a, gw* out, lf* ss, uint32_t len,
                                                uint32_t pos, lf* vl, uint32_t S, const lf* vv,
                                                lf* part, lf* misc) {
-  const uint32_t lane = threadIdx.x & 63, hd = a.hd;
-  const uint32_t wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint32_t lane = tid_x() & 63, hd = a.hd;
+  const uint32_t wv = __builtin_amdgcn_readfirstlane(tid_x() >> 6);
   const float s0 = ss[0];
   float m = -__builtin_inff();
   for (uint32_t j0 = 0; j0 < len; j0 += 256) {  // four reads in flight per lane
@@ -1321,7 +1368,7 @@ __device__ __forceinline__ void att_tail_block(const DecodeArgs& a, gw* out, lf*
   }
   const float mx = s0 != s0 ? s0 : wave_max(m);
   lds_barrier();
-  for (uint32_t j = threadIdx.x; j < len; j += kThreads) {
+  for (uint32_t j = tid_x(); j < len; j += kThreads) {
     const float dlt = ss[j] - mx;
     ss[j] = exp_pinned(dlt);
   }
@@ -1340,7 +1387,7 @@ __device__ __forceinline__ void att_tail_block(const DecodeArgs& a, gw* out, lf*
   }
   lds_barrier();
   const float den = misc[1];
-  for (uint32_t j = threadIdx.x; j < len; j += kThreads) {
+  for (uint32_t j = tid_x(); j < len; j += kThreads) {
     const float pj = ss[j] / den;
     ss[j] = pj;
   }
@@ -1392,7 +1439,7 @@ __device__ __forceinline__ void run_att(const DecodeArgs& a, uint32_t l, uint32_
   const LayerW Lw = a.layers[l];
   const Act ac = act_of(a, l);
   const uint32_t hd = a.hd, group = a.nh / a.nkv, kvh = h / group, pos = a.pos, len = pos + 1;
-  const uint32_t wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const uint32_t wv = tid_x() >> 6, lane = tid_x() & 63;
   lf* qv = s.v;
   lf* kv = qv + hd;
   lf* vv = kv + hd;
@@ -1414,7 +1461,7 @@ __device__ __forceinline__ void run_att(const DecodeArgs& a, uint32_t l, uint32_
   if (in_lds) {
     // the lane of position j forms q[d] * k_j[d] from its K row and adds
     // them in order (or by tree32 blocks)
-    for (uint32_t j = threadIdx.x; j < len; j += kThreads) {
+    for (uint32_t j = tid_x(); j < len; j += kThreads) {
       const lf* kr = j < pos ? kt + (size_t)j * KS : kv;
       const float sj = score_dot<TR>(qv, kr, hd) * a.scale;
       ss[j] = sj;
@@ -1432,14 +1479,14 @@ __device__ __forceinline__ void run_att(const DecodeArgs& a, uint32_t l, uint32_
       __syncthreads();
       scale_rows_by_row((lf4*)kt, TS >> 2, hd, (n + 3) >> 2, qv);
       __syncthreads();
-      for (uint32_t jj = threadIdx.x; jj < n; jj += kThreads)
+      for (uint32_t jj = tid_x(); jj < n; jj += kThreads)
         ss[j0 + jj] = (TR ? tree_col(kt + jj, hd, TS, 0.0f) : chain1(kt + jj, hd, TS, 0.0f)) *
                       a.scale;
       __syncthreads();
     }
-    for (uint32_t d = threadIdx.x; d < hd; d += kThreads) tmp[d] = qv[d] * kv[d];
+    for (uint32_t d = tid_x(); d < hd; d += kThreads) tmp[d] = qv[d] * kv[d];
     __syncthreads();
-    if (threadIdx.x == 0)
+    if (tid_x() == 0)
       ss[pos] = (TR ? tree_col(tmp, hd, 1, 0.0f) : chain1(tmp, hd, 1, 0.0f)) * a.scale;
   }
   if (in_lds) {
@@ -1470,11 +1517,11 @@ __device__ __forceinline__ void run_att(const DecodeArgs& a, uint32_t l, uint32_
       const lf4* p4 = (const lf4*)(ss + j0);
       scale_rows_by_col((lf4*)vt, TS >> 2, hd, (n + 3) >> 2, p4);
       __syncthreads();
-      if (threadIdx.x < hd) acc = chain_vec(vt + (size_t)threadIdx.x * TS, n, acc);
+      if (tid_x() < hd) acc = chain_vec(vt + (size_t)tid_x() * TS, n, acc);
       __syncthreads();
     }
-    if (threadIdx.x < hd) {
-      const uint32_t d = threadIdx.x;
+    if (tid_x() < hd) {
+      const uint32_t d = tid_x();
       float p = ss[pos] * vv[d];
       acc = acc + p;
       put_word(ac.att + (size_t)h * hd + d, acc, a.epoch);
@@ -1502,17 +1549,17 @@ __device__ __forceinline__ void att_group_inputs(const DecodeArgs& a, uint32_t l
   if (Lw.qn) nq = load_normw(Lw.qn, hd);
   if (Lw.kn) nk = load_normw(Lw.kn, hd);
   float csv = 0.0f;
-  if (threadIdx.x < hd) csv = G(a.rope_cs)[(size_t)a.pos * hd + threadIdx.x];
+  if (tid_x() < hd) csv = G(a.rope_cs)[(size_t)a.pos * hd + tid_x()];
   const uint32_t nq_w = ng * hd;
   gather(qv, (ng + 2) * hd, a.epoch, a.err, a.spin_cap, [=](uint32_t i) {
     return i < nq_w ? ac.q + (size_t)kvh * nq_w + i
                     : (i < nq_w + hd ? ac.k : ac.v) + (size_t)kvh * hd + (i - nq_w) % hd;
   });
-  if (threadIdx.x < hd) cs[threadIdx.x] = csv;
+  if (tid_x() < hd) cs[tid_x()] = csv;
   if (Lw.qn || Lw.kn) {  // rmsnorm of each vector that has weights
     const uint32_t nb = (hd + 31) / 32;
     if constexpr (TR) {
-      for (uint32_t t = threadIdx.x; t < nv * nb; t += kThreads) {
+      for (uint32_t t = tid_x(); t < nv * nb; t += kThreads) {
         const uint32_t v = t / nb, b = t - v * nb;
         const lf* x = qv + (size_t)v * hd + 32 * b;
         float lv[32];
@@ -1524,26 +1571,26 @@ __device__ __forceinline__ void att_group_inputs(const DecodeArgs& a, uint32_t l
         tmp[t] = tree32(lv);
       }
     } else {
-      for (uint32_t i = threadIdx.x; i < nv * hd; i += kThreads) {
+      for (uint32_t i = tid_x(); i < nv * hd; i += kThreads) {
         const float xv = qv[i];
         tmp[i] = xv * xv;
       }
     }
     __syncthreads();
-    for (uint32_t v = threadIdx.x >> 6; v < nv; v += kThreads / 64) {
+    for (uint32_t v = tid_x() >> 6; v < nv; v += kThreads / 64) {
       const float acc = TR ? chain1(tmp + (size_t)v * nb, nb, 1, 0.0f)
                            : chain_vec(tmp + (size_t)v * hd, hd, 0.0f);
       float mean = acc / (float)hd;
       float arg = mean + a.eps;
       float inv = rsqrt_cr(arg);
-      if ((threadIdx.x & 63) == 0) misc[v] = inv;
+      if ((tid_x() & 63) == 0) misc[v] = inv;
     }
     __syncthreads();
     for (uint32_t v = 0; v < nv; ++v) {
       const float inv = misc[v];
       const float* wg = v < ng ? Lw.qn : Lw.kn;
       if (!wg) continue;
-      for (uint32_t i = threadIdx.x; i < hd; i += kThreads) {
+      for (uint32_t i = tid_x(); i < hd; i += kThreads) {
         const float wv = i < kThreads ? (v < ng ? nq.v[0] : nk.v[0]) : G(wg)[i];
         float sx = qv[(size_t)v * hd + i] * inv;
         qv[(size_t)v * hd + i] = sx * wv;
@@ -1551,7 +1598,7 @@ __device__ __forceinline__ void att_group_inputs(const DecodeArgs& a, uint32_t l
     }
   }
   __syncthreads();
-  for (uint32_t idx = threadIdx.x; idx < nv * half; idx += kThreads) {
+  for (uint32_t idx = tid_x(); idx < nv * half; idx += kThreads) {
     const uint32_t v = idx / half, i = idx - v * half;
     lf* hv = qv + (size_t)v * hd;
     float c = cs[2 * i], sn = cs[2 * i + 1];
@@ -1587,51 +1634,85 @@ __device__ __forceinline__ void att_group_inputs(const DecodeArgs& a, uint32_t l
 // Each head's K and V are read by many workgroups at once instead of
 // streaming through one.
 // ---------------------------------------------------------------------------
-constexpr uint32_t kScoreKB = 128;  // K dims a score thread holds in registers
+constexpr uint32_t kScoreKB = 128;       // most head dims of a score task
+constexpr uint32_t kScoreKT = kThreads;  // positions per K tile: one per thread
 
-// acc0 (and acc1 when `two`) continue over q0[i] * k[i] (q1[i] * k[i]),
-// i < nd: one left-to-right chain per head (dot_seq, math.rs:56-62) or
-// tree32 blocks folded in order (dot_tree, math.rs:75-93).  The products of
-// one 16-dim slice at a time are formed ahead of the chain's adds.
-template <bool TR>
-__device__ __forceinline__ void score_chains(const lf* q0, const lf* q1, bool two,
-                                             const float (&k)[kScoreKB], uint32_t nd,
-                                             float& acc0, float& acc1) {
-  if constexpr (TR) {
+// acc0 (and acc1 when TWO) continue over q0[d] * k[d] (q1[d] * k[d]),
+// d < hd: one left-to-right chain per head (dot_seq, math.rs:56-62) or
+// tree32 blocks folded in order (dot_tree, math.rs:75-93).  k is this
+// thread's column of the LDS K tile (k[d] at kp[d * kScoreKT]); q0 and q1
+// are 16-byte aligned LDS vectors read as broadcasts.  Blocks of 32 dims:
+// the block's k and q values are read into registers, then its products
+// formed and added.
+template <bool TR, bool TWO>
+__device__ __forceinline__ void score_cols(const lf* q0, const lf* q1, const lf* kp, uint32_t hd,
+                                           float& acc0, float& acc1) {
+  constexpr uint32_t B = TR ? 32 : 16;  // dims per block (tree32 blocks in tree order)
+  auto qe = [](const f4 (&q)[B / 4], uint32_t i) {
+    const f4 v = q[i / 4];
+    return i % 4 == 0 ? v.x : i % 4 == 1 ? v.y : i % 4 == 2 ? v.z : v.w;
+  };
 #pragma unroll
-    for (uint32_t b = 0; b < kScoreKB; b += 32) {
-      if (b < nd) {
+  for (uint32_t b = 0; b < kScoreKB; b += B) {
+    if (b < hd) {
+      float k[B];
+      f4 qa[B / 4], qb[B / 4];
+#pragma unroll
+      for (uint32_t i = 0; i < B; ++i)
+        if (b + i < hd) k[i] = kp[(b + i) * kScoreKT];
+#pragma unroll
+      for (uint32_t u = 0; u < B / 4; ++u)
+        if (b + 4 * u < hd) {
+          qa[u] = ((const lf4*)(q0 + b))[u];
+          if (TWO) qb[u] = ((const lf4*)(q1 + b))[u];
+        }
+      if constexpr (TR) {
         float l32[32];
 #pragma unroll
-        for (uint32_t i = 0; i < 32; ++i) l32[i] = b + i < nd ? q0[b + i] * k[b + i] : 0.0f;
+        for (uint32_t i = 0; i < 32; ++i) l32[i] = b + i < hd ? qe(qa, i) * k[i] : 0.0f;
         acc0 = acc0 + tree32(l32);
-        if (two) {
+        if (TWO) {
 #pragma unroll
-          for (uint32_t i = 0; i < 32; ++i) l32[i] = b + i < nd ? q1[b + i] * k[b + i] : 0.0f;
+          for (uint32_t i = 0; i < 32; ++i) l32[i] = b + i < hd ? qe(qb, i) * k[i] : 0.0f;
           acc1 = acc1 + tree32(l32);
         }
-      }
-      __builtin_amdgcn_sched_barrier(0);
-    }
-  } else {
+      } else {
 #pragma unroll
-    for (uint32_t b = 0; b < kScoreKB; b += 16) {
-      if (b < nd) {
-#pragma unroll
-        for (uint32_t i = b; i < b + 16; ++i) {
-          if (i < nd) {
-            const float p = q0[i] * k[i];
+        for (uint32_t i = 0; i < B; ++i) {
+          if (b + i < hd) {
+            const float p = qe(qa, i) * k[i];
             acc0 = acc0 + p;
-            if (two) {
-              const float p1 = q1[i] * k[i];
+            if (TWO) {
+              const float p1 = qe(qb, i) * k[i];
               acc1 = acc1 + p1;
             }
           }
         }
       }
-      __builtin_amdgcn_sched_barrier(0);
     }
+    __builtin_amdgcn_sched_barrier(0);
   }
+}
+
+// Copies kv head kvh's cached K rows (`krows`, row stride max_pos),
+// positions js .. js+n-1 rounded up to 4 (all < max_pos: js and max_pos are
+// multiples of 4 and js + n <= pos), into LDS rows of kScoreKT floats:
+// tile[d * kScoreKT + (j - js)] = k_j[d], d < hd.  global_load_lds_dwordx4,
+// one wave instruction per dim row (n <= kScoreKT = 4 * 64), waves take the
+// rows in turn; nothing is waited for (the data is in LDS once the issuing
+// wave's vmcnt reaches 0).
+__device__ __forceinline__ void copy_k_tile(lf* tile, const float* krows, uint32_t max_pos,
+                                            uint32_t hd, uint32_t js, uint32_t n) {
+  const uint32_t n4 = (n + 3) >> 2, lane = tid_x() & 63;
+  const uint32_t w = __builtin_amdgcn_readfirstlane(tid_x() >> 6);
+  // one running source pointer (no per-row address kept live across layers)
+  const float* src = krows + (size_t)w * max_pos + js + 4 * lane;
+  const size_t step = (size_t)(kThreads / 64) * max_pos;
+#pragma unroll 1
+  for (uint32_t d = w; d < hd; d += kThreads / 64, src += step)
+    if (lane < n4)
+      __builtin_amdgcn_global_load_lds((const AS_GLB void*)src,
+                                       (AS_LDS void*)((lf4*)(tile + (size_t)d * kScoreKT)), 16, 0, 0);
 }
 
 template <bool TR>
@@ -1653,52 +1734,46 @@ __device__ __forceinline__ void run_att_score(const DecodeArgs& a, uint32_t l, u
   lf* cs = vv + hd;                     // cos/sin pairs [hd]
   lf* tmp = cs + hd;                    // [(ng+1)*hd]
   lf* misc = tmp + (size_t)(ng + 1) * hd;
-  // kv head kvh's K rows as a buffer: one per-thread offset (the position)
-  // and a scalar offset per dim keep the column's loads off the vector
-  // registers' address pairs.  With stride 0 the hardware range check
-  // covers the per-thread offset only, not the per-dim scalar one, so the
-  // loads stay in bounds by their guards: jt < pos < max_pos, d0 + i < hd,
-  // and the host's hd * max_pos * 4 <= 2^31 - 1 check.
-  const __amdgpu_buffer_rsrc_t kbuf = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)(a.kc0 + (size_t)l * a.cache_stride + (size_t)kvh * hd * a.max_pos), (short)0,
-      (int)(hd * a.max_pos * 4), 0x00020000);
-  constexpr uint32_t kNone = UINT32_MAX;
-  float k[kScoreKB];
-  uint32_t held = kNone;  // first dim of the K block in k[] for position jt
-  uint32_t jt = j0 + threadIdx.x;
-  auto load_k = [&](uint32_t d0) {
-    const uint32_t nd = min(kScoreKB, hd - d0);
-    if (jt < pos) {
-#pragma unroll
-      for (uint32_t i = 0; i < kScoreKB; ++i)
-        if (i < nd)
-          k[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
-                                              kbuf, jt * 4, (d0 + i) * a.max_pos * 4, 0));
-    } else {
-#pragma unroll
-      for (uint32_t i = 0; i < kScoreKB; ++i)
-        if (i < nd) k[i] = kv[d0 + i];
-    }
-    held = d0;
+  // the cached K columns of kScoreKT positions at a time, [hd][kScoreKT]
+  // in the weight region; the first tile's copies land during the gather
+  // of this position's q, k and v
+  lf* ktile = s.w;
+  const float* krows = a.kc0 + (size_t)l * a.cache_stride + (size_t)kvh * hd * a.max_pos;
+  auto issue = [&](uint32_t js) {
+    const uint32_t je = min(pos, js + kScoreKT);
+    if (je > js) copy_k_tile(ktile, krows, a.max_pos, hd, js, je - js);
   };
+  issue(j0);
   att_group_inputs<TR>(a, l, kvh, qv, cs, tmp, misc);
   stamp(a, l, P_ATT, t, 1);
   if (pos < j0 + P) store_kv_pos(a, l, kvh, kv, vv);
   gw* sc = (gw*)a.scw + ((size_t)l * a.nh + (size_t)kvh * ng) * a.max_pos;
-  for (; jt < jend; jt += kThreads) {
-    for (uint32_t g0 = 0; g0 < ng; g0 += 2) {
-      const bool two = g0 + 1 < ng;
-      float a0 = 0.0f, a1 = 0.0f;
-      for (uint32_t d0 = 0; d0 < hd; d0 += kScoreKB) {
-        const uint32_t nd = min(kScoreKB, hd - d0);
-        if (held != d0) load_k(d0);
-        score_chains<TR>(qv + (size_t)g0 * hd + d0, qv + (size_t)(g0 + 1) * hd + d0, two, k, nd,
-                         a0, a1);
-      }
-      put_word(sc + (size_t)g0 * a.max_pos + jt, a0 * a.scale, a.epoch);
-      if (two) put_word(sc + (size_t)(g0 + 1) * a.max_pos + jt, a1 * a.scale, a.epoch);
+  for (uint32_t js = j0; js < jend; js += kScoreKT) {
+    if (js != j0) {
+      lds_barrier();  // every thread is done with the previous tile
+      issue(js);
     }
-    held = kNone;
+    wait_vm0();
+    lds_barrier();
+    if (pos >= js && pos < js + kScoreKT) {  // this position's own k into its column
+      for (uint32_t d = tid_x(); d < hd; d += kThreads) ktile[d * kScoreKT + (pos - js)] = kv[d];
+      lds_barrier();
+    }
+    const uint32_t jt = js + tid_x();
+    if (jt < jend) {
+      const lf* kp = ktile + tid_x();
+      for (uint32_t g0 = 0; g0 < ng; g0 += 2) {
+        float a0 = 0.0f, a1 = 0.0f;
+        const lf* q0 = qv + (size_t)g0 * hd;
+        if (g0 + 1 < ng) {
+          score_cols<TR, true>(q0, q0 + hd, kp, hd, a0, a1);
+          put_word(sc + (size_t)(g0 + 1) * a.max_pos + jt, a1 * a.scale, a.epoch);
+        } else {
+          score_cols<TR, false>(q0, q0, kp, hd, a0, a1);
+        }
+        put_word(sc + (size_t)g0 * a.max_pos + jt, a0 * a.scale, a.epoch);
+      }
+    }
   }
   stamp(a, l, P_ATT, t, 3);
   stamp(a, l, P_ATT, t, 2);
@@ -1708,14 +1783,13 @@ __device__ __forceinline__ void run_att_score(const DecodeArgs& a, uint32_t l, u
 // d % 3 == w - 1.  copy_v_rows copies positions j0 .. j0+n-1 (rounded up to
 // 4, inside max_pos) of those rows of a kv head's V cache (row stride
 // max_pos) into LDS rows of stride TS with global_load_lds_dwordx4, one wave
-// instruction per 256 positions, every one in flight; the data is in LDS
-// once this wave's vmcnt reaches 0.  scale_v_rows then forms the products
-// p_j * v_j[d] of the same rows in place (p at ss[j0..]): only the wave
-// that copied a row touches it until the next barrier.
+// instruction per row and 256 positions; the data is in LDS once this
+// wave's vmcnt has counted those instructions.  Only the wave that copied a
+// row touches it until the next barrier.
 __device__ __forceinline__ void copy_v_rows(lf* dst, const float* vrows, uint32_t max_pos,
                                             uint32_t nd, uint32_t j0, uint32_t n, uint32_t TS) {
-  const uint32_t n4 = (n + 3) >> 2, lane = threadIdx.x & 63;
-  const uint32_t w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint32_t n4 = (n + 3) >> 2, lane = tid_x() & 63;
+  const uint32_t w = __builtin_amdgcn_readfirstlane(tid_x() >> 6);
   for (uint32_t d = w - 1; d < nd; d += 3)
     for (uint32_t q0 = 0; q0 < n4; q0 += 64)
       if (q0 + lane < n4)
@@ -1723,83 +1797,200 @@ __device__ __forceinline__ void copy_v_rows(lf* dst, const float* vrows, uint32_
             (const AS_GLB void*)(G4(vrows + (size_t)d * max_pos + j0) + q0 + lane),
             (AS_LDS void*)((lf4*)(dst + (size_t)d * TS) + q0), 16, 0, 0);
 }
-__device__ __forceinline__ void scale_v_rows(lf* dst, const lf* ss, uint32_t nd, uint32_t j0,
-                                             uint32_t n, uint32_t TS) {
-  const uint32_t n4 = (n + 3) >> 2, lane = threadIdx.x & 63;
-  const uint32_t w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const lf4* p4 = (const lf4*)(ss + j0);
-  for (uint32_t d = w - 1; d < nd; d += 3) {
-    lf4* r4 = (lf4*)(dst + (size_t)d * TS);
-    for (uint32_t q = lane; q < n4; q += 64) {
-      const f4 f = p4[q], v = r4[q];
-      f4 y;
-      y.x = f.x * v.x;
-      y.y = f.y * v.y;
-      y.z = f.z * v.z;
-      y.w = f.w * v.w;
-      r4[q] = y;
-    }
+
+// Softmax of one head's scores ss[0..len) up to the denominator (the
+// divide follows in the V mix):
+//  1. the value of the first maximum (a DPP block reduction over the
+//     non-NaN scores; a NaN at position 0, or scores that are all NaN, give
+//     NaN); where its bits could differ (+0 against -0), e_j =
+//     exp(s_j - max) does not: both give exp(+-0) = 1;
+//  2. e_j = exp(s_j - max) in place;
+//  3. the denominator: a strict chain (sequential order) that wave 0 runs
+//     over blocks of 1024 positions while waves 1..3 form the next block's
+//     e_j; or tree32 blocks (partials in `part`) folded from 0 (tree
+//     order).
+// Returns the denominator in every thread (after a barrier).
+template <bool TR>
+__device__ __forceinline__ float softmax_head(lf* ss, uint32_t len, lf* part, lf* misc,
+                                              AS_LDS uint32_t* red) {
+  const uint32_t wv = __builtin_amdgcn_readfirstlane(tid_x() >> 6);
+  Cand best = {0.0f, UINT32_MAX};
+  for (uint32_t j = tid_x(); j < len; j += kThreads) {
+    const float v = ss[j];
+    if (v == v) best = cand_pick(best, Cand{v, j});
   }
+  const Cand b = cand_block(best, red);
+  const float mx = (ss[0] != ss[0] || b.i == UINT32_MAX) ? ss[0] : ss[b.i];
+  // e_j for positions [j0, j1) by threads t0, t0 + nthr, ...: each
+  // thread's reads before its writes
+  auto exps = [&](uint32_t j0, uint32_t j1, uint32_t t0, uint32_t nthr) {
+    for (uint32_t jb = j0 + t0; jb < j1; jb += 4 * nthr) {
+      float v[4];
+#pragma unroll
+      for (uint32_t k = 0; k < 4; ++k)
+        if (jb + k * nthr < j1) v[k] = ss[jb + k * nthr];
+#pragma unroll
+      for (uint32_t k = 0; k < 4; ++k)
+        if (jb + k * nthr < j1) {
+          const float dlt = v[k] - mx;
+          ss[jb + k * nthr] = exp_pinned(dlt);
+        }
+    }
+  };
+  if constexpr (TR) {
+    exps(0, len, tid_x(), kThreads);
+    __syncthreads();
+    const uint32_t nbk = (len + 31) / 32;
+    for (uint32_t t = tid_x(); t < nbk; t += kThreads)
+      part[t] = tree_part(ss + 32 * t, len - 32 * t, 1);
+    __syncthreads();
+    if (wv == 0) {
+      const float acc = chain1(part, nbk, 1, 0.0f);
+      if (tid_x() == 0) misc[1] = acc;
+    }
+  } else {
+    constexpr uint32_t EB = 1024;
+    const uint32_t nb = (len + EB - 1) / EB;
+    exps(0, min(len, EB), tid_x(), kThreads);
+    __syncthreads();
+    float acc = 0.0f;
+    for (uint32_t bb = 0; bb < nb; ++bb) {
+      if (wv == 0)
+        acc = chain_vec(ss + bb * EB, min(EB, len - bb * EB), acc);
+      else if (bb + 1 < nb)
+        exps((bb + 1) * EB, min(len, (bb + 2) * EB), tid_x() - 64, kThreads - 64);
+      lds_barrier();
+    }
+    if (tid_x() == 0) misc[1] = acc;
+  }
+  __syncthreads();
+  return misc[1];
 }
 
+// Mix task u = (query head h, dim slice dc): output dims d0 = dc*16 ..
+// d0+15 of head h:
+//  - waves 1..3 start copying the first V tiles (a ring of nr tiles of tp
+//    positions, each wave its own rows) before the scores arrive;
+//  - the head's scores are gathered and softmax_head forms e_j and the
+//    denominator;
+//  - the whole workgroup divides: p_j = e_j / den in place;
+//  - lane d of wave 0 then runs one left-to-right V-mix chain
+//    out_d = fold_j (p_j * v_j[d]) over tile i while waves 1..3 form tile
+//    i+1's products p_j * v_j[d] in place from their own rows (waiting only
+//    for those rows' copies) and copy tile i+nr-1 into the slot tile i-1
+//    left;
+//  - this position's own v (gathered) is added last (main.rs:454-463).
+// One barrier per tile.
 template <bool TR>
 __device__ __forceinline__ void run_att_mix(const DecodeArgs& a, uint32_t l, uint32_t u,
                                             const Lds& s) {
   const Act ac = act_of(a, l);
   const uint32_t DVc = a.att_dvc, h = u / DVc, dc = u - h * DVc;
   const uint32_t hd = a.hd, kvh = h / (a.nh / a.nkv), pos = a.pos, len = pos + 1;
-  const uint32_t d0 = dc * kAttDV, nd = min(kAttDV, hd - d0);
+  const uint32_t d0 = dc * kAttDV, nd = hd % kAttDV == 0 ? kAttDV : min(kAttDV, hd - d0);
   const uint32_t t = a.natt_s + u;
-  const bool loader = (threadIdx.x >> 6) != 0;  // waves 1..3 copy and scale V tiles
+  const uint32_t wv = __builtin_amdgcn_readfirstlane(tid_x() >> 6), lane = tid_x() & 63;
+  const bool loader = wv != 0;  // waves 1..3 copy V tiles and form products
   lf* vv = s.v;        // v of this position, dims d0.. [kAttDV]
   lf* misc = vv + 64;  // [1] den, [4..] reduction scratch
   AS_LDS uint32_t* red = (AS_LDS uint32_t*)(misc + 4);
-  lf* ss = s.w;                    // scores / probabilities [max_pos + 64]
+  lf* ss = s.w;                    // scores -> e_j -> p_j [max_pos + 64]
   lf* part = ss + a.max_pos + 64;  // tree partials
-  const uint32_t TP = a.att_tp, TS = TP + 4, nt = (pos + TP - 1) / TP;
-  lf* vt0 = part + att_part_floats(a.max_pos);  // three V tiles [kAttDV][TS]
-  auto tile = [=](uint32_t i) { return vt0 + (size_t)(i % 3) * kAttDV * TS; };
+  const uint32_t TP = a.att_tp, TS = TP + 4, NR = a.att_nr, nt = (pos + TP - 1) / TP;
+  lf* ring = part + att_part_floats(a.max_pos);  // NR tiles [16][TS]
+  auto tile = [=](uint32_t i) { return ring + (size_t)(i % NR) * kAttDV * TS; };
   auto tile_n = [=](uint32_t i) { return min(TP, pos - i * TP); };
   const float* vrows = a.vc0 + (size_t)l * a.cache_stride + ((size_t)kvh * hd + d0) * a.max_pos;
+  // copy instructions of this wave per tile: its rows (d < nd, d % 3 ==
+  // wv - 1) times one per 256 positions
+  const uint32_t myrows = (loader && nd >= wv) ? (nd - wv + 3) / 3 : 0;
+  auto copies = [=](uint32_t i) { return myrows * ((tile_n(i) + 255) / 256); };
   stamp(a, l, P_ATT, t, 0);
-  // the first two V tiles land during the gather and the softmax
-  if (loader) {
-    if (nt > 0) copy_v_rows(tile(0), vrows, a.max_pos, nd, 0, tile_n(0), TS);
-    if (nt > 1) copy_v_rows(tile(1), vrows, a.max_pos, nd, TP, tile_n(1), TS);
-  }
-  gather(ss, len, a.epoch, a.err, a.spin_cap, [=](uint32_t i) {
-    return (const gw*)a.scw + ((size_t)l * a.nh + h) * a.max_pos + i;
-  });
-  gather(vv, nd, a.epoch, a.err, a.spin_cap, [=](uint32_t i) { return ac.v + (size_t)kvh * hd + d0 + i; });
+  uint32_t issued = 0;  // tiles whose copies have been issued (the same in every wave)
+  auto refill = [&]() {
+    if (issued < nt) {
+      if (loader) copy_v_rows(tile(issued), vrows, a.max_pos, nd, issued * TP, tile_n(issued), TS);
+      ++issued;
+    }
+  };
+  // the ring less the tile being formed next: nr - 1 tiles land during the
+  // gather and the softmax
+  while (issued < nt && issued + 1 < NR) refill();
+  gather_map<17>(len, a.epoch, a.err, a.spin_cap,
+                 [=](uint32_t i) { return (const gw*)a.scw + ((size_t)l * a.nh + h) * a.max_pos + i; },
+                 [=](uint32_t i) { return ss + i; });
+  gather(vv, nd, a.epoch, a.err, a.spin_cap,
+         [=](uint32_t i) { return ac.v + (size_t)kvh * hd + d0 + i; });
   stamp(a, l, P_ATT, t, 1);
-  __syncthreads();
-  softmax_lds<TR>(ss, len, part, misc, red);
+  const float den = softmax_head<TR>(ss, len, part, misc, red);
   stamp(a, l, P_ATT, t, 3);
-  // out_d = fold_j (p_j * v_j[d]) (main.rs:454-463): lane d of wave 0
-  // continues one left-to-right chain over tile i while waves 1..3 form the
-  // products of tile i+1 and start copying tile i+2
-  if (loader && nt > 0) {
-    wait_vm0();
-    scale_v_rows(tile(0), ss, nd, 0, tile_n(0), TS);
+  // p_j = e_j / den for positions [0, pos), by all waves (each thread's
+  // reads before its writes); this position's own p stays in registers
+  {
+    constexpr uint32_t B = 4;
+    for (uint32_t jb = tid_x(); jb < pos; jb += B * kThreads) {
+      float e[B];
+#pragma unroll
+      for (uint32_t k = 0; k < B; ++k)
+        if (jb + k * kThreads < pos) e[k] = ss[jb + k * kThreads];
+#pragma unroll
+      for (uint32_t k = 0; k < B; ++k)
+        if (jb + k * kThreads < pos) {
+          const float pj = e[k] / den;
+          ss[jb + k * kThreads] = pj;
+        }
+    }
   }
-  __syncthreads();
+  const float p_pos = ss[pos] / den;
+  lds_barrier();
+  // products of this wave's rows of tile i in place: v_j[d] <- p_j * v_j[d]
+  auto products = [&](uint32_t i) {
+    const uint32_t n4 = (tile_n(i) + 3) >> 2;
+    const lf4* p4 = (const lf4*)(ss + i * TP);
+    lf* tt = tile(i);
+    for (uint32_t d = wv - 1; d < nd; d += 3) {
+      lf4* r4 = (lf4*)(tt + (size_t)d * TS);
+      for (uint32_t q = lane; q < n4; q += 64) {
+        const f4 f = p4[q], v = r4[q];
+        f4 y;
+        y.x = f.x * v.x;
+        y.y = f.y * v.y;
+        y.z = f.z * v.z;
+        y.w = f.w * v.w;
+        r4[q] = y;
+      }
+    }
+  };
+  // tile `need` is in LDS once only the copies issued after it are outstanding
+  auto landed = [&](uint32_t need) {
+    uint32_t after = 0;
+    for (uint32_t k = need + 1; k < issued; ++k) after += copies(k);
+    wait_vmcnt(after);
+  };
+  if (nt > 0) {
+    if (loader) {
+      landed(0);
+      products(0);
+    }
+    refill();  // the slot before tile 0's in the ring
+    lds_barrier();
+  }
   float acc = 0.0f;
   for (uint32_t i = 0; i < nt; ++i) {
     if (!loader) {
-      if (threadIdx.x < nd) acc = chain_vec(tile(i) + (size_t)threadIdx.x * TS, tile_n(i), acc);
-    } else {
-      if (i + 1 < nt) {
-        wait_vm0();
-        scale_v_rows(tile(i + 1), ss, nd, (i + 1) * TP, tile_n(i + 1), TS);
-      }
-      if (i + 2 < nt) copy_v_rows(tile(i + 2), vrows, a.max_pos, nd, (i + 2) * TP, tile_n(i + 2), TS);
+      if (lane < nd) acc = chain_vec(tile(i) + (size_t)lane * TS, tile_n(i), acc);
+    } else if (i + 1 < nt) {
+      landed(i + 1);
+      products(i + 1);
     }
-    lds_barrier();  // tile i+2's copy stays in flight (waited for before its products)
+    // tile i-1's slot is free (chained before the last barrier)
+    if (i >= 1) refill();
+    lds_barrier();
   }
-  if (threadIdx.x < nd) {
-    const float p = ss[pos] * vv[threadIdx.x];
+  if (!loader && lane < nd) {
+    const float p = p_pos * vv[lane];
     acc = acc + p;
-    put_word(ac.att + (size_t)h * hd + d0 + threadIdx.x, acc, a.epoch);
+    put_word(ac.att + (size_t)h * hd + d0 + lane, acc, a.epoch);
   }
   stamp(a, l, P_ATT, t, 2);
 }
@@ -1813,11 +2004,11 @@ __device__ __forceinline__ void run_o(const DecodeArgs& a, uint32_t l, uint32_t 
   const uint32_t qd = a.qd, r0 = t * a.Ro, nr = min(a.Ro, a.H - r0);
   lf* x = s.v;        // attention output [qd]
   lf* hres = x + qd;  // this block's residual rows [nr]
-  if (!pre) prefetch_rows(Lw.wo, a.Ro, qd, t, wl);
+  if (!pre) prefetch_rows_async(Lw.wo, a.Ro, qd, t, wl);
   stamp(a, l, P_O, t, 0);
   if (l == 0) {
     gf* e = G(a.embed) + (size_t)tok * a.H + r0;
-    for (uint32_t i = threadIdx.x; i < nr; i += kThreads) hres[i] = e[i];
+    for (uint32_t i = tid_x(); i < nr; i += kThreads) hres[i] = e[i];
     gather_vec(x, ac.att, qd, a);
   } else {
     const gw* hin = act_of(a, l - 1).hout + r0;
@@ -1828,7 +2019,7 @@ __device__ __forceinline__ void run_o(const DecodeArgs& a, uint32_t l, uint32_t 
   stamp(a, l, P_O, t, 1);
   const float acc = gemv_sel<TR, 8, 32, 18, 8>(a.Ro, wl, x, qd, 1, s.pad);
   stamp(a, l, P_O, t, 3);
-  if (threadIdx.x < nr) put_word(ac.h1 + r0 + threadIdx.x, hres[threadIdx.x] + acc, a.epoch);
+  if (tid_x() < nr) put_word(ac.h1 + r0 + tid_x(), hres[tid_x()] + acc, a.epoch);
   stamp(a, l, P_O, t, 2);
 }
 
@@ -1843,7 +2034,10 @@ __device__ __forceinline__ void run_gu(const DecodeArgs& a, uint32_t l, uint32_t
   lf* ln = x + a.H;
   lf* gx = ln + a.H;  // 64 floats: gate results
   lf* s_inv = gx + 64;
-  if (!pre) prefetch_rows2(Lw.wg, Lw.wu, a.Rg, a.H, t, wl);
+  if (!pre) {
+    prefetch_rows_async(Lw.wg, a.Rg, a.H, t, wl);
+    prefetch_rows_async(Lw.wu, a.Rg, a.H, t, wl + a.Rg * a.H);
+  }
   const NormW nw = load_normw(Lw.ln2, a.H);
   stamp(a, l, P_GU, t, 0);
   gather_vec(x, ac.h1, a.H, a);
@@ -1851,7 +2045,7 @@ __device__ __forceinline__ void run_gu(const DecodeArgs& a, uint32_t l, uint32_t
   rmsnorm_lds<TR>(x, nw, a.eps, a.H, ln, ln, s_inv);
   stamp(a, l, P_GU, t, 3);
   const float acc = gemv_sel<TR, 8, 16, 8>(a.Rg, wl, ln, a.H, 2, s.pad);
-  const uint32_t wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const uint32_t wv = tid_x() >> 6, lane = tid_x() & 63;
   if (wv == 0) gx[lane] = acc;
   __syncthreads();
   if (wv == 1) {
@@ -1873,7 +2067,7 @@ __device__ __forceinline__ void run_d(const DecodeArgs& a, uint32_t l, uint32_t 
   const uint32_t I = a.I, r0 = t * a.Rd, nr = min(a.Rd, a.H - r0);
   lf* x = s.v;       // hid [I]
   lf* hres = x + I;  // residual rows [nr]
-  if (!pre) prefetch_rows(Lw.wd, a.Rd, I, t, wl);
+  if (!pre) prefetch_rows_async(Lw.wd, a.Rd, I, t, wl);
   stamp(a, l, P_D, t, 0);
   const gw* h1 = ac.h1 + r0;
   const gw* hid = ac.hid;
@@ -1884,7 +2078,7 @@ __device__ __forceinline__ void run_d(const DecodeArgs& a, uint32_t l, uint32_t 
   // deeper rings slowed the shorter GEMVs, measured)
   const float acc = gemv_sel<TR, 0, 32, 24, 12, 8>(a.Rd, wl, x, I, 1, s.pad);
   stamp(a, l, P_D, t, 3);
-  if (threadIdx.x < nr) put_word(ac.hout + r0 + threadIdx.x, hres[threadIdx.x] + acc, a.epoch);
+  if (tid_x() < nr) put_word(ac.hout + r0 + tid_x(), hres[tid_x()] + acc, a.epoch);
   stamp(a, l, P_D, t, 2);
 }
 
@@ -1915,10 +2109,10 @@ __device__ __forceinline__ gf4* lm_row_addr(const DecodeArgs& a, const LmRows& m
   return G4(a.lm) + ((size_t)b * KG + g) * 32 + m.r;
 }
 __device__ __forceinline__ void lm_rows_start(const DecodeArgs& a, LmRows& m) {
-  const uint32_t wg = blockIdx.x, lane = threadIdx.x & 63;
+  const uint32_t wg = blockIdx.x, lane = tid_x() & 63;
   m.nbw = wg < a.nl ? (a.nl - 1 - wg) / a.nwg + 1 : 0;
   m.total = ((m.nbw + 7) / 8) * (a.H >> 2);
-  m.slot = (threadIdx.x >> 6) * 2 + (lane >> 5);
+  m.slot = (tid_x() >> 6) * 2 + (lane >> 5);
   m.r = lane & 31;
   if (m.nbw == 0) return;
 #pragma unroll
@@ -1927,7 +2121,7 @@ __device__ __forceinline__ void lm_rows_start(const DecodeArgs& a, LmRows& m) {
 // The rows' chains, logits and per-block candidates; returns the number of
 // blocks this workgroup published.
 __device__ __forceinline__ uint32_t lm_rows_run(const DecodeArgs& a, LmRows& m, const lf* hn) {
-  const uint32_t KG = a.H >> 2, lane = threadIdx.x & 63;
+  const uint32_t KG = a.H >> 2, lane = tid_x() & 63;
   if (m.nbw == 0) return 0;
   AS_GLB float* logits = GW(a.logits);
   const lf4* hn4 = (const lf4*)hn;
@@ -1962,7 +2156,7 @@ __device__ __forceinline__ uint32_t lm_rows_run(const DecodeArgs& a, LmRows& m, 
 #pragma unroll
       for (uint32_t h = 0; h < 2; ++h) {  // the candidate of each half-wave's block
         const Cand ch = cand_wave_dpp((lane >> 5) == h ? c : Cand{0.0f, UINT32_MAX});
-        const uint32_t ih = (t0 / KG) * 8 + (threadIdx.x >> 6) * 2 + h;
+        const uint32_t ih = (t0 / KG) * 8 + (tid_x() >> 6) * 2 + h;
         if (lane == 0 && ih < m.nbw)
           __hip_atomic_store((gw*)a.cand + blockIdx.x + ih * a.nwg,
                              ((u64)ch.i << 32) | __float_as_uint(ch.v), __ATOMIC_RELAXED,
@@ -1977,7 +2171,7 @@ __device__ __forceinline__ uint32_t lm_rows_run(const DecodeArgs& a, LmRows& m, 
 template <bool TR>
 __device__ __forceinline__ void run_lm(const DecodeArgs& a, const Lds& s) {
   const uint32_t L = a.L, wg = blockIdx.x;
-  const uint32_t wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const uint32_t wv = tid_x() >> 6, lane = tid_x() & 63;
   lf* x = s.v;
   lf* hn = x + a.H;
   lf* misc = hn + a.H;
@@ -2052,7 +2246,7 @@ __device__ __forceinline__ void run_lm(const DecodeArgs& a, const Lds& s) {
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
   __shared__ uint32_t s_last;
-  if (threadIdx.x == 0) {
+  if (tid_x() == 0) {
     uint32_t before =
         __hip_atomic_fetch_add(GU(a.cnt), done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     s_last = (before + done == a.lm_epoch * a.nl) ? 1u : 0u;
@@ -2063,7 +2257,7 @@ __device__ __forceinline__ void run_lm(const DecodeArgs& a, const Lds& s) {
   // in flight
   Cand c = {0.0f, UINT32_MAX};
   const gw* cw = (const gw*)a.cand;
-  for (uint32_t b0 = threadIdx.x; b0 < a.nl; b0 += 8 * kThreads) {
+  for (uint32_t b0 = tid_x(); b0 < a.nl; b0 += 8 * kThreads) {
     u64 w[8];
 #pragma unroll
     for (uint32_t u = 0; u < 8; ++u)
@@ -2074,7 +2268,7 @@ __device__ __forceinline__ void run_lm(const DecodeArgs& a, const Lds& s) {
         c = cand_pick(c, Cand{__uint_as_float((uint32_t)w[u]), (uint32_t)(w[u] >> 32)});
   }
   const Cand r = cand_block(c, red);
-  if (threadIdx.x == 0) {
+  if (tid_x() == 0) {
     const uint32_t first_nan = ld_ag(a.cand + 2 * a.nl);
     *GU(a.tok_out) = (first_nan || r.i == UINT32_MAX) ? 0u : r.i;
   }
@@ -2205,7 +2399,7 @@ void k_decode(DecodeArgs a) {
   if (reads_tok) {
     tok = *(const AS_GLB uint32_t*)a.tok_in;
     if (tok >= a.V) {
-      if (threadIdx.x == 0) raise_err(a.err, 1u);
+      if (tid_x() == 0) raise_err(a.err, 1u);
       tok = 0;
     }
   }
@@ -2258,32 +2452,8 @@ void k_gemv_blk(const float* __restrict__ W, const float* __restrict__ x, float*
   copy_to_lds((lf4*)w, n4 + k4, [=](uint32_t i) { return i < n4 ? src + i : x4 + (i - n4); });
   __syncthreads();
   const float acc = gemv_lds_t<R>(w, xs, K, 1, pad);
-  const uint32_t row = b * R + threadIdx.x;
-  if (threadIdx.x < R && row < M) GW(y)[row] = acc;
-}
-
-// s_waitcnt vmcnt(n) for a run-time n.  n is clamped to the counter's 63:
-// once every load has been issued at most 63 are outstanding, and they are
-// the newest ones, so when more than 63 loads followed the ones waited for,
-// those have completed.
-__device__ __forceinline__ void wait_vmcnt(uint32_t n) {
-  switch (n < 63u ? n : 63u) {
-#define CIS2_VMW(k) \
-  case k:           \
-    __builtin_amdgcn_s_waitcnt(0x0F70 | ((k) & 15) | (((k) >> 4) << 14)); \
-    break;
-    CIS2_VMW(0) CIS2_VMW(1) CIS2_VMW(2) CIS2_VMW(3) CIS2_VMW(4) CIS2_VMW(5) CIS2_VMW(6)
-    CIS2_VMW(7) CIS2_VMW(8) CIS2_VMW(9) CIS2_VMW(10) CIS2_VMW(11) CIS2_VMW(12) CIS2_VMW(13)
-    CIS2_VMW(14) CIS2_VMW(15) CIS2_VMW(16) CIS2_VMW(17) CIS2_VMW(18) CIS2_VMW(19) CIS2_VMW(20)
-    CIS2_VMW(21) CIS2_VMW(22) CIS2_VMW(23) CIS2_VMW(24) CIS2_VMW(25) CIS2_VMW(26) CIS2_VMW(27)
-    CIS2_VMW(28) CIS2_VMW(29) CIS2_VMW(30) CIS2_VMW(31) CIS2_VMW(32) CIS2_VMW(33) CIS2_VMW(34)
-    CIS2_VMW(35) CIS2_VMW(36) CIS2_VMW(37) CIS2_VMW(38) CIS2_VMW(39) CIS2_VMW(40) CIS2_VMW(41)
-    CIS2_VMW(42) CIS2_VMW(43) CIS2_VMW(44) CIS2_VMW(45) CIS2_VMW(46) CIS2_VMW(47) CIS2_VMW(48)
-    CIS2_VMW(49) CIS2_VMW(50) CIS2_VMW(51) CIS2_VMW(52) CIS2_VMW(53) CIS2_VMW(54) CIS2_VMW(55)
-    CIS2_VMW(56) CIS2_VMW(57) CIS2_VMW(58) CIS2_VMW(59) CIS2_VMW(60) CIS2_VMW(61) CIS2_VMW(62)
-    default: __builtin_amdgcn_s_waitcnt(0x0F70 | 15 | (3 << 14)); break;
-#undef CIS2_VMW
-  }
+  const uint32_t row = b * R + tid_x();
+  if (tid_x() < R && row < M) GW(y)[row] = acc;
 }
 
 // 16-byte global->LDS loads (global_load_lds_dwordx4) of the 64-slot runs
@@ -2294,7 +2464,7 @@ __device__ __forceinline__ void wait_vmcnt(uint32_t n) {
 // load instructions is exact).  Returns that count (wave-uniform).
 __device__ __forceinline__ uint32_t load_runs(gf4* src, lf4* dst, uint32_t n4, uint32_t i0,
                                               uint32_t i1, uint32_t w, uint32_t nw) {
-  const uint32_t lane = threadIdx.x & 63;
+  const uint32_t lane = tid_x() & 63;
   uint32_t cnt = 0;
   for (uint32_t ins = i0 + w; ins < i1; ins += nw) {
     const uint32_t s0 = ins * 64;
@@ -2327,7 +2497,7 @@ void k_gemv_pipe(const float* __restrict__ W, const float* __restrict__ x, float
   lf4* xs = w4 + N4 + 64;    // x, then 64 slots of room
   lf4* pad = xs + KG + 64;   // prod_ins's idle-lane slots
   const uint32_t b = blockIdx.x;
-  const uint32_t wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint32_t wv = __builtin_amdgcn_readfirstlane(tid_x() >> 6);
   gf4* src = G4(W + (size_t)b * R * K);
   uint32_t cnt[NC];
   cnt[0] = load_runs(G4(x), xs, KG, 0, (KG + 63) / 64, wv, NW);
@@ -2339,7 +2509,7 @@ void k_gemv_pipe(const float* __restrict__ W, const float* __restrict__ x, float
   lds_barrier();
   prod_ins<R>(w4, xs, N4, 1, KG, 0, NINS / NC, wv, NW, pad);
   lds_barrier();
-  const uint32_t lane = threadIdx.x & 63, r = lane < R ? lane : R - 1;
+  const uint32_t lane = tid_x() & 63, r = lane < R ? lane : R - 1;
   float acc = 0.0f;
   for (uint32_t c = 0; c < NC; ++c) {
     const uint32_t i0 = NINS * c / NC, i1 = NINS * (c + 1) / NC;
@@ -2354,8 +2524,8 @@ void k_gemv_pipe(const float* __restrict__ W, const float* __restrict__ x, float
     }
     lds_barrier();
   }
-  const uint32_t row = b * R + threadIdx.x;
-  if (threadIdx.x < R && row < M) GW(y)[row] = acc;
+  const uint32_t row = b * R + tid_x();
+  if (tid_x() < R && row < M) GW(y)[row] = acc;
 }
 
 // A batch of n independent GEMVs in one launch (gridDim.y = n): GEMV i is
@@ -2381,8 +2551,8 @@ void k_gemv_many(const float* __restrict__ W, uint64_t w_per, uint32_t copies, u
   copy_to_lds((lf4*)w, n4 + k4, [=](uint32_t j) { return j < n4 ? src + j : x4 + (j - n4); });
   __syncthreads();
   const float acc = gemv_lds_t<R>(w, xs, K, 1, pad);
-  const uint32_t row = b * R + threadIdx.x;
-  if (threadIdx.x < R && row < M) GW(y + (size_t)i * M)[row] = acc;
+  const uint32_t row = b * R + tid_x();
+  if (tid_x() < R && row < M) GW(y + (size_t)i * M)[row] = acc;
 }
 
 }  // namespace
@@ -2454,7 +2624,12 @@ size_t decode_act_floats(uint32_t H, uint32_t I, uint32_t qd, uint32_t kvd) {
 
 bool decode_att_ok(const DecodeArgs& a) {
   const size_t wfloats = decode_wregion_bytes(a) / 4;
-  if (a.att_split) return a.att_tp >= 32 && a.nh % a.nkv == 0 && a.nh / a.nkv < 64;
+  // split: the score task stages kScoreKT positions of K ([hd][kScoreKT],
+  // hd <= kScoreKB, a multiple of 4) in the weight region
+  if (a.att_split)
+    return a.att_tp >= 32 && a.att_nr >= 3 && a.nh % a.nkv == 0 && a.nh / a.nkv < 64 &&
+           a.hd <= kScoreKB &&
+           a.hd % 4 == 0 && (size_t)a.hd * kScoreKT <= wfloats;
   // the one-task form keeps K and V in LDS when they fit (head_dim a
   // multiple of 4), else streams tiles of at least 32 positions
   return (a.hd % 4 == 0 && a.hd <= 192 &&
@@ -2485,7 +2660,7 @@ void decode_att_plan(DecodeArgs& a, bool split) {
   a.natt_s = a.nkv * a.att_chunks;
   a.att_dvc = (a.hd + kAttDV - 1) / kAttDV;
   a.natt_v = a.nh * a.att_dvc;
-  a.att_tp = att_mix_tile_positions(a.max_pos, decode_wregion_bytes(a) / 4);
+  att_mix_plan(a.max_pos, decode_wregion_bytes(a) / 4, &a.att_tp, &a.att_nr);
 }
 
 size_t decode_lds_bytes(const DecodeArgs& a) {

@@ -792,7 +792,13 @@ static bool assign_tasks(const DecodeArgs& a, std::vector<uint16_t>& table) {
     auto adjacent = [&](uint32_t w) {
       return last[w] == (int)p - 1 || (p == kPhaseD && has_qkv[w]);
     };
-    for (uint32_t t = 0; t < n[p]; ++t) {
+    // split attention: the mix tasks (long) are placed first, one per
+    // workgroup while there are workgroups left, then the score tasks
+    // (short) beside them; each workgroup's list is then put back in task
+    // order, so its score tasks run before its mix task
+    const bool mix_first = p == kPhaseATT && a.att_split;
+    for (uint32_t k = 0; k < n[p]; ++k) {
+      const uint32_t t = mix_first ? (k < a.natt_v ? a.natt_s + k : k - a.natt_v) : k;
       // attention tasks of one kv head go to one XCD (workgroups are
       // dispatched to the XCDs round-robin: workgroup w runs on XCD
       // w % kXcds), so the tasks that read the same cached K and V rows
@@ -823,6 +829,11 @@ static bool assign_tasks(const DecodeArgs& a, std::vector<uint16_t>& table) {
       last[best] = (int)p;
       if (p == kPhaseQKV) has_qkv[best] = true;
     }
+    if (mix_first)
+      for (uint32_t w = 0; w < W; ++w) {
+        uint16_t* row = &table[(size_t)w * kMaxTasks];
+        std::sort(row + cnt[w] - same[w], row + cnt[w]);
+      }
   }
   return true;
 }
