@@ -54,8 +54,7 @@ typedef AS_GLB u64 gw;
 // threadIdx.x through an opaque copy: values derived from it are formed
 // where they are used instead of being hoisted out of the layer loop and
 // kept live for the whole persistent kernel (which otherwise runs out of
-// registers and spills).  gather_map alone keeps threadIdx.x: its word
-// offsets, hoisted, gave the fewest registers of the variants compiled.
+// registers and spills).
 __device__ __forceinline__ uint32_t tid_x() {
   uint32_t t = threadIdx.x;
   asm volatile("" : "+v"(t));
@@ -253,57 +252,70 @@ __device__ __forceinline__ void wait_vmcnt(uint32_t n) {
 }
 
 // Waits until the n tagged words addr(0..n-1) carry `epoch` and copies their
-// values to dst(0..n-1).  Up to M words in flight per thread; longer
-// vectors are gathered in slices.
-template <int M = 12, class F, class D>
+// values to dst(0..n-1).  The first PW waves poll, up to M words in flight
+// per thread (longer vectors are gathered in slices).  Waves at or past PW,
+// which may have weight or tile copies into LDS outstanding (loads complete
+// in issue order, so a poll issued behind them would wait for them), do not
+// poll: they wait until at most `vmw` of their copies are outstanding
+// (kNoWait: not at all) and join the closing barrier.
+constexpr uint32_t kNoWait = UINT32_MAX;
+template <int M = 12, uint32_t PW = 4, class F, class D>
 __device__ __forceinline__ void gather_map(uint32_t n, uint32_t epoch, uint32_t* err,
-                                           uint32_t cap, F addr, D dst) {
-  for (uint32_t base = 0; base < n; base += M * kThreads) {
-    u64 w[M];
-    uint32_t spins = 0;
-    while (true) {
+                                           uint32_t cap, F addr, D dst, uint32_t vmw = 0) {
+  constexpr uint32_t NT = PW * 64;
+  const uint32_t tid = tid_x();
+  if (tid < NT) {
+    for (uint32_t base = 0; base < n; base += M * NT) {
+      u64 w[M];
+      uint32_t spins = 0;
+      while (true) {
+#pragma unroll
+        for (int u = 0; u < M; ++u) {
+          const uint32_t i = base + tid + u * NT;
+          if (i < n) w[u] = get_word(addr(i));
+        }
+        bool ok = true;
+#pragma unroll
+        for (int u = 0; u < M; ++u) {
+          const uint32_t i = base + tid + u * NT;
+          if (i < n && (uint32_t)(w[u] >> 32) != epoch) ok = false;
+        }
+        if (ok) break;
+        __builtin_amdgcn_s_sleep(1);
+        ++spins;
+        if ((spins & 255u) == 0 && ld_ag(err) != 0u) break;  // another task failed
+        if (spins > cap) {  // a.spin_cap: about 0.5 s by default
+          raise_err(err, 2u);
+          break;
+        }
+      }
 #pragma unroll
       for (int u = 0; u < M; ++u) {
-        const uint32_t i = base + threadIdx.x + u * kThreads;
-        if (i < n) w[u] = get_word(addr(i));
-      }
-      bool ok = true;
-#pragma unroll
-      for (int u = 0; u < M; ++u) {
-        const uint32_t i = base + threadIdx.x + u * kThreads;
-        if (i < n && (uint32_t)(w[u] >> 32) != epoch) ok = false;
-      }
-      if (ok) break;
-      __builtin_amdgcn_s_sleep(1);
-      ++spins;
-      if ((spins & 255u) == 0 && ld_ag(err) != 0u) break;  // another task failed
-      if (spins > cap) {  // a.spin_cap: about 0.5 s by default
-        raise_err(err, 2u);
-        break;
+        const uint32_t i = base + tid + u * NT;
+        if (i < n) *dst(i) = __uint_as_float((uint32_t)w[u]);
       }
     }
-#pragma unroll
-    for (int u = 0; u < M; ++u) {
-      const uint32_t i = base + threadIdx.x + u * kThreads;
-      if (i < n) *dst(i) = __uint_as_float((uint32_t)w[u]);
-    }
+    // every global_load_lds copy this wave issued before has landed in
+    // LDS too (loads complete in issue order)
+    wait_vm0();
+  } else if (vmw != kNoWait) {
+    asm volatile("" ::: "memory");
+    wait_vmcnt(vmw);
+    asm volatile("" ::: "memory");
   }
-  // every global_load_lds copy this wave issued before (weight blocks, K
-  // or V tiles) has landed in LDS too: loads complete in issue order, and
-  // the wait makes that explicit for waves that polled no word
-  wait_vm0();
   __syncthreads();
 }
 // The same into dst[0..n-1].
-template <class F>
+template <int M = 12, uint32_t PW = 4, class F>
 __device__ __forceinline__ void gather(lf* dst, uint32_t n, uint32_t epoch, uint32_t* err,
-                                       uint32_t cap, F addr) {
-  gather_map(n, epoch, err, cap, addr, [=](uint32_t i) { return dst + i; });
+                                       uint32_t cap, F addr, uint32_t vmw = 0) {
+  gather_map<M, PW>(n, epoch, err, cap, addr, [=](uint32_t i) { return dst + i; }, vmw);
 }
 
+template <int M = 12, uint32_t PW = 4>
 __device__ __forceinline__ void gather_vec(lf* dst, const gw* src, uint32_t n,
-                                           const DecodeArgs& a) {
-  gather(dst, n, a.epoch, a.err, a.spin_cap, [=](uint32_t i) { return src + i; });
+                                           const DecodeArgs& a, uint32_t vmw = 0) {
+  gather<M, PW>(dst, n, a.epoch, a.err, a.spin_cap, [=](uint32_t i) { return src + i; }, vmw);
 }
 
 // Copies n4 f4 (element i from src(i), global memory) to dst[i] with up to
@@ -459,12 +471,20 @@ __device__ __forceinline__ void prefetch_rows(const float* W, uint32_t R, uint32
 // loads (global_load_lds_dwordx4); each wave instruction fills 64
 // consecutive 16-byte slots.  The data is in LDS once vmcnt reaches 0, and
 // readable by other waves after a barrier.
+// Weight blocks are copied into LDS by waves 2 and 3 (the DMA waves) while
+// waves 0 and 1 poll for the task's inputs.  Copies of one block by DMA
+// wave wv: kDmaCount(n4, wv) instructions, issued in order.
+__device__ __forceinline__ uint32_t dma_count(uint32_t n4, uint32_t wv) {
+  const uint32_t o = (wv - 2) * 64;
+  return wv >= 2 && n4 > o ? (n4 - o + 127) / 128 : 0;
+}
 __device__ __forceinline__ void prefetch_rows_async(const float* W, uint32_t R, uint32_t K,
                                                     uint32_t blk, lf* dst) {
   const uint32_t n4 = R * K / 4;
   const uint32_t wv = __builtin_amdgcn_readfirstlane(tid_x() >> 6), lane = tid_x() & 63;
+  if (wv < 2) return;
   gf4* src = G4(W + (size_t)blk * R * K);
-  for (uint32_t i0 = wv * 64; i0 < n4; i0 += kThreads) {  // i0: wave-uniform
+  for (uint32_t i0 = (wv - 2) * 64; i0 < n4; i0 += 128) {  // i0: wave-uniform
     if (i0 + lane < n4)
       __builtin_amdgcn_global_load_lds((const AS_GLB void*)(src + i0 + lane),
                                        (AS_LDS void*)((lf4*)dst + i0), 16, 0, 0);
@@ -931,11 +951,13 @@ __device__ __forceinline__ float tree_col(const lf* p, uint32_t n, uint32_t st, 
 // RMSNorm of an LDS vector (code/cis2-fp/src/main.rs:245-260): squares
 // into `tmp`, one strict chain in wave 0, mean by a true divide,
 // inv = 1/sqrt(mean + eps), out = (x*inv)*w.  `out` may alias `tmp` or x.
-// The norm weights a thread scales with (elements tid_x() + 256u) are
-// loaded into registers before the input is waited for (load_normw), so the
-// scaling pass after the chain reads no global memory (n <= 1024; longer
-// vectors read the tail from global memory).
-constexpr uint32_t kNormRegs = 4;
+// Waves 0 and 1 scale: the norm weights a thread scales with (elements
+// tid_x() + 128u) are loaded into registers before the input is waited for
+// (load_normw), so the scaling pass after the chain reads no global memory
+// (n <= 1024; longer vectors read the tail from global memory).  Waves 2
+// and 3 load nothing here: a load issued behind their weight copies would
+// wait for every copy.
+constexpr uint32_t kNormRegs = 8, kNormThreads = 128;
 struct NormW {
   float v[kNormRegs];
   const float* g;
@@ -944,10 +966,11 @@ __device__ __forceinline__ NormW load_normw(const float* w_, uint32_t n) {
   NormW r;
   r.g = w_;
   gf* w = G(w_);
+  const uint32_t tid = tid_x();
 #pragma unroll
   for (uint32_t u = 0; u < kNormRegs; ++u) {
-    const uint32_t i = tid_x() + u * kThreads;
-    r.v[u] = i < n ? w[i] : 0.0f;
+    const uint32_t i = tid + u * kNormThreads;
+    r.v[u] = tid < kNormThreads && i < n ? w[i] : 0.0f;
   }
   return r;
 }
@@ -983,17 +1006,20 @@ __device__ __forceinline__ void rmsnorm_lds(const lf* x, const NormW& w, float e
   }
   __syncthreads();
   const float inv = *s_inv;
+  const uint32_t tid = tid_x();
+  if (tid < kNormThreads) {
 #pragma unroll
-  for (uint32_t u = 0; u < kNormRegs; ++u) {
-    const uint32_t i = tid_x() + u * kThreads;
-    if (i < n) {
-      float sx = x[i] * inv;
-      out[i] = sx * w.v[u];
+    for (uint32_t u = 0; u < kNormRegs; ++u) {
+      const uint32_t i = tid + u * kNormThreads;
+      if (i < n) {
+        float sx = x[i] * inv;
+        out[i] = sx * w.v[u];
+      }
     }
-  }
-  for (uint32_t i = tid_x() + kNormRegs * kThreads; i < n; i += kThreads) {
-    float sx = x[i] * inv;
-    out[i] = sx * G(w.g)[i];
+    for (uint32_t i = tid + kNormRegs * kNormThreads; i < n; i += kNormThreads) {
+      float sx = x[i] * inv;
+      out[i] = sx * G(w.g)[i];
+    }
   }
   __syncthreads();
 }
@@ -1075,7 +1101,7 @@ __device__ __forceinline__ QkvGeom qkv_geom(const DecodeArgs& a, const LayerW& L
 // One row block of q, k or v: input_layernorm, GEMV, bias (main.rs:405-413).
 template <bool TR>
 __device__ __forceinline__ void run_qkv(const DecodeArgs& a, uint32_t l, uint32_t t, const Lds& s,
-                                       uint32_t tok, lf* wl, bool pre) {
+                                       uint32_t tok, lf* wl, bool pre, uint32_t vmw) {
   const LayerW Lw = a.layers[l];
   const Act ac = act_of(a, l);
   const QkvGeom g = qkv_geom(a, Lw, ac, t);
@@ -1090,7 +1116,7 @@ __device__ __forceinline__ void run_qkv(const DecodeArgs& a, uint32_t l, uint32_
     for (uint32_t i = tid_x(); i < a.H; i += kThreads) x[i] = e[i];
     __syncthreads();
   } else {
-    gather_vec(x, act_of(a, l - 1).hout, a.H, a);
+    gather_vec<8, 2>(x, act_of(a, l - 1).hout, a.H, a, vmw);
   }
   stamp(a, l, P_QKV, t, 1);
   rmsnorm_lds<TR>(x, nw, a.eps, a.H, ln, ln, s_inv);
@@ -1551,10 +1577,11 @@ __device__ __forceinline__ void att_group_inputs(const DecodeArgs& a, uint32_t l
   float csv = 0.0f;
   if (tid_x() < hd) csv = G(a.rope_cs)[(size_t)a.pos * hd + tid_x()];
   const uint32_t nq_w = ng * hd;
-  gather(qv, (ng + 2) * hd, a.epoch, a.err, a.spin_cap, [=](uint32_t i) {
+  // waves 0..1 poll; the DMA waves may have K tile copies outstanding
+  gather<4, 2>(qv, (ng + 2) * hd, a.epoch, a.err, a.spin_cap, [=](uint32_t i) {
     return i < nq_w ? ac.q + (size_t)kvh * nq_w + i
                     : (i < nq_w + hd ? ac.k : ac.v) + (size_t)kvh * hd + (i - nq_w) % hd;
-  });
+  }, kNoWait);
   if (tid_x() < hd) cs[tid_x()] = csv;
   if (Lw.qn || Lw.kn) {  // rmsnorm of each vector that has weights
     const uint32_t nb = (hd + 31) / 32;
@@ -1591,7 +1618,7 @@ __device__ __forceinline__ void att_group_inputs(const DecodeArgs& a, uint32_t l
       const float* wg = v < ng ? Lw.qn : Lw.kn;
       if (!wg) continue;
       for (uint32_t i = tid_x(); i < hd; i += kThreads) {
-        const float wv = i < kThreads ? (v < ng ? nq.v[0] : nk.v[0]) : G(wg)[i];
+        const float wv = i < kNormThreads ? (v < ng ? nq.v[0] : nk.v[0]) : G(wg)[i];
         float sx = qv[(size_t)v * hd + i] * inv;
         qv[(size_t)v * hd + i] = sx * wv;
       }
@@ -1698,18 +1725,19 @@ __device__ __forceinline__ void score_cols(const lf* q0, const lf* q1, const lf*
 // positions js .. js+n-1 rounded up to 4 (all < max_pos: js and max_pos are
 // multiples of 4 and js + n <= pos), into LDS rows of kScoreKT floats:
 // tile[d * kScoreKT + (j - js)] = k_j[d], d < hd.  global_load_lds_dwordx4,
-// one wave instruction per dim row (n <= kScoreKT = 4 * 64), waves take the
-// rows in turn; nothing is waited for (the data is in LDS once the issuing
-// wave's vmcnt reaches 0).
+// one wave instruction per dim row (n <= kScoreKT = 4 * 64), issued by the
+// DMA waves 2 and 3 in turn; nothing is waited for (the data is in LDS once
+// the issuing wave's vmcnt reaches 0).
 __device__ __forceinline__ void copy_k_tile(lf* tile, const float* krows, uint32_t max_pos,
                                             uint32_t hd, uint32_t js, uint32_t n) {
   const uint32_t n4 = (n + 3) >> 2, lane = tid_x() & 63;
   const uint32_t w = __builtin_amdgcn_readfirstlane(tid_x() >> 6);
+  if (w < 2) return;  // the DMA waves copy (rows d = w - 2, w, ...)
   // one running source pointer (no per-row address kept live across layers)
-  const float* src = krows + (size_t)w * max_pos + js + 4 * lane;
-  const size_t step = (size_t)(kThreads / 64) * max_pos;
+  const float* src = krows + (size_t)(w - 2) * max_pos + js + 4 * lane;
+  const size_t step = (size_t)2 * max_pos;
 #pragma unroll 1
-  for (uint32_t d = w; d < hd; d += kThreads / 64, src += step)
+  for (uint32_t d = w - 2; d < hd; d += 2, src += step)
     if (lane < n4)
       __builtin_amdgcn_global_load_lds((const AS_GLB void*)src,
                                        (AS_LDS void*)((lf4*)(tile + (size_t)d * kScoreKT)), 16, 0, 0);
@@ -1810,9 +1838,12 @@ __device__ __forceinline__ void copy_v_rows(lf* dst, const float* vrows, uint32_
 //     e_j; or tree32 blocks (partials in `part`) folded from 0 (tree
 //     order).
 // Returns the denominator in every thread (after a barrier).
-template <bool TR>
+// `step` runs in every wave after each block of the chain (tree order:
+// once, after the exps): the caller issues its V copies there, a block at a
+// time, so the copies do not hold up the waves that form the exps.
+template <bool TR, class S>
 __device__ __forceinline__ float softmax_head(lf* ss, uint32_t len, lf* part, lf* misc,
-                                              AS_LDS uint32_t* red) {
+                                              AS_LDS uint32_t* red, S step) {
   const uint32_t wv = __builtin_amdgcn_readfirstlane(tid_x() >> 6);
   Cand best = {0.0f, UINT32_MAX};
   for (uint32_t j = tid_x(); j < len; j += kThreads) {
@@ -1840,6 +1871,7 @@ __device__ __forceinline__ float softmax_head(lf* ss, uint32_t len, lf* part, lf
   if constexpr (TR) {
     exps(0, len, tid_x(), kThreads);
     __syncthreads();
+    step();
     const uint32_t nbk = (len + 31) / 32;
     for (uint32_t t = tid_x(); t < nbk; t += kThreads)
       part[t] = tree_part(ss + 32 * t, len - 32 * t, 1);
@@ -1860,6 +1892,7 @@ __device__ __forceinline__ float softmax_head(lf* ss, uint32_t len, lf* part, lf
       else if (bb + 1 < nb)
         exps((bb + 1) * EB, min(len, (bb + 2) * EB), tid_x() - 64, kThreads - 64);
       lds_barrier();
+      step();
     }
     if (tid_x() == 0) misc[1] = acc;
   }
@@ -1869,10 +1902,9 @@ __device__ __forceinline__ float softmax_head(lf* ss, uint32_t len, lf* part, lf
 
 // Mix task u = (query head h, dim slice dc): output dims d0 = dc*16 ..
 // d0+15 of head h:
-//  - waves 1..3 start copying the first V tiles (a ring of nr tiles of tp
-//    positions, each wave its own rows) before the scores arrive;
-//  - the head's scores are gathered and softmax_head forms e_j and the
-//    denominator;
+//  - the head's scores are gathered; waves 1..3 then start copying the
+//    first V tiles (a ring of nr tiles of tp positions, each wave its own
+//    rows) while softmax_head forms e_j and the denominator;
 //  - the whole workgroup divides: p_j = e_j / den in place;
 //  - lane d of wave 0 then runs one left-to-right V-mix chain
 //    out_d = fold_j (p_j * v_j[d]) over tile i while waves 1..3 form tile
@@ -1913,16 +1945,20 @@ __device__ __forceinline__ void run_att_mix(const DecodeArgs& a, uint32_t l, uin
       ++issued;
     }
   };
-  // the ring less the tile being formed next: nr - 1 tiles land during the
-  // gather and the softmax
-  while (issued < nt && issued + 1 < NR) refill();
   gather_map<17>(len, a.epoch, a.err, a.spin_cap,
                  [=](uint32_t i) { return (const gw*)a.scw + ((size_t)l * a.nh + h) * a.max_pos + i; },
                  [=](uint32_t i) { return ss + i; });
   gather(vv, nd, a.epoch, a.err, a.spin_cap,
          [=](uint32_t i) { return ac.v + (size_t)kvh * hd + d0 + i; });
   stamp(a, l, P_ATT, t, 1);
-  const float den = softmax_head<TR>(ss, len, part, misc, red);
+  // the ring less the tile formed next lands during the softmax, a tile per
+  // chain block (issued after the gathers: a poll issued behind the copies
+  // would wait for them)
+  auto ahead = [&]() {
+    if (issued + 1 < NR) refill();
+  };
+  const float den = softmax_head<TR>(ss, len, part, misc, red, ahead);
+  while (issued < nt && issued + 1 < NR) refill();
   stamp(a, l, P_ATT, t, 3);
   // p_j = e_j / den for positions [0, pos), by all waves (each thread's
   // reads before its writes); this position's own p stays in registers
@@ -1998,7 +2034,7 @@ __device__ __forceinline__ void run_att_mix(const DecodeArgs& a, uint32_t l, uin
 // o_proj block + residual h1 = h + o (main.rs:470-472).
 template <bool TR>
 __device__ __forceinline__ void run_o(const DecodeArgs& a, uint32_t l, uint32_t t, const Lds& s,
-                                     uint32_t tok, lf* wl, bool pre) {
+                                     uint32_t tok, lf* wl, bool pre, uint32_t vmw) {
   const LayerW Lw = a.layers[l];
   const Act ac = act_of(a, l);
   const uint32_t qd = a.qd, r0 = t * a.Ro, nr = min(a.Ro, a.H - r0);
@@ -2009,12 +2045,12 @@ __device__ __forceinline__ void run_o(const DecodeArgs& a, uint32_t l, uint32_t 
   if (l == 0) {
     gf* e = G(a.embed) + (size_t)tok * a.H + r0;
     for (uint32_t i = tid_x(); i < nr; i += kThreads) hres[i] = e[i];
-    gather_vec(x, ac.att, qd, a);
+    gather_vec<17, 2>(x, ac.att, qd, a, vmw);
   } else {
     const gw* hin = act_of(a, l - 1).hout + r0;
     const gw* att = ac.att;
-    gather(x, qd + nr, a.epoch, a.err, a.spin_cap,
-           [=](uint32_t i) { return i < qd ? att + i : hin + (i - qd); });
+    gather<17, 2>(x, qd + nr, a.epoch, a.err, a.spin_cap,
+                  [=](uint32_t i) { return i < qd ? att + i : hin + (i - qd); }, vmw);
   }
   stamp(a, l, P_O, t, 1);
   const float acc = gemv_sel<TR, 8, 32, 18, 8>(a.Ro, wl, x, qd, 1, s.pad);
@@ -2027,7 +2063,7 @@ __device__ __forceinline__ void run_o(const DecodeArgs& a, uint32_t l, uint32_t 
 // post_attention_layernorm; hid = silu(gate) * up (main.rs:478-487).
 template <bool TR>
 __device__ __forceinline__ void run_gu(const DecodeArgs& a, uint32_t l, uint32_t t, const Lds& s,
-                                      lf* wl, bool pre) {
+                                      lf* wl, bool pre, uint32_t vmw) {
   const LayerW Lw = a.layers[l];
   const Act ac = act_of(a, l);
   lf* x = s.v;
@@ -2040,7 +2076,7 @@ __device__ __forceinline__ void run_gu(const DecodeArgs& a, uint32_t l, uint32_t
   }
   const NormW nw = load_normw(Lw.ln2, a.H);
   stamp(a, l, P_GU, t, 0);
-  gather_vec(x, ac.h1, a.H, a);
+  gather_vec<8, 2>(x, ac.h1, a.H, a, vmw);
   stamp(a, l, P_GU, t, 1);
   rmsnorm_lds<TR>(x, nw, a.eps, a.H, ln, ln, s_inv);
   stamp(a, l, P_GU, t, 3);
@@ -2061,7 +2097,7 @@ __device__ __forceinline__ void run_gu(const DecodeArgs& a, uint32_t l, uint32_t
 // down block + residual h_next = h1 + down (main.rs:489-491).
 template <bool TR>
 __device__ __forceinline__ void run_d(const DecodeArgs& a, uint32_t l, uint32_t t, const Lds& s,
-                                     lf* wl, bool pre) {
+                                     lf* wl, bool pre, uint32_t vmw) {
   const LayerW Lw = a.layers[l];
   const Act ac = act_of(a, l);
   const uint32_t I = a.I, r0 = t * a.Rd, nr = min(a.Rd, a.H - r0);
@@ -2071,8 +2107,8 @@ __device__ __forceinline__ void run_d(const DecodeArgs& a, uint32_t l, uint32_t 
   stamp(a, l, P_D, t, 0);
   const gw* h1 = ac.h1 + r0;
   const gw* hid = ac.hid;
-  gather(x, I + nr, a.epoch, a.err, a.spin_cap,
-         [=](uint32_t i) { return i < I ? hid + i : h1 + (i - I); });
+  gather<25, 2>(x, I + nr, a.epoch, a.err, a.spin_cap,
+                [=](uint32_t i) { return i < I ? hid + i : h1 + (i - I); }, vmw);
   stamp(a, l, P_D, t, 1);
   // the 1536- to 3072-long chain keeps 12 reads in flight (8 elsewhere:
   // deeper rings slowed the shorter GEMVs, measured)
@@ -2275,6 +2311,16 @@ __device__ __forceinline__ void run_lm(const DecodeArgs& a, const Lds& s) {
   stamp(a, L - 1, P_LM, wg, 3);
 }
 
+// Copy instructions DMA wave wv issues for a task's weight blocks.
+__device__ __forceinline__ uint32_t task_dma_count(const DecodeArgs& a, uint32_t ph, uint32_t wv) {
+  switch (ph) {
+    case P_QKV: return dma_count(a.Rq * a.H / 4, wv);
+    case P_O: return dma_count(a.Ro * a.qd / 4, wv);
+    case P_GU: return 2 * dma_count(a.Rg * a.H / 4, wv);
+    case P_D: return dma_count(a.Rd * a.I / 4, wv);
+    default: return 0;
+  }
+}
 // Floats of a task's weight blocks in LDS (attention: none).
 __device__ __forceinline__ uint32_t task_wfloats(const DecodeArgs& a, uint32_t ph) {
   switch (ph) {
@@ -2394,6 +2440,18 @@ void k_decode(DecodeArgs a) {
     }
     if ((size_t)tot * 4 > wbytes) slots = false;
   }
+  // slot path: the copies a DMA wave issues for the tasks after task i of a
+  // layer (what may still be outstanding when task i's inputs are in)
+  uint32_t vmw[kMaxTasks];
+  {
+    const uint32_t wv = __builtin_amdgcn_readfirstlane(tid_x() >> 6);
+    uint32_t after = 0;
+#pragma unroll
+    for (int i = kMaxTasks - 1; i >= 0; --i) {
+      vmw[i] = slots ? after : 0u;
+      if ((uint32_t)i < ntask) after += task_dma_count(a, task[i] >> 12, wv);
+    }
+  }
   if (slots) load_task_weights(a, 0, task, ntask, woff, s);
   uint32_t tok = 0;
   if (reads_tok) {
@@ -2408,15 +2466,15 @@ void k_decode(DecodeArgs a) {
       const uint32_t ph = task[i] >> 12, t = task[i] & 0xFFFu;
       lf* wl = slots ? s.w + woff[i] : s.w;
       switch (ph) {
-        case P_QKV: run_qkv<TR>(a, l, t, s, tok, wl, slots); break;
+        case P_QKV: run_qkv<TR>(a, l, t, s, tok, wl, slots, vmw[i]); break;
         case P_ATT:
           if (!a.att_split) run_att<TR>(a, l, t, s, wbytes / 4);
           else if (t < a.natt_s) run_att_score<TR>(a, l, t, s);
           else run_att_mix<TR>(a, l, t - a.natt_s, s);
           break;
-        case P_O: run_o<TR>(a, l, t, s, tok, wl, slots); break;
-        case P_GU: run_gu<TR>(a, l, t, s, wl, slots); break;
-        case P_D: run_d<TR>(a, l, t, s, wl, slots); break;
+        case P_O: run_o<TR>(a, l, t, s, tok, wl, slots, vmw[i]); break;
+        case P_GU: run_gu<TR>(a, l, t, s, wl, slots, vmw[i]); break;
+        case P_D: run_d<TR>(a, l, t, s, wl, slots, vmw[i]); break;
         default: break;
       }
       __syncthreads();
