@@ -67,6 +67,7 @@ TRAFFIC_FILE = os.path.join(ROOT, "profiles", "k_decode_smollm2_pmc.txt")
 GEMV_STREAM_FILE = os.path.join(ROOT, "profiles", "k_gemv_many_1536x576_stream.txt")
 LM_HEAD_FILE = os.path.join(ROOT, "profiles", "k_gemv_lm_head_49152x576.txt")
 GEMV_ONE_FILE = os.path.join(ROOT, "profiles", "k_gemv_pipe_1536x576.txt")
+QWEN3_FILE = os.path.join(ROOT, "profiles", "k_decode_qwen3_4096.txt")
 
 
 def decode_bytes(pos):
@@ -339,7 +340,7 @@ def qwen3_long(gen=256, n_prompt=4096, seed=6):
         algo = sum(wb + kvb * (int(p) + 1) for p in positions)
         rec["roofline"] = roofline_obj(
             algo, kernel_ms * 1e-3, "k_decode (persistent, split attention; HIP events per launch)",
-            launches=launches, us_per_launch=round(kernel_ms * 1e3 / launches, 2),
+            traffic=measured_traffic(QWEN3_FILE), launches=launches, us_per_launch=round(kernel_ms * 1e3 / launches, 2),
             algorithmic_bytes_per_launch=int(round(algo / launches)),
             positions=[int(positions[0]), int(positions[-1])])
     fx = os.path.join(ROOT, "tests", "golden", "qwen3_fixture.json")

@@ -251,17 +251,26 @@ __device__ __forceinline__ void wait_vmcnt(uint32_t n) {
   }
 }
 
+// Workgroup barrier for LDS data only: waits for this wave's LDS
+// operations, not for its outstanding global loads (HIP's __syncthreads
+// waits for those too).  The empty asm statements keep the compiler from
+// moving memory accesses across the barrier.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
 // Waits until the n tagged words addr(0..n-1) carry `epoch` and copies their
 // values to dst(0..n-1).  The first PW waves poll, up to M words in flight
 // per thread (longer vectors are gathered in slices).  Waves at or past PW,
 // which may have weight or tile copies into LDS outstanding (loads complete
 // in issue order, so a poll issued behind them would wait for them), do not
-// poll: they wait until at most `vmw` of their copies are outstanding
-// (kNoWait: not at all) and join the closing barrier.
-constexpr uint32_t kNoWait = UINT32_MAX;
+// poll: they wait for their copies and join the closing barrier.
 template <int M = 12, uint32_t PW = 4, class F, class D>
 __device__ __forceinline__ void gather_map(uint32_t n, uint32_t epoch, uint32_t* err,
-                                           uint32_t cap, F addr, D dst, uint32_t vmw = 0) {
+                                           uint32_t cap, F addr, D dst) {
   constexpr uint32_t NT = PW * 64;
   const uint32_t tid = tid_x();
   if (tid < NT) {
@@ -298,24 +307,22 @@ __device__ __forceinline__ void gather_map(uint32_t n, uint32_t epoch, uint32_t*
     // every global_load_lds copy this wave issued before has landed in
     // LDS too (loads complete in issue order)
     wait_vm0();
-  } else if (vmw != kNoWait) {
-    asm volatile("" ::: "memory");
-    wait_vmcnt(vmw);
-    asm volatile("" ::: "memory");
+  } else {
+    wait_vm0();
   }
   __syncthreads();
 }
 // The same into dst[0..n-1].
 template <int M = 12, uint32_t PW = 4, class F>
 __device__ __forceinline__ void gather(lf* dst, uint32_t n, uint32_t epoch, uint32_t* err,
-                                       uint32_t cap, F addr, uint32_t vmw = 0) {
-  gather_map<M, PW>(n, epoch, err, cap, addr, [=](uint32_t i) { return dst + i; }, vmw);
+                                       uint32_t cap, F addr) {
+  gather_map<M, PW>(n, epoch, err, cap, addr, [=](uint32_t i) { return dst + i; });
 }
 
 template <int M = 12, uint32_t PW = 4>
 __device__ __forceinline__ void gather_vec(lf* dst, const gw* src, uint32_t n,
-                                           const DecodeArgs& a, uint32_t vmw = 0) {
-  gather<M, PW>(dst, n, a.epoch, a.err, a.spin_cap, [=](uint32_t i) { return src + i; }, vmw);
+                                           const DecodeArgs& a) {
+  gather<M, PW>(dst, n, a.epoch, a.err, a.spin_cap, [=](uint32_t i) { return src + i; });
 }
 
 // Copies n4 f4 (element i from src(i), global memory) to dst[i] with up to
@@ -472,12 +479,7 @@ __device__ __forceinline__ void prefetch_rows(const float* W, uint32_t R, uint32
 // consecutive 16-byte slots.  The data is in LDS once vmcnt reaches 0, and
 // readable by other waves after a barrier.
 // Weight blocks are copied into LDS by waves 2 and 3 (the DMA waves) while
-// waves 0 and 1 poll for the task's inputs.  Copies of one block by DMA
-// wave wv: kDmaCount(n4, wv) instructions, issued in order.
-__device__ __forceinline__ uint32_t dma_count(uint32_t n4, uint32_t wv) {
-  const uint32_t o = (wv - 2) * 64;
-  return wv >= 2 && n4 > o ? (n4 - o + 127) / 128 : 0;
-}
+// waves 0 and 1 poll for the task's inputs.
 __device__ __forceinline__ void prefetch_rows_async(const float* W, uint32_t R, uint32_t K,
                                                     uint32_t blk, lf* dst) {
   const uint32_t n4 = R * K / 4;
@@ -489,17 +491,6 @@ __device__ __forceinline__ void prefetch_rows_async(const float* W, uint32_t R, 
       __builtin_amdgcn_global_load_lds((const AS_GLB void*)(src + i0 + lane),
                                        (AS_LDS void*)((lf4*)dst + i0), 16, 0, 0);
   }
-}
-
-// Workgroup barrier for LDS data only: waits for this wave's LDS
-// operations, not for its outstanding global loads (HIP's __syncthreads
-// waits for those too).  The empty asm statements keep the compiler from
-// moving memory accesses across the barrier.
-__device__ __forceinline__ void lds_barrier() {
-  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
-  asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
 }
 
 // ---------------------------------------------------------------------------
@@ -1101,7 +1092,7 @@ __device__ __forceinline__ QkvGeom qkv_geom(const DecodeArgs& a, const LayerW& L
 // One row block of q, k or v: input_layernorm, GEMV, bias (main.rs:405-413).
 template <bool TR>
 __device__ __forceinline__ void run_qkv(const DecodeArgs& a, uint32_t l, uint32_t t, const Lds& s,
-                                       uint32_t tok, lf* wl, bool pre, uint32_t vmw) {
+                                       uint32_t tok, lf* wl, bool pre) {
   const LayerW Lw = a.layers[l];
   const Act ac = act_of(a, l);
   const QkvGeom g = qkv_geom(a, Lw, ac, t);
@@ -1116,7 +1107,7 @@ __device__ __forceinline__ void run_qkv(const DecodeArgs& a, uint32_t l, uint32_
     for (uint32_t i = tid_x(); i < a.H; i += kThreads) x[i] = e[i];
     __syncthreads();
   } else {
-    gather_vec<8, 2>(x, act_of(a, l - 1).hout, a.H, a, vmw);
+    gather_vec<8, 2>(x, act_of(a, l - 1).hout, a.H, a);
   }
   stamp(a, l, P_QKV, t, 1);
   rmsnorm_lds<TR>(x, nw, a.eps, a.H, ln, ln, s_inv);
@@ -1577,11 +1568,11 @@ __device__ __forceinline__ void att_group_inputs(const DecodeArgs& a, uint32_t l
   float csv = 0.0f;
   if (tid_x() < hd) csv = G(a.rope_cs)[(size_t)a.pos * hd + tid_x()];
   const uint32_t nq_w = ng * hd;
-  // waves 0..1 poll; the DMA waves may have K tile copies outstanding
+  // waves 0..1 poll while the DMA waves' K tile copies land
   gather<4, 2>(qv, (ng + 2) * hd, a.epoch, a.err, a.spin_cap, [=](uint32_t i) {
     return i < nq_w ? ac.q + (size_t)kvh * nq_w + i
                     : (i < nq_w + hd ? ac.k : ac.v) + (size_t)kvh * hd + (i - nq_w) % hd;
-  }, kNoWait);
+  });
   if (tid_x() < hd) cs[tid_x()] = csv;
   if (Lw.qn || Lw.kn) {  // rmsnorm of each vector that has weights
     const uint32_t nb = (hd + 31) / 32;
@@ -1647,17 +1638,19 @@ __device__ __forceinline__ void att_group_inputs(const DecodeArgs& a, uint32_t l
 // (every workgroup runs its score tasks before its mix tasks, so waits stay
 // acyclic):
 //   score task (kvh, c): positions c*P .. c*P+P-1 of every query head of kv
-//     head kvh; thread j loads its column k_j[0..hd) straight from the
-//     cache once for all the group's heads (128 dims at a time) and forms
-//     dot_seq(q, k_j) (or dot_tree) * scale per head, each published as a
-//     tagged word; the chunk holding `pos` uses this position's own k and
-//     stores k and v into the caches.
-//   mix task (h, dc): output dims d0 = dc*16 .. d0+15 of head h: gathers all
-//     of the head's scores, runs the softmax (the same order as one task),
-//     then lane d of wave 0 continues its one left-to-right V-mix chain over
-//     tiles of its V rows; waves 1..3 copy each tile into LDS with
-//     global_load_lds two tiles ahead and form its products one tile ahead
-//     (the first two tiles land during the softmax).
+//     head kvh; the cached K columns are copied into LDS with
+//     global_load_lds, kScoreKT positions at a time (the first tile's copies
+//     issued before the input gather), then thread j forms dot_seq(q, k_j)
+//     (or dot_tree) * scale for the group's heads two at a time from its
+//     column, each published as a tagged word; the chunk holding `pos` uses
+//     this position's own k and stores k and v into the caches.
+//   mix task (h, dc): output dims d0 = dc*kAttDV .. d0+kAttDV-1 of head h:
+//     gathers all of the head's scores, runs the softmax (the same order as
+//     one task; the exps of the next block formed while wave 0 chains the
+//     denominator over the current one), divides once, then lane d of wave 0
+//     continues its one left-to-right V-mix chain over tiles of its V rows;
+//     waves 1..3 copy the tiles into a ring in LDS with global_load_lds and
+//     form each tile's products one tile ahead of the chain.
 // Each head's K and V are read by many workgroups at once instead of
 // streaming through one.
 // ---------------------------------------------------------------------------
@@ -1900,8 +1893,8 @@ __device__ __forceinline__ float softmax_head(lf* ss, uint32_t len, lf* part, lf
   return misc[1];
 }
 
-// Mix task u = (query head h, dim slice dc): output dims d0 = dc*16 ..
-// d0+15 of head h:
+// Mix task u = (query head h, dim slice dc): output dims d0 = dc*kAttDV ..
+// d0+kAttDV-1 of head h:
 //  - the head's scores are gathered; waves 1..3 then start copying the
 //    first V tiles (a ring of nr tiles of tp positions, each wave its own
 //    rows) while softmax_head forms e_j and the denominator;
@@ -1929,7 +1922,7 @@ __device__ __forceinline__ void run_att_mix(const DecodeArgs& a, uint32_t l, uin
   lf* ss = s.w;                    // scores -> e_j -> p_j [max_pos + 64]
   lf* part = ss + a.max_pos + 64;  // tree partials
   const uint32_t TP = a.att_tp, TS = TP + 4, NR = a.att_nr, nt = (pos + TP - 1) / TP;
-  lf* ring = part + att_part_floats(a.max_pos);  // NR tiles [16][TS]
+  lf* ring = part + att_part_floats(a.max_pos);  // NR tiles [kAttDV][TS]
   auto tile = [=](uint32_t i) { return ring + (size_t)(i % NR) * kAttDV * TS; };
   auto tile_n = [=](uint32_t i) { return min(TP, pos - i * TP); };
   const float* vrows = a.vc0 + (size_t)l * a.cache_stride + ((size_t)kvh * hd + d0) * a.max_pos;
@@ -2034,7 +2027,7 @@ __device__ __forceinline__ void run_att_mix(const DecodeArgs& a, uint32_t l, uin
 // o_proj block + residual h1 = h + o (main.rs:470-472).
 template <bool TR>
 __device__ __forceinline__ void run_o(const DecodeArgs& a, uint32_t l, uint32_t t, const Lds& s,
-                                     uint32_t tok, lf* wl, bool pre, uint32_t vmw) {
+                                     uint32_t tok, lf* wl, bool pre) {
   const LayerW Lw = a.layers[l];
   const Act ac = act_of(a, l);
   const uint32_t qd = a.qd, r0 = t * a.Ro, nr = min(a.Ro, a.H - r0);
@@ -2045,12 +2038,12 @@ __device__ __forceinline__ void run_o(const DecodeArgs& a, uint32_t l, uint32_t 
   if (l == 0) {
     gf* e = G(a.embed) + (size_t)tok * a.H + r0;
     for (uint32_t i = tid_x(); i < nr; i += kThreads) hres[i] = e[i];
-    gather_vec<17, 2>(x, ac.att, qd, a, vmw);
+    gather_vec<17, 2>(x, ac.att, qd, a);
   } else {
     const gw* hin = act_of(a, l - 1).hout + r0;
     const gw* att = ac.att;
     gather<17, 2>(x, qd + nr, a.epoch, a.err, a.spin_cap,
-                  [=](uint32_t i) { return i < qd ? att + i : hin + (i - qd); }, vmw);
+                  [=](uint32_t i) { return i < qd ? att + i : hin + (i - qd); });
   }
   stamp(a, l, P_O, t, 1);
   const float acc = gemv_sel<TR, 8, 32, 18, 8>(a.Ro, wl, x, qd, 1, s.pad);
@@ -2063,7 +2056,7 @@ __device__ __forceinline__ void run_o(const DecodeArgs& a, uint32_t l, uint32_t 
 // post_attention_layernorm; hid = silu(gate) * up (main.rs:478-487).
 template <bool TR>
 __device__ __forceinline__ void run_gu(const DecodeArgs& a, uint32_t l, uint32_t t, const Lds& s,
-                                      lf* wl, bool pre, uint32_t vmw) {
+                                      lf* wl, bool pre) {
   const LayerW Lw = a.layers[l];
   const Act ac = act_of(a, l);
   lf* x = s.v;
@@ -2076,7 +2069,7 @@ __device__ __forceinline__ void run_gu(const DecodeArgs& a, uint32_t l, uint32_t
   }
   const NormW nw = load_normw(Lw.ln2, a.H);
   stamp(a, l, P_GU, t, 0);
-  gather_vec<8, 2>(x, ac.h1, a.H, a, vmw);
+  gather_vec<8, 2>(x, ac.h1, a.H, a);
   stamp(a, l, P_GU, t, 1);
   rmsnorm_lds<TR>(x, nw, a.eps, a.H, ln, ln, s_inv);
   stamp(a, l, P_GU, t, 3);
@@ -2097,7 +2090,7 @@ __device__ __forceinline__ void run_gu(const DecodeArgs& a, uint32_t l, uint32_t
 // down block + residual h_next = h1 + down (main.rs:489-491).
 template <bool TR>
 __device__ __forceinline__ void run_d(const DecodeArgs& a, uint32_t l, uint32_t t, const Lds& s,
-                                     lf* wl, bool pre, uint32_t vmw) {
+                                     lf* wl, bool pre) {
   const LayerW Lw = a.layers[l];
   const Act ac = act_of(a, l);
   const uint32_t I = a.I, r0 = t * a.Rd, nr = min(a.Rd, a.H - r0);
@@ -2108,7 +2101,7 @@ __device__ __forceinline__ void run_d(const DecodeArgs& a, uint32_t l, uint32_t 
   const gw* h1 = ac.h1 + r0;
   const gw* hid = ac.hid;
   gather<25, 2>(x, I + nr, a.epoch, a.err, a.spin_cap,
-                [=](uint32_t i) { return i < I ? hid + i : h1 + (i - I); }, vmw);
+                [=](uint32_t i) { return i < I ? hid + i : h1 + (i - I); });
   stamp(a, l, P_D, t, 1);
   // the 1536- to 3072-long chain keeps 12 reads in flight (8 elsewhere:
   // deeper rings slowed the shorter GEMVs, measured)
@@ -2311,16 +2304,6 @@ __device__ __forceinline__ void run_lm(const DecodeArgs& a, const Lds& s) {
   stamp(a, L - 1, P_LM, wg, 3);
 }
 
-// Copy instructions DMA wave wv issues for a task's weight blocks.
-__device__ __forceinline__ uint32_t task_dma_count(const DecodeArgs& a, uint32_t ph, uint32_t wv) {
-  switch (ph) {
-    case P_QKV: return dma_count(a.Rq * a.H / 4, wv);
-    case P_O: return dma_count(a.Ro * a.qd / 4, wv);
-    case P_GU: return 2 * dma_count(a.Rg * a.H / 4, wv);
-    case P_D: return dma_count(a.Rd * a.I / 4, wv);
-    default: return 0;
-  }
-}
 // Floats of a task's weight blocks in LDS (attention: none).
 __device__ __forceinline__ uint32_t task_wfloats(const DecodeArgs& a, uint32_t ph) {
   switch (ph) {
@@ -2440,18 +2423,6 @@ void k_decode(DecodeArgs a) {
     }
     if ((size_t)tot * 4 > wbytes) slots = false;
   }
-  // slot path: the copies a DMA wave issues for the tasks after task i of a
-  // layer (what may still be outstanding when task i's inputs are in)
-  uint32_t vmw[kMaxTasks];
-  {
-    const uint32_t wv = __builtin_amdgcn_readfirstlane(tid_x() >> 6);
-    uint32_t after = 0;
-#pragma unroll
-    for (int i = kMaxTasks - 1; i >= 0; --i) {
-      vmw[i] = slots ? after : 0u;
-      if ((uint32_t)i < ntask) after += task_dma_count(a, task[i] >> 12, wv);
-    }
-  }
   if (slots) load_task_weights(a, 0, task, ntask, woff, s);
   uint32_t tok = 0;
   if (reads_tok) {
@@ -2466,15 +2437,15 @@ void k_decode(DecodeArgs a) {
       const uint32_t ph = task[i] >> 12, t = task[i] & 0xFFFu;
       lf* wl = slots ? s.w + woff[i] : s.w;
       switch (ph) {
-        case P_QKV: run_qkv<TR>(a, l, t, s, tok, wl, slots, vmw[i]); break;
+        case P_QKV: run_qkv<TR>(a, l, t, s, tok, wl, slots); break;
         case P_ATT:
           if (!a.att_split) run_att<TR>(a, l, t, s, wbytes / 4);
           else if (t < a.natt_s) run_att_score<TR>(a, l, t, s);
           else run_att_mix<TR>(a, l, t - a.natt_s, s);
           break;
-        case P_O: run_o<TR>(a, l, t, s, tok, wl, slots, vmw[i]); break;
-        case P_GU: run_gu<TR>(a, l, t, s, wl, slots, vmw[i]); break;
-        case P_D: run_d<TR>(a, l, t, s, wl, slots, vmw[i]); break;
+        case P_O: run_o<TR>(a, l, t, s, tok, wl, slots); break;
+        case P_GU: run_gu<TR>(a, l, t, s, wl, slots); break;
+        case P_D: run_d<TR>(a, l, t, s, wl, slots); break;
         default: break;
       }
       __syncthreads();

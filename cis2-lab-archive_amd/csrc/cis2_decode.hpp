@@ -63,10 +63,10 @@ struct DecodeArgs {
   // Split attention (contexts whose K/V rows do not fit one workgroup's
   // LDS): the ATT phase runs natt_s = nkv * att_chunks score tasks (all
   // query heads of one kv head over att_cpos positions, a multiple of 64 in
-  // [256, 512]) and then natt_v = nh * att_dvc mix tasks (16 output dims
-  // of one query head each, V tiles of att_tp positions in a ring of
-  // att_nr); scores pass through scw, tagged words [L][nh][max_pos]
-  // (zeroed at start).
+  // [256, 512], K columns staged in LDS) and natt_v = nh * att_dvc mix
+  // tasks (8 output dims of one query head each, att_dvc = hd / 8, V tiles
+  // of att_tp positions in a ring of att_nr); scores pass through scw,
+  // tagged words [L][nh][max_pos] (zeroed at start).
   uint32_t att_split, att_chunks, natt_s, att_dvc, natt_v, att_tp, att_cpos, att_nr;
   uint64_t* scw;
   // floats of the largest set of weight blocks one workgroup without an

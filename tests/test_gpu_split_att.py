@@ -1,8 +1,7 @@
 """Split attention in the persistent decode kernel: the ATT phase as score
-tasks (256 positions of all query heads of one kv head each, columns read
-straight from the K cache) and mix
-tasks (16 output dims each: softmax, then the V-mix chain over V tiles
-streamed into LDS).  It is chosen when a head's K/V rows do not fit one
+tasks (256 positions of all query heads of one kv head each, the K columns
+copied into an LDS tile) and mix tasks (8 output dims each: softmax, then
+the V-mix chain over V tiles streamed into LDS).  It is chosen when a head's K/V rows do not fit one
 workgroup (Qwen3 at 4352 positions, the 1200-position tree case);
 CIS2_ATT=split forces it and CIS2_ATT=one forbids it, so both attention
 forms run every fixture and must reproduce the reference's witnesses.
