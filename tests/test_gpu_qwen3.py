@@ -59,3 +59,26 @@ def test_qwen3_4096_verify_prefill(rec, model):
     assert r["argmax_digest"] == rec["argmax_digest"]
     assert np.array_equal(np.asarray(r["generated"], dtype=np.uint32),
                           np.asarray(claimed, dtype=np.uint32))
+
+
+@pytest.mark.gpu
+def test_qwen3_second_prompt_and_back(rec, model):
+    """Decodes of two different 4096-token prompts in turn on one context
+    (each position's K/V rows, scores and tagged words overwritten with the
+    other prompt's values in between): the fixture prompt reproduces the
+    reference witness after the other prompt's decode, and the other
+    prompt's decode equals the teacher-forced verifier over its own
+    generated tokens (an independent path: the row-batched kernels)."""
+    spec = artifacts.SPECS[rec["spec"]]
+    other = [int(t) for t in artifacts.prompt_ids(rec["seed"] + 1, spec.vocab, 4096)]
+    assert other != rec["prompt"]
+    for _ in range(2):
+        rb = model.decode(other, rec["gen_toks"], step_digests=False)
+        gen = [int(t) for t in rb["ids"]][4096:]
+        vb = model.verify_prefill(other, gen)
+        assert vb["first_mismatch"] == -1
+        assert rb["witness"] == vb["witness"]
+        assert rb["argmax_digest"] == vb["argmax_digest"]
+        ra = model.decode(rec["prompt"], rec["gen_toks"], step_digests=False)
+        assert ra["witness"] == rec["witness"]
+        assert ra["argmax_digest"] == rec["argmax_digest"]
