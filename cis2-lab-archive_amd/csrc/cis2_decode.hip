@@ -2390,6 +2390,9 @@ void k_decode(DecodeArgs a) {
   // profiling: workgroup entry and exit in the layer-0 LM slots (the LM
   // phase stamps the last layer's)
   if (a.L > 1) stamp(a, 0, P_LM, wg, 0);
+  // this position's token (written by the previous launch's argmax): its
+  // load goes out with the task list's, ahead of any weight copy
+  const uint32_t tok_in = *(const AS_GLB uint32_t*)a.tok_in;
   // this workgroup's tasks (the same in every layer), in phase order
   uint32_t task[kMaxTasks];
   uint32_t ntask = 0;
@@ -2426,7 +2429,7 @@ void k_decode(DecodeArgs a) {
   if (slots) load_task_weights(a, 0, task, ntask, woff, s);
   uint32_t tok = 0;
   if (reads_tok) {
-    tok = *(const AS_GLB uint32_t*)a.tok_in;
+    tok = tok_in;
     if (tok >= a.V) {
       if (tid_x() == 0) raise_err(a.err, 1u);
       tok = 0;
