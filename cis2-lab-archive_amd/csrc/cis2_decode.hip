@@ -1838,10 +1838,17 @@ template <bool TR, class S>
 __device__ __forceinline__ float softmax_head(lf* ss, uint32_t len, lf* part, lf* misc,
                                               AS_LDS uint32_t* red, S step) {
   const uint32_t wv = __builtin_amdgcn_readfirstlane(tid_x() >> 6);
+  // (four reads in flight per thread; the pick keeps the largest value and
+  // the lowest index among equals, whatever the order it sees them in)
   Cand best = {0.0f, UINT32_MAX};
-  for (uint32_t j = tid_x(); j < len; j += kThreads) {
-    const float v = ss[j];
-    if (v == v) best = cand_pick(best, Cand{v, j});
+  for (uint32_t j0 = tid_x(); j0 < len; j0 += 4 * kThreads) {
+    float v[4];
+#pragma unroll
+    for (uint32_t k = 0; k < 4; ++k)
+      if (j0 + k * kThreads < len) v[k] = ss[j0 + k * kThreads];
+#pragma unroll
+    for (uint32_t k = 0; k < 4; ++k)
+      if (j0 + k * kThreads < len && v[k] == v[k]) best = cand_pick(best, Cand{v[k], j0 + k * kThreads});
   }
   const Cand b = cand_block(best, red);
   const float mx = (ss[0] != ss[0] || b.i == UINT32_MAX) ? ss[0] : ss[b.i];
