@@ -643,8 +643,62 @@ __device__ __forceinline__ float chain_pp(const lf4* p, uint32_t n, uint32_t st,
   return acc;
 }
 
-// Strict sum of n contiguous LDS floats (16-byte aligned).
+// chain_pp's order over 16 * npair groups (16 bytes, ST groups apart, the
+// group address per lane), as one assembly loop over two fixed sets of 8
+// groups (v[192:223], v[224:255]): the next set's 8 reads go out, one wait
+// for the current set (issued a set earlier), its 32 adds.  Left to the
+// compiler, the same loop inside the decode kernel kept the sum or the
+// loop address in a register of the set read last and drained the reads
+// (lgkmcnt(0)) once or twice per 64 adds: 8 to 10 cycles per add against
+// 6.1 here (MI355X, one wave, 4096 adds).  The block starts with a full
+// drain, so the counts inside are exact (LDS reads return in order); it
+// reads 8 groups past the range (never added: the caller keeps that LDS
+// readable) and drains them before the registers are released.  The adds
+// are the same IEEE adds in the same order and operand order.  npair >= 1,
+// wave-uniform.
+#define CIS2_LD(R0, R3, K, BASE) \
+  "ds_read_b128 v[" #R0 ":" #R3 "], %[ad] offset:" BASE "+" #K "*%[s]\n\t"
+#define CIS2_ADD4(A, B, C, D)                                                   \
+  "v_add_f32 %[acc], v" #A ", %[acc]\n\tv_add_f32 %[acc], v" #B ", %[acc]\n\t" \
+  "v_add_f32 %[acc], v" #C ", %[acc]\n\tv_add_f32 %[acc], v" #D ", %[acc]\n\t"
+#define CIS2_SET_A(BASE) CIS2_LD(192, 195, 0, BASE) CIS2_LD(196, 199, 1, BASE) CIS2_LD(200, 203, 2, BASE) CIS2_LD(204, 207, 3, BASE) CIS2_LD(208, 211, 4, BASE) CIS2_LD(212, 215, 5, BASE) CIS2_LD(216, 219, 6, BASE) CIS2_LD(220, 223, 7, BASE)
+#define CIS2_SET_B(BASE) CIS2_LD(224, 227, 0, BASE) CIS2_LD(228, 231, 1, BASE) CIS2_LD(232, 235, 2, BASE) CIS2_LD(236, 239, 3, BASE) CIS2_LD(240, 243, 4, BASE) CIS2_LD(244, 247, 5, BASE) CIS2_LD(248, 251, 6, BASE) CIS2_LD(252, 255, 7, BASE)
+#define CIS2_ADDS_A CIS2_ADD4(192, 193, 194, 195) CIS2_ADD4(196, 197, 198, 199) CIS2_ADD4(200, 201, 202, 203) CIS2_ADD4(204, 205, 206, 207) CIS2_ADD4(208, 209, 210, 211) CIS2_ADD4(212, 213, 214, 215) CIS2_ADD4(216, 217, 218, 219) CIS2_ADD4(220, 221, 222, 223)
+#define CIS2_ADDS_B CIS2_ADD4(224, 225, 226, 227) CIS2_ADD4(228, 229, 230, 231) CIS2_ADD4(232, 233, 234, 235) CIS2_ADD4(236, 237, 238, 239) CIS2_ADD4(240, 241, 242, 243) CIS2_ADD4(244, 245, 246, 247) CIS2_ADD4(248, 249, 250, 251) CIS2_ADD4(252, 253, 254, 255)
+template <uint32_t ST>
+__device__ __forceinline__ float chain_lds16(const AS_LDS void* p, uint32_t npair, float acc) {
+  uint32_t ad = (uint32_t)(uintptr_t)p;
+  asm volatile(
+      "s_waitcnt lgkmcnt(0)\n\t" CIS2_SET_A("0")
+      "1:\n\t" CIS2_SET_B("8*%[s]")
+      "s_waitcnt lgkmcnt(8)\n\t" CIS2_ADDS_A
+      "v_add_u32 %[ad], 16*%[s], %[ad]\n\t" CIS2_SET_A("0")
+      "s_waitcnt lgkmcnt(8)\n\t" CIS2_ADDS_B
+      "s_sub_u32 %[n], %[n], 1\n\t"
+      "s_cmp_lg_u32 %[n], 0\n\t"
+      "s_cbranch_scc1 1b\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : [acc] "+v"(acc), [ad] "+v"(ad), [n] "+s"(npair)
+      : [s] "i"(ST * 16)
+      : "memory", "scc", "v192", "v193", "v194", "v195", "v196", "v197", "v198", "v199", "v200", "v201", "v202", "v203", "v204", "v205", "v206", "v207", "v208", "v209", "v210", "v211", "v212", "v213", "v214", "v215", "v216", "v217", "v218", "v219", "v220", "v221", "v222", "v223", "v224", "v225", "v226", "v227", "v228", "v229", "v230", "v231", "v232", "v233", "v234", "v235", "v236", "v237", "v238", "v239", "v240", "v241", "v242", "v243", "v244", "v245", "v246", "v247", "v248", "v249", "v250", "v251", "v252", "v253", "v254", "v255");
+  return acc;
+}
+#undef CIS2_LD
+#undef CIS2_ADD4
+#undef CIS2_SET_A
+#undef CIS2_SET_B
+#undef CIS2_ADDS_A
+#undef CIS2_ADDS_B
+
+// Strict sum of n contiguous LDS floats (16-byte aligned; 32 readable
+// floats after them).
 __device__ __forceinline__ float chain_vec(const lf* p, uint32_t n, float acc) {
+  const uint32_t np = __builtin_amdgcn_readfirstlane(n >> 6);
+  if (np > 0) {
+    acc = chain_lds16<1>(p, np, acc);
+    p += (size_t)np * 64;
+    n -= np * 64;
+  }
   acc = chain_pp(reinterpret_cast<const lf4*>(p), n >> 2, 1, acc);
   for (uint32_t i = n & ~3u; i < n; ++i) acc = acc + p[i];
   return acc;
@@ -775,8 +829,11 @@ __device__ __forceinline__ float gemv_lds_t(lf* W, const lf* x, uint32_t K, uint
       const uint32_t g0 = i0 * GP, g1 = min(i1 * GP, KG);
       const lf4* cp = W4 + (size_t)wv * bf4 + (size_t)g0 * R + r;
       // CD = 0: two register sets (the long down chains), else a ring of CD
-      if constexpr (CD == 0)
-        acc = chain_pp(cp, g1 - g0, R, acc);
+      if constexpr (CD == 0) {
+        const uint32_t ng = g1 - g0, np = ng >> 4;
+        if (np > 0) acc = chain_lds16<R>(cp, np, acc);
+        acc = chain_pp(cp + (size_t)np * 16 * R, ng - np * 16, R, acc);
+      }
       else
         acc = chain4<CD>(cp, g1 - g0, R, acc);
     } else if (c + 1 < NC) {
