@@ -828,7 +828,8 @@ __device__ __forceinline__ float gemv_lds_t(lf* W, const lf* x, uint32_t K, uint
     if (wv < nb) {
       const uint32_t g0 = i0 * GP, g1 = min(i1 * GP, KG);
       const lf4* cp = W4 + (size_t)wv * bf4 + (size_t)g0 * R + r;
-      // CD = 0: two register sets (the long down chains), else a ring of CD
+      // CD = 0: chain_lds16's pairs, then chain_pp (8 groups of readable
+      // LDS past each chunk at stride R), else a ring of CD
       if constexpr (CD == 0) {
         const uint32_t ng = g1 - g0, np = ng >> 4;
         if (np > 0) acc = chain_lds16<R>(cp, np, acc);
@@ -2547,7 +2548,7 @@ void k_gemv_blk(const float* __restrict__ W, const float* __restrict__ x, float*
   const uint32_t n4 = (uint32_t)(blkf / 4), k4 = K >> 2;
   copy_to_lds((lf4*)w, n4 + k4, [=](uint32_t i) { return i < n4 ? src + i : x4 + (i - n4); });
   __syncthreads();
-  const float acc = gemv_lds_t<R>(w, xs, K, 1, pad);
+  const float acc = gemv_lds_t<R, 0>(w, xs, K, 1, pad);
   const uint32_t row = b * R + tid_x();
   if (tid_x() < R && row < M) GW(y)[row] = acc;
 }
@@ -2585,9 +2586,14 @@ __device__ __forceinline__ uint32_t load_runs(gf4* src, lf4* dst, uint32_t n4, u
 template <uint32_t R, uint32_t K>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void k_gemv_pipe(const float* __restrict__ W, const float* __restrict__ x, float* y, uint32_t M) {
-  constexpr uint32_t NC = 4, GP = 64 / R, NW = kThreads / 64, KG = K / 4;
+  constexpr uint32_t NC = 3, GP = 64 / R, NW = kThreads / 64, KG = K / 4;
   constexpr uint32_t NINS = (KG + GP - 1) / GP, N4 = KG * R;
   static_assert(K % 4 == 0 && 64 % R == 0, "shape");
+  // first product instruction of chunk c: NC equal chunks.  Measured at
+  // 1536x576 (MI355X, us per launch): NC 1: 4.80, 2: 4.41, 3: 4.30, 4: 4.57,
+  // 6: 5.14, 9: 7.50; unequal chunks ending on 16-group multiples were
+  // slower than equal ones (4.80-5.06 against 4.56 at NC 4)
+  auto bound = [](uint32_t c) { return NINS * c / NC; };
   extern __shared__ f4 lds_dyn[];
   lf4* w4 = (lf4*)lds_dyn;   // the block, then 64 slots of room
   lf4* xs = w4 + N4 + 64;    // x, then 64 slots of room
@@ -2597,26 +2603,32 @@ void k_gemv_pipe(const float* __restrict__ W, const float* __restrict__ x, float
   gf4* src = G4(W + (size_t)b * R * K);
   uint32_t cnt[NC];
   cnt[0] = load_runs(G4(x), xs, KG, 0, (KG + 63) / 64, wv, NW);
-  cnt[0] += load_runs(src, w4, N4, 0, NINS / NC, wv, NW);
+  cnt[0] += load_runs(src, w4, N4, 0, bound(1), wv, NW);
   for (uint32_t c = 1; c < NC; ++c)
-    cnt[c] = wv == 0 ? 0u : load_runs(src, w4, N4, NINS * c / NC, NINS * (c + 1) / NC, wv - 1,
-                                      NW - 1);
-  wait_vmcnt(cnt[1] + cnt[2] + cnt[3]);
+    cnt[c] = wv == 0 ? 0u : load_runs(src, w4, N4, bound(c), bound(c + 1), wv - 1, NW - 1);
+  uint32_t rest = 0;  // this wave's loads of chunks 1.. (chunk 0 lands first)
+  for (uint32_t c = 1; c < NC; ++c) rest += cnt[c];
+  wait_vmcnt(rest);
   lds_barrier();
-  prod_ins<R>(w4, xs, N4, 1, KG, 0, NINS / NC, wv, NW, pad);
+  prod_ins<R>(w4, xs, N4, 1, KG, 0, bound(1), wv, NW, pad);
   lds_barrier();
   const uint32_t lane = tid_x() & 63, r = lane < R ? lane : R - 1;
   float acc = 0.0f;
   for (uint32_t c = 0; c < NC; ++c) {
-    const uint32_t i0 = NINS * c / NC, i1 = NINS * (c + 1) / NC;
+    const uint32_t i0 = bound(c), i1 = bound(c + 1);
     if (wv == 0) {
-      const uint32_t g0 = i0 * GP, g1 = min(i1 * GP, KG);
-      acc = chain4<8>(w4 + (size_t)g0 * R + r, g1 - g0, R, acc);
+      // 16-group pairs in the assembly loop (its reads past the chunk land
+      // in the next chunk's slots, or past the block in the room after it
+      // and x), then any rest in a ring
+      const uint32_t g0 = i0 * GP, g1 = min(i1 * GP, KG), ng = g1 - g0, np = ng >> 4;
+      const lf4* cp = w4 + (size_t)g0 * R + r;
+      if (np > 0) acc = chain_lds16<R>(cp, np, acc);
+      acc = chain4<8>(cp + (size_t)np * 16 * R, ng - np * 16, R, acc);
     } else if (c + 1 < NC) {
       uint32_t later = 0;
       for (uint32_t c2 = c + 2; c2 < NC; ++c2) later += cnt[c2];
       wait_vmcnt(later);
-      prod_ins<R>(w4, xs, N4, 1, KG, i1, NINS * (c + 2) / NC, wv - 1, NW - 1, pad);
+      prod_ins<R>(w4, xs, N4, 1, KG, i1, bound(c + 2), wv - 1, NW - 1, pad);
     }
     lds_barrier();
   }
@@ -2646,6 +2658,9 @@ void k_gemv_many(const float* __restrict__ W, uint64_t w_per, uint32_t copies, u
   const uint32_t n4 = (uint32_t)(blkf / 4), k4 = K >> 2;
   copy_to_lds((lf4*)w, n4 + k4, [=](uint32_t j) { return j < n4 ? src + j : x4 + (j - n4); });
   __syncthreads();
+  // the ring chain: chain_lds16's fixed registers (v192..v255) would hold
+  // the kernel at one workgroup per CU, and the overlap of one block's copy
+  // with another's chains is what keeps this launch at HBM rate
   const float acc = gemv_lds_t<R>(w, xs, K, 1, pad);
   const uint32_t row = b * R + tid_x();
   if (tid_x() < R && row < M) GW(y + (size_t)i * M)[row] = acc;
@@ -2654,7 +2669,9 @@ void k_gemv_many(const float* __restrict__ W, uint64_t w_per, uint32_t copies, u
 }  // namespace
 
 size_t gemv_blk_lds_bytes(uint32_t K, uint32_t R) {
-  return ((size_t)R * K + K) * 4 + 64 * 16;
+  // the block, x, prod_ins's 64 idle-lane slots, and room for the chains'
+  // reads of 8 groups past the block
+  return ((size_t)R * K + K) * 4 + 64 * 16 + (size_t)8 * R * 16;
 }
 
 template <uint32_t R, uint32_t KC>
@@ -2706,7 +2723,9 @@ static hipError_t launch_gemv_many_t(const float* W, uint64_t w_per, uint32_t co
 hipError_t launch_gemv_many(const float* W, uint64_t w_per, uint32_t copies, uint32_t first,
                             uint32_t n, const float* x, float* y, uint32_t M, uint32_t K,
                             uint32_t R, hipStream_t s) {
-  const size_t lds = gemv_blk_lds_bytes(K, R);
+  // k_gemv_many's ring chain reads nothing past the block: no room after it
+  // (four workgroups per CU at K = 576)
+  const size_t lds = gemv_blk_lds_bytes(K, R) - (size_t)8 * R * 16;
   if (n == 0) return hipSuccess;
   if (K % 4 || lds > 160 * 1024 - 64 || copies == 0 || n > 65535) return hipErrorInvalidValue;
   if (R == 16) return K == 576 ? launch_gemv_many_t<16, 576>(W, w_per, copies, first, n, x, y, M, K, lds, s)
