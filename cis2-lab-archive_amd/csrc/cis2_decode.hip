@@ -2089,8 +2089,10 @@ __device__ __forceinline__ void run_att_mix(const DecodeArgs& a, uint32_t l, uin
   stamp(a, l, P_ATT, t, 2);
 }
 
-// o_proj block + residual h1 = h + o (main.rs:470-472).
-template <bool TR>
+// o_proj block + residual h1 = h + o (main.rs:470-472).  OCD: the chain's
+// form (gemv_lds_t's CD: 0 for the assembly pair loop, which pays off on
+// chunks of 64+ groups, i.e. reduction lengths of 1024 and up).
+template <bool TR, uint32_t OCD = 8>
 __device__ __forceinline__ void run_o(const DecodeArgs& a, uint32_t l, uint32_t t, const Lds& s,
                                      uint32_t tok, lf* wl, bool pre) {
   const LayerW Lw = a.layers[l];
@@ -2111,7 +2113,7 @@ __device__ __forceinline__ void run_o(const DecodeArgs& a, uint32_t l, uint32_t 
                   [=](uint32_t i) { return i < qd ? att + i : hin + (i - qd); });
   }
   stamp(a, l, P_O, t, 1);
-  const float acc = gemv_sel<TR, 8, 32, 18, 8>(a.Ro, wl, x, qd, 1, s.pad);
+  const float acc = gemv_sel<TR, OCD, 32, 18, 8>(a.Ro, wl, x, qd, 1, s.pad);
   stamp(a, l, P_O, t, 3);
   if (tid_x() < nr) put_word(ac.h1 + r0 + tid_x(), hres[tid_x()] + acc, a.epoch);
   stamp(a, l, P_O, t, 2);
@@ -2422,6 +2424,10 @@ constexpr KShape kShapes[] = {
     {1024, 3072, 2048, 128, 16, 8, 16, 8, 32},    // Qwen3-0.6B
 };
 
+// The O projection's chain form for a shape instance: the assembly loop
+// where its reduction length (qd) is 1024 or more, else the ring.
+constexpr uint32_t o_chain_cd(int sh) { return sh > 0 && kShapes[sh].qd >= 1024 ? 0u : 8u; }
+
 __host__ __device__ inline bool shape_matches(const DecodeArgs& a, const KShape& k) {
   return a.H == k.H && a.I == k.I && a.qd == k.qd && a.hd == k.hd && a.Rq == k.Rq &&
          a.Ro == k.Ro && a.Rg == k.Rg && a.Rd == k.Rd && a.Rl == k.Rl;
@@ -2511,7 +2517,7 @@ void k_decode(DecodeArgs a) {
           else if (t < a.natt_s) run_att_score<TR>(a, l, t, s);
           else run_att_mix<TR>(a, l, t - a.natt_s, s);
           break;
-        case P_O: run_o<TR>(a, l, t, s, tok, wl, slots); break;
+        case P_O: run_o<TR, o_chain_cd(SH)>(a, l, t, s, tok, wl, slots); break;
         case P_GU: run_gu<TR>(a, l, t, s, wl, slots); break;
         case P_D: run_d<TR>(a, l, t, s, wl, slots); break;
         default: break;
